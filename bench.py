@@ -1,0 +1,174 @@
+"""Benchmark: synaptic events/s (GSOP/s) and HBM-roofline fraction of the 1M-neuron COBA net.
+
+Workload ("Scaled COBA LIF net"): N = 1,000,000 LIFRef neurons
+(800k E / 200k I), K = 100 fixed-num random targets per neuron (1e8 synapses, int32
+indices + fp32 weights stored per synapse: 0.6 E / 6.7 I), Expon + COBA synapses,
+dt = 0.1 ms.  One bench step = one launch of the persistent runner that advances the
+network 10,000 time steps (the config's run length), continuing from the previous state.
+Connectivity is numpy MT19937 exactly as brainstate/nn/_event_fixedprob.py:165-171.
+
+Reported: value = synaptic events / s over the timed launches (events = spikes x 100);
+roofline = algorithmic bytes per launch (33 B per neuron-step + 4 B per spike + 8 B per
+event) / average launch duration (HIP events on the launch stream) / 8 TB/s;
+cpu_baseline = the C/OpenMP restatement (oracle/c/coba_cpu.c) on this host's cores over a
+bounded sample of the same network.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM = 8.0e12
+METRIC = 'synaptic events/sec (GSOP/s) + % HBM roofline, 1M-neuron COBA, 1 GPU'
+
+
+def build_net(n, n_exc, k, seed=100):
+    idx_e = np.random.RandomState(seed + 1).randint(0, n, size=(n_exc, k)).astype(np.int32)
+    idx_i = np.random.RandomState(seed + 2).randint(0, n, size=(n - n_exc, k)).astype(np.int32)
+    V0 = np.random.RandomState(seed + 3).uniform(-60., -50., n).astype(np.float32)
+    return idx_e, idx_i, V0
+
+
+def lif_bytes(counts, n, k):
+    counts = np.asarray(counts, np.int64)
+    steps = counts.size
+    return int(steps * n * 33 + counts.sum() * 4 + counts.sum() * k * 8)
+
+
+def load_traffic():
+    p = os.path.join(ROOT, 'profiles', 'traffic_coba_lif_1m.json')
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
+
+
+def cpu_baseline(idx_e, idx_i, V0, n_exc, k, budget_s):
+    """C/OpenMP restatement on the host cores; warm 200 steps, then time >= budget_s."""
+    from oracle import cbuild, neuron
+    n = V0.size
+    F = np.float32
+    p = neuron.LIFParams()
+    we = np.full(idx_e.shape, F(0.6))
+    wi = np.full(idx_i.shape, F(6.7))
+    st = dict(V=V0.copy(), ge=np.zeros(n, F), gi=np.zeros(n, F), ref=np.zeros(n, np.int32),
+              spk=np.zeros(n, np.uint8), in_e=np.zeros(n, F), in_i=np.zeros(n, F))
+    threads = min(16, os.cpu_count() or 1)
+    cbuild.coba_lif_run(st, idx_e, idx_i, we, wi, p, n_exc, 200, nthreads=threads)
+    chunk = 100
+    total_spk = 0
+    steps = 0
+    t0 = time.perf_counter()
+    while True:
+        total_spk += cbuild.coba_lif_run(st, idx_e, idx_i, we, wi, p, n_exc, chunk,
+                                         nthreads=threads)
+        steps += chunk
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 20000:
+            break
+    cpu = 'unknown'
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    cpu = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'value': total_spk * k / el / 1e9, 'unit': 'GSOP/s', 'cores': threads,
+            'kind': 'port',
+            'sample': f'{steps} steps of the same 1M-neuron net after 200 warm-up steps '
+                      f'({el:.1f} s, {total_spk} spikes), oracle/c/coba_cpu.c, {cpu}',
+            'ms_per_sim_step': el / steps * 1e3}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=5)
+    ap.add_argument('--warmup', type=int, default=1)
+    ap.add_argument('--sim-steps', type=int, default=10000)
+    ap.add_argument('--n', type=int, default=1_000_000)
+    ap.add_argument('--blocks-per-cu', type=int, default=0)
+    ap.add_argument('--cpu-budget', type=float, default=12.0)
+    ap.add_argument('--no-cpu', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU '
+              f'sharding of this path is a design note, not part of this build.', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+
+    n = args.n
+    n_exc = n * 4 // 5
+    k = 100
+    T = args.sim_steps
+    idx_e, idx_i, V0 = build_net(n, n_exc, k)
+    runner = EINetRunner('lif', n, n_exc, idx_e, idx_i,
+                         np.full(idx_e.shape, np.float32(0.6)), np.full(idx_i.shape,
+                                                                        np.float32(6.7)),
+                         ops.lif_params(), V0, blocks_per_cu=args.blocks_per_cu)
+    counts = torch.zeros(max(args.steps, 1), T, dtype=torch.int32, device='cuda')
+    wcounts = torch.zeros(T, dtype=torch.int32, device='cuda')
+    for _ in range(args.warmup):
+        runner.run(T, counts=wcounts)
+    torch.cuda.synchronize()
+    print(f'[bench] warm-up done: {int(wcounts.sum().item())} spikes in last warm-up launch',
+          file=sys.stderr, flush=True)
+
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        ev[s][0].record(stream)
+        runner.run(T, counts=counts[s])
+        ev[s][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    cnt = counts[:args.steps].cpu().numpy()
+    spikes = int(cnt.sum())
+    events = spikes * k
+    gsops = events / wall / 1e9
+    alg = [lif_bytes(c, n, k) for c in cnt]
+    avg_kern_s = float(np.mean(kern_ms)) / 1e3
+    achieved = float(np.mean(alg)) / avg_kern_s
+    traffic = load_traffic()
+    res = {
+        'metric': METRIC, 'value': gsops, 'unit': 'GSOP/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': wall / args.steps * 1e3, 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32', 'data': 'synthetic',
+        'config': {'workload': 'coba_lif_1m (BASELINE configs[2])', 'neurons': n,
+                   'n_exc': n_exc, 'fan_out': k, 'synapses': n * k, 'dt_ms': 0.1,
+                   'sim_steps_per_bench_step': T,
+                   'weights': 'heterogeneous fp32 per synapse (0.6 E, 6.7 I)',
+                   'firing_frac_per_step': spikes / (args.steps * T * n),
+                   'us_per_sim_step': wall / (args.steps * T) * 1e6,
+                   'sim_s_per_wall_s': args.steps * T * 1e-4 / wall,
+                   'grid_workgroups': runner.grid_blocks},
+        'roofline': {'bound': 'hbm', 'achieved': achieved / 1e9, 'peak': PEAK_HBM / 1e9,
+                     'unit': 'GB/s', 'frac': achieved / PEAK_HBM,
+                     'traffic': None if traffic is None else traffic.get('bytes_per_launch'),
+                     'kernel': 'k_run<LifModel,4,true> (persistent runner)',
+                     'kernel_ms_per_launch': float(np.mean(kern_ms)),
+                     'alg_bytes_per_launch': float(np.mean(alg))},
+    }
+    if not args.no_cpu:
+        print('[bench] timing CPU baseline', file=sys.stderr, flush=True)
+        res['cpu_baseline'] = cpu_baseline(idx_e, idx_i, V0, n_exc, k, args.cpu_budget)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,204 @@
+// N2a / N2b: event-driven sparse mat-vec for fixed-num and CSR connectivity.
+//
+// Scatter (pre-major): waves stride over (active row, 64-synapse chunk) work items; each
+// lane loads one target index and weight (a row's synapses are contiguous, so a wave
+// reads 256 B of indices and 256 B of weights per chunk) and issues one hardware fp32
+// atomic add.  The number of active rows is read on the device, so the launch needs
+// no host synchronisation.
+//
+// Gather (post-major, SELL-64): one wave per slice of 64 posts, lane = post.  Each column
+// step loads 64 consecutive pre indices (256 B), tests the spike of each and adds the
+// weight in column order, so every post accumulates its incoming synapses in ascending
+// (pre, k) order -- bit-identical to a sequential pre-major scatter, with no atomics.
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__global__ __launch_bounds__(kBlock) void k_fill_f32(float* __restrict__ p, int64_t n, float v) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kBlock)
+    p[i] = v;
+}
+
+template <bool kCsr, bool kHet>
+__global__ __launch_bounds__(kBlock) void k_scatter(const int32_t* __restrict__ active,
+                                                    const int32_t* __restrict__ n_active_p,
+                                                    int32_t n_pre,
+                                                    const int32_t* __restrict__ indptr,
+                                                    const int32_t* __restrict__ indices,
+                                                    int32_t k, const float* __restrict__ w,
+                                                    float w_homo, int32_t n_post,
+                                                    float* __restrict__ out) {
+  int32_t na = *n_active_p;
+  na = na < 0 ? 0 : (na > n_pre ? n_pre : na);
+  const int lane = bs_lane();
+  const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE;
+  const int64_t nwaves = (int64_t)gridDim.x * (kBlock / BS_WAVE);
+  if (!kCsr) {
+    const int32_t cpr = (k + BS_WAVE - 1) / BS_WAVE;  // 64-synapse chunks per row
+    const int64_t items = (int64_t)na * cpr;
+    for (int64_t it = wave; it < items; it += nwaves) {
+      const int32_t a = (int32_t)(it / cpr);
+      const int32_t c = (int32_t)(it - (int64_t)a * cpr);
+      const int32_t row = active[a];
+      const int32_t t = c * BS_WAVE + lane;
+      if ((uint32_t)row < (uint32_t)n_pre && t < k) {
+        const int64_t s = (int64_t)row * k + t;
+        const int32_t j = indices[s];
+        const float v = kHet ? w[s] : w_homo;
+        if ((uint32_t)j < (uint32_t)n_post) bs_atomic_add_f32(out + j, v);
+      }
+    }
+  } else {
+    const int32_t nnz = indptr[n_pre];
+    for (int64_t a = wave; a < na; a += nwaves) {
+      const int32_t row = active[a];
+      if ((uint32_t)row >= (uint32_t)n_pre) continue;
+      int32_t beg = indptr[row], end = indptr[row + 1];
+      beg = beg < 0 ? 0 : beg;
+      end = end > nnz ? nnz : end;
+      for (int32_t s = beg + lane; s < end; s += BS_WAVE) {
+        const int32_t j = indices[s];
+        const float v = kHet ? w[s] : w_homo;
+        if ((uint32_t)j < (uint32_t)n_post) bs_atomic_add_f32(out + j, v);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ bool spk_at(const uint8_t* p, int32_t i) { return p[i] != 0; }
+__device__ __forceinline__ bool spk_at(const float* p, int32_t i) { return p[i] != 0.0f; }
+
+template <typename T, bool kHet>
+__global__ __launch_bounds__(kBlock) void k_gather(const T* __restrict__ spk, int32_t n_pre,
+                                                   const int64_t* __restrict__ slice_ptr,
+                                                   const int32_t* __restrict__ sell_pre,
+                                                   const float* __restrict__ sell_w,
+                                                   float w_homo, int32_t n_post,
+                                                   float* __restrict__ out) {
+  constexpr int kU = 8;  // columns in flight per lane
+  const int lane = bs_lane();
+  const int64_t slice = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE;
+  const int64_t n_slices = ((int64_t)n_post + BS_WAVE - 1) / BS_WAVE;
+  if (slice >= n_slices) return;
+  const int64_t beg = slice_ptr[slice];
+  const int64_t ncol = (slice_ptr[slice + 1] - beg) / BS_WAVE;
+  const int32_t* pre = sell_pre + beg + lane;
+  const float* wp = kHet ? sell_w + beg + lane : nullptr;
+  float acc = 0.0f;
+  int64_t c = 0;
+  for (; c + kU <= ncol; c += kU) {
+    int32_t i[kU];
+    bool a[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) i[u] = pre[(c + u) * BS_WAVE];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) a[u] = (uint32_t)i[u] < (uint32_t)n_pre && spk_at(spk, i[u]);
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (a[u]) acc += kHet ? wp[(c + u) * BS_WAVE] : w_homo;
+  }
+  for (; c < ncol; ++c) {
+    const int32_t i = pre[c * BS_WAVE];
+    if ((uint32_t)i < (uint32_t)n_pre && spk_at(spk, i))
+      acc += kHet ? wp[c * BS_WAVE] : w_homo;
+  }
+  const int64_t j = slice * BS_WAVE + lane;
+  if (j < n_post) out[j] = acc;
+}
+
+int grid_for(int64_t work_items_waves) {
+  const int64_t cap = (int64_t)bs_num_cus() * 16;
+  int64_t b = (work_items_waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE);
+  if (b < 1) b = 1;
+  if (b > cap) b = cap;
+  return (int)b;
+}
+
+}  // namespace
+
+int bs_fill_f32(float* p, int64_t n, float v, hipStream_t s) {
+  if (n <= 0) return BS_OK;
+  int64_t b = (n + kBlock - 1) / kBlock;
+  const int64_t cap = (int64_t)bs_num_cus() * 8;
+  if (b > cap) b = cap;
+  k_fill_f32<<<(int)b, kBlock, 0, s>>>(p, n, v);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_event_scatter_f32(const int32_t* active, const int32_t* n_active, int32_t n_pre,
+                                    const int32_t* indptr, const int32_t* indices, int32_t k,
+                                    const float* w, float w_homo, int32_t n_post, float* out,
+                                    int32_t accumulate, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "bs_event_scatter_f32: negative size");
+  BS_CHECK_ARG(indptr != nullptr || k >= 0, "bs_event_scatter_f32: k=%d < 0", k);
+  hipStream_t s = bs_stream(stream);
+  if (n_post > 0) BS_CHECK_ARG(out != nullptr, "bs_event_scatter_f32: out is NULL");
+  if (!accumulate) {
+    int rc = bs_fill_f32(out, n_post, 0.0f, s);
+    if (rc) return rc;
+  }
+  if (n_pre == 0 || n_post == 0 || (indptr == nullptr && k == 0)) return BS_OK;
+  BS_CHECK_ARG(active && n_active && indices, "bs_event_scatter_f32: NULL pointer");
+  const bool het = w != nullptr;
+  if (indptr == nullptr) {
+    const int64_t cpr = ((int64_t)k + BS_WAVE - 1) / BS_WAVE;
+    const int g = grid_for((int64_t)n_pre * cpr);
+    if (het)
+      k_scatter<false, true><<<g, kBlock, 0, s>>>(active, n_active, n_pre, nullptr, indices, k,
+                                                  w, w_homo, n_post, out);
+    else
+      k_scatter<false, false><<<g, kBlock, 0, s>>>(active, n_active, n_pre, nullptr, indices, k,
+                                                   nullptr, w_homo, n_post, out);
+  } else {
+    const int g = grid_for(n_pre);
+    if (het)
+      k_scatter<true, true><<<g, kBlock, 0, s>>>(active, n_active, n_pre, indptr, indices, 0, w,
+                                                 w_homo, n_post, out);
+    else
+      k_scatter<true, false><<<g, kBlock, 0, s>>>(active, n_active, n_pre, indptr, indices, 0,
+                                                  nullptr, w_homo, n_post, out);
+  }
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_event_gather_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                                   const int64_t* slice_ptr, const int32_t* sell_pre,
+                                   const float* sell_w, float w_homo, int32_t n_post, float* out,
+                                   bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "bs_event_gather_f32: negative size");
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_event_gather_f32: unknown spike dtype %d", spk_dtype);
+  if (n_post == 0) return BS_OK;
+  BS_CHECK_ARG(slice_ptr && sell_pre && out && (spk || n_pre == 0),
+               "bs_event_gather_f32: NULL pointer");
+  hipStream_t s = bs_stream(stream);
+  const int64_t n_slices = ((int64_t)n_post + BS_WAVE - 1) / BS_WAVE;
+  const int g = (int)((n_slices + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE));
+  const bool het = sell_w != nullptr;
+  if (spk_dtype == BS_SPK_U8) {
+    const uint8_t* p = (const uint8_t*)spk;
+    if (het)
+      k_gather<uint8_t, true><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, sell_w, w_homo,
+                                                   n_post, out);
+    else
+      k_gather<uint8_t, false><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, nullptr,
+                                                    w_homo, n_post, out);
+  } else {
+    const float* p = (const float*)spk;
+    if (het)
+      k_gather<float, true><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, sell_w, w_homo,
+                                                 n_post, out);
+    else
+      k_gather<float, false><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, nullptr, w_homo,
+                                                  n_post, out);
+  }
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}

@@ -1,0 +1,115 @@
+// N3: fused neuron + synapse state updates, one thread per neuron.
+//
+// Each neuron's state is read once and written once per step (LIF: V, g_e, g_i, ref and
+// the spike byte; HH: V, m, h, n, g_e, g_i and the spike byte).  Pure streaming: the
+// bound is HBM bandwidth.
+#include "neuron_dev.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restrict__ V,
+                                                     float* __restrict__ ge,
+                                                     float* __restrict__ gi,
+                                                     int32_t* __restrict__ ref,
+                                                     const float* __restrict__ in_e,
+                                                     const float* __restrict__ in_i,
+                                                     bs_lif_params p,
+                                                     uint8_t* __restrict__ spk) {
+  for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * kBlock) {
+    float v = V[j], e = ge[j], i = gi[j];
+    int32_t r = ref[j];
+    const bool s = bs_lif_update(p, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
+    V[j] = v;
+    ge[j] = e;
+    gi[j] = i;
+    ref[j] = r;
+    if (spk) spk[j] = s ? 1 : 0;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_hh_init(int32_t n, const float* __restrict__ V,
+                                                    float* __restrict__ m, float* __restrict__ h,
+                                                    float* __restrict__ ng) {
+  for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * kBlock) {
+    const bs_hh_rates r = bs_hh_rate(V[j]);
+    m[j] = r.am / (r.am + r.bm);
+    h[j] = r.ah / (r.ah + r.bh);
+    ng[j] = r.an / (r.an + r.bn);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_hh_step(int32_t n, float* __restrict__ V,
+                                                    float* __restrict__ m, float* __restrict__ h,
+                                                    float* __restrict__ ng,
+                                                    float* __restrict__ ge,
+                                                    float* __restrict__ gi,
+                                                    const float* __restrict__ in_e,
+                                                    const float* __restrict__ in_i,
+                                                    bs_hh_params p, uint8_t* __restrict__ spk) {
+  for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * kBlock) {
+    float v = V[j], mm = m[j], hh = h[j], nn = ng[j], e = ge[j], i = gi[j];
+    const bool s = bs_hh_update(p, v, mm, hh, nn, e, i, in_e ? in_e[j] : 0.0f,
+                                in_i ? in_i[j] : 0.0f);
+    V[j] = v;
+    m[j] = mm;
+    h[j] = hh;
+    ng[j] = nn;
+    ge[j] = e;
+    gi[j] = i;
+    if (spk) spk[j] = s ? 1 : 0;
+  }
+}
+
+int grid(int32_t n) {
+  int64_t b = ((int64_t)n + kBlock - 1) / kBlock;
+  const int64_t cap = (int64_t)bs_num_cus() * 16;
+  return (int)(b < 1 ? 1 : (b > cap ? cap : b));
+}
+
+}  // namespace
+
+extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                                const float* in_e, const float* in_i, const bs_lif_params* p,
+                                uint8_t* spk_out, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0, "bs_coba_lif_step: n=%d < 0", n);
+  BS_CHECK_ARG(p != nullptr, "bs_coba_lif_step: params are NULL");
+  BS_CHECK_ARG(p->tau != 0.0f, "bs_coba_lif_step: tau must be nonzero");
+  if (n == 0) return BS_OK;
+  BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
+  k_lif_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i, *p,
+                                                         spk_out);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng,
+                          bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0, "bs_hh_init: n=%d < 0", n);
+  if (n == 0) return BS_OK;
+  BS_CHECK_ARG(V && m && h && ng, "bs_hh_init: NULL pointer");
+  k_hh_init<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
+                               float* gi, const float* in_e, const float* in_i,
+                               const bs_hh_params* p, uint8_t* spk_out, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0, "bs_coba_hh_step: n=%d < 0", n);
+  BS_CHECK_ARG(p != nullptr, "bs_coba_hh_step: params are NULL");
+  BS_CHECK_ARG(p->C != 0.0f, "bs_coba_hh_step: C must be nonzero");
+  if (n == 0) return BS_OK;
+  BS_CHECK_ARG(V && m && h && ng && ge && gi, "bs_coba_hh_step: NULL state pointer");
+  k_hh_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng, ge, gi, in_e, in_i, *p,
+                                                        spk_out);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}

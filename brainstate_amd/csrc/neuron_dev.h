@@ -1,0 +1,90 @@
+// Per-neuron fused updates (device side), shared by the single-step kernels and the
+// persistent network runners.  Every expression is written in the operation order the
+// reference code evaluates it in (left to right), and the library is built with
+// -ffp-contract=off, so each line is a fixed sequence of correctly rounded fp32 ops.
+#pragma once
+
+#include "bs_math.h"
+#include "common.h"
+
+// brainpy.state Expon + COBA + LIFRef for one neuron; see bs_lif_params in the header.
+// Returns the spike; updates V, ge, gi, ref in place.
+__device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, float& ge,
+                                              float& gi, int32_t& ref, float in_e, float in_i) {
+  ge = ge * p.decay_e + in_e;
+  gi = gi * p.decay_i + in_i;
+  float I = p.I_ext + ge * (p.E_e - V);
+  I = I + gi * (p.E_i - V);
+  const float f = ((p.V_rest - V) + p.R * I) / p.tau;
+  const float J = (-1.0f - p.R * (ge + gi)) / p.tau;
+  const float phi = bs_exprel(p.dt * J);
+  float Vn = V + (p.dt * phi) * f;
+  bool spk = false;
+  if (ref > 0) {
+    Vn = V;
+    ref = ref - 1;
+  } else {
+    spk = Vn >= p.V_th;
+    if (spk) {
+      Vn = p.V_reset;
+      ref = p.ref_steps;
+    } else {
+      ref = 0;
+    }
+  }
+  V = Vn;
+  return spk;
+}
+
+struct bs_hh_rates {
+  float am, bm, ah, bh, an, bn;
+};
+
+// examples/100_hh_neuron_model.py:49-64 (V in mV, rates in 1/ms).
+__device__ __forceinline__ bs_hh_rates bs_hh_rate(float V) {
+  bs_hh_rates r;
+  r.am = 1.0f / bs_exprel((-(V + 40.0f)) / 10.0f);
+  r.bm = 4.0f * bs_expf((-(V + 65.0f)) / 18.0f);
+  r.ah = 0.07f * bs_expf((-(V + 65.0f)) / 20.0f);
+  r.bh = 1.0f / (1.0f + bs_expf((-(V + 35.0f)) / 10.0f));
+  r.an = 0.1f / bs_exprel((-(V + 55.0f)) / 10.0f);
+  r.bn = 0.125f * bs_expf((-(V + 65.0f)) / 80.0f);
+  return r;
+}
+
+__device__ __forceinline__ float bs_hh_gate(float x, float a, float b, float dt) {
+  const float f = a * (1.0f - x) - b * x;
+  const float J = -(a + b);
+  const float phi = bs_exprel(dt * J);
+  return x + (dt * phi) * f;
+}
+
+// Expon + COBA + HH exp-Euler for one neuron (examples/100_hh_neuron_model.py:72-93).
+__device__ __forceinline__ bool bs_hh_update(const bs_hh_params& p, float& V, float& m, float& h,
+                                             float& n, float& ge, float& gi, float in_e,
+                                             float in_i) {
+  ge = ge * p.decay_e + in_e;
+  gi = gi * p.decay_i + in_i;
+  const bs_hh_rates r = bs_hh_rate(V);
+  float I = p.I_ext + ge * (p.E_e - V);
+  I = I + gi * (p.E_i - V);
+  const float gna = p.gNa * m * m * m * h;
+  const float INa = gna * (V - p.ENa);
+  const float n2 = n * n;
+  const float gk = p.gK * n2 * n2;
+  const float IK = gk * (V - p.EK);
+  const float IL = p.gL * (V - p.EL);
+  const float f = ((((-INa) - IK) - IL) + I) / p.C;
+  const float J = ((((-gna) - gk) - p.gL) - (ge + gi)) / p.C;
+  const float phi = bs_exprel(p.dt * J);
+  const float Vn = V + (p.dt * phi) * f;
+  const float mn = bs_hh_gate(m, r.am, r.bm, p.dt);
+  const float hn = bs_hh_gate(h, r.ah, r.bh, p.dt);
+  const float nn = bs_hh_gate(n, r.an, r.bn, p.dt);
+  const bool spk = (V < p.V_th) && (Vn >= p.V_th);
+  V = Vn;
+  m = mn;
+  h = hn;
+  n = nn;
+  return spk;
+}

@@ -1,0 +1,184 @@
+"""Operator-level Python API over the C ABI (torch device tensors in, device tensors out).
+
+These are the building blocks the brainstate-compatible layers call; each maps onto one
+C entry point of include/brainstate_amd.h and raises ``NativeError`` on failure.
+"""
+import numpy as np
+import torch
+
+from . import _native as N
+
+_WS_CACHE = {}
+
+
+def _spk_dtype(spk):
+    if spk.dtype in (torch.bool, torch.uint8, torch.int8):
+        return N.BS_SPK_U8
+    if spk.dtype == torch.float32:
+        return N.BS_SPK_F32
+    raise TypeError(f'spike tensor dtype {spk.dtype} not supported (bool/uint8/float32)')
+
+
+def _spk_view(spk):
+    spk = spk.contiguous()
+    if spk.dtype == torch.bool:
+        spk = spk.view(torch.uint8)
+    return spk
+
+
+def compact_workspace(n, device):
+    """Zero-filled workspace for bs_spike_compact, cached per (device, stream, size)."""
+    nbytes = int(N.lib().bs_spike_compact_workspace_size(int(n)))
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = ws
+    return ws
+
+
+def spike_compact(spk):
+    """Ascending indices of nonzero spikes -> (idx int32 [n] (first count valid), count int32 [1])."""
+    N.require_gpu()
+    spk = _spk_view(spk)
+    n = spk.numel()
+    dev = spk.device
+    idx = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    cnt = torch.empty(1, dtype=torch.int32, device=dev)
+    ws = compact_workspace(n, dev)
+    N.check(N.lib().bs_spike_compact(N.ptr(spk), _spk_dtype(spk), n, N.ptr(idx), N.ptr(cnt),
+                                     N.ptr(ws), N.stream_handle(dev)), 'bs_spike_compact')
+    return idx, cnt
+
+
+def event_scatter(active, n_active, indices, w, n_post, k=None, indptr=None, out=None,
+                  accumulate=False):
+    """Pre-major event mat-vec over active rows (fixed-num if indptr is None)."""
+    dev = indices.device
+    n_pre = (indices.shape[0] if indptr is None else indptr.numel() - 1)
+    if indptr is None:
+        k = indices.shape[1] if indices.dim() == 2 else int(k)
+    homo = not torch.is_tensor(w) or w.numel() == 1
+    w_homo = float(w) if homo else 0.0
+    if out is None:
+        out = torch.empty(n_post, dtype=torch.float32, device=dev)
+        accumulate = False
+    N.check(N.lib().bs_event_scatter_f32(
+        N.ptr(active), N.ptr(n_active), int(n_pre), N.ptr(indptr), N.ptr(indices.contiguous()),
+        int(k or 0), None if homo else N.ptr(w.contiguous()), w_homo, int(n_post), N.ptr(out),
+        1 if accumulate else 0, N.stream_handle(dev)), 'bs_event_scatter_f32')
+    return out
+
+
+def event_gather(spk, sell, out=None):
+    """Post-major deterministic gather; ``sell`` from :func:`build_sell`."""
+    spk = _spk_view(spk)
+    dev = spk.device
+    n_post = sell['n_post']
+    if out is None:
+        out = torch.empty(n_post, dtype=torch.float32, device=dev)
+    w = sell.get('w')
+    N.check(N.lib().bs_event_gather_f32(
+        N.ptr(spk), _spk_dtype(spk), int(sell['n_pre']), N.ptr(sell['slice_ptr']),
+        N.ptr(sell['pre']), N.ptr(w), float(sell.get('w_homo', 0.0)), int(n_post), N.ptr(out),
+        N.stream_handle(dev)), 'bs_event_gather_f32')
+    return out
+
+
+def build_sell(indptr, indices, n_pre, n_post, w=None, w_homo=0.0, device='cuda'):
+    """Host-side SELL-64 post-major layout from a pre-major CSR (numpy arrays).
+
+    Incoming synapses of each post are kept in ascending (pre, k) order (a stable sort on
+    the target index), so the gather reproduces a sequential pre-major scatter.
+    """
+    indptr = np.asarray(indptr, dtype=np.int64)
+    indices = np.asarray(indices, dtype=np.int64)
+    nnz = indices.size
+    if nnz and (indices.min() < 0 or indices.max() >= n_post):
+        raise ValueError('connectivity index out of range [0, n_post)')
+    pre = np.repeat(np.arange(n_pre, dtype=np.int32), np.diff(indptr))
+    order = np.argsort(indices, kind='stable')
+    tgt_sorted = indices[order]
+    counts = np.bincount(indices, minlength=n_post).astype(np.int64)
+    n_slices = (n_post + 63) // 64
+    pad_counts = np.zeros(n_slices * 64, np.int64)
+    pad_counts[:n_post] = counts
+    width = pad_counts.reshape(n_slices, 64).max(axis=1)
+    slice_ptr = np.zeros(n_slices + 1, np.int64)
+    np.cumsum(width * 64, out=slice_ptr[1:])
+    total = int(slice_ptr[-1])
+    sell_pre = np.full(total, -1, np.int32)
+    sell_w = np.zeros(total, np.float32) if w is not None else None
+    post_start = np.zeros(n_post + 1, np.int64)
+    np.cumsum(counts, out=post_start[1:])
+    # rank of each synapse within its post's list
+    rank = np.arange(nnz, dtype=np.int64) - post_start[tgt_sorted]
+    s = tgt_sorted // 64
+    lane = tgt_sorted - s * 64
+    pos = slice_ptr[s] + rank * 64 + lane
+    sell_pre[pos] = pre[order]
+    if w is not None:
+        sell_w[pos] = np.asarray(w, np.float32).reshape(-1)[order]
+    t = lambda a: torch.from_numpy(a).to(device)
+    return dict(n_pre=n_pre, n_post=n_post, slice_ptr=t(slice_ptr), pre=t(sell_pre),
+                w=None if sell_w is None else t(sell_w), w_homo=float(w_homo),
+                padded=total, nnz=nnz)
+
+
+def event_dense(spk, W, float_as_event=True, out=None):
+    """spk [B, n_in] (or [n_in]) x W [n_in, n_out] -> [B, n_out]."""
+    squeeze = spk.dim() == 1
+    s2 = _spk_view(spk.reshape(1, -1) if squeeze else spk)
+    B, n_in = s2.shape
+    n_out = W.shape[1]
+    if out is None:
+        out = torch.empty(B, n_out, dtype=torch.float32, device=W.device)
+    N.check(N.lib().bs_event_dense_f32(N.ptr(s2), _spk_dtype(s2), B, n_in, N.ptr(W.contiguous()),
+                                       n_out, 1 if float_as_event else 0, N.ptr(out),
+                                       N.stream_handle(W.device)), 'bs_event_dense_f32')
+    return out[0] if squeeze else out
+
+
+def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., I_ext=20.,
+               E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1):
+    q = float(tau_ref) / float(dt)
+    ref_steps = max(int(np.ceil(q - 1e-9)) - 1, 0)
+    return N.LifParams(V_rest, V_th, V_reset, tau, R, I_ext, E_e, E_i, dt,
+                       float(np.float32(np.exp(-dt / tau_e))),
+                       float(np.float32(np.exp(-dt / tau_i))), ref_steps)
+
+
+def hh_params(ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03, C=1.0, V_th=20.,
+              I_ext=0., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.05):
+    return N.HhParams(ENa, gNa, EK, gK, EL, gL, C, V_th, I_ext, E_e, E_i, dt,
+                      float(np.float32(np.exp(-dt / tau_e))),
+                      float(np.float32(np.exp(-dt / tau_i))))
+
+
+def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None):
+    n = V.numel()
+    if spk_out is None:
+        spk_out = torch.empty(n, dtype=torch.uint8, device=V.device)
+    N.check(N.lib().bs_coba_lif_step(n, N.ptr(V), N.ptr(ge), N.ptr(gi), N.ptr(ref), N.ptr(in_e),
+                                     N.ptr(in_i), ctypes_ref(params), N.ptr(spk_out),
+                                     N.stream_handle(V.device)), 'bs_coba_lif_step')
+    return spk_out
+
+
+def hh_init(V, m, h, n):
+    N.check(N.lib().bs_hh_init(V.numel(), N.ptr(V), N.ptr(m), N.ptr(h), N.ptr(n),
+                               N.stream_handle(V.device)), 'bs_hh_init')
+
+
+def coba_hh_step(V, m, h, n, ge, gi, in_e, in_i, params, spk_out=None):
+    if spk_out is None:
+        spk_out = torch.empty(V.numel(), dtype=torch.uint8, device=V.device)
+    N.check(N.lib().bs_coba_hh_step(V.numel(), N.ptr(V), N.ptr(m), N.ptr(h), N.ptr(n), N.ptr(ge),
+                                    N.ptr(gi), N.ptr(in_e), N.ptr(in_i), ctypes_ref(params),
+                                    N.ptr(spk_out), N.stream_handle(V.device)), 'bs_coba_hh_step')
+    return spk_out
+
+
+def ctypes_ref(s):
+    import ctypes
+    return ctypes.byref(s)

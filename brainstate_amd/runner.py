@@ -1,0 +1,100 @@
+"""Device-resident E/I network runner over the persistent C-ABI loop (bs_coba_*_run).
+
+Holds connectivity, neuron state and the double-buffered event accumulators in HBM and
+advances the network ``steps`` at a time in one launch.  This is the compiled form of
+``brainstate.transform.for_loop(net.update, times)`` for the E/I nets of
+examples/105_COBA_HH_2007_braincell.py:54-91 and examples/400_CUBA_2005_bpu.py:36-66.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _native as N
+from . import ops
+
+
+class EINetRunner:
+    """E/I network: neurons [0, n_exc) project with (idx_e, w_e), [n_exc, n) with (idx_i, w_i).
+
+    ``model`` is 'lif' (Expon + COBA + LIFRef) or 'hh' (Expon + COBA + Hodgkin-Huxley).
+    ``w_e``/``w_i`` are scalars (homogeneous) or [n_pre, K] arrays (heterogeneous).
+    """
+
+    def __init__(self, model, n, n_exc, idx_e, idx_i, w_e, w_i, params, V0, device='cuda',
+                 blocks_per_cu=0):
+        N.require_gpu()
+        self.model = model
+        self.n, self.n_exc = int(n), int(n_exc)
+        self.device = torch.device(device)
+        dev = self.device
+        idx_e = np.asarray(idx_e, np.int32).reshape(self.n_exc, -1)
+        idx_i = np.asarray(idx_i, np.int32).reshape(self.n - self.n_exc, -1)
+        for name, idx in (('idx_e', idx_e), ('idx_i', idx_i)):
+            if idx.size and (idx.min() < 0 or idx.max() >= self.n):
+                raise ValueError(f'{name}: target index out of range [0, {self.n})')
+        self.k_e, self.k_i = idx_e.shape[1], idx_i.shape[1]
+        self.idx_e = torch.from_numpy(idx_e).to(dev)
+        self.idx_i = torch.from_numpy(idx_i).to(dev)
+        het = np.ndim(w_e) > 0 or np.ndim(w_i) > 0
+        if het:
+            we = np.broadcast_to(np.asarray(w_e, np.float32), idx_e.shape)
+            wi = np.broadcast_to(np.asarray(w_i, np.float32), idx_i.shape)
+            self.w_e = torch.from_numpy(np.ascontiguousarray(we)).to(dev)
+            self.w_i = torch.from_numpy(np.ascontiguousarray(wi)).to(dev)
+            self.w_e_homo = self.w_i_homo = 0.0
+        else:
+            self.w_e = self.w_i = None
+            self.w_e_homo, self.w_i_homo = float(np.float32(w_e)), float(np.float32(w_i))
+        self.params = params
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.acc = torch.zeros(2, 2, self.n, **f32)
+        self.spk = torch.zeros(self.n, dtype=torch.uint8, device=dev)
+        self.phase = 0
+        V0 = torch.as_tensor(np.asarray(V0, np.float32)).to(dev)
+        if model == 'lif':
+            self.state = dict(V=V0.clone(), ge=torch.zeros(self.n, **f32),
+                              gi=torch.zeros(self.n, **f32),
+                              ref=torch.zeros(self.n, dtype=torch.int32, device=dev))
+        elif model == 'hh':
+            self.state = dict(V=V0.clone(), m=torch.empty(self.n, **f32),
+                              h=torch.empty(self.n, **f32), n=torch.empty(self.n, **f32),
+                              ge=torch.zeros(self.n, **f32), gi=torch.zeros(self.n, **f32))
+            ops.hh_init(self.state['V'], self.state['m'], self.state['h'], self.state['n'])
+        else:
+            raise ValueError(f'unknown model {model!r}')
+        self.ws = torch.zeros(max(int(N.lib().bs_net_workspace_size()), 256), dtype=torch.uint8,
+                              device=dev)
+        self._net = N.Net(self.n, self.n_exc, self.k_e, self.k_i,
+                          self.idx_e.data_ptr(), None if self.w_e is None else self.w_e.data_ptr(),
+                          self.w_e_homo,
+                          self.idx_i.data_ptr(), None if self.w_i is None else self.w_i.data_ptr(),
+                          self.w_i_homo, self.acc.data_ptr(), self.spk.data_ptr(),
+                          int(blocks_per_cu))
+
+    @property
+    def grid_blocks(self):
+        return int(N.lib().bs_net_grid_blocks(ctypes.byref(self._net)))
+
+    def run(self, steps, counts=None, hashes=None, raster=None):
+        """Advance ``steps`` steps in one launch.  Optional int32/uint32 [steps] outputs and a
+        uint8 [steps, n] raster are filled on the device."""
+        s = self.state
+        stream = N.stream_handle(self.device)
+        if self.model == 'lif':
+            st = N.LifState(s['V'].data_ptr(), s['ge'].data_ptr(), s['gi'].data_ptr(),
+                            s['ref'].data_ptr())
+            rc = N.lib().bs_coba_lif_run(ctypes.byref(self._net), ctypes.byref(st),
+                                         ctypes.byref(self.params), int(steps), self.phase,
+                                         N.ptr(counts), N.ptr(hashes), N.ptr(raster),
+                                         N.ptr(self.ws), stream)
+            N.check(rc, 'bs_coba_lif_run')
+        else:
+            st = N.HhState(s['V'].data_ptr(), s['m'].data_ptr(), s['h'].data_ptr(),
+                           s['n'].data_ptr(), s['ge'].data_ptr(), s['gi'].data_ptr())
+            rc = N.lib().bs_coba_hh_run(ctypes.byref(self._net), ctypes.byref(st),
+                                        ctypes.byref(self.params), int(steps), self.phase,
+                                        N.ptr(counts), N.ptr(hashes), N.ptr(raster),
+                                        N.ptr(self.ws), stream)
+            N.check(rc, 'bs_coba_hh_run')
+        self.phase = (self.phase + int(steps)) & 1

@@ -1,0 +1,164 @@
+/*
+ * brainstate_amd -- C ABI of the MI355X (gfx950) engine for brainstate's spiking-network step.
+ *
+ * Plain C types only: device pointers, sizes, a stream handle and int status codes.
+ * All array pointers are device memory owned by the caller; the library never frees
+ * caller memory and keeps no pointer across calls.  Work is enqueued on the given
+ * stream (a hipStream_t passed as void*; NULL = the null stream) with no host
+ * synchronisation.  A nonzero status comes with a thread-local message from
+ * bs_last_error().
+ *
+ * Each entry point names the reference interface it replaces (file:line under the
+ * chaobrain/brainstate 0.5.4 tree).  The arithmetic of those interfaces lives in the
+ * un-vendored dependencies brainevent (event operators) and brainpy.state (neuron and
+ * synapse models); the reference reaches them at the cited call sites.
+ */
+#ifndef BRAINSTATE_AMD_H_
+#define BRAINSTATE_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define BS_API __attribute__((visibility("default")))
+#else
+#define BS_API
+#endif
+
+typedef void* bs_stream_t;
+
+enum bs_status {
+  BS_OK = 0,
+  BS_ERR_INVALID = 1,     /* bad shape, dtype, pointer or parameter */
+  BS_ERR_LAUNCH = 2,      /* HIP runtime / launch failure */
+  BS_ERR_UNSUPPORTED = 3  /* e.g. the device cannot co-schedule a persistent grid */
+};
+
+/* Spike vector element types accepted by the event operators: nonzero = one event
+ * (brainevent.EventArray semantics, brainstate/nn/_event_fixedprob.py:249-252). */
+enum bs_spike_dtype { BS_SPK_U8 = 0, BS_SPK_F32 = 1 };
+
+BS_API const char* bs_last_error(void);
+BS_API int bs_version(void);
+
+/* ---------------------------------------------------------------- N1 spike compaction
+ * Replaces the zero-skipping inside brainevent's event kernels (no reference symbol;
+ * the spikes reach it from brainstate/nn/_event_fixedprob.py:251).
+ * idx_out[0..count) = ascending indices i with spk[i] != 0; *count_out = count.
+ * `workspace` holds bs_spike_compact_workspace_size(n) bytes, zero-filled once when
+ * allocated; each call leaves it ready for the next.  Calls that share a workspace
+ * must be ordered on one stream. n < 2^30. */
+BS_API size_t bs_spike_compact_workspace_size(int32_t n);
+BS_API int bs_spike_compact(const void* spk, int32_t spk_dtype, int32_t n, int32_t* idx_out,
+                     int32_t* count_out, void* workspace, bs_stream_t stream);
+
+/* ---------------------------------------------------------------- N2a event scatter
+ * Replaces `EventArray(spk) @ FixedPostNumConn((w, idx))` and `... @ CSR((w, idx, indptr))`
+ * (brainstate/nn/_event_fixedprob.py:176-181,192,202-205,249-252).
+ * For each active pre row r = active[a], a < *n_active, adds w of each synapse of r to
+ * out[target].  Rows: fixed-num (indptr == NULL) -> synapses r*k .. r*k+k-1; CSR ->
+ * indptr[r] .. indptr[r+1]-1 (nnz = indptr[n_pre]).  w == NULL -> homogeneous w_homo.
+ * accumulate == 0 zero-fills out[n_post] first.  fp32 atomics: the order of additions
+ * is unspecified (sums of one repeated weight value are order-free and exact).
+ * Out-of-range rows / targets are skipped. */
+BS_API int bs_event_scatter_f32(const int32_t* active, const int32_t* n_active, int32_t n_pre,
+                         const int32_t* indptr, const int32_t* indices, int32_t k,
+                         const float* w, float w_homo, int32_t n_post, float* out,
+                         int32_t accumulate, bs_stream_t stream);
+
+/* ---------------------------------------------------------------- N2b event gather
+ * Same operator as N2a, post-major and deterministic (no atomics).  Layout SELL-64:
+ * posts are grouped in slices of 64; slice s stores its incoming synapses column-major
+ * at sell_pre[slice_ptr[s] + c*64 + lane] (lane = post - 64*s), columns in ascending
+ * (pre, k) order, padded with -1.  out[j] = 0.0f + the weights of active synapses in
+ * that order, i.e. bit-identical to a sequential pre-major scatter.
+ * sell_w == NULL -> homogeneous w_homo.  n_slices = ceil(n_post / 64). */
+BS_API int bs_event_gather_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                        const int64_t* slice_ptr, const int32_t* sell_pre,
+                        const float* sell_w, float w_homo, int32_t n_post, float* out,
+                        bs_stream_t stream);
+
+/* ---------------------------------------------------------------- N2c event x dense
+ * Replaces `EventArray(spk) @ W` / `spk @ W` of EventLinear
+ * (brainstate/nn/_event_linear.py:99-102).  spk [batch, n_in], W [n_in, n_out] row-major,
+ * out [batch, n_out].  float_as_event != 0: out[b] = sum of rows W[i] with spk[b,i] != 0,
+ * added in ascending i; otherwise out[b] = sum_i spk[b,i] * W[i] (same order). */
+BS_API int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t batch, int32_t n_in,
+                       const float* W, int32_t n_out, int32_t float_as_event, float* out,
+                       bs_stream_t stream);
+
+/* ---------------------------------------------------------------- N3 fused updates
+ * LIF / LIFRef membrane with Expon synapses and COBA output -- the per-step elementwise
+ * work of brainpy.state LIFRef + Expon + COBA + AlignPostProj as driven by
+ * brainstate/nn/_exp_euler.py:226-249 (used e.g. by examples/105_COBA_HH_2007_braincell.py:62-82).
+ *   g_e = g_e*decay_e + in_e;  g_i = g_i*decay_i + in_i
+ *   I = I_ext + g_e*(E_e - V) + g_i*(E_i - V)
+ *   V' = V + (dt*exprel(dt*J))*f,  f = ((V_rest - V) + R*I)/tau,  J = (-1 - R*(g_e+g_i))/tau
+ *   refractory (ref > 0): V held, ref -= 1;  else spike = V' >= V_th -> V' = V_reset,
+ *   ref = ref_steps. */
+typedef struct {
+  float V_rest, V_th, V_reset, tau, R, I_ext, E_e, E_i, dt, decay_e, decay_i;
+  int32_t ref_steps;
+} bs_lif_params;
+
+BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                     const float* in_e, const float* in_i, const bs_lif_params* p,
+                     uint8_t* spk_out, bs_stream_t stream);
+
+/* Hodgkin-Huxley with Expon synapses and COBA output (examples/100_hh_neuron_model.py:25-93):
+ * rates from the old V; V, m, h, n each by exp-Euler; spike = (V < V_th) & (V' >= V_th). */
+typedef struct {
+  float ENa, gNa, EK, gK, EL, gL, C, V_th, I_ext, E_e, E_i, dt, decay_e, decay_i;
+} bs_hh_params;
+
+/* Gates at steady state for V (examples/100_hh_neuron_model.py:66-70). */
+BS_API int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng, bs_stream_t stream);
+BS_API int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge, float* gi,
+                    const float* in_e, const float* in_i, const bs_hh_params* p,
+                    uint8_t* spk_out, bs_stream_t stream);
+
+/* ---------------------------------------------------------------- whole-loop runners
+ * Replace `brainstate.transform.for_loop(net.update, times)` over an E/I network
+ * (brainstate/transform/_loop_collect_return.py:487-572 -> jax.lax.scan at :268) for the
+ * two projections E: neurons [0, n_exc) -> all n, I: [n_exc, n) -> all n, each
+ * fixed-num (brainstate/nn/_event_fixedprob.py:102-205).  One persistent launch runs
+ * `steps` network steps; per step: inputs from the previous step's spikes -> fused
+ * neuron update -> compaction -> scatter of the new spikes into the next step's
+ * accumulators, then one grid barrier.
+ * acc is [2 phases][2 (E, I)][n] fp32: acc[phase] holds the inputs for the next step
+ * (zero at the start of a simulation), acc[phase^1] must be zero.  After the call the
+ * pending inputs are in acc[(phase + steps) & 1].
+ * counts_out[t] / hash_out[t] (nullable): number of spikes and the order-free digest
+ * sum_i mix32(i) mod 2^32 of step t; raster_out [steps, n] uint8 (nullable). */
+typedef struct {
+  int32_t n, n_exc, k_e, k_i;
+  const int32_t* idx_e; const float* w_e; float w_e_homo;   /* [n_exc, k_e] */
+  const int32_t* idx_i; const float* w_i; float w_i_homo;   /* [n - n_exc, k_i] */
+  float* acc;                                               /* [2][2][n] */
+  uint8_t* spk;                                             /* [n] last step's spikes */
+  int32_t blocks_per_cu;                                    /* 0 = library default */
+} bs_net;
+
+typedef struct { float* V; float* ge; float* gi; int32_t* ref; } bs_lif_state;
+typedef struct { float* V; float* m; float* h; float* n; float* ge; float* gi; } bs_hh_state;
+
+BS_API size_t bs_net_workspace_size(void);  /* zero-filled once when allocated */
+BS_API int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p,
+                    int32_t steps, int32_t phase, int32_t* counts_out, uint32_t* hash_out,
+                    uint8_t* raster_out, void* workspace, bs_stream_t stream);
+BS_API int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,
+                   int32_t steps, int32_t phase, int32_t* counts_out, uint32_t* hash_out,
+                   uint8_t* raster_out, void* workspace, bs_stream_t stream);
+
+/* Grid size (workgroups) the runners use for this net on the current device. */
+BS_API int bs_net_grid_blocks(const bs_net* net);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BRAINSTATE_AMD_H_ */

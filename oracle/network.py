@@ -1,0 +1,116 @@
+"""Whole E/I network loops (test infrastructure only).
+
+Per-step order of the reference's E/I nets (examples/105_COBA_HH_2007_braincell.py:76-82,
+examples/400_CUBA_2005_bpu.py:60-65, docs/tutorials/brain_dynamics/04_building_an_snn.ipynb
+cell 11): the spikes of the previous step drive the E projection (pre = neurons
+[0, n_exc)) and the I projection (pre = [n_exc, N)), each an event mat-vec onto all N
+neurons; then the neurons advance with those inputs (Expon decay + delta input,
+COBA current, membrane exp-Euler, spike).  Connectivity per projection is
+``EventFixedProb(n_pre, N, conn_num, w, seed)`` (brainstate/nn/_event_fixedprob.py:102-200).
+"""
+import numpy as np
+
+from . import conn as _conn
+from . import event as _event
+from . import neuron as _neuron
+
+F = np.float32
+
+
+def repeated_sum_table(w, max_count):
+    """t[c] = w + w + ... (c times) in fp32, sequentially; order-free for one value."""
+    t = np.zeros(max_count + 1, dtype=F)
+    s = F(0.0)
+    w = F(w)
+    for c in range(1, max_count + 1):
+        s = F(s + w)
+        t[c] = s
+    return t
+
+
+class Projection:
+    """One fixed-num projection (pre block of the neuron vector -> all N)."""
+
+    def __init__(self, pre_lo, pre_hi, n_post, conn_num, w, seed, het=False):
+        self.pre_lo, self.pre_hi, self.n_post = pre_lo, pre_hi, n_post
+        self.k = _conn.conn_num_from(conn_num, n_post)
+        self.idx, _ = _conn.fixed_num_indices(pre_hi - pre_lo, n_post, self.k, seed)
+        self.w_scalar = F(w)
+        self.het = het
+        self.w = np.full(self.idx.shape, F(w), F) if het else F(w)
+        self._table = None
+
+    def __call__(self, spk_pre):
+        if not self.het or np.all(self.w == self.w_scalar):
+            # one repeated weight value: counts + repeated-sum table (exact, order-free)
+            act = np.flatnonzero(spk_pre)
+            counts = np.bincount(self.idx[act].reshape(-1), minlength=self.n_post)
+            mc = int(counts.max()) if counts.size else 0
+            if self._table is None or self._table.size <= mc:
+                self._table = repeated_sum_table(self.w_scalar, max(mc, 64))
+            return self._table[counts]
+        return _event.scatter_fixed(spk_pre, self.idx, self.w, self.n_post)
+
+
+def run_coba_lif(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=None):
+    """COBA LIFRef network.  Returns dict(raster [T,N] bool, counts [T], final state)."""
+    N = V0.size
+    if init is None:
+        V = np.asarray(V0, F).copy()
+        ge = np.zeros(N, F)
+        gi = np.zeros(N, F)
+        ref = np.zeros(N, np.int32)
+        spk = np.zeros(N, bool)
+    else:
+        V, ge, gi, ref, spk = [np.array(a) for a in init]
+    raster = np.zeros((steps, N), bool) if record_raster else None
+    counts = np.zeros(steps, np.int64)
+    for t in range(steps):
+        in_e = proj_e(spk[:n_exc])
+        in_i = proj_i(spk[n_exc:])
+        V, ge, gi, ref, spk = _neuron.coba_lif_step(V, ge, gi, ref, in_e, in_i, p)
+        if record_raster:
+            raster[t] = spk
+        counts[t] = spk.sum()
+    return dict(raster=raster, counts=counts, V=V, ge=ge, gi=gi, ref=ref, spk=spk)
+
+
+def run_coba_hh(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=None):
+    """COBA Hodgkin-Huxley network (exp-Euler gates)."""
+    N = V0.size
+    if init is None:
+        V = np.asarray(V0, F).copy()
+        m, h, n = _neuron.hh_init(V)
+        ge = np.zeros(N, F)
+        gi = np.zeros(N, F)
+        spk = np.zeros(N, bool)
+    else:
+        V, m, h, n, ge, gi, spk = [np.array(a) for a in init]
+    raster = np.zeros((steps, N), bool) if record_raster else None
+    counts = np.zeros(steps, np.int64)
+    for t in range(steps):
+        in_e = proj_e(spk[:n_exc])
+        in_i = proj_i(spk[n_exc:])
+        V, m, h, n, ge, gi, spk = _neuron.hh_step(V, m, h, n, ge, gi, in_e, in_i, p)
+        if record_raster:
+            raster[t] = spk
+        counts[t] = spk.sum()
+    return dict(raster=raster, counts=counts, V=V, m=m, h=h, n=n, ge=ge, gi=gi, spk=spk)
+
+
+def spike_hash(spk):
+    """Order-free 32-bit digest of a spike set: sum over spiking i of mix32(i) mod 2^32."""
+    i = np.flatnonzero(spk).astype(np.uint64)
+    return int(np.sum(mix32(i), dtype=np.uint64) & np.uint64(0xFFFFFFFF))
+
+
+def mix32(i):
+    """32-bit integer hash (Murmur3 finaliser) on uint64 arrays, result < 2^32."""
+    M = np.uint64(0xFFFFFFFF)
+    x = np.asarray(i, np.uint64) & M
+    x = (x ^ (x >> np.uint64(16))) & M
+    x = (x * np.uint64(0x85EBCA6B)) & M
+    x = (x ^ (x >> np.uint64(13))) & M
+    x = (x * np.uint64(0xC2B2AE35)) & M
+    x = (x ^ (x >> np.uint64(16))) & M
+    return x

@@ -1,0 +1,151 @@
+"""Neuron and synapse state updates in fp32 (test infrastructure only).
+
+exp-Euler, brainstate/nn/_exp_euler.py:226-249:
+    J = d f / d x (diagonal, from ``vector_grad``),  phi = exprel(dt*J),
+    x' = x + (dt*phi)*f(x)                      (left-to-right, as ``state + dt*phi*drift``)
+Pinned by the known answers of brainstate/nn/_exp_euler_test.py:29-97,316-339 and by the
+one-step LIF value printed in docs/tutorials/brain_dynamics/04_building_an_snn.ipynb
+cell 5 (V_rest=-52, tau=10 ms, V0=-60, I=8, dt=0.1 ms -> -59.84079742 mV).
+
+The models themselves (LIF / LIFRef / Expon / COBA / AlignPostProj) live in the
+un-vendored ``brainpy.state``; their step ordering and refractory rule are restated
+from the equations and are **parity unpinned** beyond the checks above:
+  * Expon synapse: exact solution of dg/dt = -g/tau plus the delta input of the
+    step's event mat-vec, ``g' = g*exp(-dt/tau) + in`` (exp-Euler of a linear ODE is
+    this exponential; the decay factor is computed once in float64 and rounded).
+  * COBA output: ``I = I_ext + g_e*(E_e - V) + g_i*(E_i - V)`` (sum_current_inputs
+    order: external input first, then projections in registration order).
+  * LIF membrane: ``f = ((V_rest - V) + R*I)/tau``, ``J = (-1 - R*(g_e+g_i))/tau``.
+  * LIFRef: a neuron is refractory for ``ref_steps`` steps after the spike step
+    (the steps with 0 < t - t_spike < tau_ref on the dt grid); V is held there.
+    Spike when V' >= V_th; hard reset V' = V_reset.
+HH (examples/100_hh_neuron_model.py:49-93, reference-held): rates from the old V, V
+and the gates each by exp-Euler from the old state, spike = (V < V_th) & (V' >= V_th).
+"""
+import numpy as np
+
+from .bsmath import expf, exprel
+
+F = np.float32
+I32 = np.int32
+
+
+def exp_euler_step(f, jac, x, dt):
+    """Generic exp-Euler with a closed-form diagonal Jacobian (fp32 unless x is f64)."""
+    x = np.asarray(x)
+    dt = x.dtype.type(dt)
+    if x.dtype == np.float64:
+        z = dt * jac(x)
+        phi = np.where(z == 0, 1.0, np.expm1(z) / np.where(z == 0, 1.0, z))
+        return x + dt * phi * f(x)
+    z = (dt * np.asarray(jac(x), F)).astype(F)
+    phi = exprel(z)
+    return (x + (dt * phi).astype(F) * np.asarray(f(x), F)).astype(F)
+
+
+def decay_factor(dt, tau):
+    return F(np.exp(-float(dt) / float(tau)))
+
+
+def ref_steps(tau_ref, dt):
+    """Number of steps after a spike step with 0 < k*dt < tau_ref."""
+    q = float(tau_ref) / float(dt)
+    n = int(np.ceil(q - 1e-9)) - 1
+    return max(n, 0)
+
+
+class LIFParams:
+    def __init__(self, V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5.,
+                 I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1):
+        self.V_rest, self.V_th, self.V_reset = F(V_rest), F(V_th), F(V_reset)
+        self.tau, self.R, self.I_ext = F(tau), F(R), F(I_ext)
+        self.E_e, self.E_i = F(E_e), F(E_i)
+        self.dt = F(dt)
+        self.de = decay_factor(dt, tau_e)
+        self.di = decay_factor(dt, tau_i)
+        self.ref_steps = I32(ref_steps(tau_ref, dt))
+
+
+def lif_membrane(V, ge, gi, p):
+    """One exp-Euler step of the COBA LIF membrane (no refractoriness, no reset)."""
+    I = (p.I_ext + ge * (p.E_e - V)).astype(F)
+    I = (I + gi * (p.E_i - V)).astype(F)
+    f = (((p.V_rest - V) + p.R * I) / p.tau).astype(F)
+    J = ((F(-1.0) - p.R * (ge + gi)) / p.tau).astype(F)
+    phi = exprel((p.dt * J).astype(F))
+    return (V + (p.dt * phi).astype(F) * f).astype(F)
+
+
+def coba_lif_step(V, ge, gi, ref, in_e, in_i, p):
+    """Fused Expon + COBA + LIFRef step.  Returns (V, ge, gi, ref, spike)."""
+    ge = (ge * p.de + in_e).astype(F)
+    gi = (gi * p.di + in_i).astype(F)
+    Vn = lif_membrane(V, ge, gi, p)
+    refr = ref > 0
+    Vn = np.where(refr, V, Vn).astype(F)
+    spk = (~refr) & (Vn >= p.V_th)
+    Vn = np.where(spk, p.V_reset, Vn).astype(F)
+    ref = np.where(spk, p.ref_steps, np.where(refr, ref - 1, 0)).astype(I32)
+    return Vn, ge, gi, ref, spk
+
+
+# ---- Hodgkin-Huxley, examples/100_hh_neuron_model.py:25-93 ----
+
+class HHParams:
+    def __init__(self, ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03, C=1.0,
+                 V_th=20., I_ext=0., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.05):
+        self.ENa, self.gNa, self.EK, self.gK = F(ENa), F(gNa), F(EK), F(gK)
+        self.EL, self.gL, self.C, self.V_th = F(EL), F(gL), F(C), F(V_th)
+        self.I_ext, self.E_e, self.E_i = F(I_ext), F(E_e), F(E_i)
+        self.dt = F(dt)
+        self.de = decay_factor(dt, tau_e)
+        self.di = decay_factor(dt, tau_i)
+
+
+def hh_rates(V):
+    """(am, bm, ah, bh, an, bn) at membrane potential V (mV), :49-64."""
+    V = np.asarray(V, F)
+    am = (F(1.0) / exprel((-(V + F(40.0))) / F(10.0))).astype(F)
+    bm = (F(4.0) * expf((-(V + F(65.0))) / F(18.0))).astype(F)
+    ah = (F(0.07) * expf((-(V + F(65.0))) / F(20.0))).astype(F)
+    bh = (F(1.0) / (F(1.0) + expf((-(V + F(35.0))) / F(10.0)))).astype(F)
+    an = (F(0.1) / exprel((-(V + F(55.0))) / F(10.0))).astype(F)
+    bn = (F(0.125) * expf((-(V + F(65.0))) / F(80.0))).astype(F)
+    return am, bm, ah, bh, an, bn
+
+
+def hh_init(V):
+    """Gates at steady state for V (init_state, :66-70): x_inf = a / (a + b)."""
+    am, bm, ah, bh, an, bn = hh_rates(V)
+    return (am / (am + bm)).astype(F), (ah / (ah + bh)).astype(F), (an / (an + bn)).astype(F)
+
+
+def _gate(x, a, b, dt):
+    f = (a * (F(1.0) - x) - b * x).astype(F)
+    J = (-(a + b)).astype(F)
+    phi = exprel((dt * J).astype(F))
+    return (x + (dt * phi).astype(F) * f).astype(F)
+
+
+def hh_step(V, m, h, n, ge, gi, in_e, in_i, p):
+    """Fused Expon + COBA + HH step.  Returns (V, m, h, n, ge, gi, spike)."""
+    ge = (ge * p.de + in_e).astype(F)
+    gi = (gi * p.di + in_i).astype(F)
+    am, bm, ah, bh, an, bn = hh_rates(V)
+    I = (p.I_ext + ge * (p.E_e - V)).astype(F)
+    I = (I + gi * (p.E_i - V)).astype(F)
+    gna = (p.gNa * m * m * m * h).astype(F)
+    INa = (gna * (V - p.ENa)).astype(F)
+    n2 = (n * n).astype(F)
+    gk = (p.gK * n2 * n2).astype(F)
+    IK = (gk * (V - p.EK)).astype(F)
+    IL = (p.gL * (V - p.EL)).astype(F)
+    f = (((((-INa) - IK) - IL) + I) / p.C).astype(F)
+    J = (((((-gna) - gk) - p.gL) - (ge + gi)) / p.C).astype(F)
+    phi = exprel((p.dt * J).astype(F))
+    Vn = (V + (p.dt * phi).astype(F) * f).astype(F)
+    mn = _gate(m, am, bm, p.dt)
+    hn = _gate(h, ah, bh, p.dt)
+    nn = _gate(n, an, bn, p.dt)
+    spk = (V < p.V_th) & (Vn >= p.V_th)
+    return Vn, mn, hn, nn, ge, gi, spk

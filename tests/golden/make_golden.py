@@ -1,0 +1,84 @@
+"""Writes the golden fixtures in tests/golden/ from the oracle (run from the repo root).
+
+    python tests/golden/make_golden.py
+
+* conn_digests.json -- SHA-256 of the int32 index arrays that
+  ``RandomState(seed).randint(0, n_post, (n_pre, K))`` produces for the seeds and shapes
+  used by the parity configs (brainstate/nn/_event_fixedprob.py:165-171).
+* coba_lif_4000.json -- config [1]: 4000-neuron COBA E/I net, 1000 steps; per-step spike
+  counts, per-step order-free spike digests and SHA-256 of the raster / final state.
+* coba_hh_2000.json -- a 2000-neuron COBA-HH net, 600 steps, same records.
+The reference itself is not imported (it needs JAX, brainevent and brainunit, which are
+absent); these fixtures freeze the oracle so that any drift in it is caught.
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+from oracle import conn, neuron, network  # noqa: E402
+
+CONFIG1 = dict(n=4000, n_exc=3200, p=0.02, w_e=0.6, w_i=6.7, seed_e=1, seed_i=2, seed_v=3,
+               steps=1000)
+HH_NET = dict(n=2000, n_exc=1600, k=80, w_e=0.05, w_i=0.3, seed_e=11, seed_i=12, seed_v=13,
+              steps=600, I_ext=6.5)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def config1_net():
+    c = CONFIG1
+    pe = network.Projection(0, c['n_exc'], c['n'], c['p'], c['w_e'], seed=c['seed_e'])
+    pi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=c['seed_i'])
+    V0 = np.random.RandomState(c['seed_v']).uniform(-60., -50., c['n']).astype(np.float32)
+    return pe, pi, V0, neuron.LIFParams()
+
+
+def hh_net():
+    c = HH_NET
+    pe = network.Projection(0, c['n_exc'], c['n'], c['k'], c['w_e'], seed=c['seed_e'])
+    pi = network.Projection(c['n_exc'], c['n'], c['n'], c['k'], c['w_i'], seed=c['seed_i'])
+    V0 = np.random.RandomState(c['seed_v']).uniform(-70., -50., c['n']).astype(np.float32)
+    return pe, pi, V0, neuron.HHParams(I_ext=c['I_ext'])
+
+
+def run_records(res):
+    return dict(counts=res['counts'].tolist(),
+                hashes=[network.spike_hash(r) for r in res['raster']],
+                raster_sha256=sha(np.packbits(res['raster'])),
+                final_V_sha256=sha(res['V']))
+
+
+def main():
+    digests = []
+    for n_pre, n_post, k, seed in [(3200, 4000, 80, 1), (800, 4000, 80, 2), (20, 30, 6, 11),
+                                   (1600, 2000, 80, 11), (400, 2000, 80, 12)]:
+        idx, _ = conn.fixed_num_indices(n_pre, n_post, k, seed)
+        digests.append(dict(n_pre=n_pre, n_post=n_post, k=k, seed=seed, sha256=sha(idx)))
+    with open(os.path.join(HERE, 'conn_digests.json'), 'w') as f:
+        json.dump(digests, f, indent=1)
+
+    pe, pi, V0, p = config1_net()
+    res = network.run_coba_lif(V0, pe, pi, p, CONFIG1['n_exc'], CONFIG1['steps'])
+    rec = dict(config=CONFIG1, **run_records(res))
+    with open(os.path.join(HERE, 'coba_lif_4000.json'), 'w') as f:
+        json.dump(rec, f)
+    print('coba_lif_4000: total spikes', int(res['counts'].sum()))
+
+    pe, pi, V0, p = hh_net()
+    res = network.run_coba_hh(V0, pe, pi, p, HH_NET['n_exc'], HH_NET['steps'])
+    rec = dict(config=HH_NET, **run_records(res))
+    with open(os.path.join(HERE, 'coba_hh_2000.json'), 'w') as f:
+        json.dump(rec, f)
+    print('coba_hh_2000: total spikes', int(res['counts'].sum()))
+
+
+if __name__ == '__main__':
+    main()

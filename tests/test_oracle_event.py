@@ -1,0 +1,162 @@
+"""Pins of the oracle's connectivity and event operators (CPU only)."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import conn, event, network
+
+F = np.float32
+GOLD = os.path.join(os.path.dirname(__file__), 'golden')
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# ---- connectivity: brainstate/nn/_event_fixedprob.py:142-196 ----
+
+def test_conn_num_from_probability():
+    assert conn.conn_num_from(0.02, 4000) == 80          # int(n_post * p), :144
+    assert conn.conn_num_from(0.2, 30) == 6
+    assert conn.conn_num_from(7, 30) == 7
+
+
+def test_indices_are_numpy_mt19937_stream():
+    idx, _ = conn.fixed_num_indices(20, 30, 6, seed=11)
+    ref = np.random.RandomState(11).randint(0, 30, size=(20, 6)).astype(np.int32)
+    assert idx.dtype == np.int32 and np.array_equal(idx, ref)
+    assert idx.min() >= 0 and idx.max() < 30
+
+
+def test_indices_golden_digests():
+    with open(os.path.join(GOLD, 'conn_digests.json')) as f:
+        gold = json.load(f)
+    for case in gold:
+        idx, _ = conn.fixed_num_indices(case['n_pre'], case['n_post'], case['k'], case['seed'])
+        assert _sha(idx) == case['sha256'], case
+
+
+def test_csr_afferent_indptr_closed_form():
+    indptr, indices, sel = conn.csr_afferent(50, 40, 5, seed=3, afferent_ratio=0.5)
+    assert indptr[0] == 0 and indptr[-1] == indices.size == 5 * sel.sum()
+    assert np.array_equal(np.diff(indptr), np.where(sel, 5, 0))
+    # the mask is drawn after the indices from the same generator (:183-184)
+    rng = np.random.RandomState(3)
+    full = rng.randint(0, 40, size=(50, 5))
+    assert np.array_equal(sel, rng.random(50) < 0.5)
+    assert np.array_equal(indices, full[sel].reshape(-1))
+
+
+# ---- event mat-vec: brainstate/nn/_event_fixedprob_test.py:247-260 ----
+
+def test_scatter_matches_reference_np_add_at():
+    n_in, n_out = 20, 30
+    idx, _ = conn.fixed_num_indices(n_in, n_out, conn.conn_num_from(0.2, n_out), seed=11)
+    spk = (np.random.RandomState(1).rand(n_in) < 0.3).astype(float)
+    out = event.scatter_fixed(spk, idx, 1.5, n_out)
+    ref = np.zeros(n_out)
+    for i in range(n_in):
+        np.add.at(ref, idx[i], 1.5 * float(spk[i]))
+    assert np.allclose(out, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_scatter_brute_force_het_exact_order():
+    rng = np.random.RandomState(5)
+    n_pre, n_post, k = 37, 23, 9
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F)
+    spk = rng.rand(n_pre) < 0.4
+    out = event.scatter_fixed(spk, idx, w, n_post)
+    ref = np.zeros(n_post, F)
+    for i in range(n_pre):               # sequential fp32 adds in (i, k) order
+        if spk[i]:
+            for kk in range(k):
+                ref[idx[i, kk]] = F(ref[idx[i, kk]] + w[i, kk])
+    assert np.array_equal(out, ref)
+
+
+def test_scatter_invariant_total_mass():
+    rng = np.random.RandomState(6)
+    idx = rng.randint(0, 500, (400, 50)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (400, 50)).astype(F)
+    spk = rng.rand(400) < 0.1
+    out = event.scatter_fixed(spk, idx, w, 500)
+    assert np.isclose(out.astype(np.float64).sum(), w[spk].astype(np.float64).sum(), rtol=1e-5)
+
+
+def test_float_spikes_count_as_events():
+    idx = np.array([[0, 1], [1, 2]], np.int32)
+    a = event.scatter_fixed(np.array([2.5, 0.0]), idx, 1.0, 3)
+    b = event.scatter_fixed(np.array([1, 0], bool), idx, 1.0, 3)
+    assert np.array_equal(a, b) and np.array_equal(a, [1, 1, 0])
+
+
+@pytest.mark.parametrize('het', [False, True])
+def test_gather_equals_scatter_bitwise(het):
+    rng = np.random.RandomState(7)
+    n_pre, n_post, k = 300, 200, 40
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F) if het else F(0.6)
+    spk = rng.rand(n_pre) < 0.2
+    indptr, flat = conn.fixed_to_csr(idx)
+    post_ptr, pre_of, syn_of = conn.to_post_major(indptr, flat, n_post)
+    w_post = w.reshape(-1)[syn_of] if het else w
+    g = event.gather_post_major(spk, post_ptr, pre_of, w_post, n_post)
+    s = event.scatter_fixed(spk, idx, w, n_post)
+    assert np.array_equal(g, s)
+
+
+def test_homogeneous_counts_are_repeated_sums():
+    t = network.repeated_sum_table(0.6, 10)
+    assert t[0] == 0 and t[1] == F(0.6) and t[2] == F(1.2) and t[3] == F(F(1.2) + F(0.6))
+    rng = np.random.RandomState(8)
+    idx = rng.randint(0, 50, (100, 20)).astype(np.int32)
+    spk = rng.rand(100) < 0.5
+    counts = np.bincount(idx[spk].reshape(-1), minlength=50)
+    assert np.array_equal(event.scatter_fixed(spk, idx, 0.6, 50),
+                          network.repeated_sum_table(0.6, counts.max())[counts])
+
+
+def test_compact_is_flatnonzero():
+    spk = np.random.RandomState(9).rand(10000) < 0.01
+    idx, c = event.compact(spk)
+    assert c == spk.sum() and np.all(np.diff(idx) > 0) and np.array_equal(spk[idx], np.ones(c, bool))
+    assert event.compact(np.zeros(0, bool))[1] == 0
+
+
+# ---- EventLinear: brainstate/nn/_event_linear_test.py ----
+
+@pytest.mark.parametrize('bool_x', [True, False])
+@pytest.mark.parametrize('homo_w', [True, False])
+def test_event_linear_reference_test1(homo_w, bool_x):          # :26-40
+    rng = np.random.RandomState(10)
+    x = rng.rand(20) < 0.1
+    if not bool_x:
+        x = x.astype(F)
+    W = F(1.5) if homo_w else rng.uniform(-0.5, 0.5, (20, 40)).astype(F)
+    y = event.event_linear(x, W, float_as_event=bool_x, n_out=40)
+    expect = (x.sum() * W) * np.ones(40) if homo_w else x.astype(F) @ W
+    assert np.allclose(y, expect, rtol=1e-5)
+
+
+@pytest.mark.parametrize('float_as_event', [True, False])
+def test_event_linear_homogeneous_matches_dense(float_as_event):  # :127-162
+    spk = np.array([0., 2., 0., 3., 0., 0., 1., 0., 0., 5.], F)
+    homo = event.event_linear(spk, F(1.5), float_as_event, n_out=8)
+    dense = event.event_linear(spk, np.full((10, 8), 1.5, F), float_as_event)
+    assert np.allclose(homo, dense)
+    expected = (4 if float_as_event else 11) * 1.5
+    assert np.allclose(homo, np.ones(8) * expected)
+
+
+def test_event_linear_batched_equals_rows():
+    rng = np.random.RandomState(11)
+    spk = rng.rand(5, 64) < 0.2
+    W = rng.normal(0, 0.125, (64, 33)).astype(F)
+    out = event.event_linear(spk, W)
+    for b in range(5):
+        assert np.array_equal(out[b], event.event_linear(spk[b], W))
+    assert np.allclose(out, spk.astype(np.float64) @ W.astype(np.float64), atol=1e-5)
