@@ -33,7 +33,7 @@ class Net(ctypes.Structure):
     _fields_ = [('n', c_i32), ('n_exc', c_i32), ('k_e', c_i32), ('k_i', c_i32),
                 ('idx_e', c_vp), ('w_e', c_vp), ('w_e_homo', c_f32),
                 ('idx_i', c_vp), ('w_i', c_vp), ('w_i_homo', c_f32),
-                ('acc', c_vp), ('spk', c_vp), ('blocks_per_cu', c_i32)]
+                ('spk', c_vp), ('blocks_per_cu', c_i32)]
 
 
 class LifState(ctypes.Structure):
@@ -61,14 +61,16 @@ SIGNATURES = {
     'bs_hh_init': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'bs_coba_hh_step': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                        ctypes.POINTER(HhParams), c_vp, c_vp]),
-    'bs_net_workspace_size': (c_size, []),
+    'bs_net_workspace_size': (c_size, [ctypes.POINTER(Net)]),
+    'bs_net_prepare': (ctypes.c_int, [ctypes.POINTER(Net), c_vp, c_vp]),
     'bs_coba_lif_run': (ctypes.c_int, [ctypes.POINTER(Net), ctypes.POINTER(LifState),
-                                       ctypes.POINTER(LifParams), c_i32, c_i32, c_vp, c_vp, c_vp,
-                                       c_vp, c_vp]),
+                                       ctypes.POINTER(LifParams), ctypes.c_int64, c_i32, c_vp,
+                                       c_vp, c_vp, c_vp, c_vp]),
     'bs_coba_hh_run': (ctypes.c_int, [ctypes.POINTER(Net), ctypes.POINTER(HhState),
-                                      ctypes.POINTER(HhParams), c_i32, c_i32, c_vp, c_vp, c_vp,
-                                      c_vp, c_vp]),
+                                      ctypes.POINTER(HhParams), ctypes.c_int64, c_i32, c_vp,
+                                      c_vp, c_vp, c_vp, c_vp]),
     'bs_net_grid_blocks': (ctypes.c_int, [ctypes.POINTER(Net)]),
+    'bs_net_error': (ctypes.c_int, [c_vp, c_vp]),
 }
 
 _lib = None

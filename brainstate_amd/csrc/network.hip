@@ -1,30 +1,77 @@
 // Whole-loop runners for E/I networks: one persistent (cooperative) launch runs T steps.
 //
-// Why persistent: one step of the 1M-neuron COBA net moves ~34 MB, ~4 us at 8 TB/s,
-// which is the same order as a kernel launch.  A per-step chain of launches (update,
-// compaction, two scatters) would be launch-bound.  Here each workgroup owns a fixed
-// slice of neurons for the whole run and keeps their state in registers; per step it
-//   1. reads (and clears) its neurons' pending inputs acc[cur][E|I][j],
-//   2. runs the fused Expon + COBA + neuron update,
-//   3. compacts its spikes into an ordered LDS list (wave ballot + mbcnt rank),
-//   4. scatters the synapse rows of its own spiking neurons into acc[nxt] with hardware
-//      fp32 atomics (rows are contiguous: 64 lanes read 256 B of indices per chunk),
-//   5. meets the other workgroups at one grid barrier.
-// Steps 1-4 need no barrier between them because a workgroup only scatters spikes it
-// produced itself, and acc is double-buffered: nobody writes acc[cur] during step t.
+// Why persistent: one step of the 1M-neuron COBA net moves ~34 MB, ~4 us at 8 TB/s, the
+// same order as a kernel launch, so a per-step chain of launches is launch-bound.  Each
+// workgroup owns a fixed power-of-two slice of neurons for the whole run and keeps their
+// state in registers.
+//
+// Why no global atomics: scattered fp32 atomics on MI355X sustain ~20 G/s chip-wide
+// (scattered plain stores ~80 G/s), so atomically scattering ~2e5 synaptic events per
+// step would cost > 9 us by itself.  Instead events travel through per-(source, destination)
+// inboxes, which connectivity makes boundable: the number of synapses from the neurons of
+// workgroup s onto those of workgroup d is fixed, so each inbox is sized for the case in
+// which every neuron of s spikes and can never overflow (the whole structure is
+// 2 x synapses x 8 B, e.g. 1.6 GB for 1e8 synapses; HBM is 288 GB).
+//
+// Per step t, workgroup d:
+//   A. waits until every workgroup s has published its step t-1 count word for d (tagged
+//      with the step, double-buffered) and adds the entries of that inbox into LDS inputs
+//      with LDS atomics -- point-to-point dependencies, no grid barrier;
+//   B. runs the fused Expon + COBA + neuron update from those inputs;
+//   C. compacts its spikes into an LDS list (one ballot per neuron slot, one LDS prefix);
+//   D. expands its spikes into (local target | inh flag, weight) entries, written with
+//      device-scope stores at slots taken from per-destination LDS cursors, waits for its
+//      stores to complete, then publishes one tagged count word per destination.
+// Cross-workgroup data is only touched with device-scope loads/stores (emitted with the
+// device-coherence bit), so no L2 writeback/invalidate is ever needed (each costs ~5 us).
+// Deadlock freedom: every workgroup publishes step t's counts unconditionally after
+// consuming step t-1's, and all workgroups are co-resident (cooperative launch); a spin
+// limit turns a would-be hang into an error flag instead.
 #include "neuron_dev.h"
 
 namespace {
 
 constexpr int kBlock = 1024;
 constexpr int kWaves = kBlock / BS_WAVE;
+constexpr int kMaxBlocks = 512;
+constexpr int kMaxNpt = 8;
+constexpr uint32_t kInhFlag = 0x80000000u;
+constexpr uint64_t kSpinLimit = 1ull << 24;
+#define BS_AGENT __HIP_MEMORY_SCOPE_AGENT
 
-struct bs_grid_bar {
-  uint32_t count;
-  uint32_t pad0[31];
-  uint32_t gen;
-  uint32_t pad1[31];
+// ---- workspace layout (all offsets in bytes, 256-aligned) ----
+struct NetLayout {
+  int32_t nb;          // workgroups
+  int32_t npt;         // neurons per thread
+  int32_t shift;       // log2(neurons per workgroup)
+  uint32_t entry;      // bytes per entry (8 het, 4 homogeneous)
+  uint64_t total;      // inbox entries per buffer (>= valid synapses)
+  uint64_t off_cnt;    // uint64 [2][nb dst][nb src]   tagged counts
+  uint64_t off_cap;    // uint32 [nb src][nb dst]      capacities
+  uint64_t off_ofs;    // uint64 [nb dst][nb src] + 1  inbox entry offsets (dst-major)
+  uint64_t off_inbox;  // entries [2][total]
+  uint64_t bytes;
 };
+
+struct WsHeader {
+  uint32_t error;      // nonzero: a wait hit the spin limit
+  uint32_t pad[63];
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+__device__ __forceinline__ uint64_t ld_dev64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, BS_AGENT);
+}
+__device__ __forceinline__ void st_dev64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, BS_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, BS_AGENT);
+}
+__device__ __forceinline__ void st_dev32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, BS_AGENT);
+}
 
 struct NetArgs {
   int32_t n, n_exc, k_e, k_i;
@@ -34,35 +81,15 @@ struct NetArgs {
   const int32_t* idx_i;
   const float* w_i;
   float w_i_homo;
-  float* acc;
   uint8_t* spk;
-  int32_t steps, phase;
+  int64_t t0;
+  int32_t steps;
   int32_t* counts;
   uint32_t* hash;
   uint8_t* raster;
-  bs_grid_bar* bar;
+  char* ws;
+  NetLayout L;
 };
-
-// Sense-free generation barrier over all workgroups of a co-resident grid.  Every
-// workgroup arrives exactly once per call, so every wait ends.
-__device__ __forceinline__ void grid_barrier(bs_grid_bar* bar, uint32_t nblocks, uint32_t& gen) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t g = gen;
-    const uint32_t arrived =
-        __hip_atomic_fetch_add(&bar->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (arrived == nblocks - 1) {
-      __hip_atomic_store(&bar->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&bar->gen, g + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      while (__hip_atomic_load(&bar->gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g)
-        __builtin_amdgcn_s_sleep(1);
-    }
-  }
-  gen = gen + 1u;
-  __syncthreads();
-}
 
 // ---- neuron models: register-resident state, one fused update per neuron-step ----
 
@@ -109,21 +136,54 @@ struct HhModel {
   }
 };
 
+// Synapse row of neuron i (global index) in the E or I connectivity.
+struct Row {
+  const int32_t* idx;
+  const float* w;
+  int32_t k;
+  bool inh;
+};
+__device__ __forceinline__ Row row_of(const NetArgs& a, int32_t i) {
+  if (i < a.n_exc) {
+    const int64_t r = (int64_t)i * a.k_e;
+    return Row{a.idx_e + r, a.w_e ? a.w_e + r : nullptr, a.k_e, false};
+  }
+  const int64_t r = (int64_t)(i - a.n_exc) * a.k_i;
+  return Row{a.idx_i + r, a.w_i ? a.w_i + r : nullptr, a.k_i, true};
+}
+
 template <class Model, int NPT, bool kHet>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
                                                 typename Model::Params p) {
-  __shared__ int32_t s_list[NPT * kBlock];
+  constexpr int kChunk = NPT * kBlock;
+  constexpr int kBatch = 4;
+  __shared__ int32_t s_list[kChunk];
+  __shared__ float s_in[2 * kChunk];          // (E, I) inputs of this workgroup's neurons
+  __shared__ uint32_t s_cursor[kMaxBlocks];   // entries written per destination this step
+  __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
+  __shared__ uint64_t s_ofs_out[kMaxBlocks];  // inbox offset (d <- me)
   __shared__ int32_t s_wave[kWaves];
   __shared__ uint32_t s_hash;
 
+  const NetLayout& L = a.L;
+  const int nb = L.nb;
+  const int me = blockIdx.x;
   const int lane = bs_lane();
   const int wid = threadIdx.x / BS_WAVE;
-  const uint32_t nblocks = gridDim.x;
-  const int64_t base = (int64_t)blockIdx.x * (NPT * kBlock);
+  const int64_t base = (int64_t)me * kChunk;
   const int64_t n = a.n;
-  uint32_t gen = 0;
-  if (threadIdx.x == 0)
-    gen = __hip_atomic_load(&a.bar->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  WsHeader* hdr = (WsHeader*)a.ws;
+  uint64_t* cnt = (uint64_t*)(a.ws + L.off_cnt);
+  const uint64_t* ofs = (const uint64_t*)(a.ws + L.off_ofs);
+  char* inbox = a.ws + L.off_inbox;
+  const size_t buf_bytes = (size_t)L.total * L.entry;
+
+  for (int s = threadIdx.x; s < nb; s += kBlock) {
+    s_ofs_in[s] = ofs[(int64_t)me * nb + s];
+    s_ofs_out[s] = ofs[(int64_t)s * nb + me];
+    s_cursor[s] = 0;
+  }
+  for (int i = threadIdx.x; i < 2 * kChunk; i += kBlock) s_in[i] = 0.0f;
 
   typename Model::Regs r[NPT];
 #pragma unroll
@@ -134,93 +194,159 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   bool last[NPT];
 #pragma unroll
   for (int q = 0; q < NPT; ++q) last[q] = false;
-
-  const int32_t cpr_e = (a.k_e + BS_WAVE - 1) / BS_WAVE;
-  const int32_t cpr_i = (a.k_i + BS_WAVE - 1) / BS_WAVE;
-  const int32_t cpr = cpr_e > cpr_i ? cpr_e : cpr_i;
+  const int32_t kmax = a.k_e > a.k_i ? a.k_e : a.k_i;
+  int tps = 1;  // threads per source in phase A (power of two, tps * nb <= kBlock)
+  while (tps * 2 * nb <= kBlock) tps *= 2;
+  __syncthreads();
 
   for (int32_t t = 0; t < a.steps; ++t) {
-    const int cur = (a.phase + t) & 1;
-    float* acc_cur = a.acc + (int64_t)cur * 2 * n;
-    float* acc_nxt = a.acc + (int64_t)(cur ^ 1) * 2 * n;
+    const int64_t ta = a.t0 + t;  // absolute step index
 
-    // 1-2: inputs + fused update
-    float in_e[NPT], in_i[NPT];
+    // ---- A: inputs produced by step ta-1 ----
+    // tps threads per source: all poll the source's count word (one transaction per
+    // wave), then each reads every tps-th entry, up to kBatch loads in flight per thread.
+    if (ta > 0) {
+      const int bin = (int)((ta - 1) & 1);
+      const uint64_t* cin = cnt + ((int64_t)bin * nb + me) * nb;
+      const uint32_t want = (uint32_t)ta;  // step ta-1 publishes tag ta
+      const char* ib = inbox + (size_t)bin * buf_bytes;
+      for (int x = threadIdx.x; x < nb * tps; x += kBlock) {
+        const int s = x / tps;
+        const uint32_t sub = (uint32_t)(x - s * tps);
+        uint64_t v = ld_dev64(cin + s);
+        uint64_t spins = 0;
+        while ((uint32_t)(v >> 32) != want) {
+          if (++spins > kSpinLimit) {
+            st_dev32(&hdr->error, 1u);
+            v = 0;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+          v = ld_dev64(cin + s);
+        }
+        const uint32_t c = (uint32_t)v;
+        const uint64_t o = s_ofs_in[s];
+        for (uint32_t e0 = sub; e0 < c; e0 += kBatch * tps) {
+          uint64_t ent[kBatch];
 #pragma unroll
-    for (int q = 0; q < NPT; ++q) {
-      const int64_t j = base + q * kBlock + threadIdx.x;
-      in_e[q] = 0.0f;
-      in_i[q] = 0.0f;
-      if (j < n) {
-        in_e[q] = acc_cur[j];
-        in_i[q] = acc_cur[n + j];
-      }
-    }
+          for (int u = 0; u < kBatch; ++u) {
+            const uint32_t e = e0 + u * tps;
+            ent[u] = 0;
+            if (e < c) {
+              if (kHet) ent[u] = ld_dev64((const uint64_t*)ib + o + e);
+              else ent[u] = ld_dev32((const uint32_t*)ib + o + e) | (1ull << 32);
+            }
+          }
 #pragma unroll
-    for (int q = 0; q < NPT; ++q) {
-      const int64_t j = base + q * kBlock + threadIdx.x;
-      if (j < n) {
-        acc_cur[j] = 0.0f;
-        acc_cur[n + j] = 0.0f;
-        last[q] = Model::update(p, r[q], in_e[q], in_i[q]);
+          for (int u = 0; u < kBatch; ++u) {
+            if (e0 + u * tps < c) {
+              const uint32_t tgt = (uint32_t)ent[u];
+              const float w = kHet ? __uint_as_float((uint32_t)(ent[u] >> 32))
+                                   : ((tgt & kInhFlag) ? a.w_i_homo : a.w_e_homo);
+              const uint32_t loc = tgt & ~kInhFlag;
+              if (loc < (uint32_t)kChunk)
+                atomicAdd(&s_in[2 * loc + ((tgt & kInhFlag) ? 1 : 0)], w);
+            }
+          }
+        }
       }
+      __syncthreads();
     }
 
-    // 3: ordered compaction of this workgroup's spikes into LDS
-    int32_t count = 0;
+    // ---- B: fused update ----
     uint32_t h = 0;
-    if (threadIdx.x == 0) s_hash = 0;
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
       const int64_t j = base + q * kBlock + threadIdx.x;
-      const bool s = last[q];
-      const uint64_t m = bs_ballot(s);
-      if (lane == 0) s_wave[wid] = __popcll(m);
-      __syncthreads();
-      int32_t off = count, tot = 0;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const int32_t c = s_wave[w];
-        off += (w < wid) ? c : 0;
-        tot += c;
+      const int loc = q * kBlock + threadIdx.x;
+      last[q] = false;
+      if (j < n) {
+        const float2 in = *(float2*)&s_in[2 * loc];
+        *(float2*)&s_in[2 * loc] = make_float2(0.0f, 0.0f);
+        last[q] = Model::update(p, r[q], in.x, in.y);
+        if (last[q]) h += bs_mix32((uint32_t)j);
+        if (a.raster) a.raster[(int64_t)t * n + j] = last[q] ? 1 : 0;
       }
-      if (s) {
-        s_list[off + bs_rank_below(m)] = (int32_t)j;
-        h += bs_mix32((uint32_t)j);
-      }
-      if (a.raster && j < n) a.raster[(int64_t)t * n + j] = s ? 1 : 0;
-      count += tot;
-      __syncthreads();
     }
-    if (a.hash && h) atomicAdd(&s_hash, h);
 
-    // 4: scatter this workgroup's spikes (E rows for j < n_exc, I rows otherwise)
-    const int32_t items = count * cpr;
-    for (int32_t it = wid; it < items; it += kWaves) {
-      const int32_t ai = it / cpr;
-      const int32_t c = it - ai * cpr;
-      const int32_t i = s_list[ai];
-      const bool exc = i < a.n_exc;
-      const int32_t k = exc ? a.k_e : a.k_i;
-      const int32_t tt = c * BS_WAVE + lane;
-      if (tt < k) {
-        const int64_t s = (int64_t)(exc ? i : i - a.n_exc) * k + tt;
-        const int32_t tgt = exc ? a.idx_e[s] : a.idx_i[s];
-        float v;
-        if (kHet) v = exc ? a.w_e[s] : a.w_i[s];
-        else v = exc ? a.w_e_homo : a.w_i_homo;
-        if ((uint32_t)tgt < (uint32_t)n)
-          bs_atomic_add_f32(acc_nxt + (exc ? 0 : n) + tgt, v);
+    // ---- C: compaction into s_list ----
+    uint64_t m[NPT];
+    int32_t wtot = 0;
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+      m[q] = bs_ballot(last[q]);
+      wtot += __popcll(m[q]);
+    }
+    if (lane == 0) s_wave[wid] = wtot;
+    if (threadIdx.x == 0) s_hash = 0;
+    __syncthreads();
+    int32_t off = 0, count = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const int32_t c = s_wave[w];
+      off += (w < wid) ? c : 0;
+      count += c;
+    }
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+      if (last[q]) s_list[off + bs_rank_below(m[q])] = (int32_t)(base + q * kBlock + threadIdx.x);
+      off += __popcll(m[q]);
+    }
+    if (h) atomicAdd(&s_hash, h);
+    __syncthreads();
+
+    // ---- D: expand spikes into the destinations' inboxes ----
+    // kBatch synapses per thread per round, all their index/weight loads issued first.
+    const int bout = (int)(ta & 1);
+    char* ob = inbox + (size_t)bout * buf_bytes;
+    const int64_t items = (int64_t)count * kmax;
+    for (int64_t it0 = threadIdx.x; it0 < items; it0 += (int64_t)kBatch * kBlock) {
+      int32_t tgt[kBatch];
+      float wv[kBatch];
+      bool inh[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t it = it0 + (int64_t)u * kBlock;
+        tgt[u] = -1;
+        wv[u] = 0.0f;
+        inh[u] = false;
+        if (it < items) {
+          const int32_t ai = (int32_t)(it / kmax);
+          const int32_t tt = (int32_t)(it - (int64_t)ai * kmax);
+          const Row rw = row_of(a, s_list[ai]);
+          if (tt < rw.k) {
+            tgt[u] = rw.idx[tt];
+            if (kHet) wv[u] = rw.w[tt];
+            inh[u] = rw.inh;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if ((uint32_t)tgt[u] < (uint32_t)n) {
+          const int d = tgt[u] >> L.shift;
+          const uint32_t loc = (uint32_t)(tgt[u] & (kChunk - 1)) | (inh[u] ? kInhFlag : 0u);
+          const uint32_t slot = atomicAdd(&s_cursor[d], 1u);
+          const uint64_t pos = s_ofs_out[d] + slot;
+          if (kHet) st_dev64((uint64_t*)ob + pos, ((uint64_t)__float_as_uint(wv[u]) << 32) | loc);
+          else st_dev32((uint32_t*)ob + pos, loc);
+        }
       }
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     __syncthreads();
+    {
+      uint64_t* cout = cnt + (int64_t)bout * nb * nb;
+      const uint64_t tag = (uint64_t)(uint32_t)(ta + 1) << 32;
+      for (int d = threadIdx.x; d < nb; d += kBlock) {
+        st_dev64(cout + (int64_t)d * nb + me, tag | s_cursor[d]);
+        s_cursor[d] = 0;
+      }
+    }
     if (threadIdx.x == 0) {
       if (a.counts && count) atomicAdd(&a.counts[t], count);
       if (a.hash && s_hash) atomicAdd(&a.hash[t], s_hash);
     }
-
-    // 5: all inputs for step t+1 are in acc[nxt]
-    grid_barrier(a.bar, nblocks, gen);
   }
 
 #pragma unroll
@@ -233,23 +359,73 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   }
 }
 
+// ---- setup: per-(source, destination) capacities and inbox offsets ----
+
+__global__ __launch_bounds__(kBlock) void k_caps(NetArgs a, uint32_t* cap) {
+  __shared__ uint32_t hist[kMaxBlocks];
+  const int nb = a.L.nb;
+  const int me = blockIdx.x;
+  for (int d = threadIdx.x; d < nb; d += kBlock) hist[d] = 0;
+  __syncthreads();
+  const int64_t chunk = (int64_t)1 << a.L.shift;
+  const int64_t lo = (int64_t)me * chunk;
+  const int64_t hi = lo + chunk < a.n ? lo + chunk : a.n;
+  for (int64_t i = lo; i < hi; ++i) {
+    const Row rw = row_of(a, (int32_t)i);
+    for (int tt = threadIdx.x; tt < rw.k; tt += kBlock) {
+      const int32_t tgt = rw.idx[tt];
+      if ((uint32_t)tgt < (uint32_t)a.n) atomicAdd(&hist[tgt >> a.L.shift], 1u);
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < nb; d += kBlock) cap[(int64_t)me * nb + d] = hist[d];
+}
+
+// Exclusive scan of cap in destination-major order -> ofs[d][s]; one workgroup.
+__global__ __launch_bounds__(kBlock) void k_offsets(int nb, const uint32_t* cap, uint64_t* ofs,
+                                                    uint64_t* total) {
+  __shared__ uint64_t part[kBlock];
+  const int64_t m = (int64_t)nb * nb;
+  const int64_t per = (m + kBlock - 1) / kBlock;
+  const int64_t lo = threadIdx.x * per;
+  const int64_t hi = lo + per < m ? lo + per : m;
+  uint64_t sum = 0;
+  for (int64_t x = lo; x < hi; ++x) {  // x = d*nb + s
+    const int64_t d = x / nb, s = x - d * nb;
+    sum += cap[s * nb + d];
+  }
+  part[threadIdx.x] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t acc = 0;
+    for (int i = 0; i < kBlock; ++i) {
+      const uint64_t v = part[i];
+      part[i] = acc;
+      acc += v;
+    }
+    *total = acc;
+  }
+  __syncthreads();
+  uint64_t acc = part[threadIdx.x];
+  for (int64_t x = lo; x < hi; ++x) {
+    const int64_t d = x / nb, s = x - d * nb;
+    ofs[x] = acc;
+    acc += cap[s * nb + d];
+  }
+}
+
+__global__ void k_zero_u64(uint64_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0ull;
+}
+
 __global__ void k_zero_u32(uint32_t* p, int32_t n) {
   for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
     p[i] = 0u;
 }
 
-template <class Model, int NPT, bool kHet>
-int occupancy() {
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_run<Model, NPT, kHet>, kBlock, 0) !=
-      hipSuccess)
-    return 0;
-  return nb;
-}
-
-int pick_blocks_per_cu(const bs_net* net) {
-  return net->blocks_per_cu > 0 ? net->blocks_per_cu : 1;
-}
+// ---- host helpers ----
 
 int npt_for(int64_t n, int64_t threads) {
   const int64_t need = (n + threads - 1) / threads;
@@ -257,40 +433,44 @@ int npt_for(int64_t n, int64_t threads) {
   if (need <= 2) return 2;
   if (need <= 4) return 4;
   if (need <= 8) return 8;
-  if (need <= 16) return 16;
   return -1;
 }
 
-template <class Model, int NPT, bool kHet>
-int launch_one(const NetArgs& a, const typename Model::State& st, const typename Model::Params& p,
-               int grid, hipStream_t s) {
-  const int occ = occupancy<Model, NPT, kHet>();
-  if (occ * bs_num_cus() < grid) {
-    bs_set_error("runner: grid of %d workgroups cannot be co-resident (occupancy %d x %d CUs)",
-                 grid, occ, bs_num_cus());
-    return BS_ERR_UNSUPPORTED;
-  }
-  NetArgs aa = a;
-  typename Model::State ss = st;
-  typename Model::Params pp = p;
-  void* args[] = {(void*)&aa, (void*)&ss, (void*)&pp};
-  BS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)k_run<Model, NPT, kHet>, dim3(grid),
-                                          dim3(kBlock), args, 0, s));
-  return BS_OK;
+int ilog2(int64_t x) {
+  int s = 0;
+  while (((int64_t)1 << s) < x) ++s;
+  return s;
 }
 
-template <class Model, bool kHet>
-int dispatch_npt(int npt, const NetArgs& a, const typename Model::State& st,
-                 const typename Model::Params& p, int grid, hipStream_t s) {
-  switch (npt) {
-    case 1: return launch_one<Model, 1, kHet>(a, st, p, grid, s);
-    case 2: return launch_one<Model, 2, kHet>(a, st, p, grid, s);
-    case 4: return launch_one<Model, 4, kHet>(a, st, p, grid, s);
-    case 8: return launch_one<Model, 8, kHet>(a, st, p, grid, s);
-    case 16: return launch_one<Model, 16, kHet>(a, st, p, grid, s);
-  }
-  bs_set_error("runner: unsupported neurons-per-thread %d", npt);
-  return BS_ERR_UNSUPPORTED;
+// Workgroup count and slice size: as few neurons per thread as the grid allows.
+int plan(const bs_net* net, NetLayout* L) {
+  const int cus = bs_num_cus();
+  const int bpc = net->blocks_per_cu > 0 ? net->blocks_per_cu : 1;
+  int64_t grid = (int64_t)bpc * cus;
+  if (grid > kMaxBlocks) grid = kMaxBlocks;
+  const int npt = npt_for(net->n, grid * kBlock);
+  if (npt < 0) return -1;
+  const int64_t chunk = (int64_t)npt * kBlock;
+  int64_t nb = (net->n + chunk - 1) / chunk;
+  if (nb < 1) nb = 1;
+  L->nb = (int32_t)nb;
+  L->npt = npt;
+  L->shift = ilog2(chunk);
+  L->entry = net->w_e ? 8u : 4u;
+  // worst case: every synapse delivers one entry (invalid targets are never stored)
+  L->total = (uint64_t)net->n_exc * (uint64_t)net->k_e +
+             (uint64_t)(net->n - net->n_exc) * (uint64_t)net->k_i;
+  size_t o = align256(sizeof(WsHeader));
+  L->off_cnt = o;
+  o = align256(o + (size_t)2 * nb * nb * sizeof(uint64_t));
+  L->off_cap = o;
+  o = align256(o + (size_t)nb * nb * sizeof(uint32_t));
+  L->off_ofs = o;
+  o = align256(o + (size_t)(nb * nb + 1) * sizeof(uint64_t));
+  L->off_inbox = o;
+  o = align256(o + (size_t)2 * L->total * L->entry);
+  L->bytes = o;
+  return 0;
 }
 
 int check_net(const bs_net* net, const char* who) {
@@ -298,7 +478,7 @@ int check_net(const bs_net* net, const char* who) {
   BS_CHECK_ARG(net->n > 0 && net->n_exc >= 0 && net->n_exc <= net->n,
                "%s: bad sizes n=%d n_exc=%d", who, net->n, net->n_exc);
   BS_CHECK_ARG(net->k_e >= 0 && net->k_i >= 0, "%s: negative fan-out", who);
-  BS_CHECK_ARG(net->acc && net->spk, "%s: acc/spk is NULL", who);
+  BS_CHECK_ARG(net->spk != nullptr, "%s: spk is NULL", who);
   BS_CHECK_ARG(net->n_exc == 0 || net->k_e == 0 || net->idx_e, "%s: idx_e is NULL", who);
   BS_CHECK_ARG(net->n_exc == net->n || net->k_i == 0 || net->idx_i, "%s: idx_i is NULL", who);
   BS_CHECK_ARG((net->w_e == nullptr) == (net->w_i == nullptr),
@@ -306,33 +486,7 @@ int check_net(const bs_net* net, const char* who) {
   return BS_OK;
 }
 
-template <class Model>
-int run(const bs_net* net, const typename Model::State* st, const typename Model::Params* p,
-        int32_t steps, int32_t phase, int32_t* counts_out, uint32_t* hash_out,
-        uint8_t* raster_out, void* workspace, bs_stream_t stream, const char* who) {
-  bs_clear_error();
-  int rc = check_net(net, who);
-  if (rc) return rc;
-  BS_CHECK_ARG(st && p && workspace, "%s: NULL state/params/workspace", who);
-  BS_CHECK_ARG(steps >= 0, "%s: steps=%d < 0", who, steps);
-  BS_CHECK_ARG(phase == 0 || phase == 1, "%s: phase must be 0 or 1", who);
-  if (steps == 0) return BS_OK;
-  const int grid = bs_net_grid_blocks(net);
-  BS_CHECK_ARG(grid > 0, "%s: %s", who, bs_last_error());
-  const int npt = npt_for(net->n, (int64_t)grid * kBlock);
-  if (npt < 0) {
-    bs_set_error("%s: n=%d exceeds 16 neurons per thread on %d workgroups", who, net->n, grid);
-    return BS_ERR_UNSUPPORTED;
-  }
-  hipStream_t s = bs_stream(stream);
-  if (counts_out) {
-    k_zero_u32<<<(steps + 255) / 256, 256, 0, s>>>((uint32_t*)counts_out, steps);
-    BS_CHECK_LAUNCH();
-  }
-  if (hash_out) {
-    k_zero_u32<<<(steps + 255) / 256, 256, 0, s>>>(hash_out, steps);
-    BS_CHECK_LAUNCH();
-  }
+NetArgs make_args(const bs_net* net, const NetLayout& L, void* ws) {
   NetArgs a;
   a.n = net->n;
   a.n_exc = net->n_exc;
@@ -344,58 +498,168 @@ int run(const bs_net* net, const typename Model::State* st, const typename Model
   a.idx_i = net->idx_i;
   a.w_i = net->w_i;
   a.w_i_homo = net->w_i_homo;
-  a.acc = net->acc;
   a.spk = net->spk;
+  a.t0 = 0;
+  a.steps = 0;
+  a.counts = nullptr;
+  a.hash = nullptr;
+  a.raster = nullptr;
+  a.ws = (char*)ws;
+  a.L = L;
+  return a;
+}
+
+template <class Model, int NPT, bool kHet>
+int launch_one(const NetArgs& a, const typename Model::State& st, const typename Model::Params& p,
+               hipStream_t s) {
+  int occ = 0;
+  BS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_run<Model, NPT, kHet>,
+                                                            kBlock, 0));
+  if ((int64_t)occ * bs_num_cus() < a.L.nb) {
+    bs_set_error("runner: %d workgroups cannot be co-resident (occupancy %d x %d CUs)", a.L.nb,
+                 occ, bs_num_cus());
+    return BS_ERR_UNSUPPORTED;
+  }
+  NetArgs aa = a;
+  typename Model::State ss = st;
+  typename Model::Params pp = p;
+  void* args[] = {(void*)&aa, (void*)&ss, (void*)&pp};
+  BS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)k_run<Model, NPT, kHet>, dim3(a.L.nb),
+                                          dim3(kBlock), args, 0, s));
+  return BS_OK;
+}
+
+template <class Model, bool kHet>
+int dispatch_npt(const NetArgs& a, const typename Model::State& st,
+                 const typename Model::Params& p, hipStream_t s) {
+  switch (a.L.npt) {
+    case 1: return launch_one<Model, 1, kHet>(a, st, p, s);
+    case 2: return launch_one<Model, 2, kHet>(a, st, p, s);
+    case 4: return launch_one<Model, 4, kHet>(a, st, p, s);
+    case 8: return launch_one<Model, 8, kHet>(a, st, p, s);
+  }
+  bs_set_error("runner: unsupported neurons-per-thread %d", a.L.npt);
+  return BS_ERR_UNSUPPORTED;
+}
+
+template <class Model>
+int run(const bs_net* net, const typename Model::State* st, const typename Model::Params* p,
+        int64_t t0, int32_t steps, int32_t* counts_out, uint32_t* hash_out, uint8_t* raster_out,
+        void* workspace, bs_stream_t stream, const char* who) {
+  int rc = check_net(net, who);
+  if (rc) return rc;
+  BS_CHECK_ARG(st && p && workspace, "%s: NULL state/params/workspace", who);
+  BS_CHECK_ARG(steps >= 0, "%s: steps=%d < 0", who, steps);
+  BS_CHECK_ARG(t0 >= 0 && t0 + steps < ((int64_t)1 << 32) - 1, "%s: step index out of range",
+               who);
+  if (steps == 0) return BS_OK;
+  NetLayout L;
+  if (plan(net, &L)) {
+    bs_set_error("%s: n=%d needs more than %d neurons per thread", who, net->n, kMaxNpt);
+    return BS_ERR_UNSUPPORTED;
+  }
+  hipStream_t s = bs_stream(stream);
+  const int zb = (steps + 255) / 256;
+  if (counts_out) {
+    k_zero_u32<<<zb, 256, 0, s>>>((uint32_t*)counts_out, steps);
+    BS_CHECK_LAUNCH();
+  }
+  if (hash_out) {
+    k_zero_u32<<<zb, 256, 0, s>>>(hash_out, steps);
+    BS_CHECK_LAUNCH();
+  }
+  NetArgs a = make_args(net, L, workspace);
+  a.t0 = t0;
   a.steps = steps;
-  a.phase = phase;
   a.counts = counts_out;
   a.hash = hash_out;
   a.raster = raster_out;
-  a.bar = (bs_grid_bar*)workspace;
-  if (net->w_e != nullptr) return dispatch_npt<Model, true>(npt, a, *st, *p, grid, s);
-  return dispatch_npt<Model, false>(npt, a, *st, *p, grid, s);
+  if (net->w_e != nullptr) return dispatch_npt<Model, true>(a, *st, *p, s);
+  return dispatch_npt<Model, false>(a, *st, *p, s);
 }
 
 }  // namespace
 
-extern "C" size_t bs_net_workspace_size(void) { return sizeof(bs_grid_bar); }
+extern "C" size_t bs_net_workspace_size(const bs_net* net) {
+  bs_clear_error();
+  if (check_net(net, "bs_net_workspace_size")) return 0;
+  NetLayout L;
+  if (plan(net, &L)) {
+    bs_set_error("bs_net_workspace_size: n=%d too large for the grid", net->n);
+    return 0;
+  }
+  return L.bytes;
+}
 
 extern "C" int bs_net_grid_blocks(const bs_net* net) {
-  if (net == nullptr) {
-    bs_set_error("bs_net_grid_blocks: net is NULL");
+  bs_clear_error();
+  if (check_net(net, "bs_net_grid_blocks")) return -1;
+  NetLayout L;
+  if (plan(net, &L)) {
+    bs_set_error("bs_net_grid_blocks: n=%d too large for the grid", net->n);
     return -1;
   }
-  const int cus = bs_num_cus();
-  int bpc = pick_blocks_per_cu(net);
-  // never more workgroups than neurons need
-  const int64_t need = ((int64_t)net->n + kBlock - 1) / kBlock;
-  int64_t grid = (int64_t)bpc * cus;
-  if (grid > need) grid = need;
-  if (grid < 1) grid = 1;
-  return (int)grid;
+  return L.nb;
+}
+
+extern "C" int bs_net_prepare(const bs_net* net, void* workspace, bs_stream_t stream) {
+  bs_clear_error();
+  int rc = check_net(net, "bs_net_prepare");
+  if (rc) return rc;
+  BS_CHECK_ARG(workspace != nullptr, "bs_net_prepare: workspace is NULL");
+  NetLayout L;
+  if (plan(net, &L)) {
+    bs_set_error("bs_net_prepare: n=%d too large for the grid", net->n);
+    return BS_ERR_UNSUPPORTED;
+  }
+  hipStream_t s = bs_stream(stream);
+  char* ws = (char*)workspace;
+  NetArgs a = make_args(net, L, workspace);
+  // header, tagged counts, capacities and offsets are cleared; inboxes need no clearing
+  k_zero_u64<<<64, 256, 0, s>>>((uint64_t*)ws, (int64_t)(L.off_inbox / 8));
+  BS_CHECK_LAUNCH();
+  k_caps<<<L.nb, kBlock, 0, s>>>(a, (uint32_t*)(ws + L.off_cap));
+  BS_CHECK_LAUNCH();
+  uint64_t* ofs = (uint64_t*)(ws + L.off_ofs);
+  k_offsets<<<1, kBlock, 0, s>>>(L.nb, (const uint32_t*)(ws + L.off_cap), ofs,
+                                 ofs + (int64_t)L.nb * L.nb);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
 }
 
 extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p,
-                               int32_t steps, int32_t phase, int32_t* counts_out,
+                               int64_t t0, int32_t steps, int32_t* counts_out,
                                uint32_t* hash_out, uint8_t* raster_out, void* workspace,
                                bs_stream_t stream) {
+  bs_clear_error();
   if (st) {
     BS_CHECK_ARG(st->V && st->ge && st->gi && st->ref, "bs_coba_lif_run: NULL state pointer");
   }
   if (p) BS_CHECK_ARG(p->tau != 0.0f, "bs_coba_lif_run: tau must be nonzero");
-  return run<LifModel>(net, st, p, steps, phase, counts_out, hash_out, raster_out, workspace,
+  return run<LifModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
                        stream, "bs_coba_lif_run");
 }
 
 extern "C" int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,
-                              int32_t steps, int32_t phase, int32_t* counts_out,
+                              int64_t t0, int32_t steps, int32_t* counts_out,
                               uint32_t* hash_out, uint8_t* raster_out, void* workspace,
                               bs_stream_t stream) {
+  bs_clear_error();
   if (st) {
     BS_CHECK_ARG(st->V && st->m && st->h && st->n && st->ge && st->gi,
                  "bs_coba_hh_run: NULL state pointer");
   }
   if (p) BS_CHECK_ARG(p->C != 0.0f, "bs_coba_hh_run: C must be nonzero");
-  return run<HhModel>(net, st, p, steps, phase, counts_out, hash_out, raster_out, workspace,
+  return run<HhModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
                       stream, "bs_coba_hh_run");
+}
+
+extern "C" int bs_net_error(const void* workspace, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(workspace != nullptr, "bs_net_error: workspace is NULL");
+  uint32_t e = 0;
+  BS_CHECK_HIP(hipMemcpyAsync(&e, workspace, sizeof(e), hipMemcpyDeviceToHost,
+                              bs_stream(stream)));
+  BS_CHECK_HIP(hipStreamSynchronize(bs_stream(stream)));
+  return e ? -1 : 0;
 }

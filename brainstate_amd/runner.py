@@ -48,9 +48,8 @@ class EINetRunner:
             self.w_e_homo, self.w_i_homo = float(np.float32(w_e)), float(np.float32(w_i))
         self.params = params
         f32 = dict(dtype=torch.float32, device=dev)
-        self.acc = torch.zeros(2, 2, self.n, **f32)
         self.spk = torch.zeros(self.n, dtype=torch.uint8, device=dev)
-        self.phase = 0
+        self.t = 0   # absolute index of the next step
         V0 = torch.as_tensor(np.asarray(V0, np.float32)).to(dev)
         if model == 'lif':
             self.state = dict(V=V0.clone(), ge=torch.zeros(self.n, **f32),
@@ -63,14 +62,17 @@ class EINetRunner:
             ops.hh_init(self.state['V'], self.state['m'], self.state['h'], self.state['n'])
         else:
             raise ValueError(f'unknown model {model!r}')
-        self.ws = torch.zeros(max(int(N.lib().bs_net_workspace_size()), 256), dtype=torch.uint8,
-                              device=dev)
         self._net = N.Net(self.n, self.n_exc, self.k_e, self.k_i,
                           self.idx_e.data_ptr(), None if self.w_e is None else self.w_e.data_ptr(),
                           self.w_e_homo,
                           self.idx_i.data_ptr(), None if self.w_i is None else self.w_i.data_ptr(),
-                          self.w_i_homo, self.acc.data_ptr(), self.spk.data_ptr(),
-                          int(blocks_per_cu))
+                          self.w_i_homo, self.spk.data_ptr(), int(blocks_per_cu))
+        nbytes = int(N.lib().bs_net_workspace_size(ctypes.byref(self._net)))
+        if nbytes == 0:
+            N.check(N.BS_ERR_INVALID, 'bs_net_workspace_size')
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        N.check(N.lib().bs_net_prepare(ctypes.byref(self._net), N.ptr(self.ws),
+                                       N.stream_handle(dev)), 'bs_net_prepare')
 
     @property
     def grid_blocks(self):
@@ -85,7 +87,7 @@ class EINetRunner:
             st = N.LifState(s['V'].data_ptr(), s['ge'].data_ptr(), s['gi'].data_ptr(),
                             s['ref'].data_ptr())
             rc = N.lib().bs_coba_lif_run(ctypes.byref(self._net), ctypes.byref(st),
-                                         ctypes.byref(self.params), int(steps), self.phase,
+                                         ctypes.byref(self.params), self.t, int(steps),
                                          N.ptr(counts), N.ptr(hashes), N.ptr(raster),
                                          N.ptr(self.ws), stream)
             N.check(rc, 'bs_coba_lif_run')
@@ -93,8 +95,15 @@ class EINetRunner:
             st = N.HhState(s['V'].data_ptr(), s['m'].data_ptr(), s['h'].data_ptr(),
                            s['n'].data_ptr(), s['ge'].data_ptr(), s['gi'].data_ptr())
             rc = N.lib().bs_coba_hh_run(ctypes.byref(self._net), ctypes.byref(st),
-                                        ctypes.byref(self.params), int(steps), self.phase,
+                                        ctypes.byref(self.params), self.t, int(steps),
                                         N.ptr(counts), N.ptr(hashes), N.ptr(raster),
                                         N.ptr(self.ws), stream)
             N.check(rc, 'bs_coba_hh_run')
-        self.phase = (self.phase + int(steps)) & 1
+        self.t += int(steps)
+
+    def check(self):
+        """Synchronise and raise if a run's wait hit its spin limit."""
+        rc = N.lib().bs_net_error(N.ptr(self.ws), N.stream_handle(self.device))
+        if rc != 0:
+            raise N.NativeError(f'runner error {rc}: '
+                                + N.lib().bs_last_error().decode(errors='replace'))

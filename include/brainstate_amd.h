@@ -125,20 +125,21 @@ BS_API int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, f
  * Replace `brainstate.transform.for_loop(net.update, times)` over an E/I network
  * (brainstate/transform/_loop_collect_return.py:487-572 -> jax.lax.scan at :268) for the
  * two projections E: neurons [0, n_exc) -> all n, I: [n_exc, n) -> all n, each
- * fixed-num (brainstate/nn/_event_fixedprob.py:102-205).  One persistent launch runs
- * `steps` network steps; per step: inputs from the previous step's spikes -> fused
- * neuron update -> compaction -> scatter of the new spikes into the next step's
- * accumulators, then one grid barrier.
- * acc is [2 phases][2 (E, I)][n] fp32: acc[phase] holds the inputs for the next step
- * (zero at the start of a simulation), acc[phase^1] must be zero.  After the call the
- * pending inputs are in acc[(phase + steps) & 1].
+ * fixed-num (brainstate/nn/_event_fixedprob.py:102-205), in the per-step order of
+ * examples/105_COBA_HH_2007_braincell.py:76-82 (previous step's spikes -> event mat-vecs ->
+ * neuron update).  One persistent launch runs `steps` network steps with no grid barrier:
+ * events travel through per-(source, destination) workgroup inboxes sized from the
+ * connectivity, so they cannot overflow.
+ * Protocol: bs_net_prepare() once per (net, workspace) -- it sizes the inboxes and clears
+ * the pending events -- then runs with consecutive absolute step indices t0 = 0, s1,
+ * s1+s2, ...  State arrays are read at the start and written at the end of each run;
+ * spk receives the last step's spikes.  w_e/w_i == NULL -> homogeneous w_*_homo.
  * counts_out[t] / hash_out[t] (nullable): number of spikes and the order-free digest
  * sum_i mix32(i) mod 2^32 of step t; raster_out [steps, n] uint8 (nullable). */
 typedef struct {
   int32_t n, n_exc, k_e, k_i;
   const int32_t* idx_e; const float* w_e; float w_e_homo;   /* [n_exc, k_e] */
   const int32_t* idx_i; const float* w_i; float w_i_homo;   /* [n - n_exc, k_i] */
-  float* acc;                                               /* [2][2][n] */
   uint8_t* spk;                                             /* [n] last step's spikes */
   int32_t blocks_per_cu;                                    /* 0 = library default */
 } bs_net;
@@ -146,16 +147,22 @@ typedef struct {
 typedef struct { float* V; float* ge; float* gi; int32_t* ref; } bs_lif_state;
 typedef struct { float* V; float* m; float* h; float* n; float* ge; float* gi; } bs_hh_state;
 
-BS_API size_t bs_net_workspace_size(void);  /* zero-filled once when allocated */
+/* Workspace bytes for this net on the current device (0 on error; about
+ * 2 x synapses x (8 B heterogeneous | 4 B homogeneous)). */
+BS_API size_t bs_net_workspace_size(const bs_net* net);
+BS_API int bs_net_prepare(const bs_net* net, void* workspace, bs_stream_t stream);
 BS_API int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p,
-                    int32_t steps, int32_t phase, int32_t* counts_out, uint32_t* hash_out,
-                    uint8_t* raster_out, void* workspace, bs_stream_t stream);
+                           int64_t t0, int32_t steps, int32_t* counts_out, uint32_t* hash_out,
+                           uint8_t* raster_out, void* workspace, bs_stream_t stream);
 BS_API int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,
-                   int32_t steps, int32_t phase, int32_t* counts_out, uint32_t* hash_out,
-                   uint8_t* raster_out, void* workspace, bs_stream_t stream);
+                          int64_t t0, int32_t steps, int32_t* counts_out, uint32_t* hash_out,
+                          uint8_t* raster_out, void* workspace, bs_stream_t stream);
 
-/* Grid size (workgroups) the runners use for this net on the current device. */
+/* Workgroups the runners use for this net on the current device (-1 on error). */
 BS_API int bs_net_grid_blocks(const bs_net* net);
+/* Synchronises `stream`; returns 0 if every wait of the runs so far completed, -1 if one
+ * hit its spin limit (results invalid), or a positive status on a call failure. */
+BS_API int bs_net_error(const void* workspace, bs_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -55,7 +55,7 @@ def test_coba_lif_4000_raster_bit_exact(torch_cuda, het, chunks):
     for c in chunks:
         r.run(c, counts=counts[t0:t0 + c], hashes=hashes[t0:t0 + c], raster=raster[t0:t0 + c])
         t0 += c
-    torch.cuda.synchronize()
+    r.check()
     ras = raster.cpu().numpy().astype(bool)
     assert counts.cpu().numpy().tolist() == gold['counts']
     assert [int(h) & 0xFFFFFFFF for h in hashes.cpu().numpy()] == gold['hashes']
@@ -70,7 +70,7 @@ def test_coba_lif_state_matches_oracle_midway(torch_cuda):
     res = network.run_coba_lif(V0, pe, pi, p, 3200, 137, record_raster=False)
     r = _lif_runner(torch, False)
     r.run(137)
-    torch.cuda.synchronize()
+    r.check()
     for k in ('V', 'ge', 'gi', 'ref'):
         assert np.array_equal(r.state[k].cpu().numpy(), res[k]), k
     assert np.array_equal(r.spk.cpu().numpy().astype(bool), res['spk'])
@@ -91,7 +91,7 @@ def test_coba_hh_2000_raster_bit_exact(torch_cuda):
     raster = torch.zeros(T, c['n'], dtype=torch.uint8, device='cuda')
     counts = torch.zeros(T, dtype=torch.int32, device='cuda')
     r.run(T, counts=counts, raster=raster)
-    torch.cuda.synchronize()
+    r.check()
     assert counts.cpu().numpy().tolist() == gold['counts']
     assert make_golden.sha(np.packbits(raster.cpu().numpy().astype(bool))) == gold['raster_sha256']
     assert make_golden.sha(r.state['V'].cpu().numpy()) == gold['final_V_sha256']
