@@ -299,20 +299,20 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // kBatch synapses per thread per round, all their index/weight loads issued first.
     const int bout = (int)(ta & 1);
     char* ob = inbox + (size_t)bout * buf_bytes;
-    const int64_t items = (int64_t)count * kmax;
-    for (int64_t it0 = threadIdx.x; it0 < items; it0 += (int64_t)kBatch * kBlock) {
+    const uint32_t items = (uint32_t)count * (uint32_t)kmax;
+    for (uint32_t it0 = threadIdx.x; it0 < items; it0 += kBatch * kBlock) {
       int32_t tgt[kBatch];
       float wv[kBatch];
       bool inh[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const int64_t it = it0 + (int64_t)u * kBlock;
+        const uint32_t it = it0 + u * kBlock;
         tgt[u] = -1;
         wv[u] = 0.0f;
         inh[u] = false;
         if (it < items) {
-          const int32_t ai = (int32_t)(it / kmax);
-          const int32_t tt = (int32_t)(it - (int64_t)ai * kmax);
+          const uint32_t ai = it / (uint32_t)kmax;
+          const int32_t tt = (int32_t)(it - ai * (uint32_t)kmax);
           const Row rw = row_of(a, s_list[ai]);
           if (tt < rw.k) {
             tgt[u] = rw.idx[tt];
