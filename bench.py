@@ -42,11 +42,15 @@ def lif_bytes(counts, n, k):
 
 
 def load_traffic():
-    p = os.path.join(ROOT, 'profiles', 'traffic_coba_lif_1m.json')
+    """HBM bytes per 10k-step launch from the committed rocprofv3 PMC summary, if present."""
+    p = os.path.join(ROOT, 'profiles', 'coba_lif_1m_pmc.txt')
     if not os.path.exists(p):
         return None
     with open(p) as f:
-        return json.load(f)
+        for line in f:
+            if line.startswith('bytes_per_launch:'):
+                return int(line.split(':')[1])
+    return None
 
 
 def cpu_baseline(idx_e, idx_i, V0, n_exc, k, budget_s):
@@ -88,6 +92,27 @@ def cpu_baseline(idx_e, idx_i, V0, n_exc, k, budget_s):
             'ms_per_sim_step': el / steps * 1e3}
 
 
+def summarize_rocpd(path):
+    """Text summary of a rocprofv3 results database: kernel stats, and PMC counters per
+    dispatch of each kernel when the database holds them."""
+    import sqlite3
+    db = sqlite3.connect(path)
+    cur = db.cursor()
+    tabs = {r[0] for r in cur.execute("select name from sqlite_master")}
+    out = ['kernel | calls | total_us | avg_us | pct']
+    for name, calls, tot, avg, pct in cur.execute(
+            'select name, total_calls, total_duration, average, percentage from top_kernels'):
+        out.append(f'{name[:110]} | {calls} | {tot:.1f} | {avg:.1f} | {pct:.2f}')
+    if 'counters_collection' in tabs:
+        out.append('')
+        out.append('kernel | counter | dispatches | mean value per dispatch')
+        q = ('select kernel_name, counter_name, count(*), avg(value) from counters_collection '
+             'group by kernel_name, counter_name order by avg(value) desc')
+        for kname, cname, ndisp, val in cur.execute(q):
+            out.append(f'{kname[:110]} | {cname} | {ndisp} | {val:.1f}')
+    return '\n'.join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -98,7 +123,24 @@ def main():
     ap.add_argument('--blocks-per-cu', type=int, default=0)
     ap.add_argument('--cpu-budget', type=float, default=12.0)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--copy-calibration-mb', type=int, default=0,
+                    help='only run a plain device copy of this many MiB (PMC counter scale)')
+    ap.add_argument('--summarize', default=None,
+                    help='only print a text summary of a rocprofv3 results database')
     args = ap.parse_args()
+    if args.summarize:
+        print(summarize_rocpd(args.summarize))
+        return
+    if args.copy_calibration_mb:
+        import torch
+        nb = args.copy_calibration_mb << 20
+        src = torch.ones(nb // 4, dtype=torch.float32, device='cuda')
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'copy_bytes_read': nb, 'copy_bytes_written': nb, 'launches': 3}))
+        return
     if args.gpus != 1:
         print(f'bench.py runs on one GPU only (asked for --gpus {args.gpus}); the multi-GPU '
               f'sharding of this path is a design note, not part of this build.', file=sys.stderr)
@@ -159,7 +201,7 @@ def main():
                    'grid_workgroups': runner.grid_blocks},
         'roofline': {'bound': 'hbm', 'achieved': achieved / 1e9, 'peak': PEAK_HBM / 1e9,
                      'unit': 'GB/s', 'frac': achieved / PEAK_HBM,
-                     'traffic': None if traffic is None else traffic.get('bytes_per_launch'),
+                     'traffic': traffic if T == 10000 else None,
                      'kernel': 'k_run<LifModel,4,true> (persistent runner)',
                      'kernel_ms_per_launch': float(np.mean(kern_ms)),
                      'alg_bytes_per_launch': float(np.mean(alg))},
