@@ -1,0 +1,10 @@
+"""brainstate.nn surface for the spiking-network step (event connectivity, neurons, synapses)."""
+from . import init
+from ._event import EventFixedNumConn, EventFixedProb, EventLinear, FixedNumConn
+from ._fuse import fuse
+from ._module import Dynamics, Module, init_all_states
+from ._neurons import COBA, HH, LIF, AlignPostProj, Expon, LIFRef
+
+__all__ = ['init', 'Module', 'Dynamics', 'init_all_states', 'FixedNumConn', 'EventFixedNumConn',
+           'EventFixedProb', 'EventLinear', 'Expon', 'COBA', 'AlignPostProj', 'LIF', 'LIFRef',
+           'HH', 'fuse']

@@ -1,0 +1,77 @@
+"""Hand a module-built E/I network to the persistent whole-loop runner.
+
+``fuse(neuron, proj_e, proj_i, n_exc, inp)`` takes the pieces of the reference's E/I net
+(examples/105_COBA_HH_2007_braincell.py:54-82: ``N``, ``E`` fed by ``spk[:n_exc]``, ``I`` fed
+by ``spk[n_exc:]``) and returns an ``EINetRunner`` that advances the same network many steps
+per launch, with the constant external input ``inp`` the script passes as ``N(inp)``.
+``runner.write_back()`` copies the state back into the modules.
+"""
+import numpy as np
+import torch
+
+from .. import environ
+from ..runner import EINetRunner
+from ._event import FixedPostNumConn
+from ._neurons import HH, LIFRef
+
+
+def _proj_arrays(proj, n_pre, n):
+    conn = getattr(proj.comm, 'conn', None)
+    if not isinstance(conn, FixedPostNumConn):
+        raise NotImplementedError('fuse() needs fixed-num (EventFixedProb) projections')
+    if conn.shape != (n_pre, n):
+        raise ValueError(f'projection shape {conn.shape} does not match ({n_pre}, {n})')
+    idx = conn.indices.cpu().numpy()
+    w = proj.comm.weight.value
+    if torch.is_tensor(w):
+        w = w.detach().cpu().numpy()
+    w = np.asarray(w, np.float32)
+    return idx, (float(w.reshape(())) if w.size == 1 else np.broadcast_to(w, idx.shape))
+
+
+def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0):
+    if len(neuron._channels) != 2 or neuron._channels[0] is not proj_e or \
+            neuron._channels[1] is not proj_i:
+        raise ValueError('proj_e and proj_i must be the two projections onto neuron, in order')
+    if bool(neuron.spike.value.any()) or proj_e.syn.delta is not None or \
+            proj_i.syn.delta is not None:
+        raise NotImplementedError('fuse() starts from a state without pending spikes')
+    n = neuron.num
+    idx_e, w_e = _proj_arrays(proj_e, n_exc, n)
+    idx_i, w_i = _proj_arrays(proj_i, n - n_exc, n)
+    if np.ndim(w_e) != np.ndim(w_i):   # one heterogeneous -> both per synapse
+        w_e = np.broadcast_to(np.float32(w_e), idx_e.shape)
+        w_i = np.broadcast_to(np.float32(w_i), idx_i.shape)
+    V0 = neuron.V.value.detach().cpu().numpy()
+    if isinstance(neuron, HH):
+        model = 'hh'
+    elif isinstance(neuron, LIFRef):
+        model = 'lif'
+    else:
+        raise NotImplementedError(type(neuron).__name__)
+    r = EINetRunner(model, n, n_exc, idx_e, idx_i, w_e, w_i, neuron.params(float(inp)), V0)
+    # carry the current state over (the runner initialised HH gates at steady state)
+    r.state['ge'].copy_(proj_e.syn.g.value)
+    r.state['gi'].copy_(proj_i.syn.g.value)
+    if model == 'lif':
+        r.state['ref'].copy_(neuron.ref.value)
+    else:
+        r.state['m'].copy_(neuron.m.value)
+        r.state['h'].copy_(neuron.h.value)
+        r.state['n'].copy_(neuron.n.value)
+
+    def write_back():
+        neuron.V.value = r.state['V'].clone()
+        proj_e.syn.g.value = r.state['ge'].clone()
+        proj_i.syn.g.value = r.state['gi'].clone()
+        neuron.spike.value = r.spk.clone().view(torch.bool)
+        if model == 'lif':
+            neuron.ref.value = r.state['ref'].clone()
+        else:
+            neuron.m.value = r.state['m'].clone()
+            neuron.h.value = r.state['h'].clone()
+            neuron.n.value = r.state['n'].clone()
+
+    r.write_back = write_back
+    r.dt = environ.get_dt()
+    return r

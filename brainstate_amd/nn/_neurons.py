@@ -1,0 +1,236 @@
+"""Neuron / synapse models the reference's E/I scripts use, on the fused HIP step kernels.
+
+These stand in for the un-vendored ``brainpy.state`` classes that brainstate redirects to
+(brainstate/nn/__init__.py:349-415) and that examples/105_COBA_HH_2007_braincell.py:54-91,
+examples/400_CUBA_2005_bpu.py:36-66 and docs/tutorials/brain_dynamics/04_building_an_snn.ipynb
+build networks from, plus the reference-held HH neuron of examples/100_hh_neuron_model.py.
+
+Composition, as in brainpy.state: ``AlignPostProj(comm, syn=Expon, out=COBA, post=neuron)``
+registers a conductance channel on the post-synaptic neuron; calling the projection with
+spikes runs ``comm`` (the event mat-vec) and queues its output as the channel's delta
+input; calling the neuron advances every channel's Expon conductance and the membrane in
+one fused kernel (``bs_coba_lif_step`` / ``bs_coba_hh_step``): g' = g*exp(-dt/tau) + delta,
+COBA current g*(E - V), exp-Euler membrane, spike.  Up to two conductance channels per
+neuron (E and I) map onto the kernel's two; more raise NotImplementedError.
+
+Units: plain floats in mV, ms, mS (per cm^2 for HH); brainunit is not used.
+"""
+import numpy as np
+import torch
+
+from .. import environ
+from .. import ops
+from .._state import HiddenState, ShortTermState
+from . import init
+from ._module import Dynamics, Module
+
+__all__ = ['Expon', 'COBA', 'AlignPostProj', 'LIF', 'LIFRef', 'HH']
+
+
+class _Desc:
+    """``Cls.desc(...)``: a deferred constructor (brainpy.state ParamDescriber)."""
+
+    def __init__(self, cls, args, kwargs):
+        self.cls, self.args, self.kwargs = cls, args, kwargs
+
+    def __call__(self):
+        return self.cls(*self.args, **self.kwargs)
+
+
+class _Describable:
+    @classmethod
+    def desc(cls, *args, **kwargs):
+        return _Desc(cls, args, kwargs)
+
+
+def _dev():
+    from .. import _native
+    _native.require_gpu()
+    return torch.device('cuda', torch.cuda.current_device())
+
+
+class Expon(Module, _Describable):
+    """Exponential conductance dg/dt = -g/tau, g += delta input each step."""
+    __module__ = 'brainstate_amd.nn'
+    _init_first = True
+
+    def __init__(self, in_size, tau=8.0, g_initializer=0.0, name=None):
+        super().__init__(name=name)
+        self.in_size = init.to_size(in_size)
+        self.tau = float(tau)
+        self.g_initializer = g_initializer
+        self.delta = None
+
+    def init_state(self, *args, **kwargs):
+        n = int(np.prod(self.in_size))
+        g = init.param(self.g_initializer, (n,))
+        self.g = HiddenState(torch.zeros(n, device=_dev()) + (float(g) if init._is_scalar(g)
+                                                              else torch.as_tensor(g, device=_dev())))
+        self.delta = None
+
+    def add_delta_input(self, key, value):
+        self.delta = value if self.delta is None else self.delta + value
+
+
+class COBA(Module, _Describable):
+    """Conductance-based output: I = g * (E - V)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, E, name=None):
+        super().__init__(name=name)
+        self.E = float(E)
+
+
+class AlignPostProj(Module):
+    """Projection with post-aligned synapse (brainpy.state AlignPostProj)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, *modules, comm, syn, out, post, name=None):
+        super().__init__(name=name)
+        if modules:
+            raise NotImplementedError('prefetch modules before comm are not supported')
+        self.comm = comm
+        self.syn = syn() if isinstance(syn, _Desc) else syn
+        self.out = out() if isinstance(out, _Desc) else out
+        if not isinstance(self.syn, Expon) or not isinstance(self.out, COBA):
+            raise NotImplementedError('the fused kernels implement Expon synapses with COBA '
+                                      'output')
+        self.post = post
+        post._add_channel(self)
+
+    def update(self, spk):
+        current = self.comm(spk)
+        self.syn.add_delta_input(self.name or id(self), current)
+        return current
+
+
+class _COBANeuron(Dynamics):
+    def __init__(self, in_size, name=None):
+        super().__init__(in_size, name=name)
+        self._channels = []
+
+    def _add_channel(self, proj):
+        if len(self._channels) >= 2:
+            raise NotImplementedError('the fused step kernels take at most two conductance '
+                                      'channels (E and I)')
+        self._channels.append(proj)
+
+    def _channel_args(self):
+        zeros = torch.zeros(self.num, device=_dev())
+        g, ins, E, tau = [], [], [], []
+        for ch in self._channels:
+            g.append(ch.syn.g.value)
+            ins.append(ch.syn.delta)
+            E.append(ch.out.E)
+            tau.append(ch.syn.tau)
+        while len(g) < 2:
+            g.append(zeros.clone())
+            ins.append(None)
+            E.append(0.0)
+            tau.append(1.0)
+        return g, ins, E, tau
+
+    def _finish_channels(self, g):
+        for ch, gv in zip(self._channels, g):
+            ch.syn.g.value = gv
+            ch.syn.delta = None
+
+    def get_spike(self):
+        return self.spike.value
+
+
+def _ext_input(x):
+    if torch.is_tensor(x) or isinstance(x, np.ndarray):
+        if np.prod(tuple(x.shape)) != 1:
+            raise NotImplementedError('per-neuron external input arrays are not supported by '
+                                      'the fused kernel; pass a scalar')
+        return float(x.reshape(()).item() if torch.is_tensor(x) else x.reshape(()))
+    return float(x)
+
+
+class LIFRef(_COBANeuron, _Describable):
+    """Leaky integrate-and-fire with refractory period and hard reset."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, in_size, R=1., tau=5., tau_ref=5., V_th=1., V_reset=0., V_rest=0.,
+                 V_initializer=0., spk_reset='hard', name=None):
+        super().__init__(in_size, name=name)
+        if spk_reset != 'hard':
+            raise NotImplementedError("only spk_reset='hard' is implemented by the fused kernel")
+        self.R, self.tau, self.tau_ref = float(R), float(tau), float(tau_ref)
+        self.V_th, self.V_reset, self.V_rest = float(V_th), float(V_reset), float(V_rest)
+        self.V_initializer = V_initializer
+
+    def init_state(self, *args, **kwargs):
+        n = self.num
+        V = init.param(self.V_initializer, (n,))
+        if init._is_scalar(V):
+            V = np.full(n, float(V), np.float32)
+        self.V = HiddenState(torch.as_tensor(np.asarray(V, np.float32), device=_dev()).clone())
+        self.ref = HiddenState(torch.zeros(n, dtype=torch.int32, device=_dev()))
+        self.spike = ShortTermState(torch.zeros(n, dtype=torch.bool, device=_dev()))
+
+    def params(self, I_ext=0.0):
+        _, _, E, tau = self._channel_args()
+        return ops.lif_params(V_rest=self.V_rest, V_th=self.V_th, V_reset=self.V_reset,
+                              tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
+                              E_e=E[0], E_i=E[1], tau_e=tau[0], tau_i=tau[1],
+                              dt=environ.get_dt())
+
+    def update(self, x=0.):
+        g, ins, E, tau = self._channel_args()
+        p = self.params(_ext_input(x))
+        spk = ops.coba_lif_step(self.V.value, g[0], g[1], self.ref.value, ins[0], ins[1], p)
+        self._finish_channels(g)
+        self.spike.value = spk.view(torch.bool)
+        return self.spike.value
+
+
+class LIF(LIFRef):
+    """LIF without a refractory period (LIFRef with tau_ref = 0)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, in_size, R=1., tau=5., V_th=1., V_reset=0., V_rest=0., V_initializer=0.,
+                 spk_reset='hard', name=None):
+        super().__init__(in_size, R=R, tau=tau, tau_ref=0., V_th=V_th, V_reset=V_reset,
+                         V_rest=V_rest, V_initializer=V_initializer, spk_reset=spk_reset,
+                         name=name)
+
+
+class HH(_COBANeuron, _Describable):
+    """Hodgkin-Huxley neuron of examples/100_hh_neuron_model.py:25-93 (exp-Euler on V, m, h, n)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, in_size, ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03,
+                 V_th=20., C=1.0, V_initializer=-65., name=None):
+        super().__init__(in_size, name=name)
+        self.ENa, self.gNa, self.EK, self.gK = float(ENa), float(gNa), float(EK), float(gK)
+        self.EL, self.gL, self.V_th, self.C = float(EL), float(gL), float(V_th), float(C)
+        self.V_initializer = V_initializer
+
+    def init_state(self, *args, **kwargs):
+        n = self.num
+        V = init.param(self.V_initializer, (n,))
+        if init._is_scalar(V):
+            V = np.full(n, float(V), np.float32)
+        dev = _dev()
+        self.V = HiddenState(torch.as_tensor(np.asarray(V, np.float32), device=dev).clone())
+        m, h, nn_ = (torch.empty(n, device=dev) for _ in range(3))
+        ops.hh_init(self.V.value, m, h, nn_)
+        self.m, self.h, self.n = HiddenState(m), HiddenState(h), HiddenState(nn_)
+        self.spike = ShortTermState(torch.zeros(n, dtype=torch.bool, device=dev))
+
+    def params(self, I_ext=0.0):
+        _, _, E, tau = self._channel_args()
+        return ops.hh_params(ENa=self.ENa, gNa=self.gNa, EK=self.EK, gK=self.gK, EL=self.EL,
+                             gL=self.gL, C=self.C, V_th=self.V_th, I_ext=I_ext, E_e=E[0],
+                             E_i=E[1], tau_e=tau[0], tau_i=tau[1], dt=environ.get_dt())
+
+    def update(self, x=0.):
+        g, ins, E, tau = self._channel_args()
+        p = self.params(_ext_input(x))
+        spk = ops.coba_hh_step(self.V.value, self.m.value, self.h.value, self.n.value, g[0],
+                               g[1], ins[0], ins[1], p)
+        self._finish_channels(g)
+        self.spike.value = spk.view(torch.bool)
+        return self.spike.value

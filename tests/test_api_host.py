@@ -1,0 +1,124 @@
+"""Host-side behaviour of the brainstate-compatible layer (CPU only, no device work)."""
+import numpy as np
+import pytest
+import torch
+
+import brainstate_amd as bs
+from brainstate_amd.nn import init
+
+
+def test_efferent_pre_is_rejected():            # brainstate/nn/_event_fixedprob.py:123-140
+    with pytest.raises(NotImplementedError, match="efferent_target='pre'"):
+        bs.nn.EventFixedProb(10, 20, 0.1, 1.0, efferent_target='pre')
+
+
+def test_bad_arguments_assert():                 # :125, :141, :145, :147
+    with pytest.raises(AssertionError):
+        bs.nn.EventFixedProb(10, 20, 0.1, 1.0, efferent_target='both')
+    with pytest.raises(AssertionError):
+        bs.nn.EventFixedProb(10, 20, 1.5, 1.0)
+    with pytest.raises(AssertionError):
+        bs.nn.EventFixedProb(10, 20, 0.1, 1.0, afferent_ratio=2.0)
+    with pytest.raises(AssertionError):
+        bs.nn.EventFixedProb(10, 20, '3', 1.0)
+
+
+def test_zero_connections_use_fake_state():      # :198-200
+    m = bs.nn.EventFixedProb(10, 20, 0.0, 1.5)
+    assert m.conn_num == 0
+    assert isinstance(m.weight, bs.FakeState) and m.weight.value == 1.5
+
+
+def test_alias():
+    assert bs.nn.EventFixedProb is bs.nn.EventFixedNumConn
+
+
+def test_param_rules():                          # brainstate/nn/init.py:144-226
+    assert init.param(0.6, (3, 4)) == 0.6        # scalar stays scalar (homogeneous)
+    assert init.param(None, (3,)) is None
+    with pytest.raises(ValueError):
+        init.param(None, (3,), allow_none=False)
+    a = init.param(lambda s: np.ones(s), (3, 4))
+    assert a.shape == (3, 4)
+    assert init.param(np.ones((1, 4)), (3, 4)).shape == (1, 4)   # broadcastable kept
+    with pytest.raises(ValueError):
+        init.param(np.ones((2, 4)), (3, 4))
+    with pytest.raises(ValueError):
+        init.param('x', (3,))
+
+
+def test_environ_context_and_dt():
+    with pytest.raises(KeyError):
+        bs.environ.get('no_such_key')
+    bs.environ.set(dt=0.1)
+    assert bs.environ.get_dt() == 0.1
+    with bs.environ.context(dt=0.05, t=3.0):
+        assert bs.environ.get_dt() == 0.05 and bs.environ.get('t') == 3.0
+        with bs.environ.context(dt=0.01):
+            assert bs.environ.get_dt() == 0.01
+        assert bs.environ.get_dt() == 0.05
+    assert bs.environ.get_dt() == 0.1
+    assert bs.environ.dftype() == np.float32 and bs.environ.ditype() == np.int32
+    with pytest.raises(NotImplementedError):
+        bs.environ.set(precision=64)
+
+
+def test_state_value_semantics():
+    s = bs.State(torch.zeros(3))
+    s.value = torch.ones(3)
+    assert torch.equal(s.value, torch.ones(3))
+    with pytest.raises(ValueError):
+        s.value = torch.ones(4)
+    with pytest.raises(ValueError):
+        s.value = bs.State(1)
+    assert isinstance(bs.HiddenState(1), bs.ShortTermState)
+
+
+def test_for_loop_stacks_like_scan():            # brainstate/transform/_loop_collect_return.py
+    acc = bs.State(torch.zeros(()))
+
+    def f(x):
+        acc.value = acc.value + x
+        return acc.value.clone()
+
+    ys = bs.transform.for_loop(f, torch.arange(5.0))
+    assert ys.tolist() == [0, 1, 3, 6, 10]
+    ys = bs.transform.for_loop(lambda i: (torch.tensor(i), {'a': torch.tensor(2 * i)}),
+                               [0, 1, 2])
+    assert ys[0].tolist() == [0, 1, 2] and ys[1]['a'].tolist() == [0, 2, 4]
+    assert bs.transform.jit(f) is f
+
+
+def test_checkpointed_scan_known_answer_sequence():
+    # brainstate/transform/_loop_collect_return_test.py:66-79: ys = [0, 0, 2, 6, 12]
+    c = bs.State(torch.zeros(()))
+
+    def f(i):
+        out = c.value.clone()
+        c.value = c.value + 2 * i
+        return out
+
+    assert bs.transform.for_loop(f, torch.arange(5.0)).tolist() == [0, 0, 2, 6, 12]
+
+
+def test_module_tree_and_init_order():
+    class Leaf(bs.nn.Module):
+        def __init__(self, log, first=False):
+            super().__init__()
+            self.log = log
+            self._init_first = first
+
+        def init_state(self):
+            self.log.append(self)
+
+    log = []
+
+    class Net(bs.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.a = Leaf(log)
+            self.b = [Leaf(log, first=True)]
+
+    net = Net()
+    bs.nn.init_all_states(net)
+    assert log[0] is net.b[0] and log[1] is net.a

@@ -1,0 +1,194 @@
+"""GPU tests of the brainstate-compatible layer: the reference's own layer tests, and an
+E/I network built from modules, stepped eagerly and fused, against the oracle."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import event, network, neuron
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+GOLD = os.path.join(os.path.dirname(__file__), 'golden')
+sys.path.insert(0, GOLD)
+import make_golden  # noqa: E402
+
+
+@pytest.fixture(scope='module')
+def bs():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail('GPU tests need a ROCm GPU')
+    import brainstate_amd
+    return brainstate_amd
+
+
+def test_event_update_matches_dense_reference(bs):
+    """brainstate/nn/_event_fixedprob_test.py:247-260."""
+    import torch
+    print('[case] fixedprob np.add.at', flush=True)
+    n_in, n_out = 20, 30
+    fn = bs.nn.EventFixedProb(n_in, n_out, 0.2, 1.5, seed=11)
+    spk = np.random.RandomState(0).rand(n_in) < 0.3
+    out = fn(torch.tensor(spk.astype(np.float32), device='cuda')).cpu().numpy()
+    indices = fn.conn.indices.cpu().numpy()
+    ref = np.zeros((n_out,))
+    for i in range(n_in):
+        np.add.at(ref, indices[i], 1.5 * float(spk[i]))
+    assert np.allclose(out, ref, rtol=1e-4, atol=1e-4)
+    assert np.array_equal(indices, np.random.RandomState(11).randint(0, n_out, (n_in, 6)))
+
+
+def test_fixedprob_heterogeneous_and_batched(bs):
+    import torch
+    print('[case] fixedprob het batched', flush=True)
+    m = bs.nn.EventFixedProb(300, 200, 40, bs.nn.init.Normal(0.5, 0.1, seed=3), seed=5)
+    spk = np.random.RandomState(1).rand(3, 300) < 0.2
+    out = m(torch.tensor(spk, device='cuda')).cpu().numpy()
+    w = np.asarray(m.weight.value, F)
+    idx = m.conn.indices.cpu().numpy()
+    for b in range(3):
+        np.testing.assert_allclose(out[b], event.scatter_fixed(spk[b], idx, w, 200),
+                                   rtol=1e-5, atol=1e-6)
+
+
+def test_fixedprob_afferent_ratio_csr(bs):
+    import torch
+    print('[case] fixedprob csr', flush=True)
+    m = bs.nn.EventFixedProb(500, 400, 30, 0.7, seed=9, afferent_ratio=0.5)
+    from oracle import conn
+    indptr, indices, sel = conn.csr_afferent(500, 400, 30, 9, 0.5)
+    assert np.array_equal(m.conn.indptr.cpu().numpy(), indptr)
+    spk = np.random.RandomState(2).rand(500) < 0.3
+    out = m(torch.tensor(spk, device='cuda')).cpu().numpy()
+    assert np.array_equal(out, event.scatter_csr(spk, indptr, indices, F(0.7), 400))
+
+
+def test_fixedprob_zero_conn_returns_zeros(bs):
+    import torch
+    m = bs.nn.EventFixedProb(10, 7, 0.0, 1.0)
+    out = m(torch.ones(4, 10, device='cuda'))
+    assert out.shape == (4, 7) and float(out.abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize('bool_x', [True, False])
+@pytest.mark.parametrize('homo_w', [True, False])
+def test_event_linear_reference_test1(bs, homo_w, bool_x):     # _event_linear_test.py:26-40
+    import torch
+    print('[case] event linear', homo_w, bool_x, flush=True)
+    x = np.random.RandomState(4).rand(20) < 0.1
+    x = x if bool_x else x.astype(F)
+    m = bs.nn.EventLinear(20, 40, 1.5 if homo_w else bs.nn.init.Uniform(-0.5, 0.5, seed=1),
+                          float_as_event=bool_x)
+    y = m(torch.tensor(x, device='cuda')).cpu().numpy()
+    W = m.weight.value
+    expect = x.sum() * W * np.ones(40) if homo_w else x.astype(F) @ W
+    assert np.allclose(y, expect, rtol=1e-5)
+
+
+@pytest.mark.parametrize('float_as_event', [True, False])
+def test_event_linear_homogeneous_matches_dense_nonbinary(bs, float_as_event):  # :127-162
+    import torch
+    spk = torch.tensor([0., 2., 0., 3., 0., 0., 1., 0., 0., 5.], device='cuda')
+    homo = bs.nn.EventLinear(10, 8, 1.5, float_as_event=float_as_event)
+    dense = bs.nn.EventLinear(10, 8, bs.nn.init.Constant(1.5), float_as_event=float_as_event)
+    yh, yd = homo(spk).cpu().numpy(), dense(spk).cpu().numpy()
+    assert np.allclose(yh, yd)
+    assert np.allclose(yh, np.ones(8) * (4 if float_as_event else 11) * 1.5)
+
+
+def test_event_linear_batched_bit_exact(bs):
+    import torch
+    print('[case] event linear batched', flush=True)
+    rng = np.random.RandomState(7)
+    spk = rng.rand(64, 512) < 0.05
+    W = rng.normal(0, 0.125, (512, 256)).astype(F)
+    m = bs.nn.EventLinear(512, 256, W)
+    y = m(torch.tensor(spk, device='cuda')).cpu().numpy()
+    assert np.array_equal(y, event.event_linear(spk, W))
+
+
+class _EINet:
+    """examples/105_COBA_HH_2007_braincell.py:54-82 with config-[1] LIF parameters."""
+
+    def __init__(self, bs):
+        c = make_golden.CONFIG1
+        self.bs = bs
+        self.n_exc, self.num = c['n_exc'], c['n']
+        V0 = np.random.RandomState(c['seed_v']).uniform(-60., -50., c['n']).astype(F)
+        self.N = bs.nn.LIFRef(self.num, V_rest=-60., V_th=-50., V_reset=-60., tau=20.,
+                              tau_ref=5., V_initializer=lambda s: V0)
+        self.E = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=0.02, conn_weight=0.6,
+                                      seed=c['seed_e']),
+            syn=bs.nn.Expon.desc(self.num, tau=5.), out=bs.nn.COBA.desc(E=0.), post=self.N)
+        self.I = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(self.num - self.n_exc, self.num, conn_num=0.02,
+                                      conn_weight=6.7, seed=c['seed_i']),
+            syn=bs.nn.Expon.desc(self.num, tau=10.), out=bs.nn.COBA.desc(E=-80.), post=self.N)
+        for m in (self.E.syn, self.I.syn, self.N):
+            m.init_state()
+
+    def update(self, t):
+        with self.bs.environ.context(t=t):
+            spk = self.N.get_spike() != 0.
+            self.E(spk[:self.n_exc])
+            self.I(spk[self.n_exc:])
+            self.N(20.)
+            return self.N.get_spike()
+
+
+def test_module_ei_network_matches_oracle(bs):
+    """The reference's E/I script shape, stepped eagerly through the module API."""
+    import torch
+    print('[case] module E/I net eager', flush=True)
+    T = 200
+    pe, pi, V0, p = make_golden.config1_net()
+    ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
+    with bs.environ.context(dt=0.1):
+        net = _EINet(bs)
+        spikes = bs.transform.for_loop(net.update, torch.arange(T) * 0.1)
+    assert np.array_equal(spikes.cpu().numpy(), ref['raster'])
+    assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+
+
+def test_fused_network_continues_eager_state(bs):
+    import torch
+    print('[case] module E/I net fused', flush=True)
+    T = 300
+    pe, pi, V0, p = make_golden.config1_net()
+    ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
+    with bs.environ.context(dt=0.1):
+        net = _EINet(bs)
+        r = bs.nn.fuse(net.N, net.E, net.I, n_exc=net.n_exc, inp=20.)
+        raster = torch.zeros(T, net.num, dtype=torch.uint8, device='cuda')
+        r.run(T, raster=raster)
+        r.check()
+        r.write_back()
+    assert np.array_equal(raster.cpu().numpy().astype(bool), ref['raster'])
+    assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+    assert np.array_equal(net.E.syn.g.value.cpu().numpy(), ref['ge'])
+
+
+def test_hh_module_step_matches_oracle(bs):
+    import torch
+    print('[case] HH module', flush=True)
+    n = 1000
+    rng = np.random.RandomState(5)
+    V0 = rng.uniform(-70, -50, n).astype(F)
+    with bs.environ.context(dt=0.05):
+        hh = bs.nn.HH(n, V_initializer=lambda s: V0)
+        hh.init_state()
+        out = []
+        for _ in range(50):
+            out.append(hh(6.5).cpu().numpy())
+    V, m, h, nn_ = V0.copy(), *neuron.hh_init(V0)
+    ge, gi = np.zeros(n, F), np.zeros(n, F)
+    p = neuron.HHParams(I_ext=6.5, tau_e=1.0, tau_i=1.0)
+    z = np.zeros(n, F)
+    for t in range(50):
+        V, m, h, nn_, ge, gi, spk = neuron.hh_step(V, m, h, nn_, ge, gi, z, z, p)
+        assert np.array_equal(out[t], spk)
+    assert np.array_equal(hh.V.value.cpu().numpy(), V)
