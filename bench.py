@@ -113,6 +113,121 @@ def summarize_rocpd(path):
     return '\n'.join(out)
 
 
+def _timed(fn, reps, warm=2):
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / reps
+
+
+def bench_sparse(args):
+    """event CSR mat-vec 100k x 100k, K=1000, w ~ N(0.5, 0.1), p in {.001,.01,.1}.
+    Scatter (compaction + atomic scatter) and deterministic SELL-64 gather."""
+    import torch
+    from brainstate_amd import ops
+    n, k = 100_000, 1000
+    rng = np.random.RandomState(7)
+    idx = rng.randint(0, n, size=(n, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n, k)).astype(np.float32)
+    d_idx = torch.from_numpy(idx).cuda()
+    d_w = torch.from_numpy(w).cuda()
+    indptr = (np.arange(n + 1, dtype=np.int64) * k).astype(np.int32)
+    sell = ops.build_sell(indptr, idx.reshape(-1), n, n, w=w, device='cuda')
+    out = torch.empty(n, device='cuda')
+    lines = []
+    for p in (0.001, 0.01, 0.1):
+        spk = torch.from_numpy((np.random.RandomState(int(p * 1e4)).rand(n) < p)
+                               .astype(np.uint8)).cuda()
+        active = int(spk.sum().item())
+        E = active * k
+
+        def scatter():
+            act, cnt = ops.spike_compact(spk)
+            ops.event_scatter(act, cnt, d_idx, d_w, n, out=out)
+
+        def gather():
+            ops.event_gather(spk, sell, out=out)
+
+        ts = _timed(scatter, 20)
+        tg = _timed(gather, 20)
+        b_s = n * 1 + E * 8 + n * 4
+        b_g = (n + 1) * 4 + sell['padded'] * 4 + E * 4 + n + n * 4
+        lines.append({'workload': f'event_matvec_100k_K1000_p{p}', 'events': E,
+                      'scatter_us': ts * 1e6, 'scatter_GSOPs': E / ts / 1e9,
+                      'scatter_alg_GBs': b_s / ts / 1e9, 'scatter_frac': b_s / ts / PEAK_HBM,
+                      'gather_us': tg * 1e6, 'gather_GSOPs': E / tg / 1e9,
+                      'gather_alg_GBs': b_g / tg / 1e9, 'gather_frac': b_g / tg / PEAK_HBM})
+    return lines
+
+
+def bench_event_linear(args):
+    """spikes [64, 4096] @ 5 % x W [4096, 4096] N(0, 1/64), 100 recurrent steps,
+    LIF state [64, 4096] (fused update with the EventLinear output as conductance input)."""
+    import torch
+    from brainstate_amd import ops
+    B, n, T = 64, 4096, 100
+    rng = np.random.RandomState(11)
+    W = torch.from_numpy(rng.normal(0, 0.125, (n, n)).astype(np.float32)).cuda()
+    spk = torch.from_numpy((rng.rand(T, B, n) < 0.05).astype(np.uint8)).cuda()
+    V = torch.full((B * n,), -60.0, device='cuda')
+    ge = torch.zeros(B * n, device='cuda')
+    gi = torch.zeros(B * n, device='cuda')
+    ref = torch.zeros(B * n, dtype=torch.int32, device='cuda')
+    cur = torch.empty(B, n, device='cuda')
+    p = ops.lif_params()
+
+    def dense_only():
+        for t in range(T):
+            ops.event_dense(spk[t], W, out=cur)
+
+    def step_all():
+        for t in range(T):
+            ops.event_dense(spk[t], W, out=cur)
+            ops.coba_lif_step(V, ge, gi, ref, cur.view(-1), None, p)
+
+    td = _timed(dense_only, 3, 1) / T
+    tall = _timed(step_all, 3, 1) / T
+    act = spk.float().sum(1)
+    pairs = float(spk.float().sum()) / T
+    U = float((act > 0).float().sum()) / T
+    b_alg = B * n * 1 + U * n * 4 + B * n * 4 + B * n * 9
+    return [{'workload': 'event_linear_64x4096_p0.05', 'events_per_step': pairs * n,
+             'dense_kernel_us': td * 1e6, 'step_us': tall * 1e6,
+             'GSOPs': pairs * n / tall / 1e9, 'alg_GBs': b_alg / tall / 1e9,
+             'frac': b_alg / tall / PEAK_HBM}]
+
+
+def bench_hh(args):
+    """1M COBA-HH neurons, 80 fixed-num targets, dt = 0.05 ms, 4000 steps."""
+    import torch
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    n, n_exc, k, T = 1_000_000, 800_000, 80, 4000
+    idx_e, idx_i, _ = build_net(n, n_exc, k, seed=200)
+    V0 = np.random.RandomState(203).uniform(-70., -50., n).astype(np.float32)
+    we = np.full(idx_e.shape, np.float32(0.05))
+    wi = np.full(idx_i.shape, np.float32(0.3))
+    r = EINetRunner('hh', n, n_exc, idx_e, idx_i, we, wi, ops.hh_params(I_ext=6.5), V0)
+    c = torch.zeros(T, dtype=torch.int32, device='cuda')
+    r.run(T, counts=c)
+    torch.cuda.synchronize()
+    t = _timed(lambda: r.run(T, counts=c), 1, 0)
+    r.check()
+    spikes = int(c.sum().item())
+    E = spikes * k
+    b = T * n * 49 + spikes * 4 + E * 8
+    return [{'workload': 'coba_hh_1m_K80', 'steps': T, 'us_per_step': t / T * 1e6,
+             'spikes': spikes, 'GSOPs': E / t / 1e9, 'alg_GBs': b / t / 1e9,
+             'frac': b / t / PEAK_HBM, 'firing_frac_per_step': spikes / (T * n)}]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -127,7 +242,15 @@ def main():
                     help='only run a plain device copy of this many MiB (PMC counter scale)')
     ap.add_argument('--summarize', default=None,
                     help='only print a text summary of a rocprofv3 results database')
+    ap.add_argument('--workload', default='coba_lif_1m',
+                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh'],
+                    help='coba_lif_1m is the reported line; the others measure the other configs')
     args = ap.parse_args()
+    if args.workload != 'coba_lif_1m':
+        fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh}
+        for line in fn[args.workload](args):
+            print(json.dumps(line), flush=True)
+        return
     if args.summarize:
         print(summarize_rocpd(args.summarize))
         return
