@@ -1,15 +1,17 @@
 // N2c: batched event x dense weight (EventLinear).
 //
-// One wave per (batch row b, tile of 64*V output columns).  The wave walks the input
-// index i in ascending order; the spike test is wave-uniform, so inactive rows cost one
-// scalar load and a branch, and an active row is streamed as one coalesced 64*V-float
-// segment (128-bit loads when V = 4).  Each lane adds its V columns in ascending i, the
-// same order as a sequential reference loop, so results are bit-reproducible.
+// One wave per (batch row b, tile of 64*V output columns).  The wave reads 64 spikes of row b
+// per step (one byte or float per lane) and ballots them into a mask; the active inputs of
+// the mask are then streamed kBatch at a time: kBatch coalesced row segments of W (128-bit
+// loads when V = 4) are in flight before the first add.  Each lane adds its V columns in
+// ascending input order, the order of a sequential reference loop, so results are
+// bit-reproducible.
 #include "common.h"
 
 namespace {
 
 constexpr int kBlock = 256;
+constexpr int kBatch = 8;
 
 __device__ __forceinline__ float spk_val(const uint8_t* p, int64_t i) { return (float)p[i]; }
 __device__ __forceinline__ float spk_val(const float* p, int64_t i) { return p[i]; }
@@ -30,27 +32,53 @@ __global__ __launch_bounds__(kBlock) void k_event_dense(const T* __restrict__ sp
   float acc[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) acc[v] = 0.0f;
-  for (int32_t i = 0; i < n_in; ++i) {
-    const float sv = spk_val(srow, i);  // same address in every lane
-    if (sv == 0.0f) continue;
-    if (!live) continue;
-    const float* wr = W + (int64_t)i * n_out + j0;
-    if (V == 4) {
-      const float4 x = *(const float4*)wr;
-      if (kEvent) {
-        acc[0] += x.x; acc[1] += x.y; acc[2] += x.z; acc[3] += x.w;
-      } else {
-        acc[0] += sv * x.x; acc[1] += sv * x.y; acc[2] += sv * x.z; acc[3] += sv * x.w;
+  for (int32_t i0 = 0; i0 < n_in; i0 += BS_WAVE) {
+    const int32_t i = i0 + lane;
+    const float sv = i < n_in ? spk_val(srow, i) : 0.0f;
+    uint64_t m = bs_ballot(sv != 0.0f);
+    while (m) {
+      int32_t r[kBatch];
+      float sc[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        r[u] = -1;
+        sc[u] = 1.0f;
+        if (m) {
+          const int bit = __builtin_ctzll(m);
+          m &= m - 1;
+          r[u] = i0 + bit;
+          if (!kEvent) sc[u] = __shfl(sv, bit);
+        }
       }
-    } else {
-      const float x = *wr;
-      acc[0] += kEvent ? x : sv * x;
+      float x[kBatch][V];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (r[u] >= 0 && live) {
+          const float* wr = W + (int64_t)r[u] * n_out + j0;
+          if (V == 4) {
+            const float4 q = *(const float4*)wr;
+            x[u][0] = q.x;
+            x[u][V > 1 ? 1 : 0] = q.y;
+            x[u][V > 2 ? 2 : 0] = q.z;
+            x[u][V > 3 ? 3 : 0] = q.w;
+          } else {
+            x[u][0] = *wr;
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (r[u] >= 0) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[v] += kEvent ? x[u][v] : sc[u] * x[u][v];
+        }
+      }
     }
   }
   if (live) {
     float* o = out + (int64_t)b * n_out + j0;
     if (V == 4) {
-      *(float4*)o = make_float4(acc[0], acc[1], acc[2], acc[3]);
+      *(float4*)o = make_float4(acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0], acc[V > 3 ? 3 : 0]);
     } else {
       o[0] = acc[0];
     }

@@ -68,17 +68,41 @@ __global__ __launch_bounds__(kBlock) void k_scatter(const int32_t* __restrict__ 
   }
 }
 
-__device__ __forceinline__ bool spk_at(const uint8_t* p, int32_t i) { return p[i] != 0; }
-__device__ __forceinline__ bool spk_at(const float* p, int32_t i) { return p[i] != 0.0f; }
+// Spikes -> bitmap, one ballot per 64 spikes: bits[w] bit l <=> spk[32*w + l] != 0.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_pack(const T* __restrict__ spk, int32_t n,
+                                                 uint32_t* __restrict__ bits) {
+  const int lane = bs_lane();
+  const int64_t nwords = ((int64_t)n + 31) / 32;
+  for (int64_t base = ((int64_t)blockIdx.x * kBlock + threadIdx.x) - lane;
+       base < (int64_t)n; base += (int64_t)gridDim.x * kBlock) {
+    const int64_t i = base + lane;
+    const bool a = i < n && spk[i] != T(0);
+    const uint64_t m = bs_ballot(a);
+    const int64_t w = base / 32;
+    if (lane == 0 && w < nwords) bits[w] = (uint32_t)m;
+    if (lane == 1 && w + 1 < nwords) bits[w + 1] = (uint32_t)(m >> 32);
+  }
+}
 
-template <typename T, bool kHet>
-__global__ __launch_bounds__(kBlock) void k_gather(const T* __restrict__ spk, int32_t n_pre,
+// Gather over SELL-64: wave = slice of 64 posts, lane = post; kU columns of pre indices in
+// flight per lane; the spike test reads a bitmap held in LDS (kLds) or global memory.
+template <bool kHet, bool kLds>
+__global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ bits,
+                                                   int32_t n_pre,
                                                    const int64_t* __restrict__ slice_ptr,
                                                    const int32_t* __restrict__ sell_pre,
                                                    const float* __restrict__ sell_w,
                                                    float w_homo, int32_t n_post,
                                                    float* __restrict__ out) {
-  constexpr int kU = 8;  // columns in flight per lane
+  constexpr int kU = 16;
+  extern __shared__ uint32_t s_bits[];
+  const int32_t nwords = (n_pre + 31) / 32;
+  if (kLds) {
+    for (int32_t w = threadIdx.x; w < nwords; w += kBlock) s_bits[w] = bits[w];
+    __syncthreads();
+  }
+  const uint32_t* bm = kLds ? s_bits : bits;
   const int lane = bs_lane();
   const int64_t slice = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE;
   const int64_t n_slices = ((int64_t)n_post + BS_WAVE - 1) / BS_WAVE;
@@ -91,18 +115,22 @@ __global__ __launch_bounds__(kBlock) void k_gather(const T* __restrict__ spk, in
   int64_t c = 0;
   for (; c + kU <= ncol; c += kU) {
     int32_t i[kU];
-    bool a[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) i[u] = pre[(c + u) * BS_WAVE];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) a[u] = (uint32_t)i[u] < (uint32_t)n_pre && spk_at(spk, i[u]);
+    bool a[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u)
-      if (a[u]) acc += kHet ? wp[(c + u) * BS_WAVE] : w_homo;
+      a[u] = (uint32_t)i[u] < (uint32_t)n_pre && ((bm[i[u] >> 5] >> (i[u] & 31)) & 1u);
+    float w[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) w[u] = (kHet && a[u]) ? wp[(c + u) * BS_WAVE] : w_homo;
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (a[u]) acc += w[u];
   }
   for (; c < ncol; ++c) {
     const int32_t i = pre[c * BS_WAVE];
-    if ((uint32_t)i < (uint32_t)n_pre && spk_at(spk, i))
+    if ((uint32_t)i < (uint32_t)n_pre && ((bm[i >> 5] >> (i & 31)) & 1u))
       acc += kHet ? wp[c * BS_WAVE] : w_homo;
   }
   const int64_t j = slice * BS_WAVE + lane;
@@ -167,38 +195,50 @@ extern "C" int bs_event_scatter_f32(const int32_t* active, const int32_t* n_acti
   return BS_OK;
 }
 
-extern "C" int bs_event_gather_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+extern "C" int bs_spike_pack(const void* spk, int32_t spk_dtype, int32_t n, uint32_t* bits,
+                             bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0, "bs_spike_pack: n=%d < 0", n);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_spike_pack: unknown spike dtype %d", spk_dtype);
+  if (n == 0) return BS_OK;
+  BS_CHECK_ARG(spk && bits, "bs_spike_pack: NULL pointer");
+  hipStream_t s = bs_stream(stream);
+  const int g = grid_for(((int64_t)n + BS_WAVE - 1) / BS_WAVE);
+  if (spk_dtype == BS_SPK_U8) k_pack<uint8_t><<<g, kBlock, 0, s>>>((const uint8_t*)spk, n, bits);
+  else k_pack<float><<<g, kBlock, 0, s>>>((const float*)spk, n, bits);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
                                    const int64_t* slice_ptr, const int32_t* sell_pre,
                                    const float* sell_w, float w_homo, int32_t n_post, float* out,
                                    bs_stream_t stream) {
   bs_clear_error();
   BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "bs_event_gather_f32: negative size");
-  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
-               "bs_event_gather_f32: unknown spike dtype %d", spk_dtype);
   if (n_post == 0) return BS_OK;
-  BS_CHECK_ARG(slice_ptr && sell_pre && out && (spk || n_pre == 0),
+  BS_CHECK_ARG(slice_ptr && sell_pre && out && (spk_bits || n_pre == 0),
                "bs_event_gather_f32: NULL pointer");
   hipStream_t s = bs_stream(stream);
   const int64_t n_slices = ((int64_t)n_post + BS_WAVE - 1) / BS_WAVE;
   const int g = (int)((n_slices + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE));
+  const int64_t nwords = ((int64_t)n_pre + 31) / 32;
+  const bool lds = nwords * 4 <= 64 * 1024;
+  const size_t shm = lds ? (size_t)nwords * 4 : 0;
   const bool het = sell_w != nullptr;
-  if (spk_dtype == BS_SPK_U8) {
-    const uint8_t* p = (const uint8_t*)spk;
-    if (het)
-      k_gather<uint8_t, true><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, sell_w, w_homo,
-                                                   n_post, out);
-    else
-      k_gather<uint8_t, false><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, nullptr,
-                                                    w_homo, n_post, out);
-  } else {
-    const float* p = (const float*)spk;
-    if (het)
-      k_gather<float, true><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, sell_w, w_homo,
-                                                 n_post, out);
-    else
-      k_gather<float, false><<<g, kBlock, 0, s>>>(p, n_pre, slice_ptr, sell_pre, nullptr, w_homo,
-                                                  n_post, out);
-  }
+  if (het && lds)
+    k_gather<true, true><<<g, kBlock, shm, s>>>(spk_bits, n_pre, slice_ptr, sell_pre, sell_w,
+                                                w_homo, n_post, out);
+  else if (het)
+    k_gather<true, false><<<g, kBlock, 0, s>>>(spk_bits, n_pre, slice_ptr, sell_pre, sell_w,
+                                               w_homo, n_post, out);
+  else if (lds)
+    k_gather<false, true><<<g, kBlock, shm, s>>>(spk_bits, n_pre, slice_ptr, sell_pre, nullptr,
+                                                 w_homo, n_post, out);
+  else
+    k_gather<false, false><<<g, kBlock, 0, s>>>(spk_bits, n_pre, slice_ptr, sell_pre, nullptr,
+                                                w_homo, n_post, out);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

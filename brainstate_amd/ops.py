@@ -70,18 +70,30 @@ def event_scatter(active, n_active, indices, w, n_post, k=None, indptr=None, out
     return out
 
 
-def event_gather(spk, sell, out=None):
+def spike_pack(spk, bits=None):
+    """Spikes -> bitmap int32 [(n + 31) // 32] (bit i % 32 of word i // 32)."""
+    spk = _spk_view(spk)
+    n = spk.numel()
+    if bits is None:
+        bits = torch.empty(max((n + 31) // 32, 1), dtype=torch.int32, device=spk.device)
+    N.check(N.lib().bs_spike_pack(N.ptr(spk), _spk_dtype(spk), n, N.ptr(bits),
+                                  N.stream_handle(spk.device)), 'bs_spike_pack')
+    return bits
+
+
+def event_gather(spk, sell, out=None, bits=None):
     """Post-major deterministic gather; ``sell`` from :func:`build_sell`."""
     spk = _spk_view(spk)
     dev = spk.device
     n_post = sell['n_post']
     if out is None:
         out = torch.empty(n_post, dtype=torch.float32, device=dev)
+    bits = spike_pack(spk, bits)
     w = sell.get('w')
     N.check(N.lib().bs_event_gather_f32(
-        N.ptr(spk), _spk_dtype(spk), int(sell['n_pre']), N.ptr(sell['slice_ptr']),
-        N.ptr(sell['pre']), N.ptr(w), float(sell.get('w_homo', 0.0)), int(n_post), N.ptr(out),
-        N.stream_handle(dev)), 'bs_event_gather_f32')
+        N.ptr(bits), int(sell['n_pre']), N.ptr(sell['slice_ptr']), N.ptr(sell['pre']), N.ptr(w),
+        float(sell.get('w_homo', 0.0)), int(n_post), N.ptr(out), N.stream_handle(dev)),
+        'bs_event_gather_f32')
     return out
 
 

@@ -71,16 +71,19 @@ BS_API int bs_event_scatter_f32(const int32_t* active, const int32_t* n_active, 
                          int32_t accumulate, bs_stream_t stream);
 
 /* ---------------------------------------------------------------- N2b event gather
- * Same operator as N2a, post-major and deterministic (no atomics).  Layout SELL-64:
- * posts are grouped in slices of 64; slice s stores its incoming synapses column-major
- * at sell_pre[slice_ptr[s] + c*64 + lane] (lane = post - 64*s), columns in ascending
- * (pre, k) order, padded with -1.  out[j] = 0.0f + the weights of active synapses in
- * that order, i.e. bit-identical to a sequential pre-major scatter.
+ * Same operator as N2a, post-major and deterministic (no atomics).  Spikes come as a
+ * bitmap (bs_spike_pack: bit i%32 of word i/32 set <=> spk[i] != 0).  Layout SELL-64:
+ * posts are grouped in slices of 64; slice s stores its incoming synapses column-major at
+ * sell_pre[slice_ptr[s] + c*64 + lane] (lane = post - 64*s), columns in ascending
+ * (pre, k) order, padded with -1.  out[j] = 0.0f + the weights of active synapses in that
+ * order, i.e. bit-identical to a sequential pre-major scatter.
  * sell_w == NULL -> homogeneous w_homo.  n_slices = ceil(n_post / 64). */
-BS_API int bs_event_gather_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
-                        const int64_t* slice_ptr, const int32_t* sell_pre,
-                        const float* sell_w, float w_homo, int32_t n_post, float* out,
-                        bs_stream_t stream);
+BS_API int bs_spike_pack(const void* spk, int32_t spk_dtype, int32_t n, uint32_t* bits,
+                         bs_stream_t stream);
+BS_API int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
+                               const int64_t* slice_ptr, const int32_t* sell_pre,
+                               const float* sell_w, float w_homo, int32_t n_post, float* out,
+                               bs_stream_t stream);
 
 /* ---------------------------------------------------------------- N2c event x dense
  * Replaces `EventArray(spk) @ W` / `spk @ W` of EventLinear
