@@ -157,6 +157,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
                                                 typename Model::Params p) {
   constexpr int kChunk = NPT * kBlock;
   constexpr int kBatch = 4;
+  constexpr int kStage = kBatch * kBlock;     // synapses per expand round
+  constexpr int kPerLane = kMaxBlocks / BS_WAVE;
   __shared__ int32_t s_list[kChunk];
   __shared__ float s_in[2 * kChunk];          // (E, I) inputs of this workgroup's neurons
   __shared__ uint32_t s_cursor[kMaxBlocks];   // entries written per destination this step
@@ -164,6 +166,11 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   __shared__ uint64_t s_ofs_out[kMaxBlocks];  // inbox offset (d <- me)
   __shared__ int32_t s_wave[kWaves];
   __shared__ uint32_t s_hash;
+  __shared__ uint32_t s_rcnt[kMaxBlocks];     // expand round: entries per destination
+  __shared__ uint32_t s_rpre[kMaxBlocks];     // expand round: prefix over destinations
+  __shared__ uint32_t s_rtot;
+  __shared__ uint64_t s_stage[kStage];        // expand round: entries grouped by destination
+  __shared__ uint32_t s_spos[kStage];         // expand round: their inbox positions
 
   const NetLayout& L = a.L;
   const int nb = L.nb;
@@ -182,6 +189,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     s_ofs_in[s] = ofs[(int64_t)me * nb + s];
     s_ofs_out[s] = ofs[(int64_t)s * nb + me];
     s_cursor[s] = 0;
+    s_rcnt[s] = 0;
   }
   for (int i = threadIdx.x; i < 2 * kChunk; i += kBlock) s_in[i] = 0.0f;
 
@@ -296,17 +304,23 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     __syncthreads();
 
     // ---- D: expand spikes into the destinations' inboxes ----
-    // kBatch synapses per thread per round, all their index/weight loads issued first.
+    // Rounds of up to kBatch*kBlock synapses: (1) each thread loads up to kBatch synapses
+    // (all index/weight loads in flight at once) and counts them per destination in LDS;
+    // (2) one wave turns the counts into an exclusive prefix; (3) entries are placed in an
+    // LDS staging area grouped by destination together with their inbox slot; (4) the
+    // staging area is written out in order, so consecutive lanes store to consecutive
+    // addresses of each destination's region (coalesced) instead of one scattered 8-byte
+    // store per event.
     const int bout = (int)(ta & 1);
     char* ob = inbox + (size_t)bout * buf_bytes;
     const uint32_t items = (uint32_t)count * (uint32_t)kmax;
-    for (uint32_t it0 = threadIdx.x; it0 < items; it0 += kBatch * kBlock) {
+    for (uint32_t r0 = 0; r0 < items; r0 += kBatch * kBlock) {
       int32_t tgt[kBatch];
       float wv[kBatch];
       bool inh[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        const uint32_t it = it0 + u * kBlock;
+        const uint32_t it = r0 + u * kBlock + threadIdx.x;
         tgt[u] = -1;
         wv[u] = 0.0f;
         inh[u] = false;
@@ -321,17 +335,62 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           }
         }
       }
+      // (1) per-destination counts of this round
+      uint32_t rank[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        rank[u] = 0;
+        if ((uint32_t)tgt[u] < (uint32_t)n) rank[u] = atomicAdd(&s_rcnt[tgt[u] >> L.shift], 1u);
+      }
+      __syncthreads();
+      // (2) exclusive prefix of the round counts over destinations (one wave)
+      if (wid == 0) {
+        uint32_t loc[kPerLane];
+        uint32_t sum = 0;
+#pragma unroll
+        for (int v = 0; v < kPerLane; ++v) {
+          const int d = lane * kPerLane + v;
+          loc[v] = sum;
+          sum += d < nb ? s_rcnt[d] : 0u;
+        }
+        uint32_t incl = sum;
+#pragma unroll
+        for (int o = 1; o < BS_WAVE; o <<= 1) {
+          const uint32_t y = __shfl_up(incl, o);
+          if (lane >= o) incl += y;
+        }
+        const uint32_t excl = incl - sum;
+#pragma unroll
+        for (int v = 0; v < kPerLane; ++v) {
+          const int d = lane * kPerLane + v;
+          if (d < nb) s_rpre[d] = excl + loc[v];
+        }
+        if (lane == BS_WAVE - 1) s_rtot = incl;
+      }
+      __syncthreads();
+      // (3) place entries grouped by destination, with their final inbox position
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         if ((uint32_t)tgt[u] < (uint32_t)n) {
           const int d = tgt[u] >> L.shift;
+          const uint32_t e = s_rpre[d] + rank[u];
           const uint32_t loc = (uint32_t)(tgt[u] & (kChunk - 1)) | (inh[u] ? kInhFlag : 0u);
-          const uint32_t slot = atomicAdd(&s_cursor[d], 1u);
-          const uint64_t pos = s_ofs_out[d] + slot;
-          if (kHet) st_dev64((uint64_t*)ob + pos, ((uint64_t)__float_as_uint(wv[u]) << 32) | loc);
-          else st_dev32((uint32_t*)ob + pos, loc);
+          s_stage[e] = kHet ? (((uint64_t)__float_as_uint(wv[u]) << 32) | loc) : (uint64_t)loc;
+          s_spos[e] = (uint32_t)(s_ofs_out[d] + s_cursor[d] + rank[u]);
         }
       }
+      __syncthreads();
+      // (4) ordered write-out; advance the per-destination cursors
+      const uint32_t tot = s_rtot;
+      for (uint32_t e = threadIdx.x; e < tot; e += kBlock) {
+        if (kHet) st_dev64((uint64_t*)ob + s_spos[e], s_stage[e]);
+        else st_dev32((uint32_t*)ob + s_spos[e], (uint32_t)s_stage[e]);
+      }
+      for (int d = threadIdx.x; d < nb; d += kBlock) {
+        s_cursor[d] += s_rcnt[d];
+        s_rcnt[d] = 0;
+      }
+      __syncthreads();
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     __syncthreads();
@@ -460,6 +519,7 @@ int plan(const bs_net* net, NetLayout* L) {
   // worst case: every synapse delivers one entry (invalid targets are never stored)
   L->total = (uint64_t)net->n_exc * (uint64_t)net->k_e +
              (uint64_t)(net->n - net->n_exc) * (uint64_t)net->k_i;
+  if (L->total >= ((uint64_t)1 << 32)) return -1;  // inbox positions are 32-bit
   size_t o = align256(sizeof(WsHeader));
   L->off_cnt = o;
   o = align256(o + (size_t)2 * nb * nb * sizeof(uint64_t));
