@@ -20,13 +20,13 @@ c_size = ctypes.c_size_t
 
 
 class LifParams(ctypes.Structure):
-    _fields_ = [(n, c_f32) for n in ('V_rest', 'V_th', 'V_reset', 'tau', 'R', 'I_ext', 'E_e',
+    _fields_ = [(n, c_f32) for n in ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'I_ext', 'E_e',
                                        'E_i', 'dt', 'decay_e', 'decay_i')] + [('ref_steps', c_i32)]
 
 
 class HhParams(ctypes.Structure):
-    _fields_ = [(n, c_f32) for n in ('ENa', 'gNa', 'EK', 'gK', 'EL', 'gL', 'C', 'V_th', 'I_ext',
-                                       'E_e', 'E_i', 'dt', 'decay_e', 'decay_i')]
+    _fields_ = [(n, c_f32) for n in ('ENa', 'gNa', 'EK', 'gK', 'EL', 'gL', 'inv_C', 'V_th',
+                                       'I_ext', 'E_e', 'E_i', 'dt', 'decay_e', 'decay_i')]
 
 
 class Net(ctypes.Structure):

@@ -37,6 +37,9 @@ constexpr int kMaxBlocks = 512;
 constexpr int kMaxNpt = 8;
 constexpr uint32_t kInhFlag = 0x80000000u;
 constexpr uint64_t kSpinLimit = 1ull << 24;
+#ifndef BS_POLL_SLEEP
+#define BS_POLL_SLEEP 1  // s_sleep units (64 clocks) between polls of a count word
+#endif
 #define BS_AGENT __HIP_MEMORY_SCOPE_AGENT
 
 // ---- workspace layout (all offsets in bytes, 256-aligned) ----
@@ -229,7 +232,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
             v = 0;
             break;
           }
-          __builtin_amdgcn_s_sleep(1);
+          __builtin_amdgcn_s_sleep(BS_POLL_SLEEP);
           v = ld_dev64(cin + s);
         }
         const uint32_t c = (uint32_t)v;
@@ -695,7 +698,7 @@ extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const 
   if (st) {
     BS_CHECK_ARG(st->V && st->ge && st->gi && st->ref, "bs_coba_lif_run: NULL state pointer");
   }
-  if (p) BS_CHECK_ARG(p->tau != 0.0f, "bs_coba_lif_run: tau must be nonzero");
+  if (p) BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_run: inv_tau is NaN");
   return run<LifModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
                        stream, "bs_coba_lif_run");
 }
@@ -709,7 +712,7 @@ extern "C" int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs
     BS_CHECK_ARG(st->V && st->m && st->h && st->n && st->ge && st->gi,
                  "bs_coba_hh_run: NULL state pointer");
   }
-  if (p) BS_CHECK_ARG(p->C != 0.0f, "bs_coba_hh_run: C must be nonzero");
+  if (p) BS_CHECK_ARG(p->inv_C == p->inv_C, "bs_coba_hh_run: inv_C is NaN");
   return run<HhModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
                       stream, "bs_coba_hh_run");
 }

@@ -79,7 +79,7 @@ extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32
   bs_clear_error();
   BS_CHECK_ARG(n >= 0, "bs_coba_lif_step: n=%d < 0", n);
   BS_CHECK_ARG(p != nullptr, "bs_coba_lif_step: params are NULL");
-  BS_CHECK_ARG(p->tau != 0.0f, "bs_coba_lif_step: tau must be nonzero");
+  BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_step: inv_tau is NaN");
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
   k_lif_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i, *p,
@@ -105,7 +105,7 @@ extern "C" int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* n
   bs_clear_error();
   BS_CHECK_ARG(n >= 0, "bs_coba_hh_step: n=%d < 0", n);
   BS_CHECK_ARG(p != nullptr, "bs_coba_hh_step: params are NULL");
-  BS_CHECK_ARG(p->C != 0.0f, "bs_coba_hh_step: C must be nonzero");
+  BS_CHECK_ARG(p->inv_C == p->inv_C, "bs_coba_hh_step: inv_C is NaN");
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && m && h && ng && ge && gi, "bs_coba_hh_step: NULL state pointer");
   k_hh_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng, ge, gi, in_e, in_i, *p,

@@ -2,6 +2,9 @@
 // persistent network runners.  Every expression is written in the operation order the
 // reference code evaluates it in (left to right), and the library is built with
 // -ffp-contract=off, so each line is a fixed sequence of correctly rounded fp32 ops.
+// Division by a model constant (tau, C, the HH rate scales) is multiplication by its fp32
+// reciprocal: that is how the reference executes it under jit, where XLA's algebraic
+// simplifier rewrites A / Const into A * (1 / Const).  Divisions by variables stay divisions.
 #pragma once
 
 #include "bs_math.h"
@@ -15,8 +18,8 @@ __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, 
   gi = gi * p.decay_i + in_i;
   float I = p.I_ext + ge * (p.E_e - V);
   I = I + gi * (p.E_i - V);
-  const float f = ((p.V_rest - V) + p.R * I) / p.tau;
-  const float J = (-1.0f - p.R * (ge + gi)) / p.tau;
+  const float f = ((p.V_rest - V) + p.R * I) * p.inv_tau;
+  const float J = (-1.0f - p.R * (ge + gi)) * p.inv_tau;
   const float phi = bs_exprel(p.dt * J);
   float Vn = V + (p.dt * phi) * f;
   bool spk = false;
@@ -43,12 +46,14 @@ struct bs_hh_rates {
 // examples/100_hh_neuron_model.py:49-64 (V in mV, rates in 1/ms).
 __device__ __forceinline__ bs_hh_rates bs_hh_rate(float V) {
   bs_hh_rates r;
-  r.am = 1.0f / bs_exprel((-(V + 40.0f)) / 10.0f);
-  r.bm = 4.0f * bs_expf((-(V + 65.0f)) / 18.0f);
-  r.ah = 0.07f * bs_expf((-(V + 65.0f)) / 20.0f);
-  r.bh = 1.0f / (1.0f + bs_expf((-(V + 35.0f)) / 10.0f));
-  r.an = 0.1f / bs_exprel((-(V + 55.0f)) / 10.0f);
-  r.bn = 0.125f * bs_expf((-(V + 65.0f)) / 80.0f);
+  constexpr float k10 = 1.0f / 10.0f, k18 = 1.0f / 18.0f;  // fp32 reciprocals
+  constexpr float k20 = 1.0f / 20.0f, k80 = 1.0f / 80.0f;
+  r.am = 1.0f / bs_exprel((-(V + 40.0f)) * k10);
+  r.bm = 4.0f * bs_expf((-(V + 65.0f)) * k18);
+  r.ah = 0.07f * bs_expf((-(V + 65.0f)) * k20);
+  r.bh = 1.0f / (1.0f + bs_expf((-(V + 35.0f)) * k10));
+  r.an = 0.1f / bs_exprel((-(V + 55.0f)) * k10);
+  r.bn = 0.125f * bs_expf((-(V + 65.0f)) * k80);
   return r;
 }
 
@@ -74,8 +79,8 @@ __device__ __forceinline__ bool bs_hh_update(const bs_hh_params& p, float& V, fl
   const float gk = p.gK * n2 * n2;
   const float IK = gk * (V - p.EK);
   const float IL = p.gL * (V - p.EL);
-  const float f = ((((-INa) - IK) - IL) + I) / p.C;
-  const float J = ((((-gna) - gk) - p.gL) - (ge + gi)) / p.C;
+  const float f = ((((-INa) - IK) - IL) + I) * p.inv_C;
+  const float J = ((((-gna) - gk) - p.gL) - (ge + gi)) * p.inv_C;
   const float phi = bs_exprel(p.dt * J);
   const float Vn = V + (p.dt * phi) * f;
   const float mn = bs_hh_gate(m, r.am, r.bm, p.dt);

@@ -155,14 +155,16 @@ def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., 
                E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1):
     q = float(tau_ref) / float(dt)
     ref_steps = max(int(np.ceil(q - 1e-9)) - 1, 0)
-    return N.LifParams(V_rest, V_th, V_reset, tau, R, I_ext, E_e, E_i, dt,
+    inv_tau = float(np.float32(1.0) / np.float32(tau))   # fp32 reciprocal of the constant
+    return N.LifParams(V_rest, V_th, V_reset, inv_tau, R, I_ext, E_e, E_i, dt,
                        float(np.float32(np.exp(-dt / tau_e))),
                        float(np.float32(np.exp(-dt / tau_i))), ref_steps)
 
 
 def hh_params(ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03, C=1.0, V_th=20.,
               I_ext=0., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.05):
-    return N.HhParams(ENa, gNa, EK, gK, EL, gL, C, V_th, I_ext, E_e, E_i, dt,
+    inv_C = float(np.float32(1.0) / np.float32(C))
+    return N.HhParams(ENa, gNa, EK, gK, EL, gL, inv_C, V_th, I_ext, E_e, E_i, dt,
                       float(np.float32(np.exp(-dt / tau_e))),
                       float(np.float32(np.exp(-dt / tau_i))))
 

@@ -100,11 +100,12 @@ BS_API int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t batch,
  * brainstate/nn/_exp_euler.py:226-249 (used e.g. by examples/105_COBA_HH_2007_braincell.py:62-82).
  *   g_e = g_e*decay_e + in_e;  g_i = g_i*decay_i + in_i
  *   I = I_ext + g_e*(E_e - V) + g_i*(E_i - V)
- *   V' = V + (dt*exprel(dt*J))*f,  f = ((V_rest - V) + R*I)/tau,  J = (-1 - R*(g_e+g_i))/tau
+ *   V' = V + (dt*exprel(dt*J))*f,  f = ((V_rest - V) + R*I)*inv_tau,  J = (-1 - R*(g_e+g_i))*inv_tau
  *   refractory (ref > 0): V held, ref -= 1;  else spike = V' >= V_th -> V' = V_reset,
- *   ref = ref_steps. */
+ *   ref = ref_steps.
+ * inv_tau = fp32(1/tau): the reference's `/ tau` by a constant, as XLA executes it. */
 typedef struct {
-  float V_rest, V_th, V_reset, tau, R, I_ext, E_e, E_i, dt, decay_e, decay_i;
+  float V_rest, V_th, V_reset, inv_tau, R, I_ext, E_e, E_i, dt, decay_e, decay_i;
   int32_t ref_steps;
 } bs_lif_params;
 
@@ -115,8 +116,8 @@ BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* 
 /* Hodgkin-Huxley with Expon synapses and COBA output (examples/100_hh_neuron_model.py:25-93):
  * rates from the old V; V, m, h, n each by exp-Euler; spike = (V < V_th) & (V' >= V_th). */
 typedef struct {
-  float ENa, gNa, EK, gK, EL, gL, C, V_th, I_ext, E_e, E_i, dt, decay_e, decay_i;
-} bs_hh_params;
+  float ENa, gNa, EK, gK, EL, gL, inv_C, V_th, I_ext, E_e, E_i, dt, decay_e, decay_i;
+} bs_hh_params;   /* inv_C = fp32(1/C) */
 
 /* Gates at steady state for V (examples/100_hh_neuron_model.py:66-70). */
 BS_API int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng, bs_stream_t stream);

@@ -5,7 +5,8 @@
  * Same algorithm as oracle/neuron.py + oracle/network.py, in C with OpenMP:
  *   - event-driven pre-major scatter over the active rows, the organisation of
  *     brainevent's CPU kernels reached from brainstate/nn/_event_fixedprob.py:205,251;
- *   - the fp32 Expon + COBA + LIFRef update (exp-Euler, brainstate/nn/_exp_euler.py:226-249);
+ *   - the fp32 Expon + COBA + LIFRef update (exp-Euler, brainstate/nn/_exp_euler.py:226-249),
+ *     division by the constant tau taken as multiplication by fp32(1/tau) (how XLA runs it);
  *   - its own fp32 exp/exprel (Cody-Waite + degree-7 Taylor, the method the oracle fixes).
  * Built with -ffp-contract=off so every expression is the same rounded op sequence as the
  * numpy oracle.  Scatter adds use atomics when run multi-threaded: order-free (hence
@@ -59,7 +60,7 @@ static inline float o_exprel(float z) {
 }
 
 typedef struct {
-  float V_rest, V_th, V_reset, tau, R, I_ext, E_e, E_i, dt, decay_e, decay_i;
+  float V_rest, V_th, V_reset, inv_tau, R, I_ext, E_e, E_i, dt, decay_e, decay_i;
   int32_t ref_steps;
 } bso_lif_params;
 
@@ -108,8 +109,8 @@ long long bso_coba_lif_run(int n, int n_exc, int k_e, int k_i, const int32_t* id
       const float v = V[j];
       float I = p.I_ext + g_e * (p.E_e - v);
       I = I + g_i * (p.E_i - v);
-      const float f = ((p.V_rest - v) + p.R * I) / p.tau;
-      const float J = (-1.0f - p.R * (g_e + g_i)) / p.tau;
+      const float f = ((p.V_rest - v) + p.R * I) * p.inv_tau;
+      const float J = (-1.0f - p.R * (g_e + g_i)) * p.inv_tau;
       const float phi = o_exprel(p.dt * J);
       float vn = v + (p.dt * phi) * f;
       int32_t r = ref[j];

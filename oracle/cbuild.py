@@ -25,7 +25,7 @@ def build(verbose=False):
 
 
 class _LifParams(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_float) for n in ('V_rest', 'V_th', 'V_reset', 'tau', 'R', 'I_ext',
+    _fields_ = [(n, ctypes.c_float) for n in ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'I_ext',
                                                 'E_e', 'E_i', 'dt', 'decay_e', 'decay_i')] + \
                [('ref_steps', ctypes.c_int32)]
 
@@ -47,7 +47,7 @@ def lib():
 
 def lif_params(p):
     """From an oracle.neuron.LIFParams."""
-    return _LifParams(p.V_rest, p.V_th, p.V_reset, p.tau, p.R, p.I_ext, p.E_e, p.E_i, p.dt,
+    return _LifParams(p.V_rest, p.V_th, p.V_reset, p.inv_tau, p.R, p.I_ext, p.E_e, p.E_i, p.dt,
                       p.de, p.di, int(p.ref_steps))
 
 

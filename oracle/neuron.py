@@ -15,7 +15,10 @@ from the equations and are **parity unpinned** beyond the checks above:
     this exponential; the decay factor is computed once in float64 and rounded).
   * COBA output: ``I = I_ext + g_e*(E_e - V) + g_i*(E_i - V)`` (sum_current_inputs
     order: external input first, then projections in registration order).
-  * LIF membrane: ``f = ((V_rest - V) + R*I)/tau``, ``J = (-1 - R*(g_e+g_i))/tau``.
+  * LIF membrane: ``f = ((V_rest - V) + R*I)*inv_tau``, ``J = (-1 - R*(g_e+g_i))*inv_tau``
+    with ``inv_tau = fp32(1/tau)``: under jit the reference's ``/ tau`` by a constant is a
+    multiplication, XLA's algebraic simplifier rewriting ``A / Const`` into
+    ``A * InvertConstant(Const)``; the same holds for ``/ C`` and the HH rate scales.
   * LIFRef: a neuron is refractory for ``ref_steps`` steps after the spike step
     (the steps with 0 < t - t_spike < tau_ref on the dt grid); V is held there.
     Spike when V' >= V_th; hard reset V' = V_reset.
@@ -59,6 +62,7 @@ class LIFParams:
                  I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1):
         self.V_rest, self.V_th, self.V_reset = F(V_rest), F(V_th), F(V_reset)
         self.tau, self.R, self.I_ext = F(tau), F(R), F(I_ext)
+        self.inv_tau = F(F(1.0) / F(tau))
         self.E_e, self.E_i = F(E_e), F(E_i)
         self.dt = F(dt)
         self.de = decay_factor(dt, tau_e)
@@ -70,8 +74,8 @@ def lif_membrane(V, ge, gi, p):
     """One exp-Euler step of the COBA LIF membrane (no refractoriness, no reset)."""
     I = (p.I_ext + ge * (p.E_e - V)).astype(F)
     I = (I + gi * (p.E_i - V)).astype(F)
-    f = (((p.V_rest - V) + p.R * I) / p.tau).astype(F)
-    J = ((F(-1.0) - p.R * (ge + gi)) / p.tau).astype(F)
+    f = (((p.V_rest - V) + p.R * I) * p.inv_tau).astype(F)
+    J = ((F(-1.0) - p.R * (ge + gi)) * p.inv_tau).astype(F)
     phi = exprel((p.dt * J).astype(F))
     return (V + (p.dt * phi).astype(F) * f).astype(F)
 
@@ -96,6 +100,7 @@ class HHParams:
                  V_th=20., I_ext=0., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.05):
         self.ENa, self.gNa, self.EK, self.gK = F(ENa), F(gNa), F(EK), F(gK)
         self.EL, self.gL, self.C, self.V_th = F(EL), F(gL), F(C), F(V_th)
+        self.inv_C = F(F(1.0) / F(C))
         self.I_ext, self.E_e, self.E_i = F(I_ext), F(E_e), F(E_i)
         self.dt = F(dt)
         self.de = decay_factor(dt, tau_e)
@@ -105,12 +110,13 @@ class HHParams:
 def hh_rates(V):
     """(am, bm, ah, bh, an, bn) at membrane potential V (mV), :49-64."""
     V = np.asarray(V, F)
-    am = (F(1.0) / exprel((-(V + F(40.0))) / F(10.0))).astype(F)
-    bm = (F(4.0) * expf((-(V + F(65.0))) / F(18.0))).astype(F)
-    ah = (F(0.07) * expf((-(V + F(65.0))) / F(20.0))).astype(F)
-    bh = (F(1.0) / (F(1.0) + expf((-(V + F(35.0))) / F(10.0)))).astype(F)
-    an = (F(0.1) / exprel((-(V + F(55.0))) / F(10.0))).astype(F)
-    bn = (F(0.125) * expf((-(V + F(65.0))) / F(80.0))).astype(F)
+    k10, k18, k20, k80 = (F(1.0) / F(c) for c in (10.0, 18.0, 20.0, 80.0))  # fp32 reciprocals
+    am = (F(1.0) / exprel((-(V + F(40.0))) * k10)).astype(F)
+    bm = (F(4.0) * expf((-(V + F(65.0))) * k18)).astype(F)
+    ah = (F(0.07) * expf((-(V + F(65.0))) * k20)).astype(F)
+    bh = (F(1.0) / (F(1.0) + expf((-(V + F(35.0))) * k10))).astype(F)
+    an = (F(0.1) / exprel((-(V + F(55.0))) * k10)).astype(F)
+    bn = (F(0.125) * expf((-(V + F(65.0))) * k80)).astype(F)
     return am, bm, ah, bh, an, bn
 
 
@@ -140,8 +146,8 @@ def hh_step(V, m, h, n, ge, gi, in_e, in_i, p):
     gk = (p.gK * n2 * n2).astype(F)
     IK = (gk * (V - p.EK)).astype(F)
     IL = (p.gL * (V - p.EL)).astype(F)
-    f = (((((-INa) - IK) - IL) + I) / p.C).astype(F)
-    J = (((((-gna) - gk) - p.gL) - (ge + gi)) / p.C).astype(F)
+    f = (((((-INa) - IK) - IL) + I) * p.inv_C).astype(F)
+    J = (((((-gna) - gk) - p.gL) - (ge + gi)) * p.inv_C).astype(F)
     phi = exprel((p.dt * J).astype(F))
     Vn = (V + (p.dt * phi).astype(F) * f).astype(F)
     mn = _gate(m, am, bm, p.dt)
