@@ -155,11 +155,16 @@ def bench_sparse(args):
         def gather():
             ops.event_gather(spk, sell, out=out)
 
+        def fused():
+            ops.event_matvec(spk, d_idx, d_w, n, out=out)
+
         ts = _timed(scatter, 20)
         tg = _timed(gather, 20)
+        tf = _timed(fused, 20)
         b_s = n * 1 + E * 8 + n * 4
         b_g = (n + 1) * 4 + sell['padded'] * 4 + E * 4 + n + n * 4
         lines.append({'workload': f'event_matvec_100k_K1000_p{p}', 'events': E,
+                      'fused_matvec_us': tf * 1e6, 'fused_GSOPs': E / tf / 1e9,
                       'scatter_us': ts * 1e6, 'scatter_GSOPs': E / ts / 1e9,
                       'scatter_alg_GBs': b_s / ts / 1e9, 'scatter_frac': b_s / ts / PEAK_HBM,
                       'gather_us': tg * 1e6, 'gather_GSOPs': E / tg / 1e9,

@@ -52,6 +52,8 @@ SIGNATURES = {
     'bs_spike_compact': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
     'bs_event_scatter_f32': (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,
                                             c_i32, c_vp, c_i32, c_vp]),
+    'bs_event_matvec_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,
+                                           c_i32, c_vp, c_i32, c_vp]),
     'bs_spike_pack': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     'bs_event_gather_f32': (ctypes.c_int, [c_vp, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp,
                                            c_vp]),

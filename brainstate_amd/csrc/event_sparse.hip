@@ -137,6 +137,97 @@ __global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ 
   if (j < n_post) out[j] = acc;
 }
 
+// Fused event mat-vec straight from the spike vector: workgroup w owns pre rows
+// [w*rows, (w+1)*rows); it compacts its active rows into LDS (wave ballots), then adds the
+// synapses of those rows.  If the whole output fits in LDS (n_post <= kLdsPosts) and the
+// workgroup has at least kLdsRatio events per output, the events of per-synapse weights are
+// first aggregated with LDS atomics and each touched output receives one global atomic;
+// otherwise every event is one global atomic.  The choice is made per workgroup from its own
+// event count.
+constexpr int kLdsPosts = 16384;
+constexpr int kLdsRatio = 4;
+constexpr int kRowsCap = 1024;
+
+template <typename T, bool kCsr, bool kHet>
+__global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, int32_t n_pre,
+                                                   int32_t rows, const int32_t* __restrict__ indptr,
+                                                   const int32_t* __restrict__ indices, int32_t k,
+                                                   const float* __restrict__ w, float w_homo,
+                                                   int32_t n_post, float* __restrict__ out) {
+  __shared__ int32_t s_rows[kRowsCap];
+  __shared__ int32_t s_wave[kBlock / BS_WAVE];
+  __shared__ int32_t s_nev;
+  extern __shared__ float s_acc[];
+  const int lane = bs_lane();
+  const int wid = threadIdx.x / BS_WAVE;
+  const int64_t r0 = (int64_t)blockIdx.x * rows;
+  int32_t count = 0;
+  for (int32_t off = 0; off < rows; off += kBlock) {
+    const int64_t r = r0 + off + threadIdx.x;
+    const bool a = off + (int32_t)threadIdx.x < rows && r < n_pre && spk[r] != T(0);
+    const uint64_t m = bs_ballot(a);
+    if (lane == 0) s_wave[wid] = __popcll(m);
+    __syncthreads();
+    int32_t pos = count, tot = 0;
+#pragma unroll
+    for (int v = 0; v < kBlock / BS_WAVE; ++v) {
+      pos += v < wid ? s_wave[v] : 0;
+      tot += s_wave[v];
+    }
+    if (a) s_rows[pos + bs_rank_below(m)] = (int32_t)r;
+    count += tot;
+    __syncthreads();
+  }
+  if (count == 0) return;
+  // events of this workgroup
+  if (threadIdx.x == 0) {
+    int64_t ev = 0;
+    if (!kCsr) {
+      ev = (int64_t)count * k;
+    } else {
+      for (int32_t i = 0; i < count; ++i) ev += indptr[s_rows[i] + 1] - indptr[s_rows[i]];
+    }
+    s_nev = ev > 0x7FFFFFFF ? 0x7FFFFFFF : (int32_t)ev;
+  }
+  __syncthreads();
+  // Homogeneous weights always go direct: sums of one repeated value are order-free and exact
+  // only as a single chain of +w, which LDS partial sums would break.
+  const bool use_lds = kHet && n_post <= kLdsPosts && (int64_t)s_nev >= (int64_t)kLdsRatio * n_post;
+  if (use_lds) {
+    for (int32_t j = threadIdx.x; j < n_post; j += kBlock) s_acc[j] = 0.0f;
+    __syncthreads();
+  }
+  const int32_t nnz = kCsr ? indptr[n_pre] : 0;
+  for (int32_t a = wid; a < count; a += kBlock / BS_WAVE) {  // one wave per active row
+    const int32_t row = s_rows[a];
+    int64_t beg, end;
+    if (kCsr) {
+      beg = indptr[row];
+      end = indptr[row + 1];
+      beg = beg < 0 ? 0 : beg;
+      end = end > nnz ? nnz : end;
+    } else {
+      beg = (int64_t)row * k;
+      end = beg + k;
+    }
+    for (int64_t s = beg + lane; s < end; s += BS_WAVE) {
+      const int32_t j = indices[s];
+      const float v = kHet ? w[s] : w_homo;
+      if ((uint32_t)j < (uint32_t)n_post) {
+        if (use_lds) atomicAdd(&s_acc[j], v);
+        else bs_atomic_add_f32(out + j, v);
+      }
+    }
+  }
+  if (use_lds) {
+    __syncthreads();
+    for (int32_t j = threadIdx.x; j < n_post; j += kBlock) {
+      const float v = s_acc[j];
+      if (v != 0.0f) bs_atomic_add_f32(out + j, v);
+    }
+  }
+}
+
 int grid_for(int64_t work_items_waves) {
   const int64_t cap = (int64_t)bs_num_cus() * 16;
   int64_t b = (work_items_waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE);
@@ -239,6 +330,46 @@ extern "C" int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
   else
     k_gather<false, false><<<g, kBlock, 0, s>>>(spk_bits, n_pre, slice_ptr, sell_pre, nullptr,
                                                 w_homo, n_post, out);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                                   const int32_t* indptr, const int32_t* indices, int32_t k,
+                                   const float* w, float w_homo, int32_t n_post, float* out,
+                                   int32_t accumulate, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "bs_event_matvec_f32: negative size");
+  BS_CHECK_ARG(indptr != nullptr || k >= 0, "bs_event_matvec_f32: k=%d < 0", k);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_event_matvec_f32: unknown spike dtype %d", spk_dtype);
+  hipStream_t s = bs_stream(stream);
+  if (n_post > 0) BS_CHECK_ARG(out != nullptr, "bs_event_matvec_f32: out is NULL");
+  if (!accumulate) {
+    int rc = bs_fill_f32(out, n_post, 0.0f, s);
+    if (rc) return rc;
+  }
+  if (n_pre == 0 || n_post == 0 || (indptr == nullptr && k == 0)) return BS_OK;
+  BS_CHECK_ARG(spk && indices, "bs_event_matvec_f32: NULL pointer");
+  // rows per workgroup: enough workgroups to fill the chip, at most kRowsCap rows each
+  int64_t g = (int64_t)bs_num_cus() * 4;
+  int64_t rows = ((int64_t)n_pre + g - 1) / g;
+  if (rows < 64) rows = 64;
+  if (rows > kRowsCap) rows = kRowsCap;
+  g = ((int64_t)n_pre + rows - 1) / rows;
+  const size_t shm = n_post <= kLdsPosts ? (size_t)n_post * sizeof(float) : 0;
+  const bool het = w != nullptr, csr = indptr != nullptr;
+#define BS_MV(T, C, H)                                                                   \
+  k_matvec<T, C, H><<<(int)g, kBlock, shm, s>>>((const T*)spk, n_pre, (int32_t)rows, indptr, \
+                                               indices, k, w, w_homo, n_post, out)
+  if (spk_dtype == BS_SPK_U8) {
+    if (csr) { if (het) BS_MV(uint8_t, true, true); else BS_MV(uint8_t, true, false); }
+    else { if (het) BS_MV(uint8_t, false, true); else BS_MV(uint8_t, false, false); }
+  } else {
+    if (csr) { if (het) BS_MV(float, true, true); else BS_MV(float, true, false); }
+    else { if (het) BS_MV(float, false, true); else BS_MV(float, false, false); }
+  }
+#undef BS_MV
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

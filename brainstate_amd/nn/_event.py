@@ -48,11 +48,10 @@ class FixedPostNumConn:
 
     def matvec_events(self, spk):
         n_pre, n_post = self.shape
-        act, cnt = ops.spike_compact(spk)
         w = self.data
         if torch.is_tensor(w) and w.numel() > 1:
             w = w.expand(self.indices.shape) if w.shape != self.indices.shape else w
-        return ops.event_scatter(act, cnt, self.indices, w, n_post)
+        return ops.event_matvec(spk, self.indices, w, n_post)
 
 
 class CSR:
@@ -68,11 +67,10 @@ class CSR:
 
     def matvec_events(self, spk):
         n_pre, n_post = self.shape
-        act, cnt = ops.spike_compact(spk)
         w = self.data
         if torch.is_tensor(w) and w.numel() > 1 and w.shape != self.indices.shape:
             w = w.expand(self.indices.shape)
-        return ops.event_scatter(act, cnt, self.indices, w, n_post, indptr=self.indptr)
+        return ops.event_matvec(spk, self.indices, w, n_post, indptr=self.indptr)
 
 
 def _weight_for_kernel(w):

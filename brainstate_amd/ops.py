@@ -70,6 +70,29 @@ def event_scatter(active, n_active, indices, w, n_post, k=None, indptr=None, out
     return out
 
 
+def event_matvec(spk, indices, w, n_post, k=None, indptr=None, out=None, accumulate=False):
+    """Event mat-vec straight from the spike vector (one fused compaction + scatter launch)."""
+    spk = _spk_view(spk)
+    dev = indices.device
+    n_pre = spk.numel()
+    if indptr is None:
+        k = indices.shape[1] if indices.dim() == 2 else int(k)
+        if indices.shape[0] != n_pre:
+            raise ValueError(f'spike vector of {n_pre} for {indices.shape[0]} pre rows')
+    elif indptr.numel() - 1 != n_pre:
+        raise ValueError(f'spike vector of {n_pre} for {indptr.numel() - 1} pre rows')
+    homo = not torch.is_tensor(w) or w.numel() == 1
+    w_homo = float(w) if homo else 0.0
+    if out is None:
+        out = torch.empty(n_post, dtype=torch.float32, device=dev)
+        accumulate = False
+    N.check(N.lib().bs_event_matvec_f32(
+        N.ptr(spk), _spk_dtype(spk), int(n_pre), N.ptr(indptr), N.ptr(indices.contiguous()),
+        int(k or 0), None if homo else N.ptr(w.contiguous()), w_homo, int(n_post), N.ptr(out),
+        1 if accumulate else 0, N.stream_handle(dev)), 'bs_event_matvec_f32')
+    return out
+
+
 def spike_pack(spk, bits=None):
     """Spikes -> bitmap int32 [(n + 31) // 32] (bit i % 32 of word i // 32)."""
     spk = _spk_view(spk)

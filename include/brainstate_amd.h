@@ -70,6 +70,14 @@ BS_API int bs_event_scatter_f32(const int32_t* active, const int32_t* n_active, 
                          const float* w, float w_homo, int32_t n_post, float* out,
                          int32_t accumulate, bs_stream_t stream);
 
+/* Same operator taking the spike vector directly (nonzero = event): one launch compacts and
+ * scatters (plus a zero-fill unless accumulate).  With per-synapse weights, a workgroup
+ * holding >= 4 events per output aggregates them in LDS first when n_post <= 16384. */
+BS_API int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                               const int32_t* indptr, const int32_t* indices, int32_t k,
+                               const float* w, float w_homo, int32_t n_post, float* out,
+                               int32_t accumulate, bs_stream_t stream);
+
 /* ---------------------------------------------------------------- N2b event gather
  * Same operator as N2a, post-major and deterministic (no atomics).  Spikes come as a
  * bitmap (bs_spike_pack: bit i%32 of word i/32 set <=> spk[i] != 0).  Layout SELL-64:

@@ -205,3 +205,69 @@ def test_hh_init_and_step_bit_exact(torch_cuda):
     for g, e in zip(got, exp[:6]):
         assert np.array_equal(g.cpu().numpy(), e)
     assert np.array_equal(spk.cpu().numpy().astype(bool), exp[6])
+
+
+# ---------------------------------------------------------------- fused spike-vector mat-vec
+
+@pytest.mark.parametrize('n_pre,n_post,k,p,het,csr', [
+    (3200, 4000, 80, 0.02, False, False),     # config [1] E projection, direct atomics
+    (3200, 4000, 80, 0.9, True, False),       # dense activity, LDS-aggregated path
+    (3200, 4000, 80, 0.9, False, False),      # dense, homogeneous: direct (bit-exact)
+    (100_000, 100_000, 1000, 0.01, True, False),
+    (2000, 1500, 60, 0.5, True, True),        # CSR (afferent ratio)
+    (50, 10, 3, 1.0, True, False)])
+def test_event_matvec_fused(torch_cuda, n_pre, n_post, k, p, het, csr):
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('matvec fused', n_pre, n_post, k, p, het, csr)
+    rng = np.random.RandomState(k + 11)
+    if csr:
+        indptr, indices, _ = conn.csr_afferent(n_pre, n_post, k, seed=5, afferent_ratio=0.6)
+        w = rng.normal(0.5, 0.1, indices.size).astype(F) if het else F(0.6)
+        spk = rng.rand(n_pre) < p
+        ref = event.scatter_csr(spk, indptr, indices, w, n_post)
+        out = ops.event_matvec(dev(torch, spk.astype(np.uint8)), dev(torch, indices),
+                               dev(torch, w) if het else float(w), n_post,
+                               indptr=dev(torch, indptr))
+    else:
+        idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+        w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F) if het else F(0.6)
+        spk = rng.rand(n_pre) < p
+        ref = event.scatter_fixed(spk, idx, w, n_post)
+        out = ops.event_matvec(dev(torch, spk.astype(np.uint8)), dev(torch, idx),
+                               dev(torch, w) if het else float(w), n_post)
+    got = out.cpu().numpy()
+    if het:
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    else:
+        assert np.array_equal(got, ref)
+
+
+def test_gather_global_bitmap_path(torch_cuda):
+    """n_pre > 524288: the spike bitmap is read from global memory instead of LDS."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('gather global bitmap')
+    n_pre, n_post, k = 600_000, 20_000, 20
+    rng = np.random.RandomState(3)
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F)
+    spk = rng.rand(n_pre) < 0.01
+    indptr, flat = conn.fixed_to_csr(idx)
+    sell = ops.build_sell(indptr, flat, n_pre, n_post, w=w, device='cuda')
+    got = ops.event_gather(dev(torch, spk.astype(np.uint8)), sell).cpu().numpy()
+    post_ptr, pre_of, syn_of = conn.to_post_major(indptr, flat, n_post)
+    ref = event.gather_post_major(spk, post_ptr, pre_of, w.reshape(-1)[syn_of], n_post)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize('n', [1, 63, 64, 65, 1000, 100_003])
+def test_spike_pack(torch_cuda, n):
+    torch = torch_cuda
+    from brainstate_amd import ops
+    spk = np.random.RandomState(n).rand(n) < 0.3
+    bits = ops.spike_pack(dev(torch, spk.astype(np.uint8))).cpu().numpy().view(np.uint32)
+    ref = np.zeros((n + 31) // 32, np.uint32)
+    for i in np.flatnonzero(spk):
+        ref[i // 32] |= np.uint32(1) << np.uint32(i % 32)
+    assert np.array_equal(bits[:ref.size], ref)
