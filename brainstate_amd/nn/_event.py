@@ -3,8 +3,9 @@
 * ``FixedNumConn`` / ``EventFixedNumConn`` / ``EventFixedProb`` --
   brainstate/nn/_event_fixedprob.py:65-255.  Same arguments, validation and connectivity
   stream (numpy MT19937 ``randint`` with replacement, :161-171); ``update(spk)`` runs the
-  HIP spike compaction and pre-major event scatter (C ABI ``bs_spike_compact`` +
-  ``bs_event_scatter_f32``) instead of brainevent's kernel.
+  fused HIP spike-vector event mat-vec (C ABI ``bs_event_matvec_f32``: per-workgroup
+  compaction of the spike vector, then the pre-major scatter of the active rows) instead of
+  brainevent's kernel.
 * ``EventLinear`` -- brainstate/nn/_event_linear.py:32-102, on ``bs_event_dense_f32``.
 
 Tensors live on the GPU; there is no CPU path.
