@@ -42,6 +42,7 @@ constexpr uint64_t kSpinLimit = 1ull << 24;
 #endif
 #define BS_AGENT __HIP_MEMORY_SCOPE_AGENT
 
+
 // ---- workspace layout (all offsets in bytes, 256-aligned) ----
 struct NetLayout {
   int32_t nb;          // workgroups
@@ -115,6 +116,14 @@ struct LifModel {
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
     return bs_lif_update(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
   }
+  // Whether the neuron may spike this step: a zero-input forward-Euler estimate of the next
+  // V within 20 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
+  // estimate never decides a spike.
+  __device__ static bool near(const Params& p, const Regs& r) {
+    const float I = p.I_ext + r.ge * p.decay_e * (p.E_e - r.V) + r.gi * p.decay_i * (p.E_i - r.V);
+    const float vp = r.V + p.dt * p.inv_tau * ((p.V_rest - r.V) + p.R * I);
+    return r.ref <= 0 && vp >= p.V_th - 0.2f * (p.V_th - p.V_reset);
+  }
 };
 
 struct HhModel {
@@ -136,6 +145,11 @@ struct HhModel {
   }
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
     return bs_hh_update(p, r.V, r.m, r.h, r.n, r.ge, r.gi, in_e, in_i);
+  }
+  // Whether the neuron may spike this step: V on the upstroke, below threshold but within
+  // 25 mV of it.  Only steers the row prefetch.
+  __device__ static bool near(const Params& p, const Regs& r) {
+    return r.V < p.V_th && r.V >= p.V_th - 25.0f;
   }
 };
 
@@ -159,21 +173,20 @@ template <class Model, int NPT, bool kHet>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
                                                 typename Model::Params p) {
   constexpr int kChunk = NPT * kBlock;
-  constexpr int kBatch = 4;
-  constexpr int kStage = kBatch * kBlock;     // synapses per expand round
-  constexpr int kPerLane = kMaxBlocks / BS_WAVE;
-  __shared__ int32_t s_list[kChunk];
+  constexpr int kBatch = 4;                   // phase A: entry loads in flight per thread
+  constexpr int kChunks = 4;                  // phase D: 64-synapse chunks per wave and round
+  constexpr int kSlots = 8;                   // phase D: LDS slots per destination and round
+  __shared__ int32_t s_list[kChunk];          // each wave's spikes (global indices)
   __shared__ float s_in[2 * kChunk];          // (E, I) inputs of this workgroup's neurons
   __shared__ uint32_t s_cursor[kMaxBlocks];   // entries written per destination this step
   __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
   __shared__ uint64_t s_ofs_out[kMaxBlocks];  // inbox offset (d <- me)
-  __shared__ int32_t s_wave[kWaves];
+  __shared__ int32_t s_wave[kWaves];          // spikes per wave this step
+  __shared__ uint32_t s_maxch[2];             // largest per-wave chunk count, by step parity
   __shared__ uint32_t s_hash;
+  __shared__ uint32_t s_junk[BS_WAVE];        // destination of the row prefetches (never read)
   __shared__ uint32_t s_rcnt[kMaxBlocks];     // expand round: entries per destination
-  __shared__ uint32_t s_rpre[kMaxBlocks];     // expand round: prefix over destinations
-  __shared__ uint32_t s_rtot;
-  __shared__ uint64_t s_stage[kStage];        // expand round: entries grouped by destination
-  __shared__ uint32_t s_spos[kStage];         // expand round: their inbox positions
+  __shared__ uint64_t s_stage[kMaxBlocks * kSlots];  // expand round: per-destination slots
 
   const NetLayout& L = a.L;
   const int nb = L.nb;
@@ -205,13 +218,45 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   bool last[NPT];
 #pragma unroll
   for (int q = 0; q < NPT; ++q) last[q] = false;
-  const int32_t kmax = a.k_e > a.k_i ? a.k_e : a.k_i;
+  // 64-synapse chunks per E / I row; a row without synapses still takes one (empty) chunk
+  // slot in the expand walker, so it counts as one
+  const int32_t ce = a.k_e > 0 ? (a.k_e + BS_WAVE - 1) / BS_WAVE : 1;
+  const int32_t ci = a.k_i > 0 ? (a.k_i + BS_WAVE - 1) / BS_WAVE : 1;
+  if (threadIdx.x == 0) {
+    s_maxch[0] = 0;
+    s_maxch[1] = 0;
+    s_hash = 0;
+  }
   int tps = 1;  // threads per source in phase A (power of two, tps * nb <= kBlock)
   while (tps * 2 * nb <= kBlock) tps *= 2;
   __syncthreads();
 
   for (int32_t t = 0; t < a.steps; ++t) {
     const int64_t ta = a.t0 + t;  // absolute step index
+
+    // ---- prefetch: synapse rows of neurons that may spike this step, into L2 ----
+    // Issued before the waits of phase A, whose loads wait for them anyway, so they cost no
+    // latency; the expand phase then finds most spiking rows in L2 instead of HBM.  The
+    // loads write to LDS (s_junk) rather than registers, so no register is held for them.
+#pragma unroll
+    for (int q = 0; q < NPT; ++q) {
+      const int64_t j = base + q * kBlock + threadIdx.x;
+      if (j < n && Model::near(p, r[q])) {
+        int32_t jv = (int32_t)j;
+        asm volatile("" : "+v"(jv));  // keeps the row addresses from being hoisted out of the loop
+        const Row rw = row_of(a, jv);
+        const int last = rw.k - 1;
+        if (last >= 0) {
+#pragma unroll
+          for (int u = 0; u < 5; ++u) {  // every 128-byte line of the first 128 synapses + the last
+            const int o = (u < 4 && u * 32 < last) ? u * 32 : last;
+            __builtin_amdgcn_global_load_lds((const void*)(rw.idx + o), (void*)s_junk, 4, 0, 0);
+            if (kHet)
+              __builtin_amdgcn_global_load_lds((const void*)(rw.w + o), (void*)s_junk, 4, 0, 0);
+          }
+        }
+      }
+    }
 
     // ---- A: inputs produced by step ta-1 ----
     // tps threads per source: all poll the source's count word (one transaction per
@@ -280,123 +325,102 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       }
     }
 
-    // ---- C: compaction into s_list ----
-    uint64_t m[NPT];
-    int32_t wtot = 0;
+    // ---- C: each wave lists its own spikes (no block-wide compaction) ----
+    // Wave w's spikes go to s_list[w * NPT * 64 ...) in (q, lane) order; the wave also counts
+    // the 64-synapse chunks of their rows.  The block only needs the largest chunk count,
+    // which sets the number of expand rounds every wave takes part in.
+    const int wbase = wid * NPT * BS_WAVE;
+    uint32_t nsp = 0, nch = 0;
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
-      m[q] = bs_ballot(last[q]);
-      wtot += __popcll(m[q]);
+      const int64_t j = base + q * kBlock + threadIdx.x;
+      const uint64_t mq = bs_ballot(last[q]);
+      const uint64_t me_ = bs_ballot(last[q] && j < a.n_exc);
+      if (last[q]) s_list[wbase + nsp + bs_rank_below(mq)] = (int32_t)j;
+      nsp += (uint32_t)__popcll(mq);
+      nch += (uint32_t)__popcll(me_) * (uint32_t)ce + (uint32_t)__popcll(mq & ~me_) * (uint32_t)ci;
     }
-    if (lane == 0) s_wave[wid] = wtot;
-    if (threadIdx.x == 0) s_hash = 0;
-    __syncthreads();
-    int32_t off = 0, count = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const int32_t c = s_wave[w];
-      off += (w < wid) ? c : 0;
-      count += c;
-    }
-#pragma unroll
-    for (int q = 0; q < NPT; ++q) {
-      if (last[q]) s_list[off + bs_rank_below(m[q])] = (int32_t)(base + q * kBlock + threadIdx.x);
-      off += __popcll(m[q]);
+    if (lane == 0) {
+      s_wave[wid] = (int32_t)nsp;
+      if (nch) atomicMax(&s_maxch[ta & 1], nch);
     }
     if (h) atomicAdd(&s_hash, h);
-    __syncthreads();
 
     // ---- D: expand spikes into the destinations' inboxes ----
-    // Rounds of up to kBatch*kBlock synapses: (1) each thread loads up to kBatch synapses
-    // (all index/weight loads in flight at once) and counts them per destination in LDS;
-    // (2) one wave turns the counts into an exclusive prefix; (3) entries are placed in an
-    // LDS staging area grouped by destination together with their inbox slot; (4) the
-    // staging area is written out in order, so consecutive lanes store to consecutive
-    // addresses of each destination's region (coalesced) instead of one scattered 8-byte
-    // store per event.
+    // Rounds in which every wave takes up to kChunks of its own 64-synapse chunks: lane l of a
+    // chunk loads synapse c*64 + l of the row (the row address is wave-uniform), takes a rank
+    // among this round's entries for the destination from an LDS counter, and parks the entry
+    // in the destination's kSlots LDS slots (entries past them are stored directly).  After one
+    // barrier the slots are written out destination by destination, so consecutive lanes store
+    // to consecutive inbox addresses, and each destination's cursor advances.
     const int bout = (int)(ta & 1);
     char* ob = inbox + (size_t)bout * buf_bytes;
-    const uint32_t items = (uint32_t)count * (uint32_t)kmax;
-    for (uint32_t r0 = 0; r0 < items; r0 += kBatch * kBlock) {
-      int32_t tgt[kBatch];
-      float wv[kBatch];
-      bool inh[kBatch];
+    uint32_t wv_i = 0, wc = 0;  // walker over this wave's (spike, chunk) list: uniform
+    for (uint32_t rnd = 0;; ++rnd) {
+      int32_t tgt[kChunks];
+      float wv[kChunks];
+      bool inh[kChunks];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const uint32_t it = r0 + u * kBlock + threadIdx.x;
+      for (int u = 0; u < kChunks; ++u) {
         tgt[u] = -1;
         wv[u] = 0.0f;
         inh[u] = false;
-        if (it < items) {
-          const uint32_t ai = it / (uint32_t)kmax;
-          const int32_t tt = (int32_t)(it - ai * (uint32_t)kmax);
-          const Row rw = row_of(a, s_list[ai]);
+        if (wv_i < nsp) {
+          const int32_t jw = __builtin_amdgcn_readfirstlane(s_list[wbase + wv_i]);
+          const Row rw = row_of(a, jw);
+          const int32_t tt = (int32_t)(wc * BS_WAVE) + lane;
           if (tt < rw.k) {
             tgt[u] = rw.idx[tt];
             if (kHet) wv[u] = rw.w[tt];
             inh[u] = rw.inh;
           }
+          if (++wc * BS_WAVE >= (uint32_t)rw.k) {
+            wc = 0;
+            ++wv_i;
+          }
         }
       }
-      // (1) per-destination counts of this round
-      uint32_t rank[kBatch];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        rank[u] = 0;
-        if ((uint32_t)tgt[u] < (uint32_t)n) rank[u] = atomicAdd(&s_rcnt[tgt[u] >> L.shift], 1u);
-      }
-      __syncthreads();
-      // (2) exclusive prefix of the round counts over destinations (one wave)
-      if (wid == 0) {
-        uint32_t loc[kPerLane];
-        uint32_t sum = 0;
-#pragma unroll
-        for (int v = 0; v < kPerLane; ++v) {
-          const int d = lane * kPerLane + v;
-          loc[v] = sum;
-          sum += d < nb ? s_rcnt[d] : 0u;
-        }
-        uint32_t incl = sum;
-#pragma unroll
-        for (int o = 1; o < BS_WAVE; o <<= 1) {
-          const uint32_t y = __shfl_up(incl, o);
-          if (lane >= o) incl += y;
-        }
-        const uint32_t excl = incl - sum;
-#pragma unroll
-        for (int v = 0; v < kPerLane; ++v) {
-          const int d = lane * kPerLane + v;
-          if (d < nb) s_rpre[d] = excl + loc[v];
-        }
-        if (lane == BS_WAVE - 1) s_rtot = incl;
-      }
-      __syncthreads();
-      // (3) place entries grouped by destination, with their final inbox position
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
+      for (int u = 0; u < kChunks; ++u) {
         if ((uint32_t)tgt[u] < (uint32_t)n) {
           const int d = tgt[u] >> L.shift;
-          const uint32_t e = s_rpre[d] + rank[u];
+          const uint32_t rank = atomicAdd(&s_rcnt[d], 1u);
           const uint32_t loc = (uint32_t)(tgt[u] & (kChunk - 1)) | (inh[u] ? kInhFlag : 0u);
-          s_stage[e] = kHet ? (((uint64_t)__float_as_uint(wv[u]) << 32) | loc) : (uint64_t)loc;
-          s_spos[e] = (uint32_t)(s_ofs_out[d] + s_cursor[d] + rank[u]);
+          const uint64_t ent =
+              kHet ? (((uint64_t)__float_as_uint(wv[u]) << 32) | loc) : (uint64_t)loc;
+          if (rank < (uint32_t)kSlots) {
+            s_stage[d * kSlots + rank] = ent;
+          } else {  // slots full: store this one directly
+            const uint64_t pos = s_ofs_out[d] + s_cursor[d] + rank;
+            if (kHet) st_dev64((uint64_t*)ob + pos, ent);
+            else st_dev32((uint32_t*)ob + pos, (uint32_t)ent);
+          }
         }
       }
       __syncthreads();
-      // (4) ordered write-out; advance the per-destination cursors
-      const uint32_t tot = s_rtot;
-      for (uint32_t e = threadIdx.x; e < tot; e += kBlock) {
-        if (kHet) st_dev64((uint64_t*)ob + s_spos[e], s_stage[e]);
-        else st_dev32((uint32_t*)ob + s_spos[e], (uint32_t)s_stage[e]);
+      const uint32_t rounds = (s_maxch[ta & 1] + kChunks - 1) / kChunks;
+      // write-out: kSlots consecutive lanes per destination (all in one wave), then the
+      // destination's first lane advances its cursor and clears its round count
+      for (int x = threadIdx.x; x < nb * kSlots; x += kBlock) {
+        const int d = x / kSlots;
+        const uint32_t slot = (uint32_t)(x - d * kSlots);
+        const uint32_t rc = s_rcnt[d];
+        if (slot < rc) {
+          const uint64_t pos = s_ofs_out[d] + s_cursor[d] + slot;
+          if (kHet) st_dev64((uint64_t*)ob + pos, s_stage[x]);
+          else st_dev32((uint32_t*)ob + pos, (uint32_t)s_stage[x]);
+        }
+        if (slot == 0 && rc) {
+          s_cursor[d] += rc;
+          s_rcnt[d] = 0;
+        }
       }
-      for (int d = threadIdx.x; d < nb; d += kBlock) {
-        s_cursor[d] += s_rcnt[d];
-        s_rcnt[d] = 0;
-      }
-      __syncthreads();
+      if (rnd + 1 >= rounds) break;
+      __syncthreads();  // slots and round counts are reused
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     __syncthreads();
+    int32_t count = 0;
     {
       uint64_t* cout = cnt + (int64_t)bout * nb * nb;
       const uint64_t tag = (uint64_t)(uint32_t)(ta + 1) << 32;
@@ -404,10 +428,16 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         st_dev64(cout + (int64_t)d * nb + me, tag | s_cursor[d]);
         s_cursor[d] = 0;
       }
+      if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) count += s_wave[w];
+        s_maxch[(ta + 1) & 1] = 0;
+      }
     }
     if (threadIdx.x == 0) {
       if (a.counts && count) atomicAdd(&a.counts[t], count);
       if (a.hash && s_hash) atomicAdd(&a.hash[t], s_hash);
+      s_hash = 0;
     }
   }
 
