@@ -175,14 +175,13 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   constexpr int kChunk = NPT * kBlock;
   constexpr int kBatch = 4;                   // phase A: entry loads in flight per thread
   constexpr int kChunks = 4;                  // phase D: 64-synapse chunks per wave and round
-  constexpr int kSlots = 8;                   // phase D: LDS slots per destination and round
-  __shared__ int32_t s_list[kChunk];          // each wave's spikes (global indices)
+  constexpr int kSlots = NPT >= 8 ? 8 : 16;   // phase D: LDS slots per destination and round
   __shared__ float s_in[2 * kChunk];          // (E, I) inputs of this workgroup's neurons
   __shared__ uint32_t s_cursor[kMaxBlocks];   // entries written per destination this step
   __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
   __shared__ uint64_t s_ofs_out[kMaxBlocks];  // inbox offset (d <- me)
-  __shared__ int32_t s_wave[kWaves];          // spikes per wave this step
-  __shared__ uint32_t s_maxch[2];             // largest per-wave chunk count, by step parity
+  __shared__ int32_t s_list[kChunk];          // this step's spikes: E from the front, I from the back
+  __shared__ uint32_t s_nsp[2][2];            // (E, I) spike counts, by step parity
   __shared__ uint32_t s_hash;
   __shared__ uint32_t s_junk[BS_WAVE];        // destination of the row prefetches (never read)
   __shared__ uint32_t s_rcnt[kMaxBlocks];     // expand round: entries per destination
@@ -192,7 +191,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   const int nb = L.nb;
   const int me = blockIdx.x;
   const int lane = bs_lane();
-  const int wid = threadIdx.x / BS_WAVE;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / BS_WAVE);  // wave-uniform
   const int64_t base = (int64_t)me * kChunk;
   const int64_t n = a.n;
   WsHeader* hdr = (WsHeader*)a.ws;
@@ -218,13 +217,12 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   bool last[NPT];
 #pragma unroll
   for (int q = 0; q < NPT; ++q) last[q] = false;
-  // 64-synapse chunks per E / I row; a row without synapses still takes one (empty) chunk
-  // slot in the expand walker, so it counts as one
-  const int32_t ce = a.k_e > 0 ? (a.k_e + BS_WAVE - 1) / BS_WAVE : 1;
-  const int32_t ci = a.k_i > 0 ? (a.k_i + BS_WAVE - 1) / BS_WAVE : 1;
+  // chunk slots per E / I spike: 64-synapse chunks of its row, rounded up to a power of two
+  int lgE = 0, lgI = 0;
+  while ((BS_WAVE << lgE) < a.k_e) ++lgE;
+  while ((BS_WAVE << lgI) < a.k_i) ++lgI;
   if (threadIdx.x == 0) {
-    s_maxch[0] = 0;
-    s_maxch[1] = 0;
+    s_nsp[0][0] = s_nsp[0][1] = s_nsp[1][0] = s_nsp[1][1] = 0;
     s_hash = 0;
   }
   int tps = 1;  // threads per source in phase A (power of two, tps * nb <= kBlock)
@@ -325,38 +323,59 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       }
     }
 
-    // ---- C: each wave lists its own spikes (no block-wide compaction) ----
-    // Wave w's spikes go to s_list[w * NPT * 64 ...) in (q, lane) order; the wave also counts
-    // the 64-synapse chunks of their rows.  The block only needs the largest chunk count,
-    // which sets the number of expand rounds every wave takes part in.
-    const int wbase = wid * NPT * BS_WAVE;
-    uint32_t nsp = 0, nch = 0;
+    // ---- C: block list of this step's spikes ----
+    // E spikes fill s_list from the front and I spikes from the back; each wave reserves its
+    // ranges with one LDS atomic per kind (no scan, one barrier).
+    uint32_t* nsp2 = s_nsp[ta & 1];  // [0]: E spikes, [1]: I spikes of this step
+    {
+      uint64_t mE[NPT], mI[NPT];
+      uint32_t wE = 0, wI = 0;
 #pragma unroll
-    for (int q = 0; q < NPT; ++q) {
-      const int64_t j = base + q * kBlock + threadIdx.x;
-      const uint64_t mq = bs_ballot(last[q]);
-      const uint64_t me_ = bs_ballot(last[q] && j < a.n_exc);
-      if (last[q]) s_list[wbase + nsp + bs_rank_below(mq)] = (int32_t)j;
-      nsp += (uint32_t)__popcll(mq);
-      nch += (uint32_t)__popcll(me_) * (uint32_t)ce + (uint32_t)__popcll(mq & ~me_) * (uint32_t)ci;
-    }
-    if (lane == 0) {
-      s_wave[wid] = (int32_t)nsp;
-      if (nch) atomicMax(&s_maxch[ta & 1], nch);
+      for (int q = 0; q < NPT; ++q) {
+        const int64_t j = base + q * kBlock + threadIdx.x;
+        mE[q] = bs_ballot(last[q] && j < a.n_exc);
+        mI[q] = bs_ballot(last[q] && j >= a.n_exc);
+        wE += (uint32_t)__popcll(mE[q]);
+        wI += (uint32_t)__popcll(mI[q]);
+      }
+      uint32_t bE = 0, bI = 0;
+      if (lane == 0) {
+        if (wE) bE = atomicAdd(&nsp2[0], wE);
+        if (wI) bI = atomicAdd(&nsp2[1], wI);
+      }
+      bE = __builtin_amdgcn_readfirstlane(bE);
+      bI = __builtin_amdgcn_readfirstlane(bI);
+#pragma unroll
+      for (int q = 0; q < NPT; ++q) {
+        const int32_t j = (int32_t)(base + q * kBlock + threadIdx.x);
+        if (last[q]) {
+          if (j < a.n_exc) s_list[bE + bs_rank_below(mE[q])] = j;
+          else s_list[kChunk - 1 - (int)(bI + bs_rank_below(mI[q]))] = j;
+        }
+        bE += (uint32_t)__popcll(mE[q]);
+        bI += (uint32_t)__popcll(mI[q]);
+      }
     }
     if (h) atomicAdd(&s_hash, h);
+    __syncthreads();
 
     // ---- D: expand spikes into the destinations' inboxes ----
-    // Rounds in which every wave takes up to kChunks of its own 64-synapse chunks: lane l of a
-    // chunk loads synapse c*64 + l of the row (the row address is wave-uniform), takes a rank
-    // among this round's entries for the destination from an LDS counter, and parks the entry
-    // in the destination's kSlots LDS slots (entries past them are stored directly).  After one
-    // barrier the slots are written out destination by destination, so consecutive lanes store
-    // to consecutive inbox addresses, and each destination's cursor advances.
+    // Each spike's row is cut into 64-synapse chunks (cpE / cpI chunk slots per E / I spike,
+    // a power of two); chunk g goes to wave g % 16, up to kChunks per wave and round.  Lane l
+    // of a chunk loads synapse c*64 + l of the row (the row address is wave-uniform), takes a
+    // rank among this round's entries for the destination from an LDS counter and parks the
+    // entry in the destination's kSlots LDS slots (entries past them are stored directly).
+    // After one barrier the slots are written out destination by destination, so consecutive
+    // lanes store to consecutive inbox addresses, and each destination's cursor advances.
     const int bout = (int)(ta & 1);
     char* ob = inbox + (size_t)bout * buf_bytes;
-    uint32_t wv_i = 0, wc = 0;  // walker over this wave's (spike, chunk) list: uniform
-    for (uint32_t rnd = 0;; ++rnd) {
+    const uint32_t nE = __builtin_amdgcn_readfirstlane(nsp2[0]);
+    const uint32_t nI = __builtin_amdgcn_readfirstlane(nsp2[1]);
+    const uint32_t gE = nE << lgE;
+    const uint32_t G = gE + (nI << lgI);
+    constexpr uint32_t kPer = kWaves * kChunks;
+    const uint32_t rounds = (G + kPer - 1) / kPer;
+    for (uint32_t rnd = 0; rnd < rounds; ++rnd) {
       int32_t tgt[kChunks];
       float wv[kChunks];
       bool inh[kChunks];
@@ -365,18 +384,25 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         tgt[u] = -1;
         wv[u] = 0.0f;
         inh[u] = false;
-        if (wv_i < nsp) {
-          const int32_t jw = __builtin_amdgcn_readfirstlane(s_list[wbase + wv_i]);
+        const uint32_t g = rnd * kPer + (uint32_t)(u * kWaves + wid);
+        if (g < G) {
+          int32_t jw;
+          uint32_t c;
+          if (g < gE) {
+            jw = s_list[g >> lgE];
+            c = g & ((1u << lgE) - 1u);
+          } else {
+            const uint32_t g2 = g - gE;
+            jw = s_list[kChunk - 1 - (int)(g2 >> lgI)];
+            c = g2 & ((1u << lgI) - 1u);
+          }
+          jw = __builtin_amdgcn_readfirstlane(jw);
           const Row rw = row_of(a, jw);
-          const int32_t tt = (int32_t)(wc * BS_WAVE) + lane;
+          const int32_t tt = (int32_t)(c * BS_WAVE) + lane;
           if (tt < rw.k) {
             tgt[u] = rw.idx[tt];
             if (kHet) wv[u] = rw.w[tt];
             inh[u] = rw.inh;
-          }
-          if (++wc * BS_WAVE >= (uint32_t)rw.k) {
-            wc = 0;
-            ++wv_i;
           }
         }
       }
@@ -384,21 +410,20 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       for (int u = 0; u < kChunks; ++u) {
         if ((uint32_t)tgt[u] < (uint32_t)n) {
           const int d = tgt[u] >> L.shift;
-          const uint32_t rank = atomicAdd(&s_rcnt[d], 1u);
+          const uint32_t rk = atomicAdd(&s_rcnt[d], 1u);
           const uint32_t loc = (uint32_t)(tgt[u] & (kChunk - 1)) | (inh[u] ? kInhFlag : 0u);
           const uint64_t ent =
               kHet ? (((uint64_t)__float_as_uint(wv[u]) << 32) | loc) : (uint64_t)loc;
-          if (rank < (uint32_t)kSlots) {
-            s_stage[d * kSlots + rank] = ent;
+          if (rk < (uint32_t)kSlots) {
+            s_stage[d * kSlots + rk] = ent;
           } else {  // slots full: store this one directly
-            const uint64_t pos = s_ofs_out[d] + s_cursor[d] + rank;
+            const uint64_t pos = s_ofs_out[d] + s_cursor[d] + rk;
             if (kHet) st_dev64((uint64_t*)ob + pos, ent);
             else st_dev32((uint32_t*)ob + pos, (uint32_t)ent);
           }
         }
       }
       __syncthreads();
-      const uint32_t rounds = (s_maxch[ta & 1] + kChunks - 1) / kChunks;
       // write-out: kSlots consecutive lanes per destination (all in one wave), then the
       // destination's first lane advances its cursor and clears its round count
       for (int x = threadIdx.x; x < nb * kSlots; x += kBlock) {
@@ -415,8 +440,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           s_rcnt[d] = 0;
         }
       }
-      if (rnd + 1 >= rounds) break;
-      __syncthreads();  // slots and round counts are reused
+      if (rnd + 1 < rounds) __syncthreads();  // slots and round counts are reused
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     __syncthreads();
@@ -429,9 +453,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         s_cursor[d] = 0;
       }
       if (threadIdx.x == 0) {
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) count += s_wave[w];
-        s_maxch[(ta + 1) & 1] = 0;
+        count = (int32_t)(nE + nI);
+        s_nsp[(ta + 1) & 1][0] = 0;
+        s_nsp[(ta + 1) & 1][1] = 0;
       }
     }
     if (threadIdx.x == 0) {
