@@ -37,6 +37,7 @@ constexpr int kMaxBlocks = 512;
 constexpr int kMaxNpt = 8;
 constexpr uint32_t kInhFlag = 0x80000000u;
 constexpr uint64_t kSpinLimit = 1ull << 24;
+constexpr int kRunSteps = 4096;           // steps per cooperative launch (partials buffer)
 #ifndef BS_POLL_SLEEP
 #define BS_POLL_SLEEP 1  // s_sleep units (64 clocks) between polls of a count word
 #endif
@@ -53,6 +54,7 @@ struct NetLayout {
   uint64_t off_cnt;    // uint64 [2][nb dst][nb src]   tagged counts
   uint64_t off_cap;    // uint32 [nb src][nb dst]      capacities
   uint64_t off_ofs;    // uint64 [nb dst][nb src] + 1  inbox entry offsets (dst-major)
+  uint64_t off_part;   // uint32 [2][kRunSteps][nb]  per-workgroup spike counts / hashes
   uint64_t off_inbox;  // entries [2][total]
   uint64_t bytes;
 };
@@ -88,8 +90,8 @@ struct NetArgs {
   uint8_t* spk;
   int64_t t0;
   int32_t steps;
-  int32_t* counts;
-  uint32_t* hash;
+  uint32_t* counts;  // per-workgroup spike counts [steps][nb] (workspace), or NULL
+  uint32_t* hash;    // per-workgroup spike hashes [steps][nb] (workspace), or NULL
   uint8_t* raster;
   char* ws;
   NetLayout L;
@@ -146,11 +148,10 @@ struct HhModel {
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
     return bs_hh_update(p, r.V, r.m, r.h, r.n, r.ge, r.gi, in_e, in_i);
   }
-  // Whether the neuron may spike this step: V on the upstroke, below threshold but within
-  // 25 mV of it.  Only steers the row prefetch.
-  __device__ static bool near(const Params& p, const Regs& r) {
-    return r.V < p.V_th && r.V >= p.V_th - 25.0f;
-  }
+  // No row prefetch for HH: its spikes are rarer and its update is VALU-heavy, and on the
+  // 1M-neuron net prefetching the rows of neurons on the upstroke (V within 10-60 mV below
+  // threshold) made the step slower, not faster.
+  __device__ static bool near(const Params&, const Regs&) { return false; }
 };
 
 // Synapse row of neuron i (global index) in the E or I connectivity.
@@ -177,9 +178,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   constexpr int kChunks = 4;                  // phase D: 64-synapse chunks per wave and round
   constexpr int kSlots = NPT >= 8 ? 8 : 16;   // phase D: LDS slots per destination and round
   __shared__ float s_in[2 * kChunk];          // (E, I) inputs of this workgroup's neurons
-  __shared__ uint32_t s_cursor[kMaxBlocks];   // entries written per destination this step
+  __shared__ uint32_t s_pos[kMaxBlocks];      // next inbox entry per destination (d <- me)
   __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
-  __shared__ uint64_t s_ofs_out[kMaxBlocks];  // inbox offset (d <- me)
+  __shared__ uint32_t s_ofs_out[kMaxBlocks];  // first inbox entry of (d <- me)
   __shared__ int32_t s_list[kChunk];          // this step's spikes: E from the front, I from the back
   __shared__ uint32_t s_nsp[2][2];            // (E, I) spike counts, by step parity
   __shared__ uint32_t s_hash;
@@ -202,8 +203,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
 
   for (int s = threadIdx.x; s < nb; s += kBlock) {
     s_ofs_in[s] = ofs[(int64_t)me * nb + s];
-    s_ofs_out[s] = ofs[(int64_t)s * nb + me];
-    s_cursor[s] = 0;
+    s_ofs_out[s] = (uint32_t)ofs[(int64_t)s * nb + me];  // entry counts are < 2^32
+    s_pos[s] = s_ofs_out[s];
     s_rcnt[s] = 0;
   }
   for (int i = threadIdx.x; i < 2 * kChunk; i += kBlock) s_in[i] = 0.0f;
@@ -358,6 +359,10 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     }
     if (h) atomicAdd(&s_hash, h);
     __syncthreads();
+    if (threadIdx.x == 0) {  // per-workgroup partials, summed over workgroups after the launch
+      if (a.counts) a.counts[(int64_t)t * nb + me] = nsp2[0] + nsp2[1];
+      if (a.hash) a.hash[(int64_t)t * nb + me] = s_hash;
+    }
 
     // ---- D: expand spikes into the destinations' inboxes ----
     // Each spike's row is cut into 64-synapse chunks (cpE / cpI chunk slots per E / I spike,
@@ -417,7 +422,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           if (rk < (uint32_t)kSlots) {
             s_stage[d * kSlots + rk] = ent;
           } else {  // slots full: store this one directly
-            const uint64_t pos = s_ofs_out[d] + s_cursor[d] + rk;
+            const uint32_t pos = s_pos[d] + rk;
             if (kHet) st_dev64((uint64_t*)ob + pos, ent);
             else st_dev32((uint32_t*)ob + pos, (uint32_t)ent);
           }
@@ -431,12 +436,12 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         const uint32_t slot = (uint32_t)(x - d * kSlots);
         const uint32_t rc = s_rcnt[d];
         if (slot < rc) {
-          const uint64_t pos = s_ofs_out[d] + s_cursor[d] + slot;
+          const uint32_t pos = s_pos[d] + slot;
           if (kHet) st_dev64((uint64_t*)ob + pos, s_stage[x]);
           else st_dev32((uint32_t*)ob + pos, (uint32_t)s_stage[x]);
         }
         if (slot == 0 && rc) {
-          s_cursor[d] += rc;
+          s_pos[d] += rc;
           s_rcnt[d] = 0;
         }
       }
@@ -444,24 +449,18 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     __syncthreads();
-    int32_t count = 0;
     {
       uint64_t* cout = cnt + (int64_t)bout * nb * nb;
       const uint64_t tag = (uint64_t)(uint32_t)(ta + 1) << 32;
       for (int d = threadIdx.x; d < nb; d += kBlock) {
-        st_dev64(cout + (int64_t)d * nb + me, tag | s_cursor[d]);
-        s_cursor[d] = 0;
+        st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - s_ofs_out[d]));
+        s_pos[d] = s_ofs_out[d];
       }
       if (threadIdx.x == 0) {
-        count = (int32_t)(nE + nI);
         s_nsp[(ta + 1) & 1][0] = 0;
         s_nsp[(ta + 1) & 1][1] = 0;
+        s_hash = 0;
       }
-    }
-    if (threadIdx.x == 0) {
-      if (a.counts && count) atomicAdd(&a.counts[t], count);
-      if (a.hash && s_hash) atomicAdd(&a.hash[t], s_hash);
-      s_hash = 0;
     }
   }
 
@@ -536,9 +535,25 @@ __global__ void k_zero_u64(uint64_t* p, int64_t n) {
     p[i] = 0ull;
 }
 
-__global__ void k_zero_u32(uint32_t* p, int32_t n) {
-  for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
-    p[i] = 0u;
+// counts[t] = sum over workgroups of pc[t][b]; hash[t] likewise (mod 2^32).  One wave per step.
+__global__ void k_sum_parts(int nb, int32_t steps, const uint32_t* pc, const uint32_t* ph,
+                            int32_t* counts, uint32_t* hash) {
+  const int32_t t = blockIdx.x * 4 + threadIdx.x / BS_WAVE;
+  const int lane = threadIdx.x % BS_WAVE;
+  if (t >= steps) return;
+  uint32_t c = 0, h = 0;
+  for (int b = lane; b < nb; b += BS_WAVE) {
+    if (counts) c += pc[(int64_t)t * nb + b];
+    if (hash) h += ph[(int64_t)t * nb + b];
+  }
+  for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+    c += __shfl_xor(c, o);
+    h += __shfl_xor(h, o);
+  }
+  if (lane == 0) {
+    if (counts) counts[t] = (int32_t)c;
+    if (hash) hash[t] = h;
+  }
 }
 
 // ---- host helpers ----
@@ -584,6 +599,8 @@ int plan(const bs_net* net, NetLayout* L) {
   o = align256(o + (size_t)nb * nb * sizeof(uint32_t));
   L->off_ofs = o;
   o = align256(o + (size_t)(nb * nb + 1) * sizeof(uint64_t));
+  L->off_part = o;
+  o = align256(o + (size_t)2 * kRunSteps * nb * sizeof(uint32_t));
   L->off_inbox = o;
   o = align256(o + (size_t)2 * L->total * L->entry);
   L->bytes = o;
@@ -676,23 +693,30 @@ int run(const bs_net* net, const typename Model::State* st, const typename Model
     return BS_ERR_UNSUPPORTED;
   }
   hipStream_t s = bs_stream(stream);
-  const int zb = (steps + 255) / 256;
-  if (counts_out) {
-    k_zero_u32<<<zb, 256, 0, s>>>((uint32_t*)counts_out, steps);
-    BS_CHECK_LAUNCH();
+  uint32_t* part = (uint32_t*)((char*)workspace + L.off_part);
+  // Launches of at most kRunSteps steps; after each, the per-workgroup partials of every
+  // step are summed into counts_out / hash_out (plain stores in the kernel instead of one
+  // same-address atomic per workgroup and step).
+  for (int32_t done = 0; done < steps;) {
+    const int32_t len = steps - done < kRunSteps ? steps - done : kRunSteps;
+    NetArgs a = make_args(net, L, workspace);
+    a.t0 = t0 + done;
+    a.steps = len;
+    a.counts = counts_out ? part : nullptr;
+    a.hash = hash_out ? part + (size_t)kRunSteps * L.nb : nullptr;
+    a.raster = raster_out ? raster_out + (int64_t)done * net->n : nullptr;
+    rc = net->w_e != nullptr ? dispatch_npt<Model, true>(a, *st, *p, s)
+                             : dispatch_npt<Model, false>(a, *st, *p, s);
+    if (rc) return rc;
+    if (counts_out || hash_out) {
+      k_sum_parts<<<(len + 3) / 4, 256, 0, s>>>(L.nb, len, a.counts, a.hash,
+                                                counts_out ? counts_out + done : nullptr,
+                                                hash_out ? hash_out + done : nullptr);
+      BS_CHECK_LAUNCH();
+    }
+    done += len;
   }
-  if (hash_out) {
-    k_zero_u32<<<zb, 256, 0, s>>>(hash_out, steps);
-    BS_CHECK_LAUNCH();
-  }
-  NetArgs a = make_args(net, L, workspace);
-  a.t0 = t0;
-  a.steps = steps;
-  a.counts = counts_out;
-  a.hash = hash_out;
-  a.raster = raster_out;
-  if (net->w_e != nullptr) return dispatch_npt<Model, true>(a, *st, *p, s);
-  return dispatch_npt<Model, false>(a, *st, *p, s);
+  return BS_OK;
 }
 
 }  // namespace

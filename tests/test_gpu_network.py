@@ -76,6 +76,39 @@ def test_coba_lif_state_matches_oracle_midway(torch_cuda):
     assert np.array_equal(r.spk.cpu().numpy().astype(bool), res['spk'])
 
 
+def test_coba_lif_long_run_across_launches(torch_cuda):
+    """5000 steps: more than one cooperative launch (4096 steps each).  Per-step counts and
+    spike hashes and the final state equal the C restatement's; the raster of one 5000-step
+    call equals that of a 1000 + 4000 split on a second runner."""
+    from oracle import cbuild
+    torch = torch_cuda
+    say('coba lif 4000 long run', 5000)
+    pe, pi, V0, p = make_golden.config1_net()
+    n, T = V0.size, 5000
+    st = dict(V=V0.copy(), ge=np.zeros(n, F), gi=np.zeros(n, F), ref=np.zeros(n, np.int32),
+              spk=np.zeros(n, np.uint8), in_e=np.zeros(n, F), in_i=np.zeros(n, F))
+    c_ref = np.zeros(T, np.int32)
+    h_ref = np.zeros(T, np.uint32)
+    cbuild.coba_lif_run(st, pe.idx, pi.idx, pe.w_scalar, pi.w_scalar, p, 3200, T, nthreads=4,
+                        counts=c_ref, hashes=h_ref)
+    r1 = _lif_runner(torch, False)
+    r2 = _lif_runner(torch, False)
+    ras1 = torch.zeros(T, n, dtype=torch.uint8, device='cuda')
+    ras2 = torch.zeros(T, n, dtype=torch.uint8, device='cuda')
+    counts = torch.zeros(T, dtype=torch.int32, device='cuda')
+    hashes = torch.zeros(T, dtype=torch.int32, device='cuda')
+    r1.run(T, counts=counts, hashes=hashes, raster=ras1)
+    r2.run(1000, raster=ras2[:1000])
+    r2.run(4000, raster=ras2[1000:])
+    r1.check()
+    r2.check()
+    assert counts.cpu().numpy().tolist() == c_ref.tolist()
+    assert [int(h) & 0xFFFFFFFF for h in hashes.cpu().numpy()] == h_ref.tolist()
+    assert np.array_equal(r1.state['V'].cpu().numpy(), st['V'])
+    assert torch.equal(ras1, ras2)
+    assert int(ras1.sum().item()) == int(c_ref.sum())
+
+
 def test_coba_hh_2000_raster_bit_exact(torch_cuda):
     torch = torch_cuda
     from brainstate_amd import ops
