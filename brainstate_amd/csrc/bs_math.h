@@ -5,13 +5,14 @@
 // and the Hodgkin-Huxley rates of examples/100_hh_neuron_model.py:49-64 call exp and
 // exprel.  Device libm exp and glibc exp differ in the last ulp, and one ulp is enough
 // to flip a threshold crossing, so spike rasters would not be reproducible against a
-// CPU restatement.  These functions are built only from IEEE-754 +, -, *, / and rint,
+// CPU restatement.  These functions are built only from IEEE-754 +, -, *, /, fma and rint,
 // all correctly rounded on gfx950 and on x86, so the same input gives the same bits on
 // both sides (the library is compiled with -ffp-contract=off).
 //
 // Method (Cody & Waite, "Software Manual for the Elementary Functions", 1980):
-//     n = rint(x * log2(e)),  r = (x - n*L_hi) - n*L_lo,  |r| <= ln2/2
-//     e^x = 2^n * P(r),  P = degree-7 Taylor polynomial of e^r (truncation < 6e-9)
+//     n = rint(x * log2(e)),  r = fma(-n, L_lo, fma(-n, L_hi, x)),  |r| <= ln2/2
+//     e^x = 2^n * P(r),  P = degree-7 Taylor polynomial of e^r (truncation < 6e-9),
+//     evaluated by Horner's rule with fused multiply-adds
 // L_hi = ln2 rounded to 16 significant bits (so n*L_hi is exact for |n| < 128) and
 // L_lo = fl32(ln2 - L_hi).
 #pragma once
@@ -36,6 +37,10 @@ BS_HD inline float bs_pow2i(int n) {
   return v.f;
 }
 
+// a*b + c with one rounding (v_fma_f32 on the device, C99 fmaf on the host).  The library is
+// built with -ffp-contract=off, so these are the only fused operations.
+BS_HD inline float bs_fma(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
 BS_HD inline float bs_rint(float x) {
   // Round half to even (v_rndne_f32 on the device, nearbyintf on the host).
   return __builtin_rintf(x);
@@ -47,16 +52,16 @@ BS_HD inline float bs_expf(float x) {
   if (x > BS_EXP_XMAX) x = BS_EXP_XMAX;
   if (x < BS_EXP_XMIN) x = BS_EXP_XMIN;
   const float n = bs_rint(x * BS_LOG2E_F);
-  float r = x - n * BS_LN2_HI_F;
-  r = r - n * BS_LN2_LO_F;
+  float r = bs_fma(-n, BS_LN2_HI_F, x);
+  r = bs_fma(-n, BS_LN2_LO_F, r);
   float p = (float)(1.0 / 5040.0);
-  p = p * r + (float)(1.0 / 720.0);
-  p = p * r + (float)(1.0 / 120.0);
-  p = p * r + (float)(1.0 / 24.0);
-  p = p * r + (float)(1.0 / 6.0);
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
+  p = bs_fma(p, r, (float)(1.0 / 720.0));
+  p = bs_fma(p, r, (float)(1.0 / 120.0));
+  p = bs_fma(p, r, (float)(1.0 / 24.0));
+  p = bs_fma(p, r, (float)(1.0 / 6.0));
+  p = bs_fma(p, r, 0.5f);
+  p = bs_fma(p, r, 1.0f);
+  p = bs_fma(p, r, 1.0f);
   return p * bs_pow2i((int)n);
 }
 
@@ -67,13 +72,13 @@ BS_HD inline float bs_exprel(float z) {
   float az = z < 0.0f ? -z : z;
   if (az < BS_EXPREL_SERIES) {
     float p = (float)(1.0 / 40320.0);
-    p = p * z + (float)(1.0 / 5040.0);
-    p = p * z + (float)(1.0 / 720.0);
-    p = p * z + (float)(1.0 / 120.0);
-    p = p * z + (float)(1.0 / 24.0);
-    p = p * z + (float)(1.0 / 6.0);
-    p = p * z + 0.5f;
-    p = p * z + 1.0f;
+    p = bs_fma(p, z, (float)(1.0 / 5040.0));
+    p = bs_fma(p, z, (float)(1.0 / 720.0));
+    p = bs_fma(p, z, (float)(1.0 / 120.0));
+    p = bs_fma(p, z, (float)(1.0 / 24.0));
+    p = bs_fma(p, z, (float)(1.0 / 6.0));
+    p = bs_fma(p, z, 0.5f);
+    p = bs_fma(p, z, 1.0f);
     return p;
   }
   return (bs_expf(z) - 1.0f) / z;

@@ -1,7 +1,8 @@
 // Per-neuron fused updates (device side), shared by the single-step kernels and the
-// persistent network runners.  Every expression is written in the operation order the
-// reference code evaluates it in (left to right), and the library is built with
-// -ffp-contract=off, so each line is a fixed sequence of correctly rounded fp32 ops.
+// persistent network runners.  Every expression follows the operation order of the
+// reference code, with each multiply-add written as one fused multiply-add (bs_fma), and
+// the library is built with -ffp-contract=off, so each line is a fixed sequence of
+// correctly rounded fp32 operations that the CPU restatements reproduce bit for bit.
 // Division by a model constant (tau, C, the HH rate scales) is multiplication by its fp32
 // reciprocal: that is how the reference executes it under jit, where XLA's algebraic
 // simplifier rewrites A / Const into A * (1 / Const).  Divisions by variables stay divisions.
@@ -14,14 +15,14 @@
 // Returns the spike; updates V, ge, gi, ref in place.
 __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, float& ge,
                                               float& gi, int32_t& ref, float in_e, float in_i) {
-  ge = ge * p.decay_e + in_e;
-  gi = gi * p.decay_i + in_i;
-  float I = p.I_ext + ge * (p.E_e - V);
-  I = I + gi * (p.E_i - V);
-  const float f = ((p.V_rest - V) + p.R * I) * p.inv_tau;
-  const float J = (-1.0f - p.R * (ge + gi)) * p.inv_tau;
+  ge = bs_fma(ge, p.decay_e, in_e);
+  gi = bs_fma(gi, p.decay_i, in_i);
+  float I = bs_fma(ge, p.E_e - V, p.I_ext);
+  I = bs_fma(gi, p.E_i - V, I);
+  const float f = bs_fma(p.R, I, p.V_rest - V) * p.inv_tau;
+  const float J = bs_fma(-p.R, ge + gi, -1.0f) * p.inv_tau;
   const float phi = bs_exprel(p.dt * J);
-  float Vn = V + (p.dt * phi) * f;
+  float Vn = bs_fma(p.dt * phi, f, V);
   bool spk = false;
   if (ref > 0) {
     Vn = V;
@@ -58,31 +59,32 @@ __device__ __forceinline__ bs_hh_rates bs_hh_rate(float V) {
 }
 
 __device__ __forceinline__ float bs_hh_gate(float x, float a, float b, float dt) {
-  const float f = a * (1.0f - x) - b * x;
+  const float f = bs_fma(a, 1.0f - x, -(b * x));
   const float J = -(a + b);
   const float phi = bs_exprel(dt * J);
-  return x + (dt * phi) * f;
+  return bs_fma(dt * phi, f, x);
 }
 
 // Expon + COBA + HH exp-Euler for one neuron (examples/100_hh_neuron_model.py:72-93).
 __device__ __forceinline__ bool bs_hh_update(const bs_hh_params& p, float& V, float& m, float& h,
                                              float& n, float& ge, float& gi, float in_e,
                                              float in_i) {
-  ge = ge * p.decay_e + in_e;
-  gi = gi * p.decay_i + in_i;
+  ge = bs_fma(ge, p.decay_e, in_e);
+  gi = bs_fma(gi, p.decay_i, in_i);
   const bs_hh_rates r = bs_hh_rate(V);
-  float I = p.I_ext + ge * (p.E_e - V);
-  I = I + gi * (p.E_i - V);
+  float I = bs_fma(ge, p.E_e - V, p.I_ext);
+  I = bs_fma(gi, p.E_i - V, I);
   const float gna = p.gNa * m * m * m * h;
-  const float INa = gna * (V - p.ENa);
   const float n2 = n * n;
   const float gk = p.gK * n2 * n2;
-  const float IK = gk * (V - p.EK);
-  const float IL = p.gL * (V - p.EL);
-  const float f = ((((-INa) - IK) - IL) + I) * p.inv_C;
+  // (I - INa - IK - IL) / C, each channel current folded in with one fused multiply-add
+  float acc = bs_fma(-gna, V - p.ENa, I);
+  acc = bs_fma(-gk, V - p.EK, acc);
+  acc = bs_fma(-p.gL, V - p.EL, acc);
+  const float f = acc * p.inv_C;
   const float J = ((((-gna) - gk) - p.gL) - (ge + gi)) * p.inv_C;
   const float phi = bs_exprel(p.dt * J);
-  const float Vn = V + (p.dt * phi) * f;
+  const float Vn = bs_fma(p.dt * phi, f, V);
   const float mn = bs_hh_gate(m, r.am, r.bm, p.dt);
   const float hn = bs_hh_gate(h, r.ah, r.bh, p.dt);
   const float nn = bs_hh_gate(n, r.an, r.bn, p.dt);

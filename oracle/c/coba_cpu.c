@@ -9,7 +9,7 @@
  *     division by the constant tau taken as multiplication by fp32(1/tau) (how XLA runs it);
  *   - its own fp32 exp/exprel (Cody-Waite + degree-7 Taylor, the method the oracle fixes).
  * Built with -ffp-contract=off so every expression is the same rounded op sequence as the
- * numpy oracle.  Scatter adds use atomics when run multi-threaded: order-free (hence
+ * numpy oracle; the fused multiply-adds are written out as fmaf (correctly rounded in C99).  Scatter adds use atomics when run multi-threaded: order-free (hence
  * bit-exact) for one repeated weight value, tolerance-equal otherwise.
  */
 #include <math.h>
@@ -30,16 +30,16 @@ static inline float o_expf(float x) {
   if (x > 88.0f) x = 88.0f;
   if (x < -87.0f) x = -87.0f;
   const float n = nearbyintf(x * (float)1.4426950408889634);
-  float r = x - n * 0.693145751953125f;
-  r = r - n * (float)(0.6931471805599453 - 0.693145751953125);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, (float)(0.6931471805599453 - 0.693145751953125), r);
   float p = (float)(1.0 / 5040.0);
-  p = p * r + (float)(1.0 / 720.0);
-  p = p * r + (float)(1.0 / 120.0);
-  p = p * r + (float)(1.0 / 24.0);
-  p = p * r + (float)(1.0 / 6.0);
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
+  p = fmaf(p, r, (float)(1.0 / 720.0));
+  p = fmaf(p, r, (float)(1.0 / 120.0));
+  p = fmaf(p, r, (float)(1.0 / 24.0));
+  p = fmaf(p, r, (float)(1.0 / 6.0));
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
   return p * o_pow2i((int)n);
 }
 
@@ -47,13 +47,13 @@ static inline float o_exprel(float z) {
   const float az = z < 0.0f ? -z : z;
   if (az < 0.5f) {
     float p = (float)(1.0 / 40320.0);
-    p = p * z + (float)(1.0 / 5040.0);
-    p = p * z + (float)(1.0 / 720.0);
-    p = p * z + (float)(1.0 / 120.0);
-    p = p * z + (float)(1.0 / 24.0);
-    p = p * z + (float)(1.0 / 6.0);
-    p = p * z + 0.5f;
-    p = p * z + 1.0f;
+    p = fmaf(p, z, (float)(1.0 / 5040.0));
+    p = fmaf(p, z, (float)(1.0 / 720.0));
+    p = fmaf(p, z, (float)(1.0 / 120.0));
+    p = fmaf(p, z, (float)(1.0 / 24.0));
+    p = fmaf(p, z, (float)(1.0 / 6.0));
+    p = fmaf(p, z, 0.5f);
+    p = fmaf(p, z, 1.0f);
     return p;
   }
   return (o_expf(z) - 1.0f) / z;
@@ -102,17 +102,17 @@ long long bso_coba_lif_run(int n, int n_exc, int k_e, int k_i, const int32_t* id
     /* fused Expon + COBA + LIFRef update; compaction in ascending order */
 #pragma omp parallel for schedule(static) reduction(+ : h)
     for (int j = 0; j < n; ++j) {
-      float g_e = ge[j] * p.decay_e + in_e[j];
-      float g_i = gi[j] * p.decay_i + in_i[j];
+      float g_e = fmaf(ge[j], p.decay_e, in_e[j]);
+      float g_i = fmaf(gi[j], p.decay_i, in_i[j]);
       in_e[j] = 0.0f;
       in_i[j] = 0.0f;
       const float v = V[j];
-      float I = p.I_ext + g_e * (p.E_e - v);
-      I = I + g_i * (p.E_i - v);
-      const float f = ((p.V_rest - v) + p.R * I) * p.inv_tau;
-      const float J = (-1.0f - p.R * (g_e + g_i)) * p.inv_tau;
+      float I = fmaf(g_e, p.E_e - v, p.I_ext);
+      I = fmaf(g_i, p.E_i - v, I);
+      const float f = fmaf(p.R, I, p.V_rest - v) * p.inv_tau;
+      const float J = fmaf(-p.R, g_e + g_i, -1.0f) * p.inv_tau;
       const float phi = o_exprel(p.dt * J);
-      float vn = v + (p.dt * phi) * f;
+      float vn = fmaf(p.dt * phi, f, v);
       int32_t r = ref[j];
       uint8_t s = 0;
       if (r > 0) {

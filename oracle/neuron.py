@@ -3,6 +3,9 @@
 exp-Euler, brainstate/nn/_exp_euler.py:226-249:
     J = d f / d x (diagonal, from ``vector_grad``),  phi = exprel(dt*J),
     x' = x + (dt*phi)*f(x)                      (left-to-right, as ``state + dt*phi*drift``)
+Each multiply-add of the model updates is one fused multiply-add (``fma32``), as the
+device code writes it; XLA likewise contracts multiply-adds when it compiles the
+reference for a GPU, so the reference's own bits depend on such fusions.
 Pinned by the known answers of brainstate/nn/_exp_euler_test.py:29-97,316-339 and by the
 one-step LIF value printed in docs/tutorials/brain_dynamics/04_building_an_snn.ipynb
 cell 5 (V_rest=-52, tau=10 ms, V0=-60, I=8, dt=0.1 ms -> -59.84079742 mV).
@@ -27,7 +30,7 @@ and the gates each by exp-Euler from the old state, spike = (V < V_th) & (V' >= 
 """
 import numpy as np
 
-from .bsmath import expf, exprel
+from .bsmath import expf, exprel, fma32
 
 F = np.float32
 I32 = np.int32
@@ -43,7 +46,7 @@ def exp_euler_step(f, jac, x, dt):
         return x + dt * phi * f(x)
     z = (dt * np.asarray(jac(x), F)).astype(F)
     phi = exprel(z)
-    return (x + (dt * phi).astype(F) * np.asarray(f(x), F)).astype(F)
+    return fma32((dt * phi).astype(F), np.asarray(f(x), F), x)
 
 
 def decay_factor(dt, tau):
@@ -72,18 +75,19 @@ class LIFParams:
 
 def lif_membrane(V, ge, gi, p):
     """One exp-Euler step of the COBA LIF membrane (no refractoriness, no reset)."""
-    I = (p.I_ext + ge * (p.E_e - V)).astype(F)
-    I = (I + gi * (p.E_i - V)).astype(F)
-    f = (((p.V_rest - V) + p.R * I) * p.inv_tau).astype(F)
-    J = ((F(-1.0) - p.R * (ge + gi)) * p.inv_tau).astype(F)
+    V, ge, gi = (np.asarray(x, F) for x in (V, ge, gi))
+    I = fma32(ge, (p.E_e - V).astype(F), p.I_ext)
+    I = fma32(gi, (p.E_i - V).astype(F), I)
+    f = (fma32(p.R, I, (p.V_rest - V).astype(F)) * p.inv_tau).astype(F)
+    J = (fma32(-p.R, (ge + gi).astype(F), F(-1.0)) * p.inv_tau).astype(F)
     phi = exprel((p.dt * J).astype(F))
-    return (V + (p.dt * phi).astype(F) * f).astype(F)
+    return fma32((p.dt * phi).astype(F), f, V)
 
 
 def coba_lif_step(V, ge, gi, ref, in_e, in_i, p):
     """Fused Expon + COBA + LIFRef step.  Returns (V, ge, gi, ref, spike)."""
-    ge = (ge * p.de + in_e).astype(F)
-    gi = (gi * p.di + in_i).astype(F)
+    ge = fma32(ge, p.de, in_e)
+    gi = fma32(gi, p.di, in_i)
     Vn = lif_membrane(V, ge, gi, p)
     refr = ref > 0
     Vn = np.where(refr, V, Vn).astype(F)
@@ -127,29 +131,29 @@ def hh_init(V):
 
 
 def _gate(x, a, b, dt):
-    f = (a * (F(1.0) - x) - b * x).astype(F)
+    f = fma32(a, (F(1.0) - x).astype(F), (-(b * x)).astype(F))
     J = (-(a + b)).astype(F)
     phi = exprel((dt * J).astype(F))
-    return (x + (dt * phi).astype(F) * f).astype(F)
+    return fma32((dt * phi).astype(F), f, x)
 
 
 def hh_step(V, m, h, n, ge, gi, in_e, in_i, p):
     """Fused Expon + COBA + HH step.  Returns (V, m, h, n, ge, gi, spike)."""
-    ge = (ge * p.de + in_e).astype(F)
-    gi = (gi * p.di + in_i).astype(F)
+    ge = fma32(ge, p.de, in_e)
+    gi = fma32(gi, p.di, in_i)
     am, bm, ah, bh, an, bn = hh_rates(V)
-    I = (p.I_ext + ge * (p.E_e - V)).astype(F)
-    I = (I + gi * (p.E_i - V)).astype(F)
+    I = fma32(ge, (p.E_e - V).astype(F), p.I_ext)
+    I = fma32(gi, (p.E_i - V).astype(F), I)
     gna = (p.gNa * m * m * m * h).astype(F)
-    INa = (gna * (V - p.ENa)).astype(F)
     n2 = (n * n).astype(F)
     gk = (p.gK * n2 * n2).astype(F)
-    IK = (gk * (V - p.EK)).astype(F)
-    IL = (p.gL * (V - p.EL)).astype(F)
-    f = (((((-INa) - IK) - IL) + I) * p.inv_C).astype(F)
+    acc = fma32(-gna, (V - p.ENa).astype(F), I)          # (I - INa - IK - IL), fused
+    acc = fma32(-gk, (V - p.EK).astype(F), acc)
+    acc = fma32(-p.gL, (V - p.EL).astype(F), acc)
+    f = (acc * p.inv_C).astype(F)
     J = (((((-gna) - gk) - p.gL) - (ge + gi)) * p.inv_C).astype(F)
     phi = exprel((p.dt * J).astype(F))
-    Vn = (V + (p.dt * phi).astype(F) * f).astype(F)
+    Vn = fma32((p.dt * phi).astype(F), f, V)
     mn = _gate(m, am, bm, p.dt)
     hn = _gate(h, ah, bh, p.dt)
     nn = _gate(n, an, bn, p.dt)

@@ -12,6 +12,44 @@ def _ulp_err(got, ref64):
     return np.abs(got.astype(np.float64) - ref64) / np.spacing(np.abs(ref32)).astype(np.float64)
 
 
+def _libm_fmaf():
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library('m') or 'libm.so.6')
+    libm.fmaf.restype = ctypes.c_float
+    libm.fmaf.argtypes = [ctypes.c_float] * 3
+    return libm.fmaf
+
+
+def test_fma32_equals_c_fmaf():
+    """The oracle's binary32 fused multiply-add equals C99 fmaf (one rounding) bit for bit, on
+    random operands and on near-cancelling ones where a*b + c is tiny."""
+    fmaf = _libm_fmaf()
+    rs = np.random.RandomState(7)
+    a = (rs.randn(4000) * np.exp2(rs.randint(-20, 20, 4000))).astype(F)
+    b = (rs.randn(4000) * np.exp2(rs.randint(-20, 20, 4000))).astype(F)
+    for c in (rs.randn(4000).astype(F), (-(a * b)).astype(F),
+              ((a * b) * F(1 + 2 ** -12)).astype(F)):
+        got = bsmath.fma32(a, b, c)
+        ref = np.array([fmaf(float(x), float(y), float(z)) for x, y, z in zip(a, b, c)], F)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_fma32_double_rounding_traps():
+    """a*b lands exactly on a binary32 tie and c nudges the exact sum off it: one rounding goes
+    the way of c, while rounding a*b + c to float64 first and then to float32 would round to
+    even (1 + 2^-11) both times."""
+    fmaf = _libm_fmaf()
+    x = F(1 + 2 ** -12)                       # x*x = 1 + 2^-11 + 2^-24 (a tie in binary32)
+    up, down = bsmath.fma32(x, x, F(2 ** -70)), bsmath.fma32(x, x, F(-2 ** -70))
+    assert float(up) == 1 + 2 ** -11 + 2 ** -23
+    assert float(down) == 1 + 2 ** -11
+    assert float(up) == fmaf(float(x), float(x), 2 ** -70)
+    assert float(down) == fmaf(float(x), float(x), -2 ** -70)
+    naive = F(np.float64(x) * np.float64(x) + 2 ** -70)
+    assert float(naive) == 1 + 2 ** -11              # what the trap catches
+
+
 def test_expf_within_2ulp_of_float64():
     x = np.linspace(-87.0, 88.0, 1_000_001, dtype=F)
     err = _ulp_err(bsmath.expf(x), np.exp(x.astype(np.float64)))
