@@ -37,7 +37,7 @@ constexpr int kMaxBlocks = 512;
 constexpr int kMaxNpt = 8;
 constexpr uint32_t kInhFlag = 0x80000000u;
 constexpr uint64_t kSpinLimit = 1ull << 24;
-constexpr int kRunSteps = 4096;           // steps per cooperative launch (partials buffer)
+constexpr int kRunSteps = 16384;          // steps per cooperative launch (partials buffer)
 #ifndef BS_POLL_SLEEP
 #define BS_POLL_SLEEP 1  // s_sleep units (64 clocks) between polls of a count word
 #endif
@@ -119,12 +119,12 @@ struct LifModel {
     return bs_lif_update(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
   }
   // Whether the neuron may spike this step: a zero-input forward-Euler estimate of the next
-  // V within 20 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
+  // V within 15 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
   // estimate never decides a spike.
   __device__ static bool near(const Params& p, const Regs& r) {
     const float I = p.I_ext + r.ge * p.decay_e * (p.E_e - r.V) + r.gi * p.decay_i * (p.E_i - r.V);
     const float vp = r.V + p.dt * p.inv_tau * ((p.V_rest - r.V) + p.R * I);
-    return r.ref <= 0 && vp >= p.V_th - 0.2f * (p.V_th - p.V_reset);
+    return r.ref <= 0 && vp >= p.V_th - 0.15f * (p.V_th - p.V_reset);
   }
 };
 

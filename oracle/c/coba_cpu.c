@@ -84,6 +84,9 @@ int bso_max_threads(void) {
 /* Runs `steps` steps.  in_e/in_i [n] hold the pending inputs (from the spikes before the
  * first step) and are left holding the inputs for the step after the last one.
  * counts/hashes [steps] are written (nullable).  Returns the total number of spikes. */
+/* Cloned for CPUs with and without FMA3 (chosen when the library loads): fmaf is one
+ * correctly rounded operation either way, in hardware or in the C library. */
+__attribute__((target_clones("fma", "default")))
 long long bso_coba_lif_run(int n, int n_exc, int k_e, int k_i, const int32_t* idx_e,
                            const float* w_e, float w_e_homo, const int32_t* idx_i,
                            const float* w_i, float w_i_homo, const bso_lif_params* pp,

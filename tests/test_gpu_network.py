@@ -77,14 +77,14 @@ def test_coba_lif_state_matches_oracle_midway(torch_cuda):
 
 
 def test_coba_lif_long_run_across_launches(torch_cuda):
-    """5000 steps: more than one cooperative launch (4096 steps each).  Per-step counts and
-    spike hashes and the final state equal the C restatement's; the raster of one 5000-step
-    call equals that of a 1000 + 4000 split on a second runner."""
+    """17000 steps: more than one cooperative launch (16384 steps each).  Per-step counts and
+    spike hashes and the final state equal the C restatement's; the raster of one
+    17000-step call equals that of a 1000 + 16000 split on a second runner."""
     from oracle import cbuild
     torch = torch_cuda
-    say('coba lif 4000 long run', 5000)
+    say('coba lif 4000 long run', 17000)
     pe, pi, V0, p = make_golden.config1_net()
-    n, T = V0.size, 5000
+    n, T = V0.size, 17000
     st = dict(V=V0.copy(), ge=np.zeros(n, F), gi=np.zeros(n, F), ref=np.zeros(n, np.int32),
               spk=np.zeros(n, np.uint8), in_e=np.zeros(n, F), in_i=np.zeros(n, F))
     c_ref = np.zeros(T, np.int32)
@@ -99,7 +99,7 @@ def test_coba_lif_long_run_across_launches(torch_cuda):
     hashes = torch.zeros(T, dtype=torch.int32, device='cuda')
     r1.run(T, counts=counts, hashes=hashes, raster=ras1)
     r2.run(1000, raster=ras2[:1000])
-    r2.run(4000, raster=ras2[1000:])
+    r2.run(16000, raster=ras2[1000:])
     r1.check()
     r2.check()
     assert counts.cpu().numpy().tolist() == c_ref.tolist()
