@@ -1,74 +1,127 @@
 // N2c: batched event x dense weight (EventLinear).
 //
-// One wave per (batch row b, tile of 64*V output columns).  The wave reads 64 spikes of row b
-// per step (one byte or float per lane) and ballots them into a mask; the active inputs of
-// the mask are then streamed kBatch at a time: kBatch coalesced row segments of W (128-bit
-// loads when V = 4) are in flight before the first add.  Each lane adds its V columns in
+// One wave per (batch row b, tile of 64*V output columns).  Each lane turns 64 consecutive
+// spikes of row b into a 64-bit mask (coalesced 16-byte loads); the wave walks the masks in
+// order and streams the active inputs kBatch at a time across mask boundaries: kBatch
+// coalesced row segments of W (128-bit loads when V = 4) are in flight before the first add,
+// so a 5 %-dense row costs about (active inputs / kBatch) memory round trips, not one per 64
+// inputs.  Each lane adds its V columns in
 // ascending input order, the order of a sequential reference loop, so results are
 // bit-reproducible.
+//
+// XCD-aware placement: a row segment of W is needed by every batch row whose spike selects
+// it, and those waves all read the tile's segments in ascending input order.  Waves are
+// therefore numbered tile-major (all batch rows of a tile consecutive) and consecutive
+// logical workgroups are placed on the same XCD (workgroups are dispatched to the 8 XCDs
+// round-robin), so the batch rows of a tile share that XCD's L2 and each segment is fetched
+// from memory about once per step instead of once per batch row that uses it.
 #include "common.h"
 
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kBatch = 8;
+constexpr int kBatch = 16;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
-__device__ __forceinline__ float spk_val(const uint8_t* p, int64_t i) { return (float)p[i]; }
-__device__ __forceinline__ float spk_val(const float* p, int64_t i) { return p[i]; }
+
+// Spike byte/float -> event flag (any nonzero value is an event).
+__device__ __forceinline__ bool nz(uint8_t x) { return x != 0; }
+__device__ __forceinline__ bool nz(float x) { return x != 0.0f; }
+
+// Mask of the 64 inputs [i0, i0 + 64) of one spike row, built by one lane from coalesced
+// 16-byte loads (bit k = input i0 + k; inputs at or past n_in are 0).
+template <typename T>
+__device__ __forceinline__ uint64_t lane_mask(const T* row, int32_t i0, int32_t n_in) {
+  uint64_t m = 0;
+  if (i0 + 64 <= n_in && (((uintptr_t)(row + i0)) & 15) == 0) {
+    constexpr int kPer = 16 / sizeof(T);  // inputs per 16-byte load
+#pragma unroll
+    for (int c = 0; c < 64; c += kPer) {
+      const uint4 q = *(const uint4*)(row + i0 + c);
+      const T* e = (const T*)&q;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) m |= (uint64_t)nz(e[k]) << (c + k);
+    }
+  } else {
+    for (int k = 0; k < 64 && i0 + k < n_in; ++k) m |= (uint64_t)nz(row[i0 + k]) << k;
+  }
+  return m;
+}
+
+// 64-bit value of lane l (l wave-uniform).
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 template <typename T, int V, bool kEvent>
 __global__ __launch_bounds__(kBlock) void k_event_dense(const T* __restrict__ spk, int32_t batch,
                                                         int32_t n_in, const float* __restrict__ W,
                                                         int32_t n_out, float* __restrict__ out) {
   const int lane = bs_lane();
-  const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE;
+  const int32_t per_xcd = gridDim.x / kXcds;  // the grid is a multiple of kXcds
+  const int64_t lwg = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  const int64_t wave = (lwg * kBlock + threadIdx.x) / BS_WAVE;  // tile-major wave number
   const int32_t tiles = (n_out + BS_WAVE * V - 1) / (BS_WAVE * V);
   if (wave >= (int64_t)batch * tiles) return;
-  const int32_t b = (int32_t)(wave / tiles);
-  const int32_t t = (int32_t)(wave - (int64_t)b * tiles);
+  const int32_t t = (int32_t)(wave / batch);
+  const int32_t b = (int32_t)(wave - (int64_t)t * batch);
   const int32_t j0 = t * BS_WAVE * V + lane * V;
   const bool live = j0 < n_out;
   const T* srow = spk + (int64_t)b * n_in;
   float acc[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) acc[v] = 0.0f;
-  for (int32_t i0 = 0; i0 < n_in; i0 += BS_WAVE) {
-    const int32_t i = i0 + lane;
-    const float sv = i < n_in ? spk_val(srow, i) : 0.0f;
-    uint64_t m = bs_ballot(sv != 0.0f);
-    while (m) {
+  // Inputs in spans of 64 groups of 64: lane l holds the mask of group l of the span; the
+  // wave walks the groups in order (readlane, no memory access) and fills kBatch row slots
+  // across group boundaries before issuing their loads.
+  for (int32_t s0 = 0; s0 < n_in; s0 += BS_WAVE * BS_WAVE) {
+    const uint64_t mine = lane_mask(srow, s0 + lane * BS_WAVE, n_in);
+    const int ng = (n_in - s0 + BS_WAVE - 1) / BS_WAVE < BS_WAVE
+                       ? (n_in - s0 + BS_WAVE - 1) / BS_WAVE : BS_WAVE;
+    int g = 0;
+    uint64_t m = readlane64(mine, 0);
+    for (;;) {
       int32_t r[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        while (m == 0 && g + 1 < ng) m = readlane64(mine, ++g);
+        r[u] = -1;
+        if (m) {
+          r[u] = s0 + g * BS_WAVE + (int32_t)__builtin_ctzll(m);
+          m &= m - 1;
+        }
+      }
+      if (r[0] < 0) break;
+      float x[kBatch][V];
       float sc[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        r[u] = -1;
         sc[u] = 1.0f;
-        if (m) {
-          const int bit = __builtin_ctzll(m);
-          m &= m - 1;
-          r[u] = i0 + bit;
-          if (!kEvent) sc[u] = __shfl(sv, bit);
-        }
-      }
-      float x[kBatch][V];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        if (r[u] >= 0 && live) {
-          const float* wr = W + (int64_t)r[u] * n_out + j0;
-          if (V == 4) {
-            const float4 q = *(const float4*)wr;
-            x[u][0] = q.x;
-            x[u][V > 1 ? 1 : 0] = q.y;
-            x[u][V > 2 ? 2 : 0] = q.z;
-            x[u][V > 3 ? 3 : 0] = q.w;
-          } else {
-            x[u][0] = *wr;
+        if (r[u] >= 0) {
+          if (!kEvent) sc[u] = (float)srow[r[u]];
+          if (live) {
+            const float* wr = W + (int64_t)r[u] * n_out + j0;
+            if (V == 4) {
+              const float4 q = *(const float4*)wr;
+              x[u][0] = q.x;
+              x[u][V > 1 ? 1 : 0] = q.y;
+              x[u][V > 2 ? 2 : 0] = q.z;
+              x[u][V > 3 ? 3 : 0] = q.w;
+            } else if (V == 2) {
+              const float2 q = *(const float2*)wr;
+              x[u][0] = q.x;
+              x[u][V > 1 ? 1 : 0] = q.y;
+            } else {
+              x[u][0] = *wr;
+            }
           }
         }
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        if (r[u] >= 0) {
+        if (r[u] >= 0 && live) {
 #pragma unroll
           for (int v = 0; v < V; ++v) acc[v] += kEvent ? x[u][v] : sc[u] * x[u][v];
         }
@@ -79,29 +132,41 @@ __global__ __launch_bounds__(kBlock) void k_event_dense(const T* __restrict__ sp
     float* o = out + (int64_t)b * n_out + j0;
     if (V == 4) {
       *(float4*)o = make_float4(acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0], acc[V > 3 ? 3 : 0]);
+    } else if (V == 2) {
+      *(float2*)o = make_float2(acc[0], acc[V > 1 ? 1 : 0]);
     } else {
       o[0] = acc[0];
     }
   }
 }
 
+template <typename T, int V>
+int launch_v(const T* spk, int32_t batch, int32_t n_in, const float* W, int32_t n_out, bool ev,
+             float* out, hipStream_t s) {
+  const int64_t tiles = (n_out + BS_WAVE * V - 1) / (BS_WAVE * V);
+  const int64_t waves = (int64_t)batch * tiles;
+  int64_t g = (waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE);
+  g = (g + kXcds - 1) / kXcds * kXcds;
+  if (ev) k_event_dense<T, V, true><<<(int)g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
+  else k_event_dense<T, V, false><<<(int)g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+// Columns per lane: as many as alignment allows while the launch still has about 16 waves per
+// CU (4 per SIMD) to overlap the latency of the row loads.
 template <typename T>
 int launch(const T* spk, int32_t batch, int32_t n_in, const float* W, int32_t n_out, bool ev,
            float* out, hipStream_t s) {
-  const bool vec = (n_out % 4 == 0) && (((uintptr_t)W & 15) == 0) && (((uintptr_t)out & 15) == 0);
-  const int V = vec ? 4 : 1;
-  const int64_t tiles = (n_out + BS_WAVE * V - 1) / (BS_WAVE * V);
-  const int64_t waves = (int64_t)batch * tiles;
-  const int g = (int)((waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE));
-  if (vec) {
-    if (ev) k_event_dense<T, 4, true><<<g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
-    else k_event_dense<T, 4, false><<<g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
-  } else {
-    if (ev) k_event_dense<T, 1, true><<<g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
-    else k_event_dense<T, 1, false><<<g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
-  }
-  BS_CHECK_LAUNCH();
-  return BS_OK;
+  const auto al = [&](int v) {
+    return n_out % v == 0 && ((uintptr_t)W & (4 * v - 1)) == 0 &&
+           ((uintptr_t)out & (4 * v - 1)) == 0;
+  };
+  const int64_t want = (int64_t)4 * bs_num_cus();
+  const auto waves = [&](int v) { return (int64_t)batch * ((n_out + BS_WAVE * v - 1) / (BS_WAVE * v)); };
+  if (al(4) && waves(4) >= want) return launch_v<T, 4>(spk, batch, n_in, W, n_out, ev, out, s);
+  if (al(2) && waves(2) >= want) return launch_v<T, 2>(spk, batch, n_in, W, n_out, ev, out, s);
+  return launch_v<T, 1>(spk, batch, n_in, W, n_out, ev, out, s);
 }
 
 }  // namespace
