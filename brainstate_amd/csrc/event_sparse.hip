@@ -6,10 +6,11 @@
 // atomic add.  The number of active rows is read on the device, so the launch needs
 // no host synchronisation.
 //
-// Gather (post-major, SELL-64): one wave per slice of 64 posts, lane = post.  Each column
-// step loads 64 consecutive pre indices (256 B), tests the spike of each and adds the
-// weight in column order, so every post accumulates its incoming synapses in ascending
-// (pre, k) order -- bit-identical to a sequential pre-major scatter, with no atomics.
+// Gather (post-major, SELL-64x4): one wave per slice of 64 posts, lane = post.  Each step
+// loads the lane's next 4 columns of pre indices as one 16-byte word (1 KB per wave), tests
+// the spike of each and adds the weight in column order, so every post accumulates its
+// incoming synapses in ascending (pre, k) order -- bit-identical to a sequential pre-major
+// scatter, with no atomics.
 #include "common.h"
 
 namespace {
@@ -85,8 +86,9 @@ __global__ __launch_bounds__(kBlock) void k_pack(const T* __restrict__ spk, int3
   }
 }
 
-// Gather over SELL-64: wave = slice of 64 posts, lane = post; kU columns of pre indices in
-// flight per lane; the spike test reads a bitmap held in LDS (kLds) or global memory.
+// Gather over SELL-64x4: wave = slice of 64 posts, lane = post; kU 16-byte groups of 4 pre
+// indices in flight per lane; the spike test reads a bitmap held in LDS (kLds) or global
+// memory.
 template <bool kHet, bool kLds>
 __global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ bits,
                                                    int32_t n_pre,
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ 
                                                    const float* __restrict__ sell_w,
                                                    float w_homo, int32_t n_post,
                                                    float* __restrict__ out) {
-  constexpr int kU = 16;
+  constexpr int kU = 8;
   extern __shared__ uint32_t s_bits[];
   const int32_t nwords = (n_pre + 31) / 32;
   if (kLds) {
@@ -108,30 +110,41 @@ __global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ 
   const int64_t n_slices = ((int64_t)n_post + BS_WAVE - 1) / BS_WAVE;
   if (slice >= n_slices) return;
   const int64_t beg = slice_ptr[slice];
-  const int64_t ncol = (slice_ptr[slice + 1] - beg) / BS_WAVE;
-  const int32_t* pre = sell_pre + beg + lane;
-  const float* wp = kHet ? sell_w + beg + lane : nullptr;
+  const int64_t ngrp = (slice_ptr[slice + 1] - beg) / (4 * BS_WAVE);  // groups of 4 columns
+  const int4* pre4 = (const int4*)(sell_pre + beg) + lane;
   float acc = 0.0f;
-  int64_t c = 0;
-  for (; c + kU <= ncol; c += kU) {
-    int32_t i[kU];
+  const auto on = [&](int32_t i) {
+    return (uint32_t)i < (uint32_t)n_pre && ((bm[i >> 5] >> (i & 31)) & 1u);
+  };
+  const float4* w4 = kHet ? (const float4*)(sell_w + beg) + lane : nullptr;
+  int64_t g = 0;
+  for (; g + kU <= ngrp; g += kU) {  // kU 16-byte groups of indices in flight per lane
+    int4 q[kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) i[u] = pre[(c + u) * BS_WAVE];
-    bool a[kU];
+    for (int u = 0; u < kU; ++u) q[u] = pre4[(g + u) * BS_WAVE];
+    uint32_t act[kU];  // bit e: column 4(g+u)+e is an active synapse
+    float4 wq[kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
-      a[u] = (uint32_t)i[u] < (uint32_t)n_pre && ((bm[i[u] >> 5] >> (i[u] & 31)) & 1u);
-    float w[kU];
+    for (int u = 0; u < kU; ++u) {
+      act[u] = (uint32_t)on(q[u].x) | ((uint32_t)on(q[u].y) << 1) | ((uint32_t)on(q[u].z) << 2) |
+               ((uint32_t)on(q[u].w) << 3);
+      wq[u] = make_float4(w_homo, w_homo, w_homo, w_homo);
+      if (kHet && act[u]) wq[u] = w4[(g + u) * BS_WAVE];  // this lane's 4 weights, one load
+    }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) w[u] = (kHet && a[u]) ? wp[(c + u) * BS_WAVE] : w_homo;
-#pragma unroll
-    for (int u = 0; u < kU; ++u)
-      if (a[u]) acc += w[u];
+    for (int u = 0; u < kU; ++u) {
+      if (act[u] & 1u) acc += wq[u].x;
+      if (act[u] & 2u) acc += wq[u].y;
+      if (act[u] & 4u) acc += wq[u].z;
+      if (act[u] & 8u) acc += wq[u].w;
+    }
   }
-  for (; c < ncol; ++c) {
-    const int32_t i = pre[c * BS_WAVE];
-    if ((uint32_t)i < (uint32_t)n_pre && ((bm[i >> 5] >> (i & 31)) & 1u))
-      acc += kHet ? wp[c * BS_WAVE] : w_homo;
+  for (; g < ngrp; ++g) {
+    const int4 q = pre4[g * BS_WAVE];
+    const int32_t iv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (on(iv[e])) acc += kHet ? sell_w[beg + (g * BS_WAVE + lane) * 4 + e] : w_homo;
   }
   const int64_t j = slice * BS_WAVE + lane;
   if (j < n_post) out[j] = acc;
@@ -311,6 +324,8 @@ extern "C" int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
   if (n_post == 0) return BS_OK;
   BS_CHECK_ARG(slice_ptr && sell_pre && out && (spk_bits || n_pre == 0),
                "bs_event_gather_f32: NULL pointer");
+  BS_CHECK_ARG(((uintptr_t)sell_pre & 15) == 0 && ((uintptr_t)sell_w & 15) == 0,
+               "bs_event_gather_f32: sell_pre / sell_w must be 16-byte aligned");
   hipStream_t s = bs_stream(stream);
   const int64_t n_slices = ((int64_t)n_post + BS_WAVE - 1) / BS_WAVE;
   const int g = (int)((n_slices + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE));

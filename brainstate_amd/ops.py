@@ -121,10 +121,12 @@ def event_gather(spk, sell, out=None, bits=None):
 
 
 def build_sell(indptr, indices, n_pre, n_post, w=None, w_homo=0.0, device='cuda'):
-    """Host-side SELL-64 post-major layout from a pre-major CSR (numpy arrays).
+    """Host-side SELL-64x4 post-major layout from a pre-major CSR (numpy arrays).
 
     Incoming synapses of each post are kept in ascending (pre, k) order (a stable sort on
-    the target index), so the gather reproduces a sequential pre-major scatter.
+    the target index), so the gather reproduces a sequential pre-major scatter.  Column c of
+    lane l in slice s sits at ``slice_ptr[s] + (c // 4) * 256 + l * 4 + c % 4``: a lane's four
+    consecutive columns form one 16-byte word (layout contract of ``bs_event_gather_f32``).
     """
     indptr = np.asarray(indptr, dtype=np.int64)
     indices = np.asarray(indices, dtype=np.int64)
@@ -138,7 +140,7 @@ def build_sell(indptr, indices, n_pre, n_post, w=None, w_homo=0.0, device='cuda'
     n_slices = (n_post + 63) // 64
     pad_counts = np.zeros(n_slices * 64, np.int64)
     pad_counts[:n_post] = counts
-    width = pad_counts.reshape(n_slices, 64).max(axis=1)
+    width = (pad_counts.reshape(n_slices, 64).max(axis=1) + 3) // 4 * 4
     slice_ptr = np.zeros(n_slices + 1, np.int64)
     np.cumsum(width * 64, out=slice_ptr[1:])
     total = int(slice_ptr[-1])
@@ -150,7 +152,7 @@ def build_sell(indptr, indices, n_pre, n_post, w=None, w_homo=0.0, device='cuda'
     rank = np.arange(nnz, dtype=np.int64) - post_start[tgt_sorted]
     s = tgt_sorted // 64
     lane = tgt_sorted - s * 64
-    pos = slice_ptr[s] + rank * 64 + lane
+    pos = slice_ptr[s] + (rank // 4) * 256 + lane * 4 + rank % 4
     sell_pre[pos] = pre[order]
     if w is not None:
         sell_w[pos] = np.asarray(w, np.float32).reshape(-1)[order]

@@ -80,11 +80,13 @@ BS_API int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n_pre
 
 /* ---------------------------------------------------------------- N2b event gather
  * Same operator as N2a, post-major and deterministic (no atomics).  Spikes come as a
- * bitmap (bs_spike_pack: bit i%32 of word i/32 set <=> spk[i] != 0).  Layout SELL-64:
- * posts are grouped in slices of 64; slice s stores its incoming synapses column-major at
- * sell_pre[slice_ptr[s] + c*64 + lane] (lane = post - 64*s), columns in ascending
- * (pre, k) order, padded with -1.  out[j] = 0.0f + the weights of active synapses in that
- * order, i.e. bit-identical to a sequential pre-major scatter.
+ * bitmap (bs_spike_pack: bit i%32 of word i/32 set <=> spk[i] != 0).  Layout SELL-64x4:
+ * posts are grouped in slices of 64; slice s holds ncol(s) columns (a multiple of 4) of
+ * incoming synapses, column c of post lane (= post - 64*s) at
+ * sell_pre[slice_ptr[s] + (c/4)*256 + lane*4 + c%4] (each lane's 4 consecutive columns are
+ * one 16-byte word), columns in ascending (pre, k) order, padded with -1; slice_ptr[s] is a
+ * multiple of 256 and sell_pre / sell_w are 16-byte aligned.  out[j] = 0.0f + the weights
+ * of active synapses in that order, i.e. bit-identical to a sequential pre-major scatter.
  * sell_w == NULL -> homogeneous w_homo.  n_slices = ceil(n_post / 64). */
 BS_API int bs_spike_pack(const void* spk, int32_t spk_dtype, int32_t n, uint32_t* bits,
                          bs_stream_t stream);
