@@ -54,6 +54,12 @@ SIGNATURES = {
                                             c_i32, c_vp, c_i32, c_vp]),
     'bs_event_matvec_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,
                                            c_i32, c_vp, c_i32, c_vp]),
+    'bs_value_matvec_f32': (ctypes.c_int, [c_vp, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32, c_i32,
+                                           c_vp, c_i32, c_vp]),
+    'bs_event_matvec_vjp_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp,
+                                               c_f32, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    'bs_event_dense_vjp_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_vp,
+                                              c_vp, c_vp, c_vp]),
     'bs_spike_pack': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     'bs_event_gather_f32': (ctypes.c_int, [c_vp, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp,
                                            c_vp]),
@@ -117,10 +123,18 @@ def require_gpu():
 
 
 def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
+    """Device pointer of a tensor (None -> NULL).  Tensors wrapped by torch.func transforms
+    (the tangents handed to a custom Function's jvp rule) are unwrapped to the tensor that
+    holds the storage; the kernels only read such operands."""
     if t is None:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    try:
+        return ctypes.c_void_p(t.data_ptr())
+    except RuntimeError:
+        from torch._C import _functorch as ft
+        while ft.is_functorch_wrapped_tensor(t):
+            t = ft.get_unwrapped(t)
+        return ctypes.c_void_p(t.data_ptr())
 
 
 def stream_handle(device=None):

@@ -15,6 +15,7 @@
 // logical workgroups are placed on the same XCD (workgroups are dispatched to the 8 XCDs
 // round-robin), so the batch rows of a tile share that XCD's L2 and each segment is fetched
 // from memory about once per step instead of once per batch row that uses it.
+#include "bs_math.h"
 #include "common.h"
 
 namespace {
@@ -169,6 +170,113 @@ int launch(const T* spk, int32_t batch, int32_t n_in, const float* W, int32_t n_
   return launch_v<T, 1>(spk, batch, n_in, W, n_out, ev, out, s);
 }
 
+// ---- reverse mode: y[b] = sum_i x[b,i] * W[i] (x = spike value, 1 for byte spikes) ----
+
+// grad_x[b,i] = sum_j g[b,j] * W[i,j]: one wave per (input row i, kGb batch rows); lanes
+// stride the columns (16-byte loads of W and g), then each of the kGb sums is reduced across
+// the wave.
+constexpr int kGb = 8;
+template <int V>
+__global__ __launch_bounds__(kBlock) void k_dense_gx(int32_t batch, int32_t n_in,
+                                                     const float* __restrict__ W, int32_t n_out,
+                                                     const float* __restrict__ g,
+                                                     float* __restrict__ gx) {
+  const int lane = bs_lane();
+  const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE;
+  const int32_t bgroups = (batch + kGb - 1) / kGb;
+  if (wave >= (int64_t)n_in * bgroups) return;
+  const int32_t i = (int32_t)(wave / bgroups);
+  const int32_t b0 = (int32_t)(wave - (int64_t)i * bgroups) * kGb;
+  float acc[kGb];
+#pragma unroll
+  for (int u = 0; u < kGb; ++u) acc[u] = 0.0f;
+  const float* wr = W + (int64_t)i * n_out;
+  for (int32_t j = lane * V; j < n_out; j += BS_WAVE * V) {
+    float wv[V];
+    if (V == 4) {
+      const float4 q = *(const float4*)(wr + j);
+      wv[0] = q.x;
+      wv[V > 1 ? 1 : 0] = q.y;
+      wv[V > 2 ? 2 : 0] = q.z;
+      wv[V > 3 ? 3 : 0] = q.w;
+    } else {
+      wv[0] = wr[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kGb; ++u) {
+      if (b0 + u < batch) {
+        const float* gr = g + (int64_t)(b0 + u) * n_out + j;
+        if (V == 4) {
+          const float4 q = *(const float4*)gr;
+          acc[u] = bs_fma(q.x, wv[0], acc[u]);
+          acc[u] = bs_fma(q.y, wv[V > 1 ? 1 : 0], acc[u]);
+          acc[u] = bs_fma(q.z, wv[V > 2 ? 2 : 0], acc[u]);
+          acc[u] = bs_fma(q.w, wv[V > 3 ? 3 : 0], acc[u]);
+        } else {
+          acc[u] = bs_fma(gr[0], wv[0], acc[u]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kGb; ++u) {
+#pragma unroll
+    for (int o = BS_WAVE / 2; o > 0; o >>= 1) acc[u] += __shfl_xor(acc[u], o);
+  }
+  if (lane < kGb && b0 + lane < batch) {
+    float v = acc[0];
+#pragma unroll
+    for (int u = 1; u < kGb; ++u) v = lane == u ? acc[u] : v;
+    gx[(int64_t)(b0 + lane) * n_in + i] = v;
+  }
+}
+
+// grad_W[i,j] = sum_b x[b,i] * g[b,j]: one wave per (input row i, 64*V columns); the wave
+// ballots the batch rows whose spike i is nonzero (64 at a time) and adds their g rows in
+// ascending b.  Every element of grad_W is written (rows no spike selects get 0).
+template <typename T, int V>
+__global__ __launch_bounds__(kBlock) void k_dense_gw(const T* __restrict__ spk, int32_t batch,
+                                                     int32_t n_in, int32_t n_out,
+                                                     const float* __restrict__ g,
+                                                     float* __restrict__ gw) {
+  const int lane = bs_lane();
+  const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE;
+  const int32_t tiles = (n_out + BS_WAVE * V - 1) / (BS_WAVE * V);
+  if (wave >= (int64_t)n_in * tiles) return;
+  const int32_t i = (int32_t)(wave / tiles);
+  const int32_t j0 = (int32_t)(wave - (int64_t)i * tiles) * BS_WAVE * V + lane * V;
+  const bool live = j0 < n_out;
+  float acc[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
+  for (int32_t bb = 0; bb < batch; bb += BS_WAVE) {
+    const float xv = bb + lane < batch ? (float)spk[(int64_t)(bb + lane) * n_in + i] : 0.0f;
+    uint64_t m = bs_ballot(xv != 0.0f);
+    while (m) {
+      const int bit = __builtin_ctzll(m);
+      m &= m - 1;
+      const float xb = __shfl(xv, bit);
+      if (live) {
+        const float* gr = g + (int64_t)(bb + bit) * n_out + j0;
+        if (V == 4) {
+          const float4 q = *(const float4*)gr;
+          acc[0] = bs_fma(xb, q.x, acc[0]);
+          acc[V > 1 ? 1 : 0] = bs_fma(xb, q.y, acc[V > 1 ? 1 : 0]);
+          acc[V > 2 ? 2 : 0] = bs_fma(xb, q.z, acc[V > 2 ? 2 : 0]);
+          acc[V > 3 ? 3 : 0] = bs_fma(xb, q.w, acc[V > 3 ? 3 : 0]);
+        } else {
+          acc[0] = bs_fma(xb, gr[0], acc[0]);
+        }
+      }
+    }
+  }
+  if (live) {
+    float* o = gw + (int64_t)i * n_out + j0;
+    if (V == 4) *(float4*)o = make_float4(acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0], acc[V > 3 ? 3 : 0]);
+    else o[0] = acc[0];
+  }
+}
+
 }  // namespace
 
 int bs_fill_f32(float* p, int64_t n, float v, hipStream_t s);
@@ -188,4 +296,49 @@ extern "C" int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t ba
   if (spk_dtype == BS_SPK_U8)
     return launch((const uint8_t*)spk, batch, n_in, W, n_out, float_as_event != 0, out, s);
   return launch((const float*)spk, batch, n_in, W, n_out, float_as_event != 0, out, s);
+}
+
+extern "C" int bs_event_dense_vjp_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                      int32_t n_in, const float* W, int32_t n_out,
+                                      const float* grad_out, float* grad_spk, float* grad_W,
+                                      bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(batch >= 0 && n_in >= 0 && n_out >= 0, "bs_event_dense_vjp_f32: negative size");
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_event_dense_vjp_f32: unknown spike dtype %d", spk_dtype);
+  hipStream_t s = bs_stream(stream);
+  if (n_in == 0) return BS_OK;
+  if (n_out == 0 || batch == 0) {  // empty sums
+    if (grad_spk) {
+      int rc = bs_fill_f32(grad_spk, (int64_t)batch * n_in, 0.0f, s);
+      if (rc) return rc;
+    }
+    if (grad_W) return bs_fill_f32(grad_W, (int64_t)n_in * n_out, 0.0f, s);
+    return BS_OK;
+  }
+  BS_CHECK_ARG(grad_out != nullptr, "bs_event_dense_vjp_f32: grad_out is NULL");
+  const auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const bool vec = n_out % 4 == 0 && al(grad_out);
+  if (grad_spk) {
+    BS_CHECK_ARG(W != nullptr, "bs_event_dense_vjp_f32: W is NULL");
+    const int64_t waves = (int64_t)n_in * ((batch + kGb - 1) / kGb);
+    const int g = (int)((waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE));
+    if (vec && al(W)) k_dense_gx<4><<<g, kBlock, 0, s>>>(batch, n_in, W, n_out, grad_out, grad_spk);
+    else k_dense_gx<1><<<g, kBlock, 0, s>>>(batch, n_in, W, n_out, grad_out, grad_spk);
+    BS_CHECK_LAUNCH();
+  }
+  if (grad_W) {
+    BS_CHECK_ARG(spk != nullptr, "bs_event_dense_vjp_f32: spk is NULL");
+    const bool v4 = vec && al(grad_W);
+    const int V = v4 ? 4 : 1;
+    const int64_t waves = (int64_t)n_in * ((n_out + BS_WAVE * V - 1) / (BS_WAVE * V));
+    const int g = (int)((waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE));
+#define BS_GW(T, VV) \
+  k_dense_gw<T, VV><<<g, kBlock, 0, s>>>((const T*)spk, batch, n_in, n_out, grad_out, grad_W)
+    if (spk_dtype == BS_SPK_U8) { if (v4) BS_GW(uint8_t, 4); else BS_GW(uint8_t, 1); }
+    else { if (v4) BS_GW(float, 4); else BS_GW(float, 1); }
+#undef BS_GW
+    BS_CHECK_LAUNCH();
+  }
+  return BS_OK;
 }

@@ -161,7 +161,8 @@ constexpr int kLdsPosts = 16384;
 constexpr int kLdsRatio = 4;
 constexpr int kRowsCap = 1024;
 
-template <typename T, bool kCsr, bool kHet>
+// kVal: each event is weighted by its spike value (sum_i x[i] * w[i,k]); otherwise by 1.
+template <typename T, bool kCsr, bool kHet, bool kVal = false>
 __global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, int32_t n_pre,
                                                    int32_t rows, const int32_t* __restrict__ indptr,
                                                    const int32_t* __restrict__ indices, int32_t k,
@@ -205,7 +206,8 @@ __global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, in
   __syncthreads();
   // Homogeneous weights always go direct: sums of one repeated value are order-free and exact
   // only as a single chain of +w, which LDS partial sums would break.
-  const bool use_lds = kHet && n_post <= kLdsPosts && (int64_t)s_nev >= (int64_t)kLdsRatio * n_post;
+  const bool use_lds =
+      (kHet || kVal) && n_post <= kLdsPosts && (int64_t)s_nev >= (int64_t)kLdsRatio * n_post;
   if (use_lds) {
     for (int32_t j = threadIdx.x; j < n_post; j += kBlock) s_acc[j] = 0.0f;
     __syncthreads();
@@ -213,6 +215,7 @@ __global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, in
   const int32_t nnz = kCsr ? indptr[n_pre] : 0;
   for (int32_t a = wid; a < count; a += kBlock / BS_WAVE) {  // one wave per active row
     const int32_t row = s_rows[a];
+    const float xv = kVal ? (float)spk[row] : 1.0f;
     int64_t beg, end;
     if (kCsr) {
       beg = indptr[row];
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, in
     }
     for (int64_t s = beg + lane; s < end; s += BS_WAVE) {
       const int32_t j = indices[s];
-      const float v = kHet ? w[s] : w_homo;
+      const float v = kVal ? (kHet ? w[s] : w_homo) * xv : (kHet ? w[s] : w_homo);
       if ((uint32_t)j < (uint32_t)n_post) {
         if (use_lds) atomicAdd(&s_acc[j], v);
         else bs_atomic_add_f32(out + j, v);
@@ -237,6 +240,57 @@ __global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, in
     for (int32_t j = threadIdx.x; j < n_post; j += kBlock) {
       const float v = s_acc[j];
       if (v != 0.0f) bs_atomic_add_f32(out + j, v);
+    }
+  }
+}
+
+// Reverse mode of the event mat-vec y[j] = sum_{i,k: idx[i,k]=j} x[i] * w[i,k] (x = spike
+// value; 1 for byte spikes): one wave per pre row i gathers g[idx[i,k]] over the row and
+//   grad_x[i]   = sum_k w[i,k] * g[idx[i,k]]            (lane partials, then a wave sum)
+//   grad_w[i,k] = x[i] * g[idx[i,k]]                    (per-synapse weights)
+//   grad_w[0]  += x[i] * sum_k g[idx[i,k]]              (homogeneous weight; one atomic/row)
+// Synapses with out-of-range targets contribute nothing, as in the forward pass.
+template <typename T, bool kCsr, bool kHet>
+__global__ __launch_bounds__(kBlock) void k_matvec_vjp(const T* __restrict__ spk, int32_t n_pre,
+                                                       const int32_t* __restrict__ indptr,
+                                                       const int32_t* __restrict__ indices,
+                                                       int32_t k, const float* __restrict__ w,
+                                                       float w_homo, int32_t n_post,
+                                                       const float* __restrict__ g,
+                                                       float* __restrict__ gx,
+                                                       float* __restrict__ gw) {
+  const int lane = bs_lane();
+  const int64_t nw = (int64_t)gridDim.x * (kBlock / BS_WAVE);
+  const int32_t nnz = kCsr ? indptr[n_pre] : 0;
+  for (int64_t row = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE; row < n_pre;
+       row += nw) {
+    int64_t beg, end;
+    if (kCsr) {
+      beg = indptr[row];
+      end = indptr[row + 1];
+      beg = beg < 0 ? 0 : beg;
+      end = end > nnz ? nnz : end;
+    } else {
+      beg = row * k;
+      end = beg + k;
+    }
+    const float xv = (float)spk[row];
+    float sx = 0.0f, sg = 0.0f;
+    for (int64_t s = beg + lane; s < end; s += BS_WAVE) {
+      const int32_t j = indices[s];
+      const float gj = (uint32_t)j < (uint32_t)n_post ? g[j] : 0.0f;
+      if (gx) sx += (kHet ? w[s] : w_homo) * gj;
+      if (kHet && gw) gw[s] = xv * gj;
+      sg += gj;
+    }
+#pragma unroll
+    for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+      sx += __shfl_xor(sx, o);
+      sg += __shfl_xor(sg, o);
+    }
+    if (lane == 0) {
+      if (gx) gx[row] = sx;
+      if (!kHet && gw && xv != 0.0f) bs_atomic_add_f32(gw, xv * sg);
     }
   }
 }
@@ -349,23 +403,25 @@ extern "C" int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
   return BS_OK;
 }
 
-extern "C" int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
-                                   const int32_t* indptr, const int32_t* indices, int32_t k,
-                                   const float* w, float w_homo, int32_t n_post, float* out,
-                                   int32_t accumulate, bs_stream_t stream) {
-  bs_clear_error();
-  BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "bs_event_matvec_f32: negative size");
-  BS_CHECK_ARG(indptr != nullptr || k >= 0, "bs_event_matvec_f32: k=%d < 0", k);
-  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
-               "bs_event_matvec_f32: unknown spike dtype %d", spk_dtype);
-  hipStream_t s = bs_stream(stream);
-  if (n_post > 0) BS_CHECK_ARG(out != nullptr, "bs_event_matvec_f32: out is NULL");
+namespace {
+
+// Shared launcher of the fused mat-vec (event or value-weighted).
+template <bool kVal>
+int matvec_launch(const void* spk, int32_t spk_dtype, int32_t n_pre, const int32_t* indptr,
+                  const int32_t* indices, int32_t k, const float* w, float w_homo,
+                  int32_t n_post, float* out, int32_t accumulate, hipStream_t s,
+                  const char* who) {
+  BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "%s: negative size", who);
+  BS_CHECK_ARG(indptr != nullptr || k >= 0, "%s: k=%d < 0", who, k);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32, "%s: unknown spike dtype %d",
+               who, spk_dtype);
+  if (n_post > 0) BS_CHECK_ARG(out != nullptr, "%s: out is NULL", who);
   if (!accumulate) {
     int rc = bs_fill_f32(out, n_post, 0.0f, s);
     if (rc) return rc;
   }
   if (n_pre == 0 || n_post == 0 || (indptr == nullptr && k == 0)) return BS_OK;
-  BS_CHECK_ARG(spk && indices, "bs_event_matvec_f32: NULL pointer");
+  BS_CHECK_ARG(spk && indices, "%s: NULL pointer", who);
   // rows per workgroup: enough workgroups to fill the chip, at most kRowsCap rows each
   int64_t g = (int64_t)bs_num_cus() * 4;
   int64_t rows = ((int64_t)n_pre + g - 1) / g;
@@ -375,8 +431,8 @@ extern "C" int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n
   const size_t shm = n_post <= kLdsPosts ? (size_t)n_post * sizeof(float) : 0;
   const bool het = w != nullptr, csr = indptr != nullptr;
 #define BS_MV(T, C, H)                                                                   \
-  k_matvec<T, C, H><<<(int)g, kBlock, shm, s>>>((const T*)spk, n_pre, (int32_t)rows, indptr, \
-                                               indices, k, w, w_homo, n_post, out)
+  k_matvec<T, C, H, kVal><<<(int)g, kBlock, shm, s>>>((const T*)spk, n_pre, (int32_t)rows, \
+                                                      indptr, indices, k, w, w_homo, n_post, out)
   if (spk_dtype == BS_SPK_U8) {
     if (csr) { if (het) BS_MV(uint8_t, true, true); else BS_MV(uint8_t, true, false); }
     else { if (het) BS_MV(uint8_t, false, true); else BS_MV(uint8_t, false, false); }
@@ -385,6 +441,68 @@ extern "C" int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n
     else { if (het) BS_MV(float, false, true); else BS_MV(float, false, false); }
   }
 #undef BS_MV
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+}  // namespace
+
+extern "C" int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                                   const int32_t* indptr, const int32_t* indices, int32_t k,
+                                   const float* w, float w_homo, int32_t n_post, float* out,
+                                   int32_t accumulate, bs_stream_t stream) {
+  bs_clear_error();
+  return matvec_launch<false>(spk, spk_dtype, n_pre, indptr, indices, k, w, w_homo, n_post, out,
+                              accumulate, bs_stream(stream), "bs_event_matvec_f32");
+}
+
+extern "C" int bs_value_matvec_f32(const float* x, int32_t n_pre, const int32_t* indptr,
+                                   const int32_t* indices, int32_t k, const float* w,
+                                   float w_homo, int32_t n_post, float* out, int32_t accumulate,
+                                   bs_stream_t stream) {
+  bs_clear_error();
+  return matvec_launch<true>(x, BS_SPK_F32, n_pre, indptr, indices, k, w, w_homo, n_post, out,
+                             accumulate, bs_stream(stream), "bs_value_matvec_f32");
+}
+
+extern "C" int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                                       const int32_t* indptr, const int32_t* indices, int32_t k,
+                                       const float* w, float w_homo, int32_t n_post,
+                                       const float* grad_out, float* grad_spk, float* grad_w,
+                                       bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "bs_event_matvec_vjp_f32: negative size");
+  BS_CHECK_ARG(indptr != nullptr || k >= 0, "bs_event_matvec_vjp_f32: k=%d < 0", k);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_event_matvec_vjp_f32: unknown spike dtype %d", spk_dtype);
+  hipStream_t s = bs_stream(stream);
+  const bool het = w != nullptr, csr = indptr != nullptr;
+  if (grad_w && !het) {  // homogeneous: one scalar, accumulated with atomics below
+    int rc = bs_fill_f32(grad_w, 1, 0.0f, s);
+    if (rc) return rc;
+  }
+  if (n_pre == 0 || (!grad_spk && !grad_w)) return BS_OK;
+  BS_CHECK_ARG(spk && indices && (grad_out || n_post == 0),
+               "bs_event_matvec_vjp_f32: NULL pointer");
+  if (n_post == 0 || (!csr && k == 0)) {  // no synapse: every gradient is zero
+    if (grad_spk) {
+      int rc = bs_fill_f32(grad_spk, n_pre, 0.0f, s);
+      if (rc) return rc;
+    }
+    return BS_OK;
+  }
+  const int g = grid_for(n_pre);
+#define BS_VJP(T, C, H)                                                                   \
+  k_matvec_vjp<T, C, H><<<g, kBlock, 0, s>>>((const T*)spk, n_pre, indptr, indices, k, w, \
+                                             w_homo, n_post, grad_out, grad_spk, grad_w)
+  if (spk_dtype == BS_SPK_U8) {
+    if (csr) { if (het) BS_VJP(uint8_t, true, true); else BS_VJP(uint8_t, true, false); }
+    else { if (het) BS_VJP(uint8_t, false, true); else BS_VJP(uint8_t, false, false); }
+  } else {
+    if (csr) { if (het) BS_VJP(float, true, true); else BS_VJP(float, true, false); }
+    else { if (het) BS_VJP(float, false, true); else BS_VJP(float, false, false); }
+  }
+#undef BS_VJP
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

@@ -8,6 +8,13 @@
   brainevent's kernel.
 * ``EventLinear`` -- brainstate/nn/_event_linear.py:32-102, on ``bs_event_dense_f32``.
 
+Both are differentiable (torch autograd, reverse and forward mode) with the gradients the
+reference tests pin (brainstate/nn/_event_fixedprob_test.py:56-126,
+brainstate/nn/_event_linear_test.py:51-125): those of the value formulation
+``sum_i x[i] * w[i, :]`` / ``x @ W`` with the spike values x, on the HIP reverse-mode kernels
+(``bs_event_matvec_vjp_f32``, ``bs_event_dense_vjp_f32``) and tangents built from
+``bs_value_matvec_f32`` / ``bs_event_dense_f32``.
+
 Tensors live on the GPU; there is no CPU path.
 """
 import numpy as np
@@ -33,6 +40,61 @@ def _to_dev(a, dtype):
     return torch.as_tensor(np.ascontiguousarray(np.asarray(a)), dtype=dtype, device=_device())
 
 
+def _kw(w):
+    """Weight argument for the kernels: a float for one (homogeneous) value, else the tensor."""
+    return float(w.reshape(())) if w.numel() == 1 else w
+
+
+class _EventMatvecFn(torch.autograd.Function):
+    """out = mat-vec of spk with weights w over (indices, indptr): every nonzero spike is one
+    event (value=False) or weighs by its value (value=True).  Differentiable in the spike
+    values and the weights, with the derivatives of the value formulation in both modes."""
+
+    @staticmethod
+    def forward(spk, w, indices, indptr, n_post, value=False):
+        if value:
+            return ops.value_matvec(spk.reshape(-1), indices, _kw(w), n_post, indptr=indptr)
+        return ops.event_matvec(spk, indices, _kw(w), n_post, indptr=indptr)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        spk, w, indices, indptr, n_post, _ = inputs
+        ctx.save_for_backward(spk, w, indices, indptr)
+        ctx.save_for_forward(spk, w, indices, indptr)
+        ctx.n_post = n_post
+
+    @staticmethod
+    def backward(ctx, g):
+        spk, w, indices, indptr = ctx.saved_tensors
+        gs, gw = ops.event_matvec_vjp(spk, indices, _kw(w), ctx.n_post, g, indptr=indptr,
+                                      need_spk=ctx.needs_input_grad[0],
+                                      need_w=ctx.needs_input_grad[1])
+        if gs is not None:
+            gs = gs.reshape(spk.shape).to(spk.dtype)
+        if gw is not None:
+            gw = gw.reshape(w.shape)
+        return gs, gw, None, None, None, None
+
+    @staticmethod
+    def jvp(ctx, dspk, dw, *_):
+        spk, w, indices, indptr = ctx.saved_tensors
+        t = torch.zeros(ctx.n_post, dtype=torch.float32, device=indices.device)
+        if dspk is not None:
+            ops.value_matvec(dspk.reshape(-1), indices, _kw(w), ctx.n_post, indptr=indptr, out=t,
+                             accumulate=True)
+        if dw is not None:
+            ops.value_matvec(spk.reshape(-1).to(torch.float32), indices, _kw(dw), ctx.n_post,
+                             indptr=indptr, out=t, accumulate=True)
+        return t
+
+
+def _wants_grad(*ts):
+    """Route through the autograd Functions whenever autodiff may be recording: grad mode on
+    and a tensor operand (forward-mode dual tensors do not set requires_grad).  Under
+    torch.no_grad the kernels are called directly."""
+    return torch.is_grad_enabled() and any(torch.is_tensor(t) for t in ts)
+
+
 class FixedPostNumConn:
     """Fixed-num (pre-major) connectivity: ``indices [n_pre, K]`` int32, weight scalar or
     ``[n_pre, K]``; the object brainevent.FixedPostNumConn stands for at
@@ -47,12 +109,17 @@ class FixedPostNumConn:
     def with_data(self, w):
         return FixedPostNumConn((w, self.indices), self.shape)
 
-    def matvec_events(self, spk):
+    def matvec_events(self, spk, value=False):
         n_pre, n_post = self.shape
         w = self.data
         if torch.is_tensor(w) and w.numel() > 1:
             w = w.expand(self.indices.shape) if w.shape != self.indices.shape else w
-        return ops.event_matvec(spk, self.indices, w, n_post)
+        if _wants_grad(spk, w):
+            return _EventMatvecFn.apply(spk, w, self.indices, None, n_post, value)
+        wk = _kw(w) if torch.is_tensor(w) else w
+        if value:
+            return ops.value_matvec(spk.reshape(-1), self.indices, wk, n_post)
+        return ops.event_matvec(spk, self.indices, wk, n_post)
 
 
 class CSR:
@@ -66,20 +133,27 @@ class CSR:
     def with_data(self, w):
         return CSR((w, self.indices, self.indptr), self.shape)
 
-    def matvec_events(self, spk):
+    def matvec_events(self, spk, value=False):
         n_pre, n_post = self.shape
         w = self.data
         if torch.is_tensor(w) and w.numel() > 1 and w.shape != self.indices.shape:
             w = w.expand(self.indices.shape)
-        return ops.event_matvec(spk, self.indices, w, n_post, indptr=self.indptr)
+        if _wants_grad(spk, w):
+            return _EventMatvecFn.apply(spk, w, self.indices, self.indptr, n_post, value)
+        wk = _kw(w) if torch.is_tensor(w) else w
+        if value:
+            return ops.value_matvec(spk.reshape(-1), self.indices, wk, n_post, indptr=self.indptr)
+        return ops.event_matvec(spk, self.indices, wk, n_post, indptr=self.indptr)
 
 
 def _weight_for_kernel(w):
-    """Scalar (homogeneous) stays a float; arrays become fp32 device tensors."""
+    """fp32 device tensor of the weight (0-d for one homogeneous value); a tensor that
+    requires grad keeps its autograd graph."""
+    if torch.is_tensor(w):
+        return _to_dev(w, torch.float32)
     if init._is_scalar(w):
-        return float(w)
-    t = _to_dev(w, torch.float32)
-    return float(t.reshape(()).item()) if t.numel() == 1 else t
+        return torch.tensor(float(w), dtype=torch.float32, device=_device())
+    return _to_dev(w, torch.float32)
 
 
 class FixedNumConn(Module):
@@ -142,7 +216,7 @@ class FixedNumConn(Module):
         else:
             self.weight = FakeState(init.param(conn_weight, (), allow_none=False))
 
-    def _matvec(self, x):
+    def _matvec(self, x, value=False):
         if self.conn_num < 1:
             lead = tuple(x.shape[:-1]) if torch.is_tensor(x) else ()
             return torch.zeros(lead + (self.out_size[-1],), dtype=torch.float32,
@@ -152,17 +226,17 @@ class FixedNumConn(Module):
         if x.device.type != 'cuda':
             x = x.to(_device())
         if x.dim() == 1:
-            return conn.matvec_events(x)
+            return conn.matvec_events(x, value)
         flat = x.reshape(-1, x.shape[-1])
-        out = torch.stack([conn.matvec_events(row) for row in flat])
+        out = torch.stack([conn.matvec_events(row, value) for row in flat])
         return out.reshape(tuple(x.shape[:-1]) + (self.out_size[-1],))
 
     def update(self, x):
-        if torch.is_tensor(x) and x.dtype != torch.bool and x.dtype != torch.uint8:
-            raise NotImplementedError(
-                'FixedNumConn on non-event (value) inputs is a value-weighted sparse mat-vec, '
-                'outside the event path; wrap spikes with EventFixedNumConn or pass bool spikes')
-        return self._matvec(x)
+        """``x @ conn`` (:202-209): bool spikes are events; any other dtype is a
+        value-weighted sparse mat-vec (sum_i x[i] * w[i, :])."""
+        value = not (torch.is_tensor(x) and x.dtype in (torch.bool, torch.uint8)) and not (
+            isinstance(x, np.ndarray) and x.dtype == np.bool_)
+        return self._matvec(x, value)
 
 
 class EventFixedNumConn(FixedNumConn):
@@ -174,6 +248,83 @@ class EventFixedNumConn(FixedNumConn):
 
 
 EventFixedProb = EventFixedNumConn
+
+
+class _EventDenseFn(torch.autograd.Function):
+    """out = spk @ W (rows of W selected by the nonzero spikes when float_as_event, else
+    weighted by the spike values); derivatives of spk_values @ W in both modes."""
+
+    @staticmethod
+    def forward(spk, W, float_as_event):
+        return ops.event_dense(spk, W, float_as_event=float_as_event)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        spk, W, fae = inputs
+        ctx.save_for_backward(spk, W)
+        ctx.save_for_forward(spk, W)
+        ctx.fae = fae
+
+    @staticmethod
+    def backward(ctx, g):
+        spk, W = ctx.saved_tensors
+        gs, gw = ops.event_dense_vjp(spk, W, g, need_spk=ctx.needs_input_grad[0],
+                                     need_w=ctx.needs_input_grad[1])
+        if gs is not None:
+            gs = gs.reshape(spk.shape).to(spk.dtype)
+        return gs, gw, None
+
+    @staticmethod
+    def jvp(ctx, dspk, dW, _):
+        spk, W = ctx.saved_tensors
+        t = None
+        if dspk is not None:
+            t = ops.event_dense(dspk.to(torch.float32), W, float_as_event=False)
+        if dW is not None:
+            u = ops.event_dense(spk, dW.contiguous(), float_as_event=ctx.fae)
+            t = u if t is None else t + u
+        return t
+
+
+class _HomoLinearFn(torch.autograd.Function):
+    """EventLinear's homogeneous shortcut (brainstate/nn/_event_linear.py:77-97): every output
+    is (count of nonzero spikes, or their sum) * w.  Derivatives of x @ (ones * w), as the
+    reference pins them (brainstate/nn/_event_linear_test.py:51-125)."""
+
+    @staticmethod
+    def forward(x, w, n_out, float_as_event):
+        red = (x != 0).sum(-1).to(torch.float32) if float_as_event else x.to(torch.float32).sum(-1)
+        return torch.ones(tuple(x.shape[:-1]) + (n_out,), device=x.device) * \
+            (red * w.reshape(()).to(torch.float32)).unsqueeze(-1)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        x, w, n_out, fae = inputs
+        ctx.save_for_backward(x, w)
+        ctx.save_for_forward(x, w)
+        ctx.n_out, ctx.fae = n_out, fae
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        gsum = g.sum(-1)
+        gx = gw = None
+        if ctx.needs_input_grad[0]:
+            gx = (gsum.unsqueeze(-1) * w.reshape(())).expand(x.shape).to(x.dtype)
+        if ctx.needs_input_grad[1]:
+            gw = (gsum * x.to(torch.float32).sum(-1)).sum().reshape(w.shape).to(w.dtype)
+        return gx, gw, None, None
+
+    @staticmethod
+    def jvp(ctx, dx, dw, *_):
+        x, w = ctx.saved_tensors
+        red = (x != 0).sum(-1).to(torch.float32) if ctx.fae else x.to(torch.float32).sum(-1)
+        t = torch.zeros(tuple(x.shape[:-1]), dtype=torch.float32, device=x.device)
+        if dx is not None:
+            t = t + dx.to(torch.float32).sum(-1) * w.reshape(())
+        if dw is not None:
+            t = t + red * dw.reshape(())
+        return t.unsqueeze(-1).expand(tuple(x.shape[:-1]) + (ctx.n_out,)).contiguous()
 
 
 class EventLinear(Module):
@@ -198,15 +349,12 @@ class EventLinear(Module):
         n_w = 1 if init._is_scalar(w) else int(np.prod(w.shape))
         if n_w == 1:
             # homogeneous shortcut, :77-97 (reference-owned arithmetic on the reduction)
-            wv = float(np.asarray(w.cpu() if torch.is_tensor(w) else w).reshape(()))
-            if self.float_as_event:
-                reduced = (x != 0).sum(-1).to(torch.float32)
-            else:
-                reduced = x.to(torch.float32).sum(-1)
-            return torch.ones(tuple(x.shape[:-1]) + (self.out_size[-1],), device=x.device) * \
-                (reduced * np.float32(wv)).unsqueeze(-1)
+            wt = _weight_for_kernel(w).reshape(())
+            return _HomoLinearFn.apply(x, wt, self.out_size[-1], self.float_as_event)
         W = _to_dev(w, torch.float32)
         W = W.expand(self.in_size[-1], self.out_size[-1]).contiguous()
         if x.dtype not in (torch.bool, torch.uint8, torch.float32):
             x = x.to(torch.float32)
+        if _wants_grad(x, W):
+            return _EventDenseFn.apply(x, W, self.float_as_event)
         return ops.event_dense(x, W, float_as_event=self.float_as_event)

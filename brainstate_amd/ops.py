@@ -93,6 +93,73 @@ def event_matvec(spk, indices, w, n_post, k=None, indptr=None, out=None, accumul
     return out
 
 
+def _rows(n_pre, indices, k, indptr):
+    if indptr is None:
+        k = indices.shape[1] if indices.dim() == 2 else int(k)
+        if indices.shape[0] != n_pre:
+            raise ValueError(f'vector of {n_pre} for {indices.shape[0]} pre rows')
+    elif indptr.numel() - 1 != n_pre:
+        raise ValueError(f'vector of {n_pre} for {indptr.numel() - 1} pre rows')
+    return int(k or 0)
+
+
+def value_matvec(x, indices, w, n_post, k=None, indptr=None, out=None, accumulate=False):
+    """Value-weighted sparse mat-vec: out[j] = sum_{i,k: idx[i,k]=j} x[i] * w[i,k] (fp32 x)."""
+    x = x.to(torch.float32).contiguous()
+    dev = indices.device
+    n_pre = x.numel()
+    k = _rows(n_pre, indices, k, indptr)
+    homo = not torch.is_tensor(w) or w.numel() == 1
+    if out is None:
+        out = torch.empty(n_post, dtype=torch.float32, device=dev)
+        accumulate = False
+    N.check(N.lib().bs_value_matvec_f32(
+        N.ptr(x), int(n_pre), N.ptr(indptr), N.ptr(indices.contiguous()), k,
+        None if homo else N.ptr(w.contiguous()), float(w) if homo else 0.0, int(n_post),
+        N.ptr(out), 1 if accumulate else 0, N.stream_handle(dev)), 'bs_value_matvec_f32')
+    return out
+
+
+def event_matvec_vjp(spk, indices, w, n_post, grad_out, k=None, indptr=None, need_spk=True,
+                     need_w=True):
+    """Reverse mode of event_matvec: (grad_spk [n_pre] or None, grad_w or None); grad_w has
+    the shape of the per-synapse weights, or is a 0-d tensor for a homogeneous weight."""
+    spk = _spk_view(spk)
+    dev = indices.device
+    n_pre = spk.numel()
+    k = _rows(n_pre, indices, k, indptr)
+    homo = not torch.is_tensor(w) or w.numel() == 1
+    g = grad_out.to(torch.float32).contiguous()
+    gs = torch.empty(n_pre, dtype=torch.float32, device=dev) if need_spk else None
+    gw = None
+    if need_w:
+        gw = torch.empty((), dtype=torch.float32, device=dev) if homo else \
+            torch.empty(w.shape, dtype=torch.float32, device=dev)
+    N.check(N.lib().bs_event_matvec_vjp_f32(
+        N.ptr(spk), _spk_dtype(spk), int(n_pre), N.ptr(indptr), N.ptr(indices.contiguous()), k,
+        None if homo else N.ptr(w.contiguous()), float(w) if homo else 0.0, int(n_post),
+        N.ptr(g), N.ptr(gs), N.ptr(gw), N.stream_handle(dev)), 'bs_event_matvec_vjp_f32')
+    return gs, gw
+
+
+def event_dense_vjp(spk, W, grad_out, need_spk=True, need_w=True):
+    """Reverse mode of event_dense: (grad_spk [B, n_in] or None, grad_W [n_in, n_out] or None),
+    the gradients of spk_values @ W."""
+    squeeze = spk.dim() == 1
+    s2 = _spk_view(spk.reshape(1, -1) if squeeze else spk)
+    B, n_in = s2.shape
+    n_out = W.shape[1]
+    g = grad_out.reshape(B, n_out).to(torch.float32).contiguous()
+    gs = torch.empty(B, n_in, dtype=torch.float32, device=W.device) if need_spk else None
+    gw = torch.empty(n_in, n_out, dtype=torch.float32, device=W.device) if need_w else None
+    N.check(N.lib().bs_event_dense_vjp_f32(
+        N.ptr(s2), _spk_dtype(s2), B, n_in, N.ptr(W.contiguous()), n_out, N.ptr(g), N.ptr(gs),
+        N.ptr(gw), N.stream_handle(W.device)), 'bs_event_dense_vjp_f32')
+    if gs is not None and squeeze:
+        gs = gs[0]
+    return gs, gw
+
+
 def spike_pack(spk, bits=None):
     """Spikes -> bitmap int32 [(n + 31) // 32] (bit i % 32 of word i // 32)."""
     spk = _spk_view(spk)

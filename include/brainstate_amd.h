@@ -78,6 +78,30 @@ BS_API int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n_pre
                                const float* w, float w_homo, int32_t n_post, float* out,
                                int32_t accumulate, bs_stream_t stream);
 
+/* Value-weighted form of the same operator: out[j] (+)= sum_{i,k: idx[i,k]=j} x[i] * w[i,k]
+ * for fp32 x (rows with x[i] == 0 are skipped).  Used for the forward-mode derivative of the
+ * event mat-vec: d(out) = value_matvec(dx, w) + value_matvec(x, dw).  No counterpart call in
+ * brainstate itself; replaces the tangent rule of brainevent's event mat-vec primitive, whose
+ * numerics the reference pins at brainstate/nn/_event_fixedprob_test.py:90-126. */
+BS_API int bs_value_matvec_f32(const float* x, int32_t n_pre, const int32_t* indptr,
+                               const int32_t* indices, int32_t k, const float* w, float w_homo,
+                               int32_t n_post, float* out, int32_t accumulate,
+                               bs_stream_t stream);
+
+/* Reverse mode of the event mat-vec (the VJP the reference checks at
+ * brainstate/nn/_event_fixedprob_test.py:56-88): with g = grad_out[n_post] and x[i] the spike
+ * value (0/1 for byte spikes),
+ *   grad_spk[i] = sum_k w[i,k] * g[idx[i,k]]                      (nullable, [n_pre])
+ *   grad_w[s]   = x[i] * g[idx[s]] for every synapse s of row i    (w != NULL; [nnz or n_pre*k])
+ *   grad_w[0]   = sum_i x[i] * sum_k g[idx[i,k]]                    (w == NULL; one scalar)
+ * Rows are fixed-num (indptr == NULL) or CSR as in bs_event_scatter_f32.  Out-of-range targets
+ * contribute nothing.  Sums are fp32 in an unspecified order. */
+BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
+                                   const int32_t* indptr, const int32_t* indices, int32_t k,
+                                   const float* w, float w_homo, int32_t n_post,
+                                   const float* grad_out, float* grad_spk, float* grad_w,
+                                   bs_stream_t stream);
+
 /* ---------------------------------------------------------------- N2b event gather
  * Same operator as N2a, post-major and deterministic (no atomics).  Spikes come as a
  * bitmap (bs_spike_pack: bit i%32 of word i/32 set <=> spk[i] != 0).  Layout SELL-64x4:
@@ -103,6 +127,19 @@ BS_API int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
 BS_API int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t batch, int32_t n_in,
                        const float* W, int32_t n_out, int32_t float_as_event, float* out,
                        bs_stream_t stream);
+
+/* Reverse mode of EventLinear's heterogeneous product (the VJP the reference checks at
+ * brainstate/nn/_event_linear_test.py:51-89; its "true gradient" is that of x @ W with the
+ * spike values x, 0/1 for byte spikes, in both float_as_event modes):
+ *   grad_spk[b,i] = sum_j grad_out[b,j] * W[i,j]     (nullable, [batch, n_in])
+ *   grad_W[i,j]   = sum_b x[b,i] * grad_out[b,j]     (nullable, [n_in, n_out]; every element
+ *                                                     written, rows no spike selects get 0)
+ * fp32 with fused multiply-adds; grad_spk sums are reduced across a wave, grad_W sums run
+ * in ascending b. */
+BS_API int bs_event_dense_vjp_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                  int32_t n_in, const float* W, int32_t n_out,
+                                  const float* grad_out, float* grad_spk, float* grad_W,
+                                  bs_stream_t stream);
 
 /* ---------------------------------------------------------------- N3 fused updates
  * LIF / LIFRef membrane with Expon synapses and COBA output -- the per-step elementwise

@@ -14,6 +14,13 @@ lives in the un-vendored ``brainevent>=0.0.7`` (pyproject.toml:60), which is abs
     ``spk @ W``.  Pinned by brainstate/nn/_event_linear_test.py:26-40,127-162.
   * spike compaction has no reference function (brainevent skips zeros inside its
     loops); it is ``np.flatnonzero`` (ascending), pinned as a textbook routine.
+  * Derivatives (brainstate/nn/_event_fixedprob_test.py:56-126,
+    brainstate/nn/_event_linear_test.py:51-125): the reference's "true gradients" are those
+    of the value formulations ``y[j] = sum_{i,k: idx=j} x[i] * w[i,k]`` and ``y = x @ W``
+    (x = spike values), with a homogeneous weight broadcast to every synapse.  ``*_vjp``
+    and ``*_jvp`` below restate them in float64; they are pinned by the adjoint identity
+    <g, A v> = <A^T g, v>, by the exact bilinear expansion of f(x + dx, w + dw), and by the
+    dense-matrix formulas (tests/test_oracle_event.py).
 
 Summation order: the oracle adds events to ``out[j]`` in ascending (pre i, k) order
 starting from 0.0f.  brainevent's own order is unpinned (no reference vector fixes
@@ -128,3 +135,60 @@ def event_linear(spk, W, float_as_event=True, n_out=None):
             for i in np.flatnonzero(x[b] != 0):
                 out[b] = (out[b] + F(x[b, i]) * W[i]).astype(F)
     return out.reshape(spk.shape[:-1] + (W.shape[1],))
+
+
+# ---- derivatives (float64) ----
+
+def _rows_of(idx, indptr):
+    """(row of each synapse, target of each synapse) for fixed-num or CSR connectivity."""
+    if indptr is None:
+        idx = np.asarray(idx)
+        return np.repeat(np.arange(idx.shape[0]), idx.shape[1]), idx.reshape(-1)
+    indptr = np.asarray(indptr, np.int64)
+    return np.repeat(np.arange(indptr.size - 1), np.diff(indptr)), np.asarray(idx).reshape(-1)
+
+
+def value_matvec(x, idx, w, n_post, indptr=None):
+    """y[j] = sum_{s: tgt[s] = j} x[row[s]] * w[s] in float64 (w scalar: homogeneous)."""
+    row, tgt = _rows_of(idx, indptr)
+    ws = np.broadcast_to(np.asarray(w, np.float64), tgt.shape) if np.ndim(w) == 0 else \
+        np.asarray(w, np.float64).reshape(-1)
+    y = np.zeros(n_post, np.float64)
+    np.add.at(y, tgt, np.asarray(x, np.float64)[row] * ws)
+    return y
+
+
+def matvec_vjp(x, idx, w, n_post, g, indptr=None):
+    """(grad_x [n_pre], grad_w) of <g, value_matvec(x, idx, w)>; grad_w has w's shape (a
+    float for a scalar w)."""
+    row, tgt = _rows_of(idx, indptr)
+    g = np.asarray(g, np.float64)
+    x = np.asarray(x, np.float64)
+    gt = g[tgt]
+    n_pre = x.size
+    if np.ndim(w) == 0:
+        gx = np.bincount(row, weights=gt * float(w), minlength=n_pre)
+        gw = float(np.sum(x[row] * gt))
+    else:
+        ws = np.asarray(w, np.float64).reshape(-1)
+        gx = np.bincount(row, weights=gt * ws, minlength=n_pre)
+        gw = (x[row] * gt).reshape(np.shape(w))
+    return gx, gw
+
+
+def matvec_jvp(x, dx, idx, w, dw, n_post, indptr=None):
+    """Tangent of value_matvec at (x, w) along (dx, dw): A(w) dx + A(dw) x."""
+    t = np.zeros(n_post, np.float64)
+    if dx is not None:
+        t += value_matvec(dx, idx, w, n_post, indptr)
+    if dw is not None:
+        t += value_matvec(x, idx, dw, n_post, indptr)
+    return t
+
+
+def dense_vjp(x, W, g):
+    """(grad_x, grad_W) of <g, x @ W> for x [B, n_in], W [n_in, n_out], g [B, n_out]."""
+    x = np.asarray(x, np.float64)
+    W = np.asarray(W, np.float64)
+    g = np.asarray(g, np.float64)
+    return g @ W.T, x.T @ g

@@ -160,3 +160,62 @@ def test_event_linear_batched_equals_rows():
     for b in range(5):
         assert np.array_equal(out[b], event.event_linear(spk[b], W))
     assert np.allclose(out, spk.astype(np.float64) @ W.astype(np.float64), atol=1e-5)
+
+
+# ---- derivative restatements: pinned by identities, not by retyping the formulas ----
+
+def _conn(seed, n_pre=40, n_post=30, k=5):
+    rs = np.random.RandomState(seed)
+    idx = rs.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rs.randn(n_pre, k)
+    x = rs.rand(n_pre) * (rs.rand(n_pre) < 0.4)
+    return rs, idx, w, x
+
+
+@pytest.mark.parametrize('homo', [False, True])
+def test_matvec_vjp_adjoint_identity(homo):
+    """<g, A(w) v> == <grad_x(g), v> for every v, and <g, A(u) x> == <grad_w(g), u>: a dropped
+    term, a wrong index or a transposed operand breaks one of them."""
+    rs, idx, w, x = _conn(3)
+    if homo:
+        w = 1.7
+    g = rs.randn(30)
+    gx, gw = event.matvec_vjp(x, idx, w, 30, g)
+    for _ in range(3):
+        v = rs.randn(40)
+        assert np.isclose(g @ event.value_matvec(v, idx, w, 30), gx @ v)
+        u = rs.randn() if homo else rs.randn(*idx.shape)
+        assert np.isclose(g @ event.value_matvec(x, idx, u, 30), np.sum(np.asarray(gw) * u))
+
+
+def test_matvec_vjp_against_dense_matrix_and_csr():
+    rs, idx, w, x = _conn(5)
+    A = np.zeros((40, 30))
+    np.add.at(A, (np.repeat(np.arange(40), 5), idx.reshape(-1)), w.reshape(-1))
+    g = rs.randn(30)
+    gx, gw = event.matvec_vjp(x, idx, w, 30, g)
+    assert np.allclose(gx, A @ g)
+    assert np.allclose(gw, x[:, None] * g[idx])
+    # CSR with the same rows gives the same gradients
+    indptr = np.arange(41) * 5
+    gx2, gw2 = event.matvec_vjp(x, idx.reshape(-1), w.reshape(-1), 30, g, indptr=indptr)
+    assert np.allclose(gx2, gx) and np.allclose(gw2.reshape(40, 5), gw)
+
+
+def test_matvec_jvp_is_bilinear_difference():
+    """value_matvec is bilinear in (x, w): f(x+dx, w+dw) - f(x, w) - f(dx, dw) equals the
+    tangent exactly (up to float64 rounding)."""
+    rs, idx, w, x = _conn(9)
+    dx, dw = rs.randn(40), rs.randn(*idx.shape)
+    f = lambda a, b: event.value_matvec(a, idx, b, 30)
+    t = event.matvec_jvp(x, dx, idx, w, dw, 30)
+    assert np.allclose(t, f(x + dx, w + dw) - f(x, w) - f(dx, dw))
+
+
+def test_dense_vjp_adjoint_identity():
+    rs = np.random.RandomState(2)
+    x, W, g = rs.randn(3, 7), rs.randn(7, 5), rs.randn(3, 5)
+    gx, gW = event.dense_vjp(x, W, g)
+    v, U = rs.randn(3, 7), rs.randn(7, 5)
+    assert np.isclose(np.sum(g * (v @ W)), np.sum(gx * v))
+    assert np.isclose(np.sum(g * (x @ U)), np.sum(gW * U))
