@@ -241,6 +241,9 @@ def main():
     ap.add_argument('--sim-steps', type=int, default=10000)
     ap.add_argument('--n', type=int, default=1_000_000)
     ap.add_argument('--blocks-per-cu', type=int, default=0)
+    ap.add_argument('--delay-steps', type=int, default=0,
+                    help='synaptic delay D in steps (inputs from the spikes of step t-1-D); '
+                         'the reported line is D = 0, as the config')
     ap.add_argument('--cpu-budget', type=float, default=12.0)
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--copy-calibration-mb', type=int, default=0,
@@ -286,7 +289,8 @@ def main():
     runner = EINetRunner('lif', n, n_exc, idx_e, idx_i,
                          np.full(idx_e.shape, np.float32(0.6)), np.full(idx_i.shape,
                                                                         np.float32(6.7)),
-                         ops.lif_params(), V0, blocks_per_cu=args.blocks_per_cu)
+                         ops.lif_params(), V0, blocks_per_cu=args.blocks_per_cu,
+                         delay_steps=args.delay_steps)
     counts = torch.zeros(max(args.steps, 1), T, dtype=torch.int32, device='cuda')
     wcounts = torch.zeros(T, dtype=torch.int32, device='cuda')
     for _ in range(args.warmup):
@@ -319,7 +323,9 @@ def main():
         'metric': METRIC, 'value': gsops, 'unit': 'GSOP/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': wall / args.steps * 1e3, 'higher_is_better': True,
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32', 'data': 'synthetic',
-        'config': {'workload': 'coba_lif_1m (BASELINE configs[2])', 'neurons': n,
+        'config': {'workload': 'coba_lif_1m (BASELINE configs[2])' if not args.delay_steps
+                   else f'coba_lif_1m with a {args.delay_steps}-step synaptic delay',
+                   'neurons': n, 'delay_steps': args.delay_steps,
                    'n_exc': n_exc, 'fan_out': k, 'synapses': n * k, 'dt_ms': 0.1,
                    'sim_steps_per_bench_step': T,
                    'weights': 'heterogeneous fp32 per synapse (0.6 E, 6.7 I)',

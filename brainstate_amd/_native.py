@@ -33,7 +33,7 @@ class Net(ctypes.Structure):
     _fields_ = [('n', c_i32), ('n_exc', c_i32), ('k_e', c_i32), ('k_i', c_i32),
                 ('idx_e', c_vp), ('w_e', c_vp), ('w_e_homo', c_f32),
                 ('idx_i', c_vp), ('w_i', c_vp), ('w_i_homo', c_f32),
-                ('spk', c_vp), ('blocks_per_cu', c_i32)]
+                ('spk', c_vp), ('blocks_per_cu', c_i32), ('delay_steps', c_i32)]
 
 
 class LifState(ctypes.Structure):

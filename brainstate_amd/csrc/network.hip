@@ -14,9 +14,10 @@
 // 2 x synapses x 8 B, e.g. 1.6 GB for 1e8 synapses; HBM is 288 GB).
 //
 // Per step t, workgroup d:
-//   A. waits until every workgroup s has published its step t-1 count word for d (tagged
-//      with the step, double-buffered) and adds the entries of that inbox into LDS inputs
-//      with LDS atomics -- point-to-point dependencies, no grid barrier;
+//   A. waits until every workgroup s has published its step t-1-D count word for d (tagged
+//      with the step; D = synaptic delay in steps, 0 by default) and adds the entries of
+//      that inbox into LDS inputs with LDS atomics -- point-to-point dependencies, no grid
+//      barrier;
 //   B. runs the fused Expon + COBA + neuron update from those inputs;
 //   C. compacts its spikes into an LDS list (one ballot per neuron slot, one LDS prefix);
 //   D. expands its spikes into (local target | inh flag, weight) entries, written with
@@ -25,8 +26,13 @@
 // Cross-workgroup data is only touched with device-scope loads/stores (emitted with the
 // device-coherence bit), so no L2 writeback/invalidate is ever needed (each costs ~5 us).
 // Deadlock freedom: every workgroup publishes step t's counts unconditionally after
-// consuming step t-1's, and all workgroups are co-resident (cooperative launch); a spin
+// consuming step t-1-D's, and all workgroups are co-resident (cooperative launch); a spin
 // limit turns a would-be hang into an error flag instead.
+// Ring of R = 2(D+1) inbox / count-word slots, step u in slot u mod R: a workgroup at step t
+// has seen every workgroup's step t-1-D publication, so none is more than D+1 steps behind
+// it; the slowest one, at step t-D, still reads step t-2D-1's entries, and R slots keep those
+// (and everything newer) from being overwritten.  With D = 0 this is double buffering; with
+// D > 0 the entries a step consumes were published D steps earlier, so its waits are short.
 #include "neuron_dev.h"
 
 namespace {
@@ -38,6 +44,7 @@ constexpr int kMaxNpt = 8;
 constexpr uint32_t kInhFlag = 0x80000000u;
 constexpr uint64_t kSpinLimit = 1ull << 24;
 constexpr int kRunSteps = 16384;          // steps per cooperative launch (partials buffer)
+constexpr int kMaxDelay = 1023;           // synaptic delay in steps (ring of 2(D+1) slots)
 #ifndef BS_POLL_SLEEP
 #define BS_POLL_SLEEP 1  // s_sleep units (64 clocks) between polls of a count word
 #endif
@@ -50,12 +57,14 @@ struct NetLayout {
   int32_t npt;         // neurons per thread
   int32_t shift;       // log2(neurons per workgroup)
   uint32_t entry;      // bytes per entry (8 het, 4 homogeneous)
-  uint64_t total;      // inbox entries per buffer (>= valid synapses)
-  uint64_t off_cnt;    // uint64 [2][nb dst][nb src]   tagged counts
+  int32_t delay;       // synaptic delay D in steps
+  int32_t ring;        // inbox / count-word slots R = 2(D+1)
+  uint64_t total;      // inbox entries per slot (>= valid synapses)
+  uint64_t off_cnt;    // uint64 [R][nb dst][nb src]   tagged counts
   uint64_t off_cap;    // uint32 [nb src][nb dst]      capacities
   uint64_t off_ofs;    // uint64 [nb dst][nb src] + 1  inbox entry offsets (dst-major)
   uint64_t off_part;   // uint32 [2][kRunSteps][nb]  per-workgroup spike counts / hashes
-  uint64_t off_inbox;  // entries [2][total]
+  uint64_t off_inbox;  // entries [R][total]
   uint64_t bytes;
 };
 
@@ -90,6 +99,8 @@ struct NetArgs {
   uint8_t* spk;
   int64_t t0;
   int32_t steps;
+  int32_t slot_rd;   // ring slot of step t0-1-D (the entries the first step consumes)
+  int32_t slot_wr;   // ring slot of step t0
   uint32_t* counts;  // per-workgroup spike counts [steps][nb] (workspace), or NULL
   uint32_t* hash;    // per-workgroup spike hashes [steps][nb] (workspace), or NULL
   uint8_t* raster;
@@ -228,6 +239,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   }
   int tps = 1;  // threads per source in phase A (power of two, tps * nb <= kBlock)
   while (tps * 2 * nb <= kBlock) tps *= 2;
+  const int ring = L.ring;
+  const int64_t dly = L.delay;
+  int slot_rd = a.slot_rd, slot_wr = a.slot_wr;  // advance by one slot per step
   __syncthreads();
 
   for (int32_t t = 0; t < a.steps; ++t) {
@@ -257,14 +271,13 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       }
     }
 
-    // ---- A: inputs produced by step ta-1 ----
+    // ---- A: inputs produced by step ta-1-D ----
     // tps threads per source: all poll the source's count word (one transaction per
     // wave), then each reads every tps-th entry, up to kBatch loads in flight per thread.
-    if (ta > 0) {
-      const int bin = (int)((ta - 1) & 1);
-      const uint64_t* cin = cnt + ((int64_t)bin * nb + me) * nb;
-      const uint32_t want = (uint32_t)ta;  // step ta-1 publishes tag ta
-      const char* ib = inbox + (size_t)bin * buf_bytes;
+    if (ta > dly) {
+      const uint64_t* cin = cnt + ((int64_t)slot_rd * nb + me) * nb;
+      const uint32_t want = (uint32_t)(ta - dly);  // step u publishes tag u + 1
+      const char* ib = inbox + (size_t)slot_rd * buf_bytes;
       for (int x = threadIdx.x; x < nb * tps; x += kBlock) {
         const int s = x / tps;
         const uint32_t sub = (uint32_t)(x - s * tps);
@@ -372,8 +385,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // entry in the destination's kSlots LDS slots (entries past them are stored directly).
     // After one barrier the slots are written out destination by destination, so consecutive
     // lanes store to consecutive inbox addresses, and each destination's cursor advances.
-    const int bout = (int)(ta & 1);
-    char* ob = inbox + (size_t)bout * buf_bytes;
+    char* ob = inbox + (size_t)slot_wr * buf_bytes;
     const uint32_t nE = __builtin_amdgcn_readfirstlane(nsp2[0]);
     const uint32_t nI = __builtin_amdgcn_readfirstlane(nsp2[1]);
     const uint32_t gE = nE << lgE;
@@ -450,7 +462,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     __syncthreads();
     {
-      uint64_t* cout = cnt + (int64_t)bout * nb * nb;
+      uint64_t* cout = cnt + (int64_t)slot_wr * nb * nb;
       const uint64_t tag = (uint64_t)(uint32_t)(ta + 1) << 32;
       for (int d = threadIdx.x; d < nb; d += kBlock) {
         st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - s_ofs_out[d]));
@@ -462,6 +474,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         s_hash = 0;
       }
     }
+    slot_rd = slot_rd + 1 == ring ? 0 : slot_rd + 1;
+    slot_wr = slot_wr + 1 == ring ? 0 : slot_wr + 1;
   }
 
 #pragma unroll
@@ -592,9 +606,11 @@ int plan(const bs_net* net, NetLayout* L) {
   L->total = (uint64_t)net->n_exc * (uint64_t)net->k_e +
              (uint64_t)(net->n - net->n_exc) * (uint64_t)net->k_i;
   if (L->total >= ((uint64_t)1 << 32)) return -1;  // inbox positions are 32-bit
+  L->delay = net->delay_steps;
+  L->ring = 2 * (net->delay_steps + 1);
   size_t o = align256(sizeof(WsHeader));
   L->off_cnt = o;
-  o = align256(o + (size_t)2 * nb * nb * sizeof(uint64_t));
+  o = align256(o + (size_t)L->ring * nb * nb * sizeof(uint64_t));
   L->off_cap = o;
   o = align256(o + (size_t)nb * nb * sizeof(uint32_t));
   L->off_ofs = o;
@@ -602,7 +618,7 @@ int plan(const bs_net* net, NetLayout* L) {
   L->off_part = o;
   o = align256(o + (size_t)2 * kRunSteps * nb * sizeof(uint32_t));
   L->off_inbox = o;
-  o = align256(o + (size_t)2 * L->total * L->entry);
+  o = align256(o + (size_t)L->ring * L->total * L->entry);
   L->bytes = o;
   return 0;
 }
@@ -617,6 +633,8 @@ int check_net(const bs_net* net, const char* who) {
   BS_CHECK_ARG(net->n_exc == net->n || net->k_i == 0 || net->idx_i, "%s: idx_i is NULL", who);
   BS_CHECK_ARG((net->w_e == nullptr) == (net->w_i == nullptr),
                "%s: w_e and w_i must both be given or both be NULL", who);
+  BS_CHECK_ARG(net->delay_steps >= 0 && net->delay_steps <= kMaxDelay,
+               "%s: delay_steps=%d outside [0, %d]", who, net->delay_steps, kMaxDelay);
   return BS_OK;
 }
 
@@ -635,6 +653,8 @@ NetArgs make_args(const bs_net* net, const NetLayout& L, void* ws) {
   a.spk = net->spk;
   a.t0 = 0;
   a.steps = 0;
+  a.slot_rd = 0;
+  a.slot_wr = 0;
   a.counts = nullptr;
   a.hash = nullptr;
   a.raster = nullptr;
@@ -702,6 +722,9 @@ int run(const bs_net* net, const typename Model::State* st, const typename Model
     NetArgs a = make_args(net, L, workspace);
     a.t0 = t0 + done;
     a.steps = len;
+    const int64_t R = L.ring;
+    a.slot_wr = (int32_t)(a.t0 % R);
+    a.slot_rd = (int32_t)(((a.t0 - 1 - L.delay) % R + R) % R);
     a.counts = counts_out ? part : nullptr;
     a.hash = hash_out ? part + (size_t)kRunSteps * L.nb : nullptr;
     a.raster = raster_out ? raster_out + (int64_t)done * net->n : nullptr;

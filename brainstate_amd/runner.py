@@ -1,6 +1,6 @@
 """Device-resident E/I network runner over the persistent C-ABI loop (bs_coba_*_run).
 
-Holds connectivity, neuron state and the double-buffered event accumulators in HBM and
+Holds connectivity, neuron state and the ring of event inboxes in HBM and
 advances the network ``steps`` at a time in one launch.  This is the compiled form of
 ``brainstate.transform.for_loop(net.update, times)`` for the E/I nets of
 examples/105_COBA_HH_2007_braincell.py:54-91 and examples/400_CUBA_2005_bpu.py:36-66.
@@ -19,11 +19,14 @@ class EINetRunner:
 
     ``model`` is 'lif' (Expon + COBA + LIFRef) or 'hh' (Expon + COBA + Hodgkin-Huxley).
     ``w_e``/``w_i`` are scalars (homogeneous) or [n_pre, K] arrays (heterogeneous).
+    ``delay_steps`` D: step t's synaptic inputs come from the spikes of step t-1-D (the
+    reference's ``N.prefetch_delay('spike', D*dt)``; no spikes before the first step).
     """
 
     def __init__(self, model, n, n_exc, idx_e, idx_i, w_e, w_i, params, V0, device='cuda',
-                 blocks_per_cu=0):
+                 blocks_per_cu=0, delay_steps=0):
         N.require_gpu()
+        self.delay_steps = int(delay_steps)
         self.model = model
         self.n, self.n_exc = int(n), int(n_exc)
         self.device = torch.device(device)
@@ -66,7 +69,8 @@ class EINetRunner:
                           self.idx_e.data_ptr(), None if self.w_e is None else self.w_e.data_ptr(),
                           self.w_e_homo,
                           self.idx_i.data_ptr(), None if self.w_i is None else self.w_i.data_ptr(),
-                          self.w_i_homo, self.spk.data_ptr(), int(blocks_per_cu))
+                          self.w_i_homo, self.spk.data_ptr(), int(blocks_per_cu),
+                          self.delay_steps)
         nbytes = int(N.lib().bs_net_workspace_size(ctypes.byref(self._net)))
         if nbytes == 0:
             N.check(N.BS_ERR_INVALID, 'bs_net_workspace_size')

@@ -193,13 +193,17 @@ typedef struct {
   const int32_t* idx_i; const float* w_i; float w_i_homo;   /* [n - n_exc, k_i] */
   uint8_t* spk;                                             /* [n] last step's spikes */
   int32_t blocks_per_cu;                                    /* 0 = library default */
+  int32_t delay_steps;   /* synaptic delay D in [0, 1023]: step t's inputs come from the spikes
+                            of step t-1-D, as `N.prefetch_delay('spike', D*dt)` gives
+                            (brainstate/nn/_dynamics.py:222-262, _delay.py:762-790); no spikes
+                            before the first step; workspace grows as 2(D+1) inbox slots */
 } bs_net;
 
 typedef struct { float* V; float* ge; float* gi; int32_t* ref; } bs_lif_state;
 typedef struct { float* V; float* m; float* h; float* n; float* ge; float* gi; } bs_hh_state;
 
 /* Workspace bytes for this net on the current device (0 on error; about
- * 2 x synapses x (8 B heterogeneous | 4 B homogeneous)). */
+ * 2(D+1) x synapses x (8 B heterogeneous | 4 B homogeneous)). */
 BS_API size_t bs_net_workspace_size(const bs_net* net);
 BS_API int bs_net_prepare(const bs_net* net, void* workspace, bs_stream_t stream);
 BS_API int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p,

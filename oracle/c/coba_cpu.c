@@ -81,8 +81,11 @@ int bso_max_threads(void) {
 #endif
 }
 
-/* Runs `steps` steps.  in_e/in_i [n] hold the pending inputs (from the spikes before the
- * first step) and are left holding the inputs for the step after the last one.
+/* Runs `steps` steps, the first with absolute index t0.  With a synaptic delay of D steps the
+ * inputs form a ring of D+1 slots, in_e/in_i [(D+1) * n]: step t consumes (and clears) slot
+ * t mod (D+1), and its spikes are scattered into the same slot, which step t+1+D consumes --
+ * an input-side formulation of the spike history the projections read through a Delay.
+ * The ring holds the pending inputs before the first step and after the last one.
  * counts/hashes [steps] are written (nullable).  Returns the total number of spikes. */
 /* Cloned for CPUs with and without FMA3 (chosen when the library loads): fmaf is one
  * correctly rounded operation either way, in hardware or in the C library. */
@@ -91,8 +94,8 @@ long long bso_coba_lif_run(int n, int n_exc, int k_e, int k_i, const int32_t* id
                            const float* w_e, float w_e_homo, const int32_t* idx_i,
                            const float* w_i, float w_i_homo, const bso_lif_params* pp,
                            float* V, float* ge, float* gi, int32_t* ref, uint8_t* spk,
-                           float* in_e, float* in_i, int steps, int32_t* counts,
-                           uint32_t* hashes, int nthreads) {
+                           float* in_e_ring, float* in_i_ring, int steps, int32_t* counts,
+                           uint32_t* hashes, int nthreads, int delay, long long t0) {
   const bso_lif_params p = *pp;
   int32_t* active = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n > 0 ? n : 1));
   long long total = 0;
@@ -102,6 +105,9 @@ long long bso_coba_lif_run(int n, int n_exc, int k_e, int k_i, const int32_t* id
   for (int t = 0; t < steps; ++t) {
     int na = 0;
     uint32_t h = 0;
+    const long long slot = (t0 + t) % (long long)(delay + 1);
+    float* in_e = in_e_ring + slot * (long long)n;
+    float* in_i = in_i_ring + slot * (long long)n;
     /* fused Expon + COBA + LIFRef update; compaction in ascending order */
 #pragma omp parallel for schedule(static) reduction(+ : h)
     for (int j = 0; j < n; ++j) {

@@ -52,13 +52,21 @@ def lif_params(p):
 
 
 def coba_lif_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, counts=None,
-                 hashes=None):
-    """Advance ``state`` (dict of numpy arrays V, ge, gi, ref, spk, in_e, in_i) in place."""
+                 hashes=None, delay=0):
+    """Advance ``state`` (dict of numpy arrays V, ge, gi, ref, spk, in_e, in_i) in place.
+
+    With ``delay`` D > 0, in_e / in_i are rings of D+1 input slots ([(D+1) * n]) and
+    ``state['t']`` (absolute index of the next step, default 0) is advanced."""
     import numpy as np
     P = ctypes.c_void_p
     f = lambda a: a.ctypes.data_as(P) if a is not None else None
     het = np.ndim(w_e) > 0
     n = state['V'].size
+    for key in ('in_e', 'in_i'):
+        if state[key].size != (delay + 1) * n:
+            raise ValueError(f'{key} must hold (delay + 1) * n = {(delay + 1) * n} floats')
+    t0 = int(state.get('t', 0))
+    state['t'] = t0 + int(steps)
     return lib().bso_coba_lif_run(
         ctypes.c_int(n), ctypes.c_int(n_exc), ctypes.c_int(idx_e.shape[1]),
         ctypes.c_int(idx_i.shape[1]), f(idx_e), f(w_e) if het else None,
@@ -66,4 +74,4 @@ def coba_lif_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, cou
         ctypes.c_float(0.0 if het else float(w_i)), ctypes.byref(lif_params(p)),
         f(state['V']), f(state['ge']), f(state['gi']), f(state['ref']), f(state['spk']),
         f(state['in_e']), f(state['in_i']), ctypes.c_int(steps), f(counts), f(hashes),
-        ctypes.c_int(nthreads))
+        ctypes.c_int(nthreads), ctypes.c_int(delay), ctypes.c_longlong(t0))

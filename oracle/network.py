@@ -7,10 +7,16 @@ cell 11): the spikes of the previous step drive the E projection (pre = neurons
 neurons; then the neurons advance with those inputs (Expon decay + delta input,
 COBA current, membrane exp-Euler, spike).  Connectivity per projection is
 ``EventFixedProb(n_pre, N, conn_num, w, seed)`` (brainstate/nn/_event_fixedprob.py:102-200).
+
+With a synaptic delay of D steps the projections read the neurons' spikes through a
+``Delay`` (restated in ``oracle.delay``) updated after every step and read at step D --
+what ``N.prefetch_delay('spike', D*dt)`` gives (brainstate/nn/_dynamics.py:222-262,
+686-745): step t's inputs come from step t-1-D's spikes, and from no spikes before step 0.
 """
 import numpy as np
 
 from . import conn as _conn
+from . import delay as _delay
 from . import event as _event
 from . import neuron as _neuron
 
@@ -52,9 +58,25 @@ class Projection:
         return _event.scatter_fixed(spk_pre, self.idx, self.w, self.n_post)
 
 
-def run_coba_lif(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=None):
+def _spike_delay(N, delay_steps, delay_state):
+    """Spike history read at step D (None for D = 0: the previous step's spikes)."""
+    if not delay_steps:
+        return None
+    d = _delay.Delay((N,), np.bool_)
+    d.register_entry('spike', None)
+    d.max_length = int(delay_steps) + 1
+    d.init_state()
+    if delay_state is not None:
+        d.history[...] = delay_state[0]
+        d.write_ptr = int(delay_state[1])
+    return d
+
+
+def run_coba_lif(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=None,
+                 delay_steps=0, delay_state=None):
     """COBA LIFRef network.  Returns dict(raster [T,N] bool, counts [T], final state)."""
     N = V0.size
+    hist = _spike_delay(N, delay_steps, delay_state)
     if init is None:
         V = np.asarray(V0, F).copy()
         ge = np.zeros(N, F)
@@ -66,18 +88,24 @@ def run_coba_lif(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=N
     raster = np.zeros((steps, N), bool) if record_raster else None
     counts = np.zeros(steps, np.int64)
     for t in range(steps):
-        in_e = proj_e(spk[:n_exc])
-        in_i = proj_i(spk[n_exc:])
+        src = spk if hist is None else hist.retrieve_at_step(delay_steps)
+        in_e = proj_e(src[:n_exc])
+        in_i = proj_i(src[n_exc:])
         V, ge, gi, ref, spk = _neuron.coba_lif_step(V, ge, gi, ref, in_e, in_i, p)
+        if hist is not None:
+            hist.update(spk)
         if record_raster:
             raster[t] = spk
         counts[t] = spk.sum()
-    return dict(raster=raster, counts=counts, V=V, ge=ge, gi=gi, ref=ref, spk=spk)
+    return dict(raster=raster, counts=counts, V=V, ge=ge, gi=gi, ref=ref, spk=spk,
+                delay_state=None if hist is None else (hist.history.copy(), hist.write_ptr))
 
 
-def run_coba_hh(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=None):
+def run_coba_hh(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=None,
+                delay_steps=0, delay_state=None):
     """COBA Hodgkin-Huxley network (exp-Euler gates)."""
     N = V0.size
+    hist = _spike_delay(N, delay_steps, delay_state)
     if init is None:
         V = np.asarray(V0, F).copy()
         m, h, n = _neuron.hh_init(V)
@@ -89,13 +117,17 @@ def run_coba_hh(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=No
     raster = np.zeros((steps, N), bool) if record_raster else None
     counts = np.zeros(steps, np.int64)
     for t in range(steps):
-        in_e = proj_e(spk[:n_exc])
-        in_i = proj_i(spk[n_exc:])
+        src = spk if hist is None else hist.retrieve_at_step(delay_steps)
+        in_e = proj_e(src[:n_exc])
+        in_i = proj_i(src[n_exc:])
         V, m, h, n, ge, gi, spk = _neuron.hh_step(V, m, h, n, ge, gi, in_e, in_i, p)
+        if hist is not None:
+            hist.update(spk)
         if record_raster:
             raster[t] = spk
         counts[t] = spk.sum()
-    return dict(raster=raster, counts=counts, V=V, m=m, h=h, n=n, ge=ge, gi=gi, spk=spk)
+    return dict(raster=raster, counts=counts, V=V, m=m, h=h, n=n, ge=ge, gi=gi, spk=spk,
+                delay_state=None if hist is None else (hist.history.copy(), hist.write_ptr))
 
 
 def spike_hash(spk):

@@ -28,7 +28,7 @@ def say(*a):
     print('[case]', *a, flush=True)
 
 
-def _lif_runner(torch, het, blocks_per_cu=0):
+def _lif_runner(torch, het, blocks_per_cu=0, delay_steps=0):
     from brainstate_amd import ops
     from brainstate_amd.runner import EINetRunner
     pe, pi, V0, _ = make_golden.config1_net()
@@ -36,7 +36,96 @@ def _lif_runner(torch, het, blocks_per_cu=0):
     return EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx,
                        np.full(pe.idx.shape, F(c['w_e'])) if het else c['w_e'],
                        np.full(pi.idx.shape, F(c['w_i'])) if het else c['w_i'],
-                       ops.lif_params(), V0, blocks_per_cu=blocks_per_cu)
+                       ops.lif_params(), V0, blocks_per_cu=blocks_per_cu,
+                       delay_steps=delay_steps)
+
+
+def _c_lif(idx_e, idx_i, w_e, w_i, p, n_exc, V0, T, D, nthreads=8):
+    """C restatement with a D-step synaptic delay: per-step counts, hashes, final state."""
+    from oracle import cbuild
+    n = V0.size
+    st = dict(V=V0.copy(), ge=np.zeros(n, F), gi=np.zeros(n, F), ref=np.zeros(n, np.int32),
+              spk=np.zeros(n, np.uint8), in_e=np.zeros((D + 1) * n, F),
+              in_i=np.zeros((D + 1) * n, F))
+    c = np.zeros(T, np.int32)
+    h = np.zeros(T, np.uint32)
+    cbuild.coba_lif_run(st, idx_e, idx_i, w_e, w_i, p, n_exc, T, nthreads=nthreads, counts=c,
+                        hashes=h, delay=D)
+    return c, h, st
+
+
+def _run_chunks(torch, r, T, chunks):
+    counts = torch.zeros(T, dtype=torch.int32, device='cuda')
+    hashes = torch.zeros(T, dtype=torch.int32, device='cuda')
+    t0 = 0
+    for c in chunks:
+        r.run(c, counts=counts[t0:t0 + c], hashes=hashes[t0:t0 + c])
+        t0 += c
+    r.check()
+    return counts.cpu().numpy(), np.array([int(x) & 0xFFFFFFFF for x in hashes.cpu().numpy()],
+                                          np.uint32)
+
+
+@pytest.mark.parametrize('D,chunks', [(1, [1000]), (4, [300, 700]), (37, [1, 38, 961])])
+def test_coba_lif_delay_matches_c_ring(torch_cuda, D, chunks):
+    """Synaptic delay of D steps (inputs of step t from the spikes of step t-1-D): per-step
+    counts and hashes, final V and spikes equal the C restatement's, across split runs."""
+    torch = torch_cuda
+    say('coba lif 4000 delay', D, chunks)
+    pe, pi, V0, p = make_golden.config1_net()
+    T = sum(chunks)
+    c_ref, h_ref, st = _c_lif(pe.idx, pi.idx, pe.w_scalar, pi.w_scalar, p, 3200, V0, T, D)
+    r = _lif_runner(torch, False, delay_steps=D)
+    counts, hashes = _run_chunks(torch, r, T, chunks)
+    assert c_ref.sum() > 1000
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    assert np.array_equal(r.state['V'].cpu().numpy(), st['V'])
+    assert np.array_equal(r.spk.cpu().numpy(), st['spk'])
+
+
+def test_coba_lif_delay_large_grid(torch_cuda):
+    """262,144 neurons (256 workgroups, K = 100, as the 1M net per neuron): the ring of
+    2(D+1) inbox slots under real cross-workgroup skew; counts, hashes and final V equal the
+    C restatement's."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    torch = torch_cuda
+    n, D, T = 262144, 3, 3000
+    n_exc = n * 4 // 5
+    say('coba lif delay large grid', n, D, T)
+    idx_e = np.random.RandomState(101).randint(0, n, size=(n_exc, 100)).astype(np.int32)
+    idx_i = np.random.RandomState(102).randint(0, n, size=(n - n_exc, 100)).astype(np.int32)
+    V0 = np.random.RandomState(103).uniform(-60., -50., n).astype(F)
+    c_ref, h_ref, st = _c_lif(idx_e, idx_i, F(0.6), F(6.7), neuron.LIFParams(), n_exc, V0, T, D,
+                              nthreads=16)
+    r = EINetRunner('lif', n, n_exc, idx_e, idx_i, 0.6, 6.7, ops.lif_params(), V0,
+                    delay_steps=D)
+    assert r.grid_blocks == 256
+    counts, hashes = _run_chunks(torch, r, T, [T])
+    assert c_ref.sum() > 10 * T
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    assert np.array_equal(r.state['V'].cpu().numpy(), st['V'])
+
+
+def test_coba_hh_delay_matches_oracle(torch_cuda):
+    """HH net with a 5-step synaptic delay against the numpy oracle's spike-history Delay."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    torch = torch_cuda
+    c = make_golden.HH_NET
+    D, T = 5, 600
+    say('coba hh delay', D, T)
+    pe, pi, V0, p = make_golden.hh_net()
+    ref = network.run_coba_hh(V0, pe, pi, p, c['n_exc'], T, record_raster=False, delay_steps=D)
+    r = EINetRunner('hh', c['n'], c['n_exc'], pe.idx, pi.idx, c['w_e'], c['w_i'],
+                    ops.hh_params(I_ext=c['I_ext']), V0, delay_steps=D)
+    counts, _ = _run_chunks(torch, r, T, [200, 400])
+    assert ref['counts'].sum() > 100
+    assert counts.tolist() == ref['counts'].tolist()
+    assert np.array_equal(r.state['V'].cpu().numpy(), ref['V'])
 
 
 @pytest.mark.parametrize('het,chunks', [(False, [1000]), (True, [1000]), (False, [1, 9, 90, 900])])
