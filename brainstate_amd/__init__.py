@@ -5,9 +5,9 @@ The public surface mirrors brainstate's for this path: ``State`` classes, ``envi
 the HIP library ``_lib/libbsamd.so`` through the C ABI of include/brainstate_amd.h.
 """
 from . import environ, nn, transform
-from ._state import FakeState, HiddenState, ParamState, ShortTermState, State
+from ._state import DelayState, FakeState, HiddenState, ParamState, ShortTermState, State
 
 __version__ = '0.1.0'
 
-__all__ = ['State', 'ShortTermState', 'HiddenState', 'ParamState', 'FakeState', 'environ',
-           'transform', 'nn']
+__all__ = ['State', 'ShortTermState', 'HiddenState', 'ParamState', 'FakeState', 'DelayState',
+           'environ', 'transform', 'nn']

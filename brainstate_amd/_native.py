@@ -46,6 +46,11 @@ class HhState(ctypes.Structure):
 
 # name -> (restype, argtypes); every symbol declared in include/brainstate_amd.h
 SIGNATURES = {
+    'bs_delay_write': (ctypes.c_int, [c_vp, c_i32, ctypes.c_int64, c_i32, c_vp, c_vp]),
+    'bs_delay_gather': (ctypes.c_int, [c_vp, c_i32, ctypes.c_int64, c_i32, c_i32, c_i32, c_vp,
+                                       c_vp, ctypes.c_int64, c_vp, c_vp]),
+    'bs_delay_taps_f32': (ctypes.c_int, [c_vp, c_i32, ctypes.c_int64, c_i32, c_vp, c_vp, c_vp,
+                                         ctypes.c_int64, c_vp, c_vp]),
     'bs_last_error': (ctypes.c_char_p, []),
     'bs_version': (ctypes.c_int, []),
     'bs_spike_compact_workspace_size': (c_size, [c_i32]),

@@ -1,5 +1,5 @@
 """State containers mirroring brainstate/_state.py (State :264, ShortTermState :1166,
-HiddenState :1258, ParamState :1872, FakeState :1897).
+HiddenState :1258, ParamState :1872, FakeState :1897, DelayState).
 
 Values are torch device tensors (or Python scalars for homogeneous parameters).  There is
 no tracing: the simulation loop is compiled by the whole-loop runner instead of XLA, so a
@@ -50,6 +50,11 @@ class HiddenState(ShortTermState):
 
 
 class ParamState(State):
+    pass
+
+
+class DelayState(ShortTermState):
+    """History buffer of a Delay (brainstate/_state.py DelayState)."""
     pass
 
 

@@ -24,6 +24,15 @@ def set(**kwargs):  # noqa: A001 - mirrors brainstate.environ.set
     _settings.update(kwargs)
 
 
+def pop(key, default=None):
+    """Remove a global setting and return its value (brainstate/environ.py pop)."""
+    if key not in _settings:
+        if default is not None:
+            return default
+        raise KeyError(f'"{key}" is not a global setting')
+    return _settings.pop(key)
+
+
 def get(key, default=None, desc=None):
     for frame in reversed(_stack()):
         if key in frame:

@@ -1,5 +1,8 @@
 """brainstate.nn surface for the spiking-network step (event connectivity, neurons, synapses)."""
 from . import init
+from ._delay import (Delay, DelayAccess, InterpolationRegistry, OutputDelayAt, Prefetch,
+                     PrefetchDelay, PrefetchDelayAt, StateWithDelay, not_receive_update_output,
+                     receive_update_output)
 from ._event import EventFixedNumConn, EventFixedProb, EventLinear, FixedNumConn
 from ._fuse import fuse
 from ._module import Dynamics, Module, init_all_states
@@ -7,4 +10,6 @@ from ._neurons import COBA, HH, LIF, AlignPostProj, Expon, LIFRef
 
 __all__ = ['init', 'Module', 'Dynamics', 'init_all_states', 'FixedNumConn', 'EventFixedNumConn',
            'EventFixedProb', 'EventLinear', 'Expon', 'COBA', 'AlignPostProj', 'LIF', 'LIFRef',
-           'HH', 'fuse']
+           'HH', 'fuse', 'Delay', 'DelayAccess', 'StateWithDelay', 'InterpolationRegistry',
+           'Prefetch', 'PrefetchDelay', 'PrefetchDelayAt', 'OutputDelayAt',
+           'receive_update_output', 'not_receive_update_output']

@@ -1,0 +1,661 @@
+"""Ring-buffer delays mirroring brainstate/nn/_delay.py (Delay :399, DelayAccess :363,
+StateWithDelay :960, InterpolationRegistry :88) and the prefetch helpers of
+brainstate/nn/_dynamics.py (Prefetch :503, PrefetchDelay :608, PrefetchDelayAt :655,
+OutputDelayAt :748).
+
+The history of every delayed leaf is one device tensor ``[max_length, (batch,) *shape]``; all
+reads and writes go through the HIP library (``bs_delay_write``, ``bs_delay_gather``,
+``bs_delay_taps_f32``).  The ring arithmetic follows the reference exactly:
+
+* ``max_length`` = ceil(time / dt) + 1 (ratio rounded to float32 first, as ``jnp.ceil`` of a
+  Python float does with x64 off), grown to max(step) + 1 by every registration;
+* ``update`` writes slot ``write_ptr // update_every_step`` (every call, or only when
+  ``write_ptr % update_every_step == 0``) and advances ``write_ptr`` modulo
+  ``max_length * update_every_step``;
+* ``retrieve_at_step(d, *idx)`` reads slot ``((write_ptr - 1) // update_every_step - d) mod
+  max_length`` with numpy fancy indexing of the remaining dimensions;
+* ``retrieve_at_time`` evaluates ``(t - t_delay) / slot_dt`` in float32; 'linear' blends the
+  floor / ceil steps as ``a * (1 - t) + b * t``, 'nearest' rounds half to even, the other
+  registered methods interpolate at the float ring index ``cur - fts`` from 2-4 slots.
+
+Units (brainunit) are not available here: ``take_aware_unit`` is accepted and has no effect.
+"""
+import math
+import numbers
+import warnings
+from collections import namedtuple
+
+import numpy as np
+import torch
+
+from .. import _native as N
+from .. import environ
+from .._state import DelayState, ShortTermState, State
+from ._module import Dynamics, Module
+
+__all__ = ['Delay', 'DelayAccess', 'StateWithDelay', 'InterpolationRegistry', 'ShapeDtype',
+           'Prefetch', 'PrefetchDelay', 'PrefetchDelayAt', 'OutputDelayAt',
+           'receive_update_output', 'not_receive_update_output']
+
+_DELAY_ROTATE = 'rotation'
+_DELAY_CONCAT = 'concat'
+_INTERP_LINEAR = 'linear_interp'
+_INTERP_ROUND = 'round'
+INTERP_ALIAS_MAP = {'linear_interp': 'linear', 'round': 'nearest'}
+
+F32 = np.float32
+ShapeDtype = namedtuple('ShapeDtype', ['shape', 'dtype'])
+
+_NP_TO_TORCH = {np.dtype(np.float32): torch.float32, np.dtype(np.float64): torch.float64,
+                np.dtype(np.float16): torch.float16, np.dtype(np.int32): torch.int32,
+                np.dtype(np.int64): torch.int64, np.dtype(np.int16): torch.int16,
+                np.dtype(np.int8): torch.int8, np.dtype(np.uint8): torch.uint8,
+                np.dtype(np.bool_): torch.bool}
+
+
+def _device():
+    N.require_gpu()
+    return torch.device('cuda', torch.cuda.current_device())
+
+
+def _torch_dtype(dt):
+    if isinstance(dt, torch.dtype):
+        return dt
+    return _NP_TO_TORCH[np.dtype(dt)]
+
+
+def _np_dtype(dt):
+    return torch.empty((), dtype=dt).numpy().dtype
+
+
+def _is_leaf(x):
+    return not isinstance(x, (dict, list, tuple)) or isinstance(x, ShapeDtype)
+
+
+def _tree_map(f, *trees):
+    t0 = trees[0]
+    if _is_leaf(t0):
+        return f(*trees)
+    if isinstance(t0, dict):
+        return {k: _tree_map(f, *(t[k] for t in trees)) for k in t0}
+    return type(t0)(_tree_map(f, *xs) for xs in zip(*trees))
+
+
+def _info_of(a):
+    """(shape, torch dtype) of a template leaf: tensor, array, number or (shape, dtype)."""
+    if isinstance(a, ShapeDtype) or (hasattr(a, 'shape') and hasattr(a, 'dtype')
+                                     and not torch.is_tensor(a) and not isinstance(a, np.ndarray)):
+        return ShapeDtype(tuple(int(s) for s in a.shape), _torch_dtype(a.dtype))
+    if torch.is_tensor(a):
+        return ShapeDtype(tuple(a.shape), a.dtype)
+    arr = np.asarray(a)
+    if arr.dtype == np.float64:
+        arr = arr.astype(np.float32)
+    return ShapeDtype(tuple(arr.shape), _torch_dtype(arr.dtype))
+
+
+def _get_delay(delay_time, dt):
+    """(time, ceil(time / dt)) with the ratio in float32 (brainstate/nn/_delay.py:351-360)."""
+    if delay_time is None:
+        return 0.0, 0
+    if torch.is_tensor(delay_time):
+        delay_time = delay_time.detach().cpu().numpy()
+    if np.ndim(delay_time) == 0 and not isinstance(delay_time, np.ndarray):
+        ratio = F32(float(delay_time) / float(dt))
+    else:
+        ratio = np.asarray(delay_time, F32) / F32(dt)
+    steps = np.ceil(ratio).astype(np.int32)
+    return delay_time, (int(steps) if np.ndim(steps) == 0 else steps)
+
+
+def _is_integer(x):
+    if torch.is_tensor(x):
+        return not x.dtype.is_floating_point and x.dtype != torch.bool
+    return np.issubdtype(np.asarray(x).dtype, np.integer)
+
+
+def _index_array(x):
+    return x.detach().cpu().numpy() if torch.is_tensor(x) else np.asarray(x)
+
+
+# ---------------------------------------------------------------- device reads
+
+def _plan(slot_shape, steps, indices):
+    """Broadcast (steps, *indices) as numpy fancy indexing does; return per-output steps and
+    slot-relative element offsets (both flat) and the output shape."""
+    if len(indices) > len(slot_shape):
+        raise IndexError(f'too many indices ({len(indices)}) for a delayed value of shape '
+                         f'{tuple(slot_shape)}')
+    arrs = [np.asarray(steps, np.int64)] + [_index_array(i).astype(np.int64) for i in indices]
+    b = np.broadcast_arrays(*arrs)
+    shape = b[0].shape
+    strides = np.cumprod((list(slot_shape[1:]) + [1])[::-1])[::-1]
+    base = np.zeros(shape, np.int64)
+    for m, idx in enumerate(b[1:]):
+        dim = slot_shape[m]
+        if np.any(idx >= dim) or np.any(idx < -dim):
+            raise IndexError(f'index out of bounds for axis {m + 1} with size {dim}')
+        base = base + np.where(idx < 0, idx + dim, idx) * int(strides[m])
+    rest = tuple(slot_shape[len(indices):])
+    nrest = int(np.prod(rest)) if rest else 1
+    cols = (base.reshape(-1, 1) + np.arange(nrest, dtype=np.int64)[None, :]).reshape(-1)
+    st = np.repeat(b[0].reshape(-1), nrest)
+    return st.astype(np.int32), cols, tuple(shape) + rest
+
+
+class _Read:
+    """A read of one leaf: per-output steps and columns, uploaded once."""
+
+    def __init__(self, slot_shape, steps, indices, device):
+        st, cols, self.shape = _plan(slot_shape, steps, indices)
+        self.n = int(cols.size)
+        self.steps = torch.as_tensor(st, device=device)
+        self.cols = torch.as_tensor(cols, device=device)
+
+
+def _gather(hist, length, cur, step, read=None):
+    slot_shape = tuple(hist.shape[1:])
+    slot_elems = int(np.prod(slot_shape)) if slot_shape else 1
+    if read is None:
+        out = torch.empty(slot_shape, dtype=hist.dtype, device=hist.device)
+        n_out, steps, cols = slot_elems, None, None
+    else:
+        out = torch.empty(read.shape, dtype=hist.dtype, device=hist.device)
+        n_out, steps, cols = read.n, read.steps, read.cols
+    N.check(N.lib().bs_delay_gather(N.ptr(hist), int(length), slot_elems, hist.element_size(),
+                                    int(cur), int(step), N.ptr(steps), N.ptr(cols), n_out,
+                                    N.ptr(out), N.stream_handle(hist.device)), 'bs_delay_gather')
+    return out
+
+
+def _taps(hist, slots, weights, read=None):
+    if hist.dtype != torch.float32:
+        raise NotImplementedError(f'interpolated delay reads need a float32 history, got '
+                                  f'{hist.dtype}')
+    length = hist.shape[0]
+    slot_shape = tuple(hist.shape[1:])
+    slot_elems = int(np.prod(slot_shape)) if slot_shape else 1
+    if read is None:
+        out = torch.empty(slot_shape, dtype=torch.float32, device=hist.device)
+        n_out, cols = slot_elems, None
+    else:
+        out = torch.empty(read.shape, dtype=torch.float32, device=hist.device)
+        n_out, cols = read.n, read.cols
+    sl = (N.c_i32 * 4)(*[int(s) for s in slots])
+    w = (N.c_f32 * 4)(*[float(x) for x in weights])
+    N.check(N.lib().bs_delay_taps_f32(N.ptr(hist), int(length), slot_elems, len(slots), sl, w,
+                                      N.ptr(cols), n_out, N.ptr(out),
+                                      N.stream_handle(hist.device)), 'bs_delay_taps_f32')
+    return out
+
+
+def _index_read(hist, indices):
+    """_Read for indexing a slot with ``indices`` (no per-element steps), or None."""
+    if not indices:
+        return None
+    return _Read(tuple(hist.shape[1:]), 0, indices, hist.device)
+
+
+# ---------------------------------------------------------------- interpolation
+
+def _tap_weights(method, t):
+    """(tap offsets from floor(index), fp32 weights) of the reference's formulas (:193-338)."""
+    t = F32(t)
+    one, half = F32(1.0), F32(0.5)
+    t2, t3 = t * t, t * t * t
+    if method == 'linear':
+        return (0, 1), [one - t, t]
+    if method == 'cubic':
+        return (-1, 0, 1, 2), [-half * t3 + t2 - half * t, F32(1.5) * t3 - F32(2.5) * t2 + one,
+                               F32(-1.5) * t3 + F32(2.0) * t2 + half * t, half * t3 - half * t2]
+    if method == 'hermite':
+        # h00 v0 + h10 (v1 - v_-1)/2 + h01 v1 + h11 (v2 - v0)/2, collected per tap
+        h00 = F32(2) * t3 - F32(3) * t2 + one
+        h10 = t3 - F32(2) * t2 + t
+        h01 = F32(-2) * t3 + F32(3) * t2
+        h11 = t3 - t2
+        return (-1, 0, 1, 2), [-half * h10, h00 - half * h11, h01 + half * h10, half * h11]
+    if method == 'polynomial2':
+        return (-1, 0, 1), [half * t * (t - one), (one - t) * (one + t), half * t * (t + one)]
+    if method == 'polynomial3':
+        return (-1, 0, 1, 2), [-t * (t - one) * (t - F32(2)) / F32(6),
+                               (t + one) * (t - one) * (t - F32(2)) / F32(2),
+                               -t * (t + one) * (t - F32(2)) / F32(2),
+                               t * (t + one) * (t - one) / F32(6)]
+    raise ValueError(method)
+
+
+def _method_fn(method):
+    def interp(history, indices, float_idx, max_length):
+        fi = F32(float_idx)
+        i0 = int(math.floor(float(fi)))
+        offs, w = _tap_weights(method, fi - F32(i0))
+        slots = [(i0 + o) % int(max_length) for o in offs]
+        return _tree_map(lambda h: _taps(h, slots, w, _index_read(h, indices)), history)
+    interp.__name__ = f'_{method}_interpolation'
+    return interp
+
+
+def _nearest_interpolation(history, indices, float_idx, max_length):
+    """Round the float ring index (half to even) and read that slot (:163-171)."""
+    i = int(np.round(F32(float_idx))) % int(max_length)
+    return _tree_map(lambda h: _gather(h, h.shape[0], i, 0, _index_read(h, indices)), history)
+
+
+_linear_interpolation = _method_fn('linear')
+_cubic_interpolation = _method_fn('cubic')
+_hermite_interpolation = _method_fn('hermite')
+_polynomial2_interpolation = _method_fn('polynomial2')
+_polynomial3_interpolation = _method_fn('polynomial3')
+
+
+class InterpolationRegistry:
+    """Named interpolation methods for continuous-time delay reads (:88-160)."""
+    _methods = {}
+
+    @classmethod
+    def register(cls, name, method):
+        cls._methods[name] = method
+
+    @classmethod
+    def get(cls, name):
+        if name not in cls._methods:
+            raise ValueError(f'Unknown interpolation method: {name}. '
+                             f'Available methods: {cls.list_methods()}')
+        return cls._methods[name]
+
+    @classmethod
+    def list_methods(cls):
+        return list(cls._methods.keys())
+
+
+InterpolationRegistry.register('nearest', _nearest_interpolation)
+InterpolationRegistry.register('round', _nearest_interpolation)
+InterpolationRegistry.register('linear', _linear_interpolation)
+InterpolationRegistry.register('linear_interp', _linear_interpolation)
+InterpolationRegistry.register('cubic', _cubic_interpolation)
+InterpolationRegistry.register('hermite', _hermite_interpolation)
+InterpolationRegistry.register('polynomial2', _polynomial2_interpolation)
+InterpolationRegistry.register('polynomial3', _polynomial3_interpolation)
+
+
+# ---------------------------------------------------------------- Delay
+
+class DelayAccess(Module):
+    """Accessor for a named entry of a Delay (:363-396)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, delay, *time, entry):
+        super().__init__()
+        self.delay = delay
+        assert isinstance(delay, Delay), 'The input delay should be an instance of Delay.'
+        self._delay_entry = entry
+        self.delay_info = delay.register_entry(self._delay_entry, *time)
+
+    def __call__(self, *args, **kwargs):
+        return self.delay.at(self._delay_entry)
+
+
+class Delay(Module):
+    """Delay variable for short-term history (:399-957); history resident in device memory."""
+    __module__ = 'brainstate_amd.nn'
+    _init_last = True
+
+    def __init__(self, target_info, time=None, init=None, entries=None, interpolation=None,
+                 take_aware_unit=False, update_every=None, delay_method=_DELAY_ROTATE,
+                 interp_method=_INTERP_LINEAR):
+        super().__init__()
+        self.target_info = None if target_info is None else _tree_map(_info_of, target_info)
+        if delay_method is None:
+            delay_method = _DELAY_ROTATE
+        if delay_method == _DELAY_CONCAT:
+            warnings.warn("delay_method='concat' is deprecated. The unified ring buffer "
+                          "implementation now uses rotation for all delays, providing better "
+                          "performance.", DeprecationWarning, stacklevel=2)
+        self.delay_method = _DELAY_ROTATE
+        if interpolation is None:
+            interpolation = INTERP_ALIAS_MAP.get(interp_method, interp_method)
+        if isinstance(interpolation, str):
+            if interpolation not in InterpolationRegistry.list_methods():
+                raise ValueError(f'Unknown interpolation method: {interpolation}. '
+                                 f'Available methods: {InterpolationRegistry.list_methods()}')
+            self.interp_method = interpolation
+        elif callable(interpolation):
+            self.interp_method = interpolation
+        else:
+            raise TypeError(f'interpolation must be str or callable, got {type(interpolation)}')
+        dt = environ.get_dt()
+        self.max_time, length = _get_delay(time, dt if update_every is None else update_every)
+        self.max_length = length + 1
+        if init is not None and not isinstance(init, (numbers.Number, np.ndarray, torch.Tensor)) \
+                and not callable(init):
+            raise TypeError(f'init should be Array, Callable, or None. But got {init}')
+        self._init = init
+        self.take_aware_unit = take_aware_unit
+        self._unit = None
+        if update_every is not None:
+            if update_every < dt:
+                raise ValueError(f'update_every must be >= dt ({dt}), got {update_every}')
+            self.update_every = update_every
+            self.update_every_step = int(update_every / dt)
+        else:
+            self.update_every = None
+            self.update_every_step = 1
+        self._registered_entries = dict()
+        self._reads = dict()
+        self.history = None
+        self.write_ptr = None
+        if entries is not None:
+            for entry, time_and_idx in entries.items():
+                if isinstance(time_and_idx, (tuple, list)):
+                    self.register_entry(entry, *time_and_idx)
+                else:
+                    self.register_entry(entry, time_and_idx)
+
+    # -- state
+    def _f_to_init(self, info, batch_size, length):
+        shape = [length] + ([batch_size] if batch_size is not None else []) + list(info.shape)
+        dev = _device()
+        if isinstance(self._init, (numbers.Number, np.ndarray, torch.Tensor)):
+            v = torch.as_tensor(self._init, device=dev).to(info.dtype)
+            return torch.broadcast_to(v, shape).contiguous()
+        if callable(self._init):
+            v = self._init(tuple(shape), dtype=_np_dtype(info.dtype))
+            return torch.as_tensor(np.asarray(v) if not torch.is_tensor(v) else v,
+                                   device=dev).to(info.dtype).reshape(shape).contiguous()
+        return torch.zeros(shape, dtype=info.dtype, device=dev)
+
+    def init_state(self, batch_size=None, **kwargs):
+        self.write_ptr = ShortTermState(np.int32(0))
+        self.history = DelayState(_tree_map(
+            lambda i: self._f_to_init(i, batch_size, self.max_length), self.target_info))
+        self._reads = dict()
+
+    def reset_state(self, batch_size=None, **kwargs):
+        self.write_ptr.value = np.int32(0)
+        self.history.value = _tree_map(
+            lambda i: self._f_to_init(i, batch_size, self.max_length), self.target_info)
+        self._reads = dict()
+
+    # -- registration
+    def register_delay(self, *time_and_idx):
+        assert len(time_and_idx) >= 1, 'You should provide at least one delay time.'
+        for d in time_and_idx[1:]:
+            assert _is_integer(d), f'The index should be integer. But got {d}.'
+        if time_and_idx[0] is None:
+            return None
+        time, delay_step = _get_delay(time_and_idx[0], environ.get_dt()
+                                      if self.update_every is None else self.update_every)
+        max_delay_step = int(np.max(delay_step))
+        self.max_time = max(float(self.max_time), float(np.max(_index_array(time))))
+        if self.max_length <= max_delay_step + 1:
+            self.max_length = int(max_delay_step + 1)
+        return (delay_step, *time_and_idx[1:])
+
+    def register_entry(self, entry, *time_and_idx):
+        if entry in self._registered_entries:
+            raise KeyError(f'Entry {entry} has been registered. '
+                           f'The existing delay for the key {entry} is '
+                           f'{self._registered_entries[entry]}. '
+                           f'The new delay for the key {entry} is {time_and_idx}. '
+                           f'You can use another key. ')
+        delay_info = self.register_delay(*time_and_idx)
+        self._registered_entries[entry] = delay_info
+        return delay_info
+
+    def access(self, entry, *time_and_idx):
+        return DelayAccess(self, *time_and_idx, entry=entry)
+
+    # -- reads
+    def _check_ready(self):
+        assert self.history is not None, 'The delay history is not initialized.'
+        for h in _leaves(self.history.value):
+            if h.shape[0] != self.max_length:
+                raise RuntimeError(f'the delay was registered up to {self.max_length - 1} steps '
+                                   f'after init_state built {h.shape[0]} slots; call '
+                                   f'init_state() again')
+
+    def _current(self):
+        return (int(self.write_ptr.value) - 1) // self.update_every_step
+
+    def at(self, entry):
+        assert isinstance(entry, str), (f'entry should be a string for describing the entry of '
+                                        f'the delay data. But we got {entry}.')
+        if entry not in self._registered_entries:
+            raise KeyError(f'Does not find delay entry "{entry}".')
+        delay_step = self._registered_entries[entry]
+        if delay_step is None:
+            delay_step = (0,)
+        return self._retrieve(delay_step[0], delay_step[1:], cache_key=entry)
+
+    def retrieve_at_step(self, delay_step, *indices):
+        return self._retrieve(delay_step, indices)
+
+    def _retrieve(self, delay_step, indices, cache_key=None):
+        self._check_ready()
+        assert delay_step is not None, 'The delay step should be given.'
+        if torch.is_tensor(delay_step):
+            delay_step = delay_step.detach().cpu().numpy()
+        if environ.get('jit_error_check', False) and np.any(np.asarray(delay_step) >=
+                                                             self.max_length):
+            raise ValueError(f'The request delay length should be less than the maximum delay '
+                             f'{self.max_length - 1}. But we got {delay_step}')
+        cur = self._current()
+        if np.ndim(delay_step) == 0 and not indices:
+            return _tree_map(lambda h: _gather(h, self.max_length, cur, int(delay_step)),
+                             self.history.value)
+
+        def read(h, key):
+            r = self._reads.get(key) if cache_key is not None else None
+            if r is None:
+                r = _Read(tuple(h.shape[1:]), delay_step, indices, h.device)
+                if cache_key is not None:
+                    self._reads[key] = r
+            return _gather(h, self.max_length, cur, 0, r)
+
+        leaves = _leaves(self.history.value)
+        keyed = iter(range(len(leaves)))
+        return _tree_map(lambda h: read(h, (cache_key, next(keyed))), self.history.value)
+
+    def retrieve_at_time(self, delay_time, *indices):
+        self._check_ready()
+        assert delay_time is not None, 'The delay time should be given.'
+        current_time = environ.get('t', desc='The current time.')
+        dt = environ.get_dt()
+        if np.ndim(_index_array(delay_time)) != 0:
+            raise NotImplementedError('retrieve_at_time takes one delay time')
+        delay_time = float(_index_array(delay_time))
+        if environ.get('jit_error_check', False) and (
+                delay_time > current_time or delay_time < current_time - self.max_time - dt):
+            raise ValueError(f'The request delay time should be within '
+                             f'[{current_time - self.max_time - dt}, {current_time}], '
+                             f'but we got {delay_time}')
+        diff = F32(current_time) - F32(delay_time)
+        slot_dt = dt if self.update_every is None else self.update_every
+        fts = diff / F32(slot_dt)
+        m = self.interp_method
+        if m in ('linear', 'linear_interp'):
+            lo, hi = int(np.floor(fts)), int(np.ceil(fts))
+            t = fts - np.floor(fts)
+            if environ.get('jit_error_check', False) and hi >= self.max_length:
+                raise ValueError(f'The request delay length should be less than the maximum '
+                                 f'delay {self.max_length - 1}. But we got {hi}')
+            cur = self._current()
+            slots = [(cur - lo) % self.max_length, (cur - hi) % self.max_length]
+            w = [F32(1) - t, t]
+            return _tree_map(lambda h: _taps(h, slots, w, _index_read(h, indices)),
+                             self.history.value)
+        if m in ('nearest', 'round'):
+            return self.retrieve_at_step(int(np.round(fts)), *indices)
+        fidx = F32(self._current()) - fts
+        fn = InterpolationRegistry.get(m) if isinstance(m, str) else m
+        return fn(self.history.value, indices, fidx, self.max_length)
+
+    # -- writes
+    def _write_to_buffer(self, value):
+        idx = int(self.write_ptr.value) // self.update_every_step
+
+        def write(h, v):
+            v = torch.as_tensor(v, device=h.device).to(h.dtype)
+            v = torch.broadcast_to(v, tuple(h.shape[1:])).contiguous()
+            N.check(N.lib().bs_delay_write(N.ptr(h), int(h.shape[0]),
+                                           v.numel() * v.element_size(), idx, N.ptr(v),
+                                           N.stream_handle(h.device)), 'bs_delay_write')
+        _tree_map(write, self.history.value, value)
+
+    def _advance_write_ptr(self):
+        period = self.max_length * self.update_every_step
+        self.write_ptr.value = np.int32((int(self.write_ptr.value) + 1) % period)
+
+    def update(self, current):
+        assert self.history is not None, 'The delay history is not initialized.'
+        self._check_ready()
+        if self.take_aware_unit and self._unit is None:
+            self._unit = _tree_map(lambda x: None, current)
+        if self.update_every is None or int(self.write_ptr.value) % self.update_every_step == 0:
+            self._write_to_buffer(current)
+        self._advance_write_ptr()
+
+
+def _leaves(tree):
+    out = []
+    _tree_map(lambda x: out.append(x), tree)
+    return out
+
+
+class StateWithDelay(Delay):
+    """Delayed history of a module's State (:960-1079)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, target, item, init=None, interpolation=_INTERP_ROUND, **kwargs):
+        super().__init__(None, init=init, interpolation=interpolation, **kwargs)
+        self._target = target
+        self._target_term = item
+
+    @property
+    def state(self):
+        r = getattr(self._target, self._target_term)
+        if not isinstance(r, State):
+            raise TypeError(f'The term "{self._target_term}" in the module "{self._target}" is '
+                            f'not a State.')
+        return r
+
+    def init_state(self, *args, **kwargs):
+        self.target_info = _tree_map(_info_of, self.state.value)
+        super().init_state(*args, **kwargs)
+
+    def update(self, *args):
+        return super().update(self.state.value)
+
+
+# ---------------------------------------------------------------- prefetch (Dynamics helpers)
+
+def receive_update_output(obj):
+    """Mark an after-update hook to be called with the update's return value (:870-885)."""
+    if hasattr(obj, '_not_receive_update_output'):
+        delattr(obj, '_not_receive_update_output')
+    return obj
+
+
+def not_receive_update_output(obj):
+    """Mark an after-update hook to be called without arguments (:887-900)."""
+    obj._not_receive_update_output = True
+    return obj
+
+
+def _prefetch_item(target):
+    item = getattr(target.module, target.item, None)
+    if item is None:
+        raise AttributeError(f'The target {target.module} should have an `{target.item}` '
+                             f'attribute.')
+    return item
+
+
+class Prefetch(Module):
+    """Reference to a module's state, resolved when called (:503-606)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, module, item):
+        super().__init__()
+        self.module = module
+        self.item = item
+
+    @property
+    def delay(self):
+        return PrefetchDelay(self.module, self.item)
+
+    def __call__(self, *args, **kwargs):
+        item = _prefetch_item(self)
+        return item.value if isinstance(item, State) else item
+
+    def get_item_value(self):
+        return self()
+
+    def get_item(self):
+        return _prefetch_item(self)
+
+
+class PrefetchDelay(Module):
+    """``prefetch(item).delay``; ``.at(time)`` registers a delayed read (:608-653)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, module, item):
+        super().__init__()
+        self.module = module
+        self.item = item
+
+    def at(self, *delay_time):
+        return PrefetchDelayAt(self.module, self.item, delay_time)
+
+
+class PrefetchDelayAt(Module):
+    """A module state read ``time`` ago through a StateWithDelay after-update hook
+    (:655-745)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, module, item, *time_and_index, delay_init=None, interpolation=None,
+                 update_every=None, **kwargs):
+        super().__init__()
+        assert isinstance(module, Dynamics), 'The module should be an instance of Dynamics.'
+        self.module = module
+        self.item = item
+        if len(time_and_index) == 1 and isinstance(time_and_index[0], (tuple, list)):
+            time_and_index = time_and_index[0]
+        if not isinstance(time_and_index, (tuple, list)):
+            time_and_index = (time_and_index,)
+        self.delay_time = time_and_index
+        if len(time_and_index) > 0:
+            key = f'{item}-prefetch-delay-{update_every}'
+            if not module.has_after_update(key):
+                delay = StateWithDelay(module, item, init=delay_init, interpolation=interpolation,
+                                       update_every=update_every, **kwargs)
+                module.add_after_update(key, not_receive_update_output(delay))
+            self.state_delay = module.get_after_update(key)
+            self.delay_info = self.state_delay.register_delay(*time_and_index)
+
+    def __call__(self, *args, **kwargs):
+        if len(self.delay_time) == 0:
+            return _prefetch_item(self).value
+        return self.state_delay.retrieve_at_step(*self.delay_info)
+
+
+class OutputDelayAt(Module):
+    """The module's update output read ``time`` ago (:748-800)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, module, *delay_time, delay_init=None, interpolation=None,
+                 update_every=None, **kwargs):
+        super().__init__()
+        assert isinstance(module, Dynamics), 'The module should be an instance of Dynamics.'
+        self.module = module
+        key = f'output-delay-{update_every}'
+        if not module.has_after_update(key):
+            delay = Delay(ShapeDtype(tuple(module.out_size), torch.float32), take_aware_unit=True,
+                          init=delay_init, interpolation=interpolation, update_every=update_every,
+                          **kwargs)
+            module.add_after_update(key, receive_update_output(delay))
+        self.out_delay = module.get_after_update(key)
+        self.delay_info = self.out_delay.register_delay(*delay_time)
+
+    def __call__(self, *args, **kwargs):
+        return self.out_delay.retrieve_at_step(*self.delay_info)

@@ -4,13 +4,17 @@
 (examples/105_COBA_HH_2007_braincell.py:54-82: ``N``, ``E`` fed by ``spk[:n_exc]``, ``I`` fed
 by ``spk[n_exc:]``) and returns an ``EINetRunner`` that advances the same network many steps
 per launch, with the constant external input ``inp`` the script passes as ``N(inp)``.
-``runner.write_back()`` copies the state back into the modules.
+``delay`` (ms) is the synaptic delay of a net whose projections read
+``N.prefetch_delay('spike', delay)()`` instead of the previous step's spikes; it becomes
+ceil(delay / dt) steps as brainstate's Delay computes them.  ``runner.write_back()`` copies the
+state back into the modules.
 """
 import numpy as np
 import torch
 
 from .. import environ
 from ..runner import EINetRunner
+from ._delay import _get_delay, _leaves
 from ._event import FixedPostNumConn
 from ._neurons import HH, LIFRef
 
@@ -29,13 +33,18 @@ def _proj_arrays(proj, n_pre, n):
     return idx, (float(w.reshape(())) if w.size == 1 else np.broadcast_to(w, idx.shape))
 
 
-def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0):
+def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     if len(neuron._channels) != 2 or neuron._channels[0] is not proj_e or \
             neuron._channels[1] is not proj_i:
         raise ValueError('proj_e and proj_i must be the two projections onto neuron, in order')
     if bool(neuron.spike.value.any()) or proj_e.syn.delta is not None or \
             proj_i.syn.delta is not None:
         raise NotImplementedError('fuse() starts from a state without pending spikes')
+    for hook in neuron.after_updates.values():   # spike histories of prefetch_delay readers
+        hist = getattr(hook, 'history', None)
+        if hist is not None and any(bool(h.any()) for h in _leaves(hist.value)):
+            raise NotImplementedError('fuse() starts from a state without pending spikes '
+                                      '(a delay history holds spikes)')
     n = neuron.num
     idx_e, w_e = _proj_arrays(proj_e, n_exc, n)
     idx_i, w_i = _proj_arrays(proj_i, n - n_exc, n)
@@ -49,7 +58,9 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0):
         model = 'lif'
     else:
         raise NotImplementedError(type(neuron).__name__)
-    r = EINetRunner(model, n, n_exc, idx_e, idx_i, w_e, w_i, neuron.params(float(inp)), V0)
+    delay_steps = _get_delay(delay, environ.get_dt())[1]
+    r = EINetRunner(model, n, n_exc, idx_e, idx_i, w_e, w_i, neuron.params(float(inp)), V0,
+                    delay_steps=delay_steps)
     # carry the current state over (the runner initialised HH gates at steady state)
     r.state['ge'].copy_(proj_e.syn.g.value)
     r.state['gi'].copy_(proj_i.syn.g.value)

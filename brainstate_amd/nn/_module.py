@@ -1,8 +1,10 @@
 """Module / Dynamics bases mirroring brainstate/nn/_module.py and brainstate/nn/_dynamics.py.
 
 ``Module.__call__`` runs ``update`` (brainstate/nn/_module.py:242-243).  ``Dynamics`` adds
-before-update hooks run ahead of ``update`` (brainstate/nn/_dynamics.py:477-500), which is
-how a post-synaptic neuron advances the synapses projecting onto it.
+before-update hooks run ahead of ``update`` and after-update hooks run after it
+(brainstate/nn/_dynamics.py:477-500): the first is how a post-synaptic neuron advances the
+synapses projecting onto it, the second how delays record a state after every step
+(``prefetch_delay`` / ``output_delay``, :222-298).
 """
 from collections import OrderedDict
 
@@ -64,6 +66,7 @@ class Dynamics(Module):
         self.in_size = _size(in_size)
         self.out_size = self.in_size
         self._before_updates = OrderedDict()
+        self._after_updates = OrderedDict()
 
     @property
     def varshape(self):
@@ -73,35 +76,88 @@ class Dynamics(Module):
     def num(self):
         return int(np.prod(self.in_size))
 
+    @property
+    def before_updates(self):
+        return self._before_updates
+
+    @property
+    def after_updates(self):
+        return self._after_updates
+
     def add_before_update(self, key, fn):
         if key in self._before_updates:
-            raise KeyError(f'before-update "{key}" already registered')
+            raise KeyError(f'{key} has been registered in before_updates of {self}')
         self._before_updates[key] = fn
+
+    def add_after_update(self, key, fn):
+        if key in self._after_updates:
+            raise KeyError(f'{key} has been registered in after_updates of {self}')
+        self._after_updates[key] = fn
+
+    def get_before_update(self, key):
+        if key not in self._before_updates:
+            raise KeyError(f'{key} is not registered in before_updates of {self}')
+        return self._before_updates[key]
+
+    def get_after_update(self, key):
+        if key not in self._after_updates:
+            raise KeyError(f'{key} is not registered in after_updates of {self}')
+        return self._after_updates[key]
 
     def has_before_update(self, key):
         return key in self._before_updates
 
+    def has_after_update(self, key):
+        return key in self._after_updates
+
+    def prefetch(self, item):
+        """Reference to a state that may not exist yet (brainstate/nn/_dynamics.py:192-220)."""
+        from ._delay import Prefetch
+        return Prefetch(self, item)
+
+    def prefetch_delay(self, state, *time_and_index, init=None, interpolation=None, **kwargs):
+        """The state ``time`` ago, recorded after every update (:222-262)."""
+        from ._delay import PrefetchDelayAt
+        return PrefetchDelayAt(self, state, *time_and_index, delay_init=init,
+                               interpolation=interpolation, **kwargs)
+
+    def output_delay(self, *time_and_index, init=None, interpolation=None, **kwargs):
+        """The update's output ``time`` ago (:264-298)."""
+        from ._delay import OutputDelayAt
+        return OutputDelayAt(self, *time_and_index, interpolation=interpolation,
+                             delay_init=init, **kwargs)
+
     def children(self):
         yield from super().children()
-        for fn in self._before_updates.values():
+        for fn in list(self._before_updates.values()) + list(self._after_updates.values()):
             if isinstance(fn, Module):
                 yield fn
 
     def __call__(self, *args, **kwargs):
         for fn in self._before_updates.values():
-            fn()
-        return self.update(*args, **kwargs)
+            if hasattr(fn, '_receive_update_input'):
+                fn(*args, **kwargs)
+            else:
+                fn()
+        ret = self.update(*args, **kwargs)
+        for fn in self._after_updates.values():
+            if hasattr(fn, '_not_receive_update_output'):
+                fn()
+            else:
+                fn(ret)
+        return ret
 
 
 def init_all_states(target, *args, **kwargs):
     """Call ``init_state`` on every module of the tree (brainstate/nn/_collective_ops.py:299-346).
 
-    Synapses first, then everything else, so that neurons find their conductance channels
-    initialised.
+    Synapses first, delays last (they size their history from the states they record, as
+    brainstate's call_order(3) on Delay.init_state arranges), everything else in between.
     """
     nodes = target.nodes()
     first = [m for m in nodes if getattr(m, '_init_first', False)]
-    rest = [m for m in nodes if not getattr(m, '_init_first', False)]
-    for m in first + rest:
+    last = [m for m in nodes if getattr(m, '_init_last', False)]
+    rest = [m for m in nodes if m not in first and m not in last]
+    for m in first + rest + last:
         m.init_state(*args, **kwargs)
     return target

@@ -219,6 +219,33 @@ BS_API int bs_net_grid_blocks(const bs_net* net);
  * hit its spin limit (results invalid), or a positive status on a call failure. */
 BS_API int bs_net_error(const void* workspace, bs_stream_t stream);
 
+/* ---------------------------------------------------------------- ring-buffer delay
+ * Device side of brainstate's Delay / StateWithDelay (brainstate/nn/_delay.py:399-1079): a
+ * history of `length` slots, slot-major, each `slot_elems` elements (a slot holds one value of
+ * the delayed state, batch included).  The ring index arithmetic -- write slot
+ * write_ptr // update_every_step, newest slot cur = (write_ptr - 1) // update_every_step,
+ * read slot (cur - step) mod length (:772-790, :909-928) -- is the caller's; these copy.
+ *
+ * bs_delay_write: copy `slot_bytes` from src into slot `slot` (replaces
+ * `history.at[idx].set(value)`, _delay.py:917-921). */
+BS_API int bs_delay_write(void* hist, int32_t length, int64_t slot_bytes, int32_t slot,
+                          const void* src, bs_stream_t stream);
+/* bs_delay_gather: out[j] = hist[((cur - s_j) mod length) * slot_elems + c_j] for elements of
+ * elem_bytes in {1, 2, 4, 8}, with s_j = steps ? steps[j] : step and c_j = cols ? cols[j] : j
+ * (cols, when given, must lie in [0, slot_elems)).  Replaces `retrieve_at_step(delay_step,
+ * *indices)` (:762-790): a scalar step copies one slot; step / index arrays are the fancy
+ * indexing of vector delays, broadcast and flattened to (steps, cols) by the caller. */
+BS_API int bs_delay_gather(const void* hist, int32_t length, int64_t slot_elems,
+                           int32_t elem_bytes, int32_t cur, int32_t step, const int32_t* steps,
+                           const int64_t* cols, int64_t n_out, void* out, bs_stream_t stream);
+/* bs_delay_taps_f32: out[j] = sum_{q < taps} weights[q] * hist[slots[q] * slot_elems + c_j],
+ * products rounded then added left to right; slots / weights are host arrays of at most 4.
+ * Replaces the continuous-time reads of `retrieve_at_time` (:798-907) with the interpolation
+ * methods of :163-338 (linear: 2 taps; polynomial2: 3; cubic, hermite, polynomial3: 4). */
+BS_API int bs_delay_taps_f32(const float* hist, int32_t length, int64_t slot_elems, int32_t taps,
+                             const int32_t* slots, const float* weights, const int64_t* cols,
+                             int64_t n_out, float* out, bs_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
