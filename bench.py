@@ -233,6 +233,36 @@ def bench_hh(args):
              'frac': b / t / PEAK_HBM, 'firing_frac_per_step': spikes / (T * n)}]
 
 
+def bench_conn(args):
+    """Connectivity of config [3] (E 800k x 100 from seed 101, I 200k x 100 from seed 102,
+    targets in [0, 1M)) drawn on the device, bit-equal to numpy's RandomState stream, against
+    numpy on the host plus the copy to the device."""
+    import torch
+    from brainstate_amd import ops
+    n = 1_000_000
+    ops.conn_fixed_num(1, 1000, 100, n)
+    torch.cuda.synchronize()
+    dev = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ie, _ = ops.conn_fixed_num(101, 800_000, 100, n)
+        ii, _ = ops.conn_fixed_num(102, 200_000, 100, n)
+        torch.cuda.synchronize()
+        dev.append(time.perf_counter() - t0)
+    t0 = time.perf_counter()
+    he = np.random.RandomState(101).randint(0, n, size=(800_000, 100)).astype(np.int32)
+    hi = np.random.RandomState(102).randint(0, n, size=(200_000, 100)).astype(np.int32)
+    host = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    de, di = torch.from_numpy(he).cuda(), torch.from_numpy(hi).cuda()
+    torch.cuda.synchronize()
+    h2d = time.perf_counter() - t0
+    equal = bool(torch.equal(de, ie) and torch.equal(di, ii))
+    return [{'workload': 'conn_fixed_num_1e8 (configs[2] connectivity)', 'synapses': n * 100,
+             'device_ms': min(dev) * 1e3, 'numpy_ms': host * 1e3, 'h2d_ms': h2d * 1e3,
+             'speedup': (host + h2d) / min(dev), 'bit_equal_to_numpy': equal}]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -251,11 +281,12 @@ def main():
     ap.add_argument('--summarize', default=None,
                     help='only print a text summary of a rocprofv3 results database')
     ap.add_argument('--workload', default='coba_lif_1m',
-                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh'],
+                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn'],
                     help='coba_lif_1m is the reported line; the others measure the other configs')
     args = ap.parse_args()
     if args.workload != 'coba_lif_1m':
-        fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh}
+        fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh,
+              'conn': bench_conn}
         for line in fn[args.workload](args):
             print(json.dumps(line), flush=True)
         return

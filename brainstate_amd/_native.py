@@ -46,6 +46,12 @@ class HhState(ctypes.Structure):
 
 # name -> (restype, argtypes); every symbol declared in include/brainstate_amd.h
 SIGNATURES = {
+    'bs_conn_fixed_num_workspace_size': (c_size, [c_i32, c_i32, c_i32, c_i32]),
+    'bs_conn_fixed_num': (ctypes.c_int, [ctypes.c_uint32, c_i32, c_i32, c_i32, c_vp,
+                                         ctypes.c_double, c_vp, c_vp, c_size, c_vp]),
+    'bs_csr_from_selected': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    'bs_conn_fixed_num_unique': (ctypes.c_int, [ctypes.c_uint64, c_i32, c_i32, c_i32, c_vp,
+                                                c_vp]),
     'bs_delay_write': (ctypes.c_int, [c_vp, c_i32, ctypes.c_int64, c_i32, c_vp, c_vp]),
     'bs_delay_gather': (ctypes.c_int, [c_vp, c_i32, ctypes.c_int64, c_i32, c_i32, c_i32, c_vp,
                                        c_vp, ctypes.c_int64, c_vp, c_vp]),

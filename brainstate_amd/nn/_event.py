@@ -183,10 +183,14 @@ class FixedNumConn(Module):
         self.conn_num = conn_num
         self.seed = seed
         self.allow_multi_conn = allow_multi_conn
-        if self.conn_num >= 1:
+        if self.conn_num >= 1 and seed is not None:
+            self._build_on_device(n_pre=self.in_size[-1], n_post=self.out_size[-1],
+                                  conn_weight=conn_weight, afferent_ratio=afferent_ratio,
+                                  param_type=param_type)
+        elif self.conn_num >= 1:
             n_post = self.out_size[-1]
             n_pre = self.in_size[-1]
-            rng = np.random if seed is None else np.random.RandomState(seed)
+            rng = np.random  # seed=None: the global numpy stream, as the reference (:163)
             if allow_multi_conn:
                 indices = rng.randint(0, n_post, size=(n_pre, self.conn_num))
             else:
@@ -215,6 +219,31 @@ class FixedNumConn(Module):
                                 shape=(n_pre, n_post))
         else:
             self.weight = FakeState(init.param(conn_weight, (), allow_none=False))
+
+    def _build_on_device(self, n_pre, n_post, conn_weight, afferent_ratio, param_type):
+        """Index draws on the device (bs_conn_fixed_num*): with replacement they equal
+        RandomState(seed).randint(0, n_post, (n_pre, K)) bit for bit (:163-168), and the
+        afferent selection is the same stream's next random(n_pre) < afferent_ratio (:186).
+        Without replacement (the reference's JAX draws, :39-62) the rows come from Philox."""
+        k, seed = self.conn_num, int(self.seed)
+        ratio = None if afferent_ratio == 1. else float(afferent_ratio)
+        if self.allow_multi_conn:
+            indices, sel = ops.conn_fixed_num(seed, n_pre, k, n_post, ratio)
+        else:
+            if k > n_post:
+                raise ValueError('conn_num exceeds n_post without replacement')
+            indices = ops.conn_fixed_num_unique(seed, n_pre, k, n_post)
+            sel = None if ratio is None else ops.conn_fixed_num(seed, n_pre, 0, n_post, ratio)[1]
+        if ratio is None:
+            w = init.param(conn_weight, (n_pre, k), allow_none=False)
+            self.weight = param_type(w)
+            self.conn = FixedPostNumConn((w, indices), shape=(n_pre, n_post))
+        else:
+            self.pre_selected = sel.cpu().numpy()
+            indptr, csr_indices = ops.csr_from_selected(indices, sel)
+            w = init.param(conn_weight, (csr_indices.numel(),), allow_none=False)
+            self.weight = param_type(w)
+            self.conn = CSR((w, csr_indices, indptr), shape=(n_pre, n_post))
 
     def _matvec(self, x, value=False):
         if self.conn_num < 1:

@@ -243,6 +243,56 @@ def event_dense(spk, W, float_as_event=True, out=None):
     return out[0] if squeeze else out
 
 
+def conn_fixed_num(seed, n_pre, k, n_post, afferent_ratio=None, device=None):
+    """numpy.random.RandomState(seed).randint(0, n_post, (n_pre, k)) drawn on the device
+    (int32 [n_pre, k]) and, if ``afferent_ratio`` is given, the next ``random(n_pre) <
+    afferent_ratio`` of the same stream (bool [n_pre])."""
+    N.require_gpu()
+    dev = torch.device('cuda', torch.cuda.current_device()) if device is None else device
+    if not 0 <= int(seed) < 2 ** 32:
+        raise ValueError('Seed must be between 0 and 2**32 - 1')
+    sel_on = afferent_ratio is not None
+    nbytes = int(N.lib().bs_conn_fixed_num_workspace_size(int(n_pre), int(k), int(n_post),
+                                                          int(sel_on)))
+    if nbytes == 0:
+        N.check(N.BS_ERR_INVALID, 'bs_conn_fixed_num_workspace_size')
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    idx = torch.empty((int(n_pre), int(k)), dtype=torch.int32, device=dev)
+    sel = torch.empty(int(n_pre), dtype=torch.uint8, device=dev) if sel_on else None
+    N.check(N.lib().bs_conn_fixed_num(int(seed), int(n_pre), int(k), int(n_post), N.ptr(idx),
+                                      float(afferent_ratio) if sel_on else 0.0, N.ptr(sel),
+                                      N.ptr(ws), nbytes, N.stream_handle(dev)),
+            'bs_conn_fixed_num')
+    return idx, (sel.view(torch.bool) if sel_on else None)
+
+
+def csr_from_selected(indices, selected):
+    """(indptr int32 [n_pre + 1], indices int32 [nnz]) of the selected rows of ``indices``."""
+    n_pre, k = indices.shape
+    dev = indices.device
+    sel = selected.contiguous().view(torch.uint8)
+    indptr = torch.empty(n_pre + 1, dtype=torch.int32, device=dev)
+    s = N.stream_handle(dev)
+    N.check(N.lib().bs_csr_from_selected(N.ptr(indices), n_pre, k, N.ptr(sel), N.ptr(indptr),
+                                         None, s), 'bs_csr_from_selected')
+    nnz = int(indptr[-1].item())
+    out = torch.empty(nnz, dtype=torch.int32, device=dev)
+    N.check(N.lib().bs_csr_from_selected(N.ptr(indices.contiguous()), n_pre, k, N.ptr(sel),
+                                         N.ptr(indptr), N.ptr(out), s), 'bs_csr_from_selected')
+    return indptr, out
+
+
+def conn_fixed_num_unique(seed, n_pre, k, n_post, device=None):
+    """k distinct targets per row (int32 [n_pre, k]), Philox4x32-10 keyed by ``seed``."""
+    N.require_gpu()
+    dev = torch.device('cuda', torch.cuda.current_device()) if device is None else device
+    idx = torch.empty((int(n_pre), int(k)), dtype=torch.int32, device=dev)
+    N.check(N.lib().bs_conn_fixed_num_unique(int(seed) & (2 ** 64 - 1), int(n_pre), int(k),
+                                             int(n_post), N.ptr(idx), N.stream_handle(dev)),
+            'bs_conn_fixed_num_unique')
+    return idx
+
+
 def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., I_ext=20.,
                E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1):
     q = float(tau_ref) / float(dt)

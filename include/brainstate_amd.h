@@ -219,6 +219,31 @@ BS_API int bs_net_grid_blocks(const bs_net* net);
  * hit its spin limit (results invalid), or a positive status on a call failure. */
 BS_API int bs_net_error(const void* workspace, bs_stream_t stream);
 
+/* ---------------------------------------------------------------- connectivity on the device
+ * FixedNumConn's index draws (brainstate/nn/_event_fixedprob.py:142-196) without the host.
+ *
+ * bs_conn_fixed_num: indices [n_pre * k] equal, bit for bit, to
+ * numpy.random.RandomState(seed).randint(0, n_post, (n_pre, k)) (:163-168); when `selected`
+ * is given, selected[i] = (rng.random(n_pre) < afferent_ratio)[i] drawn next from the same
+ * stream (:186).  With k == 0 `selected` is the first n_pre draws of random().  Synchronises
+ * `stream` once (the generator reports how far the stream was consumed).  Workspace:
+ * bs_conn_fixed_num_workspace_size (about 4 B per draw). */
+BS_API size_t bs_conn_fixed_num_workspace_size(int32_t n_pre, int32_t k, int32_t n_post,
+                                               int32_t with_selection);
+BS_API int bs_conn_fixed_num(uint32_t seed, int32_t n_pre, int32_t k, int32_t n_post,
+                             int32_t* indices, double afferent_ratio, uint8_t* selected,
+                             void* workspace, size_t workspace_bytes, bs_stream_t stream);
+/* CSR of the selected rows (:185-196): indptr[i + 1] = k * (selected rows <= i); when `out` is
+ * given, the selected rows of indices [n_pre, k] are copied to out[indptr[i] ..] in order. */
+BS_API int bs_csr_from_selected(const int32_t* indices, int32_t n_pre, int32_t k,
+                                const uint8_t* selected, int32_t* indptr, int32_t* out,
+                                bs_stream_t stream);
+/* allow_multi_conn=False (init_indices_without_replace, :39-62): k <= 2048 distinct targets
+ * per row, uniform over [0, n_post), from Philox4x32-10 keyed by `seed`.  The reference draws
+ * these with its JAX generator, whose stream is not reproduced. */
+BS_API int bs_conn_fixed_num_unique(uint64_t seed, int32_t n_pre, int32_t k, int32_t n_post,
+                                    int32_t* indices, bs_stream_t stream);
+
 /* ---------------------------------------------------------------- ring-buffer delay
  * Device side of brainstate's Delay / StateWithDelay (brainstate/nn/_delay.py:399-1079): a
  * history of `length` slots, slot-major, each `slot_elems` elements (a slot holds one value of
