@@ -233,6 +233,50 @@ def bench_hh(args):
              'frac': b / t / PEAK_HBM, 'firing_frac_per_step': spikes / (T * n)}]
 
 
+def bench_batch(args):
+    """Batched simulation: B = 64 replicas of config [1] (4000 COBA-LIF neurons, K = 80,
+    homogeneous 0.6 / 6.7, each replica its own V0) in one runner over the block-diagonal
+    union, against one replica alone (4 workgroups) and the 64 replicas one after another."""
+    import torch
+    from brainstate_amd import ops
+    from brainstate_amd.nn._fuse import _union_perm
+    from brainstate_amd.runner import EINetRunner
+    B, n, n_exc, T = 64, 4000, 3200, 10000
+    idx_e = np.random.RandomState(1).randint(0, n, size=(n_exc, 80)).astype(np.int32)
+    idx_i = np.random.RandomState(2).randint(0, n, size=(n - n_exc, 80)).astype(np.int32)
+    V0s = np.stack([np.random.RandomState(300 + b).uniform(-60., -50., n).astype(np.float32)
+                    for b in range(B)])
+    perm = _union_perm(B, n, n_exc)
+    ue = np.concatenate([perm[b][idx_e] for b in range(B)]).astype(np.int32)
+    ui = np.concatenate([perm[b][idx_i] for b in range(B)]).astype(np.int32)
+    V0u = np.empty(B * n, np.float32)
+    V0u[perm.reshape(-1)] = V0s.reshape(-1)
+
+    def timed(r, steps):
+        c = torch.zeros(steps, dtype=torch.int32, device='cuda')
+        r.run(steps, counts=c)
+        torch.cuda.synchronize()
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        r.run(steps, counts=c)
+        e.record()
+        torch.cuda.synchronize()
+        r.check()
+        return a.elapsed_time(e) / 1e3, int(c.sum().item())
+
+    union = EINetRunner('lif', B * n, B * n_exc, ue, ui, 0.6, 6.7, ops.lif_params(), V0u)
+    t_u, spk_u = timed(union, T)
+    one = EINetRunner('lif', n, n_exc, idx_e, idx_i, 0.6, 6.7, ops.lif_params(), V0s[0])
+    t_1, spk_1 = timed(one, T)
+    return [{'workload': f'coba_lif_4000 x {B} replicas (configs[0], batched)', 'replicas': B,
+             'steps': T, 'union_us_per_step': t_u / T * 1e6,
+             'union_GSOPs': spk_u * 80 / t_u / 1e9, 'union_grid_workgroups': union.grid_blocks,
+             'single_us_per_step': t_1 / T * 1e6, 'single_GSOPs': spk_1 * 80 / t_1 / 1e9,
+             'replica_steps_per_s_union': B * T / t_u,
+             'replica_steps_per_s_sequential': T / t_1,
+             'speedup_vs_sequential': (B * t_1) / t_u}]
+
+
 def bench_conn(args):
     """Connectivity of config [3] (E 800k x 100 from seed 101, I 200k x 100 from seed 102,
     targets in [0, 1M)) drawn on the device, bit-equal to numpy's RandomState stream, against
@@ -281,12 +325,12 @@ def main():
     ap.add_argument('--summarize', default=None,
                     help='only print a text summary of a rocprofv3 results database')
     ap.add_argument('--workload', default='coba_lif_1m',
-                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn'],
+                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn', 'batch'],
                     help='coba_lif_1m is the reported line; the others measure the other configs')
     args = ap.parse_args()
     if args.workload != 'coba_lif_1m':
         fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh,
-              'conn': bench_conn}
+              'conn': bench_conn, 'batch': bench_batch}
         for line in fn[args.workload](args):
             print(json.dumps(line), flush=True)
         return

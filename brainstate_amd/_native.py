@@ -46,6 +46,10 @@ class HhState(ctypes.Structure):
 
 # name -> (restype, argtypes); every symbol declared in include/brainstate_amd.h
 SIGNATURES = {
+    'bs_event_matvec_batch_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_i32,
+                                                 c_vp, c_f32, c_i32, c_vp, c_i32, c_vp]),
+    'bs_value_matvec_batch_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp,
+                                                 c_f32, c_i32, c_vp, c_i32, c_vp]),
     'bs_conn_fixed_num_workspace_size': (c_size, [c_i32, c_i32, c_i32, c_i32]),
     'bs_conn_fixed_num': (ctypes.c_int, [ctypes.c_uint32, c_i32, c_i32, c_i32, c_vp,
                                          ctypes.c_double, c_vp, c_vp, c_size, c_vp]),

@@ -162,12 +162,16 @@ constexpr int kLdsRatio = 4;
 constexpr int kRowsCap = 1024;
 
 // kVal: each event is weighted by its spike value (sum_i x[i] * w[i,k]); otherwise by 1.
+// Batched: blockIdx.y selects the batch row (spike row b at spk + b * n_pre, output row at
+// out + b * n_post); the connectivity is shared by every row.
 template <typename T, bool kCsr, bool kHet, bool kVal = false>
 __global__ __launch_bounds__(kBlock) void k_matvec(const T* __restrict__ spk, int32_t n_pre,
                                                    int32_t rows, const int32_t* __restrict__ indptr,
                                                    const int32_t* __restrict__ indices, int32_t k,
                                                    const float* __restrict__ w, float w_homo,
                                                    int32_t n_post, float* __restrict__ out) {
+  spk += (int64_t)blockIdx.y * n_pre;
+  out += (int64_t)blockIdx.y * n_post;
   __shared__ int32_t s_rows[kRowsCap];
   __shared__ int32_t s_wave[kBlock / BS_WAVE];
   __shared__ int32_t s_nev;
@@ -407,32 +411,34 @@ namespace {
 
 // Shared launcher of the fused mat-vec (event or value-weighted).
 template <bool kVal>
-int matvec_launch(const void* spk, int32_t spk_dtype, int32_t n_pre, const int32_t* indptr,
-                  const int32_t* indices, int32_t k, const float* w, float w_homo,
-                  int32_t n_post, float* out, int32_t accumulate, hipStream_t s,
+int matvec_launch(const void* spk, int32_t spk_dtype, int32_t batch, int32_t n_pre,
+                  const int32_t* indptr, const int32_t* indices, int32_t k, const float* w,
+                  float w_homo, int32_t n_post, float* out, int32_t accumulate, hipStream_t s,
                   const char* who) {
   BS_CHECK_ARG(n_pre >= 0 && n_post >= 0, "%s: negative size", who);
+  BS_CHECK_ARG(batch >= 1 && batch <= 65535, "%s: batch %d outside [1, 65535]", who, batch);
   BS_CHECK_ARG(indptr != nullptr || k >= 0, "%s: k=%d < 0", who, k);
   BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32, "%s: unknown spike dtype %d",
                who, spk_dtype);
   if (n_post > 0) BS_CHECK_ARG(out != nullptr, "%s: out is NULL", who);
   if (!accumulate) {
-    int rc = bs_fill_f32(out, n_post, 0.0f, s);
+    int rc = bs_fill_f32(out, (int64_t)batch * n_post, 0.0f, s);
     if (rc) return rc;
   }
   if (n_pre == 0 || n_post == 0 || (indptr == nullptr && k == 0)) return BS_OK;
   BS_CHECK_ARG(spk && indices, "%s: NULL pointer", who);
-  // rows per workgroup: enough workgroups to fill the chip, at most kRowsCap rows each
+  // rows per workgroup: enough workgroups (over all batch rows) to fill the chip, at most
+  // kRowsCap rows each
   int64_t g = (int64_t)bs_num_cus() * 4;
-  int64_t rows = ((int64_t)n_pre + g - 1) / g;
+  int64_t rows = ((int64_t)n_pre * batch + g - 1) / g;
   if (rows < 64) rows = 64;
   if (rows > kRowsCap) rows = kRowsCap;
   g = ((int64_t)n_pre + rows - 1) / rows;
   const size_t shm = n_post <= kLdsPosts ? (size_t)n_post * sizeof(float) : 0;
   const bool het = w != nullptr, csr = indptr != nullptr;
-#define BS_MV(T, C, H)                                                                   \
-  k_matvec<T, C, H, kVal><<<(int)g, kBlock, shm, s>>>((const T*)spk, n_pre, (int32_t)rows, \
-                                                      indptr, indices, k, w, w_homo, n_post, out)
+#define BS_MV(T, C, H)                                                                \
+  k_matvec<T, C, H, kVal><<<dim3((unsigned)g, (unsigned)batch), kBlock, shm, s>>>(       \
+      (const T*)spk, n_pre, (int32_t)rows, indptr, indices, k, w, w_homo, n_post, out)
   if (spk_dtype == BS_SPK_U8) {
     if (csr) { if (het) BS_MV(uint8_t, true, true); else BS_MV(uint8_t, true, false); }
     else { if (het) BS_MV(uint8_t, false, true); else BS_MV(uint8_t, false, false); }
@@ -452,8 +458,19 @@ extern "C" int bs_event_matvec_f32(const void* spk, int32_t spk_dtype, int32_t n
                                    const float* w, float w_homo, int32_t n_post, float* out,
                                    int32_t accumulate, bs_stream_t stream) {
   bs_clear_error();
-  return matvec_launch<false>(spk, spk_dtype, n_pre, indptr, indices, k, w, w_homo, n_post, out,
-                              accumulate, bs_stream(stream), "bs_event_matvec_f32");
+  return matvec_launch<false>(spk, spk_dtype, 1, n_pre, indptr, indices, k, w, w_homo, n_post,
+                              out, accumulate, bs_stream(stream), "bs_event_matvec_f32");
+}
+
+extern "C" int bs_event_matvec_batch_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                         int32_t n_pre, const int32_t* indptr,
+                                         const int32_t* indices, int32_t k, const float* w,
+                                         float w_homo, int32_t n_post, float* out,
+                                         int32_t accumulate, bs_stream_t stream) {
+  bs_clear_error();
+  return matvec_launch<false>(spk, spk_dtype, batch, n_pre, indptr, indices, k, w, w_homo,
+                              n_post, out, accumulate, bs_stream(stream),
+                              "bs_event_matvec_batch_f32");
 }
 
 extern "C" int bs_value_matvec_f32(const float* x, int32_t n_pre, const int32_t* indptr,
@@ -461,8 +478,17 @@ extern "C" int bs_value_matvec_f32(const float* x, int32_t n_pre, const int32_t*
                                    float w_homo, int32_t n_post, float* out, int32_t accumulate,
                                    bs_stream_t stream) {
   bs_clear_error();
-  return matvec_launch<true>(x, BS_SPK_F32, n_pre, indptr, indices, k, w, w_homo, n_post, out,
-                             accumulate, bs_stream(stream), "bs_value_matvec_f32");
+  return matvec_launch<true>(x, BS_SPK_F32, 1, n_pre, indptr, indices, k, w, w_homo, n_post,
+                             out, accumulate, bs_stream(stream), "bs_value_matvec_f32");
+}
+
+extern "C" int bs_value_matvec_batch_f32(const float* x, int32_t batch, int32_t n_pre,
+                                         const int32_t* indptr, const int32_t* indices, int32_t k,
+                                         const float* w, float w_homo, int32_t n_post,
+                                         float* out, int32_t accumulate, bs_stream_t stream) {
+  bs_clear_error();
+  return matvec_launch<true>(x, BS_SPK_F32, batch, n_pre, indptr, indices, k, w, w_homo, n_post,
+                             out, accumulate, bs_stream(stream), "bs_value_matvec_batch_f32");
 }
 
 extern "C" int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,

@@ -48,12 +48,13 @@ def _kw(w):
 class _EventMatvecFn(torch.autograd.Function):
     """out = mat-vec of spk with weights w over (indices, indptr): every nonzero spike is one
     event (value=False) or weighs by its value (value=True).  Differentiable in the spike
-    values and the weights, with the derivatives of the value formulation in both modes."""
+    values and the weights, with the derivatives of the value formulation in both modes.
+    ``spk`` may carry leading batch dimensions ([..., n_pre] -> [..., n_post])."""
 
     @staticmethod
     def forward(spk, w, indices, indptr, n_post, value=False):
         if value:
-            return ops.value_matvec(spk.reshape(-1), indices, _kw(w), n_post, indptr=indptr)
+            return ops.value_matvec(spk, indices, _kw(w), n_post, indptr=indptr)
         return ops.event_matvec(spk, indices, _kw(w), n_post, indptr=indptr)
 
     @staticmethod
@@ -66,11 +67,19 @@ class _EventMatvecFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         spk, w, indices, indptr = ctx.saved_tensors
-        gs, gw = ops.event_matvec_vjp(spk, indices, _kw(w), ctx.n_post, g, indptr=indptr,
-                                      need_spk=ctx.needs_input_grad[0],
-                                      need_w=ctx.needs_input_grad[1])
-        if gs is not None:
-            gs = gs.reshape(spk.shape).to(spk.dtype)
+        need_s, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        n_pre = spk.shape[-1] if spk.dim() else 1
+        rows = spk.reshape(-1, n_pre)
+        grows = g.reshape(-1, ctx.n_post)
+        gs_rows, gw = [], None
+        for b in range(rows.shape[0]):   # per batch row; weight gradients add up
+            gs_b, gw_b = ops.event_matvec_vjp(rows[b], indices, _kw(w), ctx.n_post,
+                                              grows[b].contiguous(), indptr=indptr,
+                                              need_spk=need_s, need_w=need_w)
+            gs_rows.append(gs_b)
+            if gw_b is not None:
+                gw = gw_b if gw is None else gw + gw_b
+        gs = torch.stack(gs_rows).reshape(spk.shape).to(spk.dtype) if need_s else None
         if gw is not None:
             gw = gw.reshape(w.shape)
         return gs, gw, None, None, None, None
@@ -78,12 +87,13 @@ class _EventMatvecFn(torch.autograd.Function):
     @staticmethod
     def jvp(ctx, dspk, dw, *_):
         spk, w, indices, indptr = ctx.saved_tensors
-        t = torch.zeros(ctx.n_post, dtype=torch.float32, device=indices.device)
+        lead = tuple(spk.shape[:-1])
+        t = torch.zeros(lead + (ctx.n_post,), dtype=torch.float32, device=indices.device)
         if dspk is not None:
-            ops.value_matvec(dspk.reshape(-1), indices, _kw(w), ctx.n_post, indptr=indptr, out=t,
-                             accumulate=True)
+            ops.value_matvec(dspk.reshape(spk.shape), indices, _kw(w), ctx.n_post,
+                             indptr=indptr, out=t, accumulate=True)
         if dw is not None:
-            ops.value_matvec(spk.reshape(-1).to(torch.float32), indices, _kw(dw), ctx.n_post,
+            ops.value_matvec(spk.to(torch.float32), indices, _kw(dw), ctx.n_post,
                              indptr=indptr, out=t, accumulate=True)
         return t
 
@@ -118,7 +128,7 @@ class FixedPostNumConn:
             return _EventMatvecFn.apply(spk, w, self.indices, None, n_post, value)
         wk = _kw(w) if torch.is_tensor(w) else w
         if value:
-            return ops.value_matvec(spk.reshape(-1), self.indices, wk, n_post)
+            return ops.value_matvec(spk, self.indices, wk, n_post)
         return ops.event_matvec(spk, self.indices, wk, n_post)
 
 
@@ -142,7 +152,7 @@ class CSR:
             return _EventMatvecFn.apply(spk, w, self.indices, self.indptr, n_post, value)
         wk = _kw(w) if torch.is_tensor(w) else w
         if value:
-            return ops.value_matvec(spk.reshape(-1), self.indices, wk, n_post, indptr=self.indptr)
+            return ops.value_matvec(spk, self.indices, wk, n_post, indptr=self.indptr)
         return ops.event_matvec(spk, self.indices, wk, n_post, indptr=self.indptr)
 
 
@@ -254,11 +264,7 @@ class FixedNumConn(Module):
         x = x if torch.is_tensor(x) else _to_dev(x, torch.float32)
         if x.device.type != 'cuda':
             x = x.to(_device())
-        if x.dim() == 1:
-            return conn.matvec_events(x, value)
-        flat = x.reshape(-1, x.shape[-1])
-        out = torch.stack([conn.matvec_events(row, value) for row in flat])
-        return out.reshape(tuple(x.shape[:-1]) + (self.out_size[-1],))
+        return conn.matvec_events(x, value)   # [..., n_pre] -> [..., n_post], one launch
 
     def update(self, x):
         """``x @ conn`` (:202-209): bool spikes are events; any other dtype is a

@@ -6,8 +6,10 @@ by ``spk[n_exc:]``) and returns an ``EINetRunner`` that advances the same networ
 per launch, with the constant external input ``inp`` the script passes as ``N(inp)``.
 ``delay`` (ms) is the synaptic delay of a net whose projections read
 ``N.prefetch_delay('spike', delay)()`` instead of the previous step's spikes; it becomes
-ceil(delay / dt) steps as brainstate's Delay computes them.  ``runner.write_back()`` copies the
-state back into the modules.
+ceil(delay / dt) steps as brainstate's Delay computes them.  A net initialised with
+``init_all_states(..., batch_size=B)`` ([B, n] states, the replicas sharing connectivity)
+becomes one runner over the block-diagonal union of the B replicas.  ``runner.write_back()``
+copies the state back into the modules.
 """
 import numpy as np
 import torch
@@ -33,6 +35,14 @@ def _proj_arrays(proj, n_pre, n):
     return idx, (float(w.reshape(())) if w.size == 1 else np.broadcast_to(w, idx.shape))
 
 
+def _union_perm(B, n, n_exc):
+    """Runner index of neuron j of replica b ([B, n]): the runner takes excitatory neurons
+    first, so the union of B replicas lists every replica's E neurons, then every I neuron."""
+    j = np.arange(n, dtype=np.int64)[None, :]
+    b = np.arange(B, dtype=np.int64)[:, None]
+    return np.where(j < n_exc, b * n_exc + j, B * n_exc + b * (n - n_exc) + (j - n_exc))
+
+
 def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     if len(neuron._channels) != 2 or neuron._channels[0] is not proj_e or \
             neuron._channels[1] is not proj_i:
@@ -46,12 +56,30 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
             raise NotImplementedError('fuse() starts from a state without pending spikes '
                                       '(a delay history holds spikes)')
     n = neuron.num
+    Vs = neuron.V.value
+    B = int(Vs.shape[0]) if Vs.dim() == 2 else 1   # init_all_states(batch_size=B)
     idx_e, w_e = _proj_arrays(proj_e, n_exc, n)
     idx_i, w_i = _proj_arrays(proj_i, n - n_exc, n)
     if np.ndim(w_e) != np.ndim(w_i):   # one heterogeneous -> both per synapse
         w_e = np.broadcast_to(np.float32(w_e), idx_e.shape)
         w_i = np.broadcast_to(np.float32(w_i), idx_i.shape)
-    V0 = neuron.V.value.detach().cpu().numpy()
+    perm = _union_perm(B, n, n_exc)
+    if B > 1:   # block-diagonal union of the replicas, one runner
+        idx_e = np.concatenate([perm[b][idx_e] for b in range(B)]).astype(np.int32)
+        idx_i = np.concatenate([perm[b][idx_i] for b in range(B)]).astype(np.int32)
+        if np.ndim(w_e):
+            w_e, w_i = np.tile(w_e, (B, 1)), np.tile(w_i, (B, 1))
+    pt = torch.as_tensor(perm.reshape(-1), device=Vs.device)
+
+    def to_runner(x):
+        out = torch.empty(B * n, dtype=x.dtype, device=x.device)
+        out[pt] = x.reshape(-1)
+        return out
+
+    def from_runner(x):
+        return x[pt].reshape(Vs.shape).clone()
+
+    V0 = to_runner(Vs).cpu().numpy()
     if isinstance(neuron, HH):
         model = 'hh'
     elif isinstance(neuron, LIFRef):
@@ -59,30 +87,31 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     else:
         raise NotImplementedError(type(neuron).__name__)
     delay_steps = _get_delay(delay, environ.get_dt())[1]
-    r = EINetRunner(model, n, n_exc, idx_e, idx_i, w_e, w_i, neuron.params(float(inp)), V0,
-                    delay_steps=delay_steps)
+    r = EINetRunner(model, B * n, B * n_exc, idx_e, idx_i, w_e, w_i, neuron.params(float(inp)),
+                    V0, delay_steps=delay_steps)
     # carry the current state over (the runner initialised HH gates at steady state)
-    r.state['ge'].copy_(proj_e.syn.g.value)
-    r.state['gi'].copy_(proj_i.syn.g.value)
+    r.state['ge'].copy_(to_runner(proj_e.syn.g.value))
+    r.state['gi'].copy_(to_runner(proj_i.syn.g.value))
     if model == 'lif':
-        r.state['ref'].copy_(neuron.ref.value)
+        r.state['ref'].copy_(to_runner(neuron.ref.value))
     else:
-        r.state['m'].copy_(neuron.m.value)
-        r.state['h'].copy_(neuron.h.value)
-        r.state['n'].copy_(neuron.n.value)
+        r.state['m'].copy_(to_runner(neuron.m.value))
+        r.state['h'].copy_(to_runner(neuron.h.value))
+        r.state['n'].copy_(to_runner(neuron.n.value))
 
     def write_back():
-        neuron.V.value = r.state['V'].clone()
-        proj_e.syn.g.value = r.state['ge'].clone()
-        proj_i.syn.g.value = r.state['gi'].clone()
-        neuron.spike.value = r.spk.clone().view(torch.bool)
+        neuron.V.value = from_runner(r.state['V'])
+        proj_e.syn.g.value = from_runner(r.state['ge'])
+        proj_i.syn.g.value = from_runner(r.state['gi'])
+        neuron.spike.value = from_runner(r.spk).view(torch.bool)
         if model == 'lif':
-            neuron.ref.value = r.state['ref'].clone()
+            neuron.ref.value = from_runner(r.state['ref'])
         else:
-            neuron.m.value = r.state['m'].clone()
-            neuron.h.value = r.state['h'].clone()
-            neuron.n.value = r.state['n'].clone()
+            neuron.m.value = from_runner(r.state['m'])
+            neuron.h.value = from_runner(r.state['h'])
+            neuron.n.value = from_runner(r.state['n'])
 
     r.write_back = write_back
+    r.replica_index = perm   # runner neuron of (replica b, neuron j), for rasters
     r.dt = environ.get_dt()
     return r

@@ -61,11 +61,13 @@ class Expon(Module, _Describable):
         self.g_initializer = g_initializer
         self.delta = None
 
-    def init_state(self, *args, **kwargs):
+    def init_state(self, batch_size=None, **kwargs):
         n = int(np.prod(self.in_size))
-        g = init.param(self.g_initializer, (n,))
-        self.g = HiddenState(torch.zeros(n, device=_dev()) + (float(g) if init._is_scalar(g)
-                                                              else torch.as_tensor(g, device=_dev())))
+        shape = (n,) if batch_size is None else (int(batch_size), n)
+        g = init.param(self.g_initializer, (n,), batch_size)
+        self.g = HiddenState(torch.zeros(shape, device=_dev()) + (
+            float(g) if init._is_scalar(g) else torch.as_tensor(np.asarray(g, np.float32),
+                                                                device=_dev()).reshape(shape)))
         self.delta = None
 
     def add_delta_input(self, key, value):
@@ -116,7 +118,7 @@ class _COBANeuron(Dynamics):
         self._channels.append(proj)
 
     def _channel_args(self):
-        zeros = torch.zeros(self.num, device=_dev())
+        zeros = torch.zeros_like(self.V.value)
         g, ins, E, tau = [], [], [], []
         for ch in self._channels:
             g.append(ch.syn.g.value)
@@ -137,6 +139,20 @@ class _COBANeuron(Dynamics):
 
     def get_spike(self):
         return self.spike.value
+
+
+def _state_shape(n, batch_size):
+    """[n], or [batch_size, n] under init_all_states(batch_size=...) (states gain a leading
+    batch axis; the step kernels run over all batch_size * n neurons at once)."""
+    return (n,) if batch_size is None else (int(batch_size), n)
+
+
+def _initial_V(V_initializer, n, batch_size, shape):
+    V = init.param(V_initializer, (n,), batch_size)
+    if init._is_scalar(V):
+        V = np.full(shape, float(V), np.float32)
+    V = V.detach().cpu().numpy() if torch.is_tensor(V) else np.asarray(V)
+    return torch.as_tensor(np.ascontiguousarray(V, np.float32).reshape(shape), device=_dev())
 
 
 def _ext_input(x):
@@ -161,14 +177,11 @@ class LIFRef(_COBANeuron, _Describable):
         self.V_th, self.V_reset, self.V_rest = float(V_th), float(V_reset), float(V_rest)
         self.V_initializer = V_initializer
 
-    def init_state(self, *args, **kwargs):
-        n = self.num
-        V = init.param(self.V_initializer, (n,))
-        if init._is_scalar(V):
-            V = np.full(n, float(V), np.float32)
-        self.V = HiddenState(torch.as_tensor(np.asarray(V, np.float32), device=_dev()).clone())
-        self.ref = HiddenState(torch.zeros(n, dtype=torch.int32, device=_dev()))
-        self.spike = ShortTermState(torch.zeros(n, dtype=torch.bool, device=_dev()))
+    def init_state(self, batch_size=None, **kwargs):
+        shape = _state_shape(self.num, batch_size)
+        self.V = HiddenState(_initial_V(self.V_initializer, self.num, batch_size, shape))
+        self.ref = HiddenState(torch.zeros(shape, dtype=torch.int32, device=_dev()))
+        self.spike = ShortTermState(torch.zeros(shape, dtype=torch.bool, device=_dev()))
 
     def params(self, I_ext=0.0):
         _, _, E, tau = self._channel_args()
@@ -182,7 +195,7 @@ class LIFRef(_COBANeuron, _Describable):
         p = self.params(_ext_input(x))
         spk = ops.coba_lif_step(self.V.value, g[0], g[1], self.ref.value, ins[0], ins[1], p)
         self._finish_channels(g)
-        self.spike.value = spk.view(torch.bool)
+        self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value
 
 
@@ -208,17 +221,14 @@ class HH(_COBANeuron, _Describable):
         self.EL, self.gL, self.V_th, self.C = float(EL), float(gL), float(V_th), float(C)
         self.V_initializer = V_initializer
 
-    def init_state(self, *args, **kwargs):
-        n = self.num
-        V = init.param(self.V_initializer, (n,))
-        if init._is_scalar(V):
-            V = np.full(n, float(V), np.float32)
+    def init_state(self, batch_size=None, **kwargs):
+        shape = _state_shape(self.num, batch_size)
         dev = _dev()
-        self.V = HiddenState(torch.as_tensor(np.asarray(V, np.float32), device=dev).clone())
-        m, h, nn_ = (torch.empty(n, device=dev) for _ in range(3))
+        self.V = HiddenState(_initial_V(self.V_initializer, self.num, batch_size, shape))
+        m, h, nn_ = (torch.empty(shape, device=dev) for _ in range(3))
         ops.hh_init(self.V.value, m, h, nn_)
         self.m, self.h, self.n = HiddenState(m), HiddenState(h), HiddenState(nn_)
-        self.spike = ShortTermState(torch.zeros(n, dtype=torch.bool, device=dev))
+        self.spike = ShortTermState(torch.zeros(shape, dtype=torch.bool, device=dev))
 
     def params(self, I_ext=0.0):
         _, _, E, tau = self._channel_args()
@@ -232,5 +242,5 @@ class HH(_COBANeuron, _Describable):
         spk = ops.coba_hh_step(self.V.value, self.m.value, self.h.value, self.n.value, g[0],
                                g[1], ins[0], ins[1], p)
         self._finish_channels(g)
-        self.spike.value = spk.view(torch.bool)
+        self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value

@@ -30,7 +30,8 @@ def _broadcastable(a, b):
 
 def param(parameter, sizes, batch_size=None, allow_none=True, allow_scalar=True):
     """None / scalar pass through (a scalar weight stays homogeneous, :188-189); a callable
-    is called with the shape; an array must broadcast to ``sizes`` (:208-210)."""
+    is called with the shape (batch first); an array must broadcast to ``sizes`` (:208-210)
+    and is repeated along a leading batch axis when ``batch_size`` is given (:214-224)."""
     if parameter is None:
         if allow_none:
             return None
@@ -52,6 +53,16 @@ def param(parameter, sizes, batch_size=None, allow_none=True, allow_scalar=True)
     if not _broadcastable(value.shape, sizes):
         raise ValueError(f'The shape of the parameter {tuple(value.shape)} does not match with '
                          f'the given size {sizes}')
+    if batch_size is not None:   # :214-224: repeat along a new leading batch axis
+        if value.ndim <= len(sizes):
+            lib = torch if torch.is_tensor(value) else np
+            value = lib.broadcast_to(value, tuple(sizes)) if tuple(value.shape) != tuple(sizes) \
+                else value
+            value = value[None].repeat(batch_size, *([1] * len(sizes))) if torch.is_tensor(value) \
+                else np.repeat(value[None], batch_size, axis=0)
+        elif value.shape[0] != batch_size:
+            raise ValueError(f'The batch size of the parameter {value.shape[0]} does not match '
+                             f'with the given batch size {batch_size}')
     return type(parameter)(value) if isinstance(parameter, State) else value
 
 

@@ -70,26 +70,38 @@ def event_scatter(active, n_active, indices, w, n_post, k=None, indptr=None, out
     return out
 
 
+def _batch_of(x):
+    """(leading shape, batch rows, row length) of a [..., n] operand."""
+    lead = tuple(x.shape[:-1])
+    return lead, int(np.prod(lead)) if lead else 1, int(x.shape[-1]) if x.dim() else 1
+
+
 def event_matvec(spk, indices, w, n_post, k=None, indptr=None, out=None, accumulate=False):
-    """Event mat-vec straight from the spike vector (one fused compaction + scatter launch)."""
+    """Event mat-vec straight from the spike vector (one fused compaction + scatter launch);
+    ``spk`` [..., n_pre] with leading batch dimensions gives [..., n_post] in one launch."""
     spk = _spk_view(spk)
     dev = indices.device
-    n_pre = spk.numel()
-    if indptr is None:
-        k = indices.shape[1] if indices.dim() == 2 else int(k)
-        if indices.shape[0] != n_pre:
-            raise ValueError(f'spike vector of {n_pre} for {indices.shape[0]} pre rows')
-    elif indptr.numel() - 1 != n_pre:
-        raise ValueError(f'spike vector of {n_pre} for {indptr.numel() - 1} pre rows')
+    lead, batch, n_pre = _batch_of(spk)
+    k = _rows(n_pre, indices, k, indptr)
     homo = not torch.is_tensor(w) or w.numel() == 1
     w_homo = float(w) if homo else 0.0
     if out is None:
-        out = torch.empty(n_post, dtype=torch.float32, device=dev)
+        out = torch.empty(lead + (n_post,), dtype=torch.float32, device=dev)
         accumulate = False
-    N.check(N.lib().bs_event_matvec_f32(
-        N.ptr(spk), _spk_dtype(spk), int(n_pre), N.ptr(indptr), N.ptr(indices.contiguous()),
-        int(k or 0), None if homo else N.ptr(w.contiguous()), w_homo, int(n_post), N.ptr(out),
-        1 if accumulate else 0, N.stream_handle(dev)), 'bs_event_matvec_f32')
+    args = (N.ptr(indptr), N.ptr(indices.contiguous()), k,
+            None if homo else N.ptr(w.contiguous()), w_homo, int(n_post), N.ptr(out),
+            1 if accumulate else 0, N.stream_handle(dev))
+    if spk.dim() <= 1:
+        N.check(N.lib().bs_event_matvec_f32(N.ptr(spk), _spk_dtype(spk), n_pre, *args),
+                'bs_event_matvec_f32')
+    else:
+        for b0 in range(0, batch, 65535):
+            nb = min(65535, batch - b0)
+            rows = spk.reshape(batch, n_pre)[b0:b0 + nb]
+            dst = out.reshape(batch, n_post)[b0:b0 + nb]
+            N.check(N.lib().bs_event_matvec_batch_f32(
+                N.ptr(rows), _spk_dtype(spk), nb, n_pre, *args[:6], N.ptr(dst), *args[7:]),
+                'bs_event_matvec_batch_f32')
     return out
 
 
@@ -104,19 +116,29 @@ def _rows(n_pre, indices, k, indptr):
 
 
 def value_matvec(x, indices, w, n_post, k=None, indptr=None, out=None, accumulate=False):
-    """Value-weighted sparse mat-vec: out[j] = sum_{i,k: idx[i,k]=j} x[i] * w[i,k] (fp32 x)."""
+    """Value-weighted sparse mat-vec: out[j] = sum_{i,k: idx[i,k]=j} x[i] * w[i,k] (fp32 x);
+    leading batch dimensions of ``x`` are rows of one batched launch."""
     x = x.to(torch.float32).contiguous()
     dev = indices.device
-    n_pre = x.numel()
+    lead, batch, n_pre = _batch_of(x)
     k = _rows(n_pre, indices, k, indptr)
     homo = not torch.is_tensor(w) or w.numel() == 1
     if out is None:
-        out = torch.empty(n_post, dtype=torch.float32, device=dev)
+        out = torch.empty(lead + (n_post,), dtype=torch.float32, device=dev)
         accumulate = False
-    N.check(N.lib().bs_value_matvec_f32(
-        N.ptr(x), int(n_pre), N.ptr(indptr), N.ptr(indices.contiguous()), k,
-        None if homo else N.ptr(w.contiguous()), float(w) if homo else 0.0, int(n_post),
-        N.ptr(out), 1 if accumulate else 0, N.stream_handle(dev)), 'bs_value_matvec_f32')
+    wp, wh = (None, float(w)) if homo else (N.ptr(w.contiguous()), 0.0)
+    if x.dim() <= 1:
+        N.check(N.lib().bs_value_matvec_f32(
+            N.ptr(x), n_pre, N.ptr(indptr), N.ptr(indices.contiguous()), k, wp, wh, int(n_post),
+            N.ptr(out), 1 if accumulate else 0, N.stream_handle(dev)), 'bs_value_matvec_f32')
+    else:
+        for b0 in range(0, batch, 65535):
+            nb = min(65535, batch - b0)
+            N.check(N.lib().bs_value_matvec_batch_f32(
+                N.ptr(x.reshape(batch, n_pre)[b0:b0 + nb]), nb, n_pre, N.ptr(indptr),
+                N.ptr(indices.contiguous()), k, wp, wh, int(n_post),
+                N.ptr(out.reshape(batch, n_post)[b0:b0 + nb]), 1 if accumulate else 0,
+                N.stream_handle(dev)), 'bs_value_matvec_batch_f32')
     return out
 
 

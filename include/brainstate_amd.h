@@ -88,6 +88,19 @@ BS_API int bs_value_matvec_f32(const float* x, int32_t n_pre, const int32_t* ind
                                int32_t n_post, float* out, int32_t accumulate,
                                bs_stream_t stream);
 
+/* Batched forms: `batch` spike / value rows [batch, n_pre] against one connectivity, outputs
+ * [batch, n_post], one launch.  Replaces `EventArray(spk) @ conn` with a leading batch
+ * dimension (brainstate/nn/_event_fixedprob.py:202-209 under init_all_states(batch_size),
+ * and vmap2 over replicas, brainstate/transform/_mapping2.py:289).  batch <= 65535. */
+BS_API int bs_event_matvec_batch_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                     int32_t n_pre, const int32_t* indptr, const int32_t* indices,
+                                     int32_t k, const float* w, float w_homo, int32_t n_post,
+                                     float* out, int32_t accumulate, bs_stream_t stream);
+BS_API int bs_value_matvec_batch_f32(const float* x, int32_t batch, int32_t n_pre,
+                                     const int32_t* indptr, const int32_t* indices, int32_t k,
+                                     const float* w, float w_homo, int32_t n_post, float* out,
+                                     int32_t accumulate, bs_stream_t stream);
+
 /* Reverse mode of the event mat-vec (the VJP the reference checks at
  * brainstate/nn/_event_fixedprob_test.py:56-88): with g = grad_out[n_post] and x[i] the spike
  * value (0/1 for byte spikes),
