@@ -1,173 +1,416 @@
 // N2c: batched event x dense weight (EventLinear).
 //
-// One wave per (batch row b, tile of 64*V output columns).  Each lane turns 64 consecutive
-// spikes of row b into a 64-bit mask (coalesced 16-byte loads); the wave walks the masks in
-// order and streams the active inputs kBatch at a time across mask boundaries: kBatch
-// coalesced row segments of W (128-bit loads when V = 4) are in flight before the first add,
-// so a 5 %-dense row costs about (active inputs / kBatch) memory round trips, not one per 64
-// inputs.  Each lane adds its V columns in
-// ascending input order, the order of a sequential reference loop, so results are
-// bit-reproducible.
+// out[b, j] = sum of W[i, j] over the inputs i with spk[b, i] != 0 (or spk[b, i] * W[i, j]).
+// At config [4] (64 x 4096 spikes at 5 %, W 4096 x 4096 fp32) about 3,940 of the 4,096 rows
+// of W are selected by at least one batch row, so every step reads almost all of W (64 MiB),
+// while the (batch row, active input) pairs number ~13,100: a kernel that fetches a W row
+// segment once per pair moves ~210 MB from L2, one that fetches it once per step 64 MiB.
 //
-// XCD-aware placement: a row segment of W is needed by every batch row whose spike selects
-// it, and those waves all read the tile's segments in ascending input order.  Waves are
-// therefore numbered tile-major (all batch rows of a tile consecutive) and consecutive
-// logical workgroups are placed on the same XCD (workgroups are dispatched to the 8 XCDs
-// round-robin), so the batch rows of a tile share that XCD's L2 and each segment is fetched
-// from memory about once per step instead of once per batch row that uses it.
+// Tiling: a workgroup owns 64*V output columns (lane = V consecutive columns) of 64 batch
+// rows (16 waves, 4 batch rows each) over one chunk of consecutive input rows.  It stages W
+// through LDS in blocks of 64 rows, prefetched kDepth blocks ahead in registers, so each
+// element of W is fetched once per step and shared by all 64 batch rows.  For each block a
+// wave turns the spikes of its 4 batch rows into LDS lists of active rows (one ballot and
+// one LDS write per row: lane l holds input l of the block; an active lane writes its row's
+// byte offset at its rank, inactive lanes write padding that points at a zero row), reads
+// the first 8 entries back before the barrier, and after it issues all its W reads at once
+// and adds in ascending input order (the padding adds +0.0, which leaves every sum as is).
+// Cost model from the hardware counters: the kernel is bound by VALU issue (~160 VALU per
+// wave per block, most of it per-(batch row, block) list work rather than per event).
+//
+// Chunks: bs_event_dense_chunks() splits the inputs into S chunks of L rows so that the grid
+// fills the chip (about 256 workgroups) when the output is narrow.  Each chunk's sum is
+// formed in ascending input order from 0; with S > 1 every workgroup stores its partial
+// sums with device-scope stores, waits for them to complete, and takes a ticket on its
+// (column tile, batch group) counter; the workgroup that draws the last ticket adds the S
+// partials in chunk order, ((P_0 + P_1) + P_2) + ..., and writes out (device-scope loads:
+// no cache writeback or invalidate is needed).  It also clears the counter, so the
+// workspace stays ready for the next call.  The order depends only on (batch, n_in, n_out),
+// so results are reproducible run to run and device to device.
+//
+// XCD-aware placement: workgroups are dispatched to the 8 XCDs round-robin; logical
+// workgroups are renumbered so that consecutive ones (the column tiles of one chunk, which
+// read the same spike bytes) share an XCD and its L2.
 #include "bs_math.h"
 #include "common.h"
 
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kBatch = 16;
-constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
+constexpr int kBlock = 256;   // reverse-mode kernels
+constexpr int kXcds = 8;      // MI355X: 8 XCDs, each with its own L2
 
+constexpr int kDB = 1024;                 // forward: threads per workgroup
+constexpr int kDWaves = kDB / BS_WAVE;    // 16
+constexpr int kGroupRows = 64;            // batch rows per workgroup
+constexpr int kRowsPerWave = kGroupRows / kDWaves;  // 4
+constexpr int kBlk = 64;                  // input rows per LDS block (one ballot)
+constexpr int kList = kBlk + 12;          // list entries per (wave, batch row): 64 + padding
+constexpr int kDump = kList - 1;          // slot written by lanes with nothing to record
+// Measured on MI355X at config [4] (64 x 4096 @ 5 %, W 4096^2): V = 2 with 8 chunks 28 us,
+// V = 1 with 4 chunks 30 us, V = 4 120 us (LDS of 152 KiB per workgroup and 64 KiB partials);
+// a 256-workgroup launch alone costs ~4.3 us.
+constexpr int kV = 2;                     // output columns per lane (workgroup: 64 * V)
+constexpr int kTileCols = BS_WAVE * kV;
+constexpr int kTargetGroups = 256;        // workgroups the chunk plan aims for
+constexpr int kDepth = 2;                 // W blocks in flight per thread (registers)
+constexpr int kMaxChunks = 8;             // chunk partials the last workgroup adds
 
 // Spike byte/float -> event flag (any nonzero value is an event).
 __device__ __forceinline__ bool nz(uint8_t x) { return x != 0; }
 __device__ __forceinline__ bool nz(float x) { return x != 0.0f; }
 
-// Mask of the 64 inputs [i0, i0 + 64) of one spike row, built by one lane from coalesced
-// 16-byte loads (bit k = input i0 + k; inputs at or past n_in are 0).
-template <typename T>
-__device__ __forceinline__ uint64_t lane_mask(const T* row, int32_t i0, int32_t n_in) {
-  uint64_t m = 0;
-  if (i0 + 64 <= n_in && (((uintptr_t)(row + i0)) & 15) == 0) {
-    constexpr int kPer = 16 / sizeof(T);  // inputs per 16-byte load
-#pragma unroll
-    for (int c = 0; c < 64; c += kPer) {
-      const uint4 q = *(const uint4*)(row + i0 + c);
-      const T* e = (const T*)&q;
-#pragma unroll
-      for (int k = 0; k < kPer; ++k) m |= (uint64_t)nz(e[k]) << (c + k);
-    }
-  } else {
-    for (int k = 0; k < 64 && i0 + k < n_in; ++k) m |= (uint64_t)nz(row[i0 + k]) << k;
-  }
-  return m;
+struct DensePlan {
+  int32_t tiles;       // column tiles of 64 * V
+  int32_t groups;      // batch groups of 64
+  int32_t chunks;      // S
+  int32_t chunk_rows;  // L (a multiple of 64)
+};
+
+// Chunk plan: a function of the shape only (never of the device), so the order of the
+// additions is fixed.  Chunks hold at least 4 blocks (256 rows) each; at most kMaxChunks.
+DensePlan dense_plan(int32_t batch, int32_t n_in, int32_t n_out) {
+  DensePlan pl;
+  pl.tiles = (n_out + kTileCols - 1) / kTileCols;
+  pl.groups = (batch + kGroupRows - 1) / kGroupRows;
+  const int64_t blocks = ((int64_t)n_in + kBlk - 1) / kBlk;
+  const int64_t wgs = (int64_t)pl.tiles * pl.groups;
+  int64_t s0 = kTargetGroups / (wgs > 0 ? wgs : 1);
+  const int64_t smax = blocks / 4;
+  if (s0 > smax) s0 = smax;
+  if (s0 > kMaxChunks) s0 = kMaxChunks;
+  if (s0 < 1) s0 = 1;
+  const int64_t per = blocks > 0 ? (blocks + s0 - 1) / s0 : 1;  // blocks per chunk
+  pl.chunks = blocks > 0 ? (int32_t)((blocks + per - 1) / per) : 1;
+  pl.chunk_rows = (int32_t)(per * kBlk);
+  return pl;
 }
 
-// 64-bit value of lane l (l wave-uniform).
-__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
-  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
-  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
-  return ((uint64_t)hi << 32) | lo;
+// Workspace: [0, ticket bytes) one counter per (batch group, column tile), zero on entry and
+// on return; then the partial sums [S][batch][n_out].
+size_t dense_ticket_bytes(const DensePlan& pl) {
+  if (pl.chunks <= 1) return 0;
+  return ((size_t)pl.tiles * pl.groups * sizeof(uint32_t) + 255) & ~(size_t)255;
+}
+size_t dense_ws_bytes(const DensePlan& pl, int32_t batch, int32_t n_out) {
+  if (pl.chunks <= 1) return 0;
+  return dense_ticket_bytes(pl) + (size_t)pl.chunks * batch * n_out * sizeof(float);
 }
 
-template <typename T, int V, bool kEvent>
-__global__ __launch_bounds__(kBlock) void k_event_dense(const T* __restrict__ spk, int32_t batch,
-                                                        int32_t n_in, const float* __restrict__ W,
-                                                        int32_t n_out, float* __restrict__ out) {
-  const int lane = bs_lane();
+template <int V>
+struct VecF;
+template <>
+struct VecF<1> { using T = float; };
+template <>
+struct VecF<2> { using T = float2; };
+template <>
+struct VecF<4> { using T = float4; };
+
+template <int V>
+__device__ __forceinline__ void add_vec(float* acc, const typename VecF<V>::T& x) {
+  const float* e = (const float*)&x;
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] += e[v];
+}
+template <int V>
+__device__ __forceinline__ void fma_vec(float* acc, float s, const typename VecF<V>::T& x) {
+  const float* e = (const float*)&x;
+#pragma unroll
+  for (int v = 0; v < V; ++v) acc[v] += s * e[v];  // product rounded, then the sum
+}
+
+template <typename T, bool kEvent, bool kVec>
+__global__ __launch_bounds__(kDB) void k_event_dense(const T* __restrict__ spk, int32_t batch,
+                                                     int32_t n_in, const float* __restrict__ W,
+                                                     int32_t n_out, float* __restrict__ out,
+                                                     DensePlan pl, float* part, uint32_t* tick) {
+  using VT = typename VecF<kV>::T;
+  constexpr int kRowF4 = kTileCols / 4;             // float4 per block row
+  constexpr int kStage = kBlk * kRowF4 / kDB;       // float4 staged per thread per block
+  constexpr uint32_t kZeroOff = kBlk * kTileCols * 4;  // byte offset of the zero row
+  __shared__ __align__(16) float s_w[2][(kBlk + 1) * kTileCols];  // row kBlk stays zero
+  __shared__ __align__(16) uint32_t s_list[kDWaves][kRowsPerWave][kList];
+  __shared__ __align__(16) float s_val[kEvent ? 1 : kDWaves][kRowsPerWave][kList];
+  __shared__ uint32_t s_last;
+
   const int32_t per_xcd = gridDim.x / kXcds;  // the grid is a multiple of kXcds
-  const int64_t lwg = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  const int64_t wave = (lwg * kBlock + threadIdx.x) / BS_WAVE;  // tile-major wave number
-  const int32_t tiles = (n_out + BS_WAVE * V - 1) / (BS_WAVE * V);
-  if (wave >= (int64_t)batch * tiles) return;
-  const int32_t t = (int32_t)(wave / batch);
-  const int32_t b = (int32_t)(wave - (int64_t)t * batch);
-  const int32_t j0 = t * BS_WAVE * V + lane * V;
-  const bool live = j0 < n_out;
-  const T* srow = spk + (int64_t)b * n_in;
-  float acc[V];
+  const int32_t lwg = (int32_t)(blockIdx.x % kXcds) * per_xcd + (int32_t)(blockIdx.x / kXcds);
+  if (lwg >= pl.tiles * pl.groups * pl.chunks) return;  // whole workgroup
+  const int32_t ct = lwg % pl.tiles;
+  const int32_t rest = lwg / pl.tiles;
+  const int32_t bg = rest % pl.groups;
+  const int32_t kc = rest / pl.groups;
+  const int lane = bs_lane();
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / BS_WAVE));
+  const int32_t col = ct * kTileCols + lane * kV;
+  const int32_t r_lo = kc * pl.chunk_rows;
+  const int32_t r_hi = r_lo + pl.chunk_rows < n_in ? r_lo + pl.chunk_rows : n_in;
+  const int32_t nblk = (r_hi - r_lo + kBlk - 1) / kBlk;
+
+  for (int x = threadIdx.x; x < kTileCols; x += kDB) {
+    s_w[0][kBlk * kTileCols + x] = 0.0f;
+    s_w[1][kBlk * kTileCols + x] = 0.0f;
+  }
+
+  // staging: float4 q of thread t is element t + q*kDB of the block, row-major
+  auto load_block = [&](int32_t k, float4* dst) {
 #pragma unroll
-  for (int v = 0; v < V; ++v) acc[v] = 0.0f;
-  // Inputs in spans of 64 groups of 64: lane l holds the mask of group l of the span; the
-  // wave walks the groups in order (readlane, no memory access) and fills kBatch row slots
-  // across group boundaries before issuing their loads.
-  for (int32_t s0 = 0; s0 < n_in; s0 += BS_WAVE * BS_WAVE) {
-    const uint64_t mine = lane_mask(srow, s0 + lane * BS_WAVE, n_in);
-    const int ng = (n_in - s0 + BS_WAVE - 1) / BS_WAVE < BS_WAVE
-                       ? (n_in - s0 + BS_WAVE - 1) / BS_WAVE : BS_WAVE;
-    int g = 0;
-    uint64_t m = readlane64(mine, 0);
-    for (;;) {
-      int32_t r[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        while (m == 0 && g + 1 < ng) m = readlane64(mine, ++g);
-        r[u] = -1;
-        if (m) {
-          r[u] = s0 + g * BS_WAVE + (int32_t)__builtin_ctzll(m);
-          m &= m - 1;
+    for (int q = 0; q < kStage; ++q) {
+      const int e = (int)threadIdx.x + q * kDB;
+      const int row = e / kRowF4;
+      const int32_t c = ct * kTileCols + (e - row * kRowF4) * 4;
+      const int32_t i = r_lo + k * kBlk + row;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (k < nblk && i < r_hi) {
+        const float* p = W + (int64_t)i * n_out + c;
+        if (kVec) {
+          if (c < n_out) v = *(const float4*)p;  // n_out % 4 == 0
+        } else {
+          if (c < n_out) v.x = p[0];
+          if (c + 1 < n_out) v.y = p[1];
+          if (c + 2 < n_out) v.z = p[2];
+          if (c + 3 < n_out) v.w = p[3];
         }
       }
-      if (r[0] < 0) break;
-      float x[kBatch][V];
-      float sc[kBatch];
+      dst[q] = v;
+    }
+  };
+  // spikes: lane l of the wave holds input ib + l of each of its batch rows; the load is
+  // unconditional (clamped address), the flag says whether the input exists
+  auto load_spk = [&](int32_t k, T* dst, bool* ok) {
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        sc[u] = 1.0f;
-        if (r[u] >= 0) {
-          if (!kEvent) sc[u] = (float)srow[r[u]];
-          if (live) {
-            const float* wr = W + (int64_t)r[u] * n_out + j0;
-            if (V == 4) {
-              const float4 q = *(const float4*)wr;
-              x[u][0] = q.x;
-              x[u][V > 1 ? 1 : 0] = q.y;
-              x[u][V > 2 ? 2 : 0] = q.z;
-              x[u][V > 3 ? 3 : 0] = q.w;
-            } else if (V == 2) {
-              const float2 q = *(const float2*)wr;
-              x[u][0] = q.x;
-              x[u][V > 1 ? 1 : 0] = q.y;
-            } else {
-              x[u][0] = *wr;
-            }
+    for (int u = 0; u < kRowsPerWave; ++u) {
+      const int32_t b = bg * kGroupRows + wid + kDWaves * u;
+      const int32_t i = r_lo + k * kBlk + lane;
+      ok[u] = k < nblk && b < batch && i < r_hi;
+      dst[u] = spk[ok[u] ? (int64_t)b * n_in + i : 0];
+    }
+  };
+
+  float acc[kRowsPerWave][kV];
+#pragma unroll
+  for (int u = 0; u < kRowsPerWave; ++u)
+#pragma unroll
+    for (int v = 0; v < kV; ++v) acc[u][v] = 0.0f;
+
+  float4 pre[kDepth][kStage];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) load_block(d, pre[d]);
+  T sp[kRowsPerWave];
+  bool sok[kRowsPerWave];
+  load_spk(0, sp, sok);
+
+  for (int32_t k0 = 0; k0 < nblk; k0 += kDepth) {
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+      const int32_t k = k0 + d;
+      if (k >= nblk) break;  // uniform
+      float* sw = s_w[k & 1];
+#pragma unroll
+      for (int q = 0; q < kStage; ++q) {
+        const int e = (int)threadIdx.x + q * kDB;
+        const int row = e / kRowF4;
+        *(float4*)&sw[row * kTileCols + (e - row * kRowF4) * 4] = pre[d][q];
+      }
+      // this wave's lists for block k: byte offsets of the active rows, ascending, padded
+      // with the zero row to a multiple of 4 (8 entries are always valid).  One LDS write per
+      // row for all lanes: an active lane writes its entry at its rank, the first 8 inactive
+      // lanes write the padding after the last entry, the others a slot that is never read.
+      uint32_t cnt[kRowsPerWave];
+#pragma unroll
+      for (int u = 0; u < kRowsPerWave; ++u) {
+        const bool on = sok[u] && nz(sp[u]);
+        const uint64_t m = bs_ballot(on);
+        cnt[u] = (uint32_t)__popcll(m);
+        const uint32_t below = (uint32_t)bs_rank_below(m);
+        const uint32_t idle = (uint32_t)lane - below;  // inactive lanes below this one
+        const uint32_t pos = on ? below : (idle < 8 ? cnt[u] + idle : (uint32_t)kDump);
+        s_list[wid][u][pos] = on ? (uint32_t)lane * (kTileCols * 4) : kZeroOff;
+        if (!kEvent) s_val[kEvent ? 0 : wid][u][pos] = on ? (float)sp[u] : 0.0f;
+      }
+      // next spikes first, then the next W block: a wait for the spikes never waits for W
+      load_spk(k + 1, sp, sok);
+      load_block(k + kDepth, pre[d]);
+      // read the first 8 entries of each row back now (this wave wrote them), so only the
+      // W reads wait behind the barrier
+      uint4 e0[kRowsPerWave], e1[kRowsPerWave];
+      float4 sv0[kRowsPerWave], sv1[kRowsPerWave];
+#pragma unroll
+      for (int u = 0; u < kRowsPerWave; ++u) {
+        e0[u] = *(const uint4*)&s_list[wid][u][0];
+        e1[u] = *(const uint4*)&s_list[wid][u][4];
+        if (!kEvent) {
+          sv0[u] = *(const float4*)&s_val[kEvent ? 0 : wid][u][0];
+          sv1[u] = *(const float4*)&s_val[kEvent ? 0 : wid][u][4];
+        }
+      }
+      __syncthreads();
+
+      const char* wb = (const char*)sw + lane * kV * 4;
+      VT x0[kRowsPerWave][4], x1[kRowsPerWave][4];
+#pragma unroll
+      for (int u = 0; u < kRowsPerWave; ++u) {
+        x0[u][0] = *(const VT*)(wb + e0[u].x);
+        x0[u][1] = *(const VT*)(wb + e0[u].y);
+        x0[u][2] = *(const VT*)(wb + e0[u].z);
+        x0[u][3] = *(const VT*)(wb + e0[u].w);
+      }
+#pragma unroll
+      for (int u = 0; u < kRowsPerWave; ++u) {
+        if (cnt[u] > 4) {  // uniform
+          x1[u][0] = *(const VT*)(wb + e1[u].x);
+          x1[u][1] = *(const VT*)(wb + e1[u].y);
+          x1[u][2] = *(const VT*)(wb + e1[u].z);
+          x1[u][3] = *(const VT*)(wb + e1[u].w);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kRowsPerWave; ++u) {
+        if (kEvent) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) add_vec<kV>(acc[u], x0[u][q]);
+        } else {
+          fma_vec<kV>(acc[u], sv0[u].x, x0[u][0]);
+          fma_vec<kV>(acc[u], sv0[u].y, x0[u][1]);
+          fma_vec<kV>(acc[u], sv0[u].z, x0[u][2]);
+          fma_vec<kV>(acc[u], sv0[u].w, x0[u][3]);
+        }
+        if (cnt[u] > 4) {
+          if (kEvent) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) add_vec<kV>(acc[u], x1[u][q]);
+          } else {
+            fma_vec<kV>(acc[u], sv1[u].x, x1[u][0]);
+            fma_vec<kV>(acc[u], sv1[u].y, x1[u][1]);
+            fma_vec<kV>(acc[u], sv1[u].z, x1[u][2]);
+            fma_vec<kV>(acc[u], sv1[u].w, x1[u][3]);
           }
         }
       }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        if (r[u] >= 0 && live) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) acc[v] += kEvent ? x[u][v] : sc[u] * x[u][v];
+      for (int u = 0; u < kRowsPerWave; ++u) {
+        for (uint32_t j = 8; j < cnt[u]; j += 4) {  // rows with more than 8 events
+          const uint4 e = *(const uint4*)&s_list[wid][u][j];
+          const VT x1 = *(const VT*)(wb + e.x);
+          const VT x2 = *(const VT*)(wb + e.y);
+          const VT x3 = *(const VT*)(wb + e.z);
+          const VT x4 = *(const VT*)(wb + e.w);
+          if (kEvent) {
+            add_vec<kV>(acc[u], x1);
+            add_vec<kV>(acc[u], x2);
+            add_vec<kV>(acc[u], x3);
+            add_vec<kV>(acc[u], x4);
+          } else {
+            const float4 sv = *(const float4*)&s_val[kEvent ? 0 : wid][u][j];
+            fma_vec<kV>(acc[u], sv.x, x1);
+            fma_vec<kV>(acc[u], sv.y, x2);
+            fma_vec<kV>(acc[u], sv.z, x3);
+            fma_vec<kV>(acc[u], sv.w, x4);
+          }
         }
       }
     }
   }
-  if (live) {
-    float* o = out + (int64_t)b * n_out + j0;
-    if (V == 4) {
-      *(float4*)o = make_float4(acc[0], acc[V > 1 ? 1 : 0], acc[V > 2 ? 2 : 0], acc[V > 3 ? 3 : 0]);
-    } else if (V == 2) {
-      *(float2*)o = make_float2(acc[0], acc[V > 1 ? 1 : 0]);
-    } else {
-      o[0] = acc[0];
+
+  auto store_row = [&](float* dst, const float* a) {  // V columns at dst (col < n_out)
+#pragma unroll
+    for (int v = 0; v < kV; ++v)
+      if (col + v < n_out) dst[v] = a[v];
+  };
+  if (pl.chunks == 1) {
+#pragma unroll
+    for (int u = 0; u < kRowsPerWave; ++u) {
+      const int32_t b = bg * kGroupRows + wid + kDWaves * u;
+      if (b < batch) store_row(out + (int64_t)b * n_out + col, acc[u]);
     }
+    return;
+  }
+  // partial sums of this chunk, then a ticket; the last workgroup adds them in chunk order
+#pragma unroll
+  for (int u = 0; u < kRowsPerWave; ++u) {
+    const int32_t b = bg * kGroupRows + wid + kDWaves * u;
+    if (b < batch) {
+      uint32_t* pp = (uint32_t*)part + ((int64_t)kc * batch + b) * n_out + col;
+#pragma unroll
+      for (int v = 0; v < kV; ++v)
+        if (col + v < n_out)
+          __hip_atomic_store(pp + v, __float_as_uint(acc[u][v]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partials are complete at device scope
+  __syncthreads();
+  uint32_t* tk = tick + (int64_t)bg * pl.tiles + ct;
+  if (threadIdx.x == 0) {
+    const uint32_t old =
+        __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old + 1 == (uint32_t)pl.chunks ? 1u : 0u;
+    if (s_last) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // every partial of this thread's outputs in flight at once, then the sums in chunk order
+  float pv[kMaxChunks][kRowsPerWave][kV];
+#pragma unroll
+  for (int c = 0; c < kMaxChunks; ++c) {
+#pragma unroll
+    for (int u = 0; u < kRowsPerWave; ++u) {
+      const int32_t b = bg * kGroupRows + wid + kDWaves * u;
+      const uint32_t* pp = (const uint32_t*)part + ((int64_t)c * batch + b) * n_out + col;
+#pragma unroll
+      for (int v = 0; v < kV; ++v) {
+        pv[c][u][v] = acc[u][v];
+        if (c < pl.chunks && c != kc && b < batch && col + v < n_out)
+          pv[c][u][v] = __uint_as_float(
+              __hip_atomic_load(pp + v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kRowsPerWave; ++u) {
+    const int32_t b = bg * kGroupRows + wid + kDWaves * u;
+    float tot[kV];
+#pragma unroll
+    for (int v = 0; v < kV; ++v) {
+      tot[v] = pv[0][u][v];
+#pragma unroll
+      for (int c = 1; c < kMaxChunks; ++c)
+        if (c < pl.chunks) tot[v] = tot[v] + pv[c][u][v];
+    }
+    if (b < batch) store_row(out + (int64_t)b * n_out + col, tot);
   }
 }
 
-template <typename T, int V>
-int launch_v(const T* spk, int32_t batch, int32_t n_in, const float* W, int32_t n_out, bool ev,
-             float* out, hipStream_t s) {
-  const int64_t tiles = (n_out + BS_WAVE * V - 1) / (BS_WAVE * V);
-  const int64_t waves = (int64_t)batch * tiles;
-  int64_t g = (waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE);
-  g = (g + kXcds - 1) / kXcds * kXcds;
-  if (ev) k_event_dense<T, V, true><<<(int)g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
-  else k_event_dense<T, V, false><<<(int)g, kBlock, 0, s>>>(spk, batch, n_in, W, n_out, out);
-  BS_CHECK_LAUNCH();
-  return BS_OK;
-}
-
-// Columns per lane: as many as alignment allows while the launch still has about 16 waves per
-// CU (4 per SIMD) to overlap the latency of the row loads.
 template <typename T>
 int launch(const T* spk, int32_t batch, int32_t n_in, const float* W, int32_t n_out, bool ev,
-           float* out, hipStream_t s) {
-  const auto al = [&](int v) {
-    return n_out % v == 0 && ((uintptr_t)W & (4 * v - 1)) == 0 &&
-           ((uintptr_t)out & (4 * v - 1)) == 0;
-  };
-  const int64_t want = (int64_t)4 * bs_num_cus();
-  const auto waves = [&](int v) { return (int64_t)batch * ((n_out + BS_WAVE * v - 1) / (BS_WAVE * v)); };
-  if (al(4) && waves(4) >= want) return launch_v<T, 4>(spk, batch, n_in, W, n_out, ev, out, s);
-  if (al(2) && waves(2) >= want) return launch_v<T, 2>(spk, batch, n_in, W, n_out, ev, out, s);
-  return launch_v<T, 1>(spk, batch, n_in, W, n_out, ev, out, s);
+           float* out, void* ws, size_t ws_bytes, hipStream_t s) {
+  const DensePlan pl = dense_plan(batch, n_in, n_out);
+  float* part = nullptr;
+  uint32_t* tick = nullptr;
+  if (pl.chunks > 1) {
+    const size_t need = dense_ws_bytes(pl, batch, n_out);
+    if (ws == nullptr || ws_bytes < need) {
+      bs_set_error("bs_event_dense_f32: workspace of %zu bytes needed (got %zu)", need,
+                   ws == nullptr ? (size_t)0 : ws_bytes);
+      return BS_ERR_INVALID;
+    }
+    tick = (uint32_t*)ws;
+    part = (float*)((char*)ws + dense_ticket_bytes(pl));
+  }
+  int64_t g = (int64_t)pl.tiles * pl.groups * pl.chunks;
+  if (g > INT32_MAX - kXcds) {
+    bs_set_error("bs_event_dense_f32: %lld workgroups exceed the grid limit", (long long)g);
+    return BS_ERR_INVALID;
+  }
+  g = (g + kXcds - 1) / kXcds * kXcds;
+  const bool vec = n_out % 4 == 0 && ((uintptr_t)W & 15) == 0;
+#define BS_DENSE(E, VV)                                                                 \
+  k_event_dense<T, E, VV><<<(int)g, kDB, 0, s>>>(spk, batch, n_in, W, n_out, out, pl, part, \
+                                                 tick)
+  if (ev) { if (vec) BS_DENSE(true, true); else BS_DENSE(true, false); }
+  else { if (vec) BS_DENSE(false, true); else BS_DENSE(false, false); }
+#undef BS_DENSE
+  BS_CHECK_LAUNCH();
+  return BS_OK;
 }
 
 // ---- reverse mode: y[b] = sum_i x[b,i] * W[i] (x = spike value, 1 for byte spikes) ----
@@ -281,9 +524,31 @@ __global__ __launch_bounds__(kBlock) void k_dense_gw(const T* __restrict__ spk, 
 
 int bs_fill_f32(float* p, int64_t n, float v, hipStream_t s);
 
+extern "C" int bs_event_dense_chunks(int32_t batch, int32_t n_in, int32_t n_out,
+                                     int32_t* chunk_rows) {
+  bs_clear_error();
+  BS_CHECK_ARG(batch >= 0 && n_in >= 0 && n_out >= 0, "bs_event_dense_chunks: negative size");
+  const DensePlan pl = dense_plan(batch, n_in, n_out);
+  if (chunk_rows) *chunk_rows = pl.chunk_rows;
+  return pl.chunks;
+}
+
+extern "C" size_t bs_event_dense_workspace_size(int32_t batch, int32_t n_in, int32_t n_out) {
+  bs_clear_error();
+  if (batch <= 0 || n_in <= 0 || n_out <= 0) return 0;
+  return dense_ws_bytes(dense_plan(batch, n_in, n_out), batch, n_out);
+}
+
+extern "C" size_t bs_event_dense_ticket_bytes(int32_t batch, int32_t n_in, int32_t n_out) {
+  bs_clear_error();
+  if (batch <= 0 || n_in <= 0 || n_out <= 0) return 0;
+  return dense_ticket_bytes(dense_plan(batch, n_in, n_out));
+}
+
 extern "C" int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t batch, int32_t n_in,
                                   const float* W, int32_t n_out, int32_t float_as_event,
-                                  float* out, bs_stream_t stream) {
+                                  float* out, void* workspace, size_t workspace_bytes,
+                                  bs_stream_t stream) {
   bs_clear_error();
   BS_CHECK_ARG(batch >= 0 && n_in >= 0 && n_out >= 0, "bs_event_dense_f32: negative size");
   BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
@@ -293,9 +558,12 @@ extern "C" int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t ba
   hipStream_t s = bs_stream(stream);
   if (n_in == 0) return bs_fill_f32(out, (int64_t)batch * n_out, 0.0f, s);
   BS_CHECK_ARG(spk && W, "bs_event_dense_f32: NULL pointer");
+  const bool ev = float_as_event != 0;
   if (spk_dtype == BS_SPK_U8)
-    return launch((const uint8_t*)spk, batch, n_in, W, n_out, float_as_event != 0, out, s);
-  return launch((const float*)spk, batch, n_in, W, n_out, float_as_event != 0, out, s);
+    return launch((const uint8_t*)spk, batch, n_in, W, n_out, ev, out, workspace,
+                  workspace_bytes, s);
+  return launch((const float*)spk, batch, n_in, W, n_out, ev, out, workspace, workspace_bytes,
+                s);
 }
 
 extern "C" int bs_event_dense_vjp_f32(const void* spk, int32_t spk_dtype, int32_t batch,

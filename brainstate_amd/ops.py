@@ -3,6 +3,8 @@
 These are the building blocks the brainstate-compatible layers call; each maps onto one
 C entry point of include/brainstate_amd.h and raises ``NativeError`` on failure.
 """
+import ctypes
+
 import numpy as np
 import torch
 
@@ -259,10 +261,33 @@ def event_dense(spk, W, float_as_event=True, out=None):
     n_out = W.shape[1]
     if out is None:
         out = torch.empty(B, n_out, dtype=torch.float32, device=W.device)
+    nbytes = int(N.lib().bs_event_dense_workspace_size(B, n_in, n_out))
+    ws = None
+    if nbytes > 0:
+        # ticket counters lead the workspace: zero on entry, left zero by every call; the
+        # bytes after them hold partial sums, so bytes past the previous call's counters
+        # are zeroed before a call that needs more counters
+        tick = int(N.lib().bs_event_dense_ticket_bytes(B, n_in, n_out))
+        key = ('dense', W.device.index, torch.cuda.current_stream(W.device).cuda_stream)
+        ws, zero = _WS_CACHE.get(key, (None, 0))
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=W.device)
+            zero = ws.numel()
+        if tick > zero:
+            ws[zero:tick].zero_()
+        _WS_CACHE[key] = (ws, tick)
     N.check(N.lib().bs_event_dense_f32(N.ptr(s2), _spk_dtype(s2), B, n_in, N.ptr(W.contiguous()),
                                        n_out, 1 if float_as_event else 0, N.ptr(out),
+                                       N.ptr(ws) if ws is not None else None, nbytes,
                                        N.stream_handle(W.device)), 'bs_event_dense_f32')
     return out[0] if squeeze else out
+
+
+def event_dense_chunks(batch, n_in, n_out):
+    """(S, L): the chunk plan that fixes the order of bs_event_dense_f32's additions."""
+    L = ctypes.c_int32(0)
+    S = int(N.lib().bs_event_dense_chunks(int(batch), int(n_in), int(n_out), ctypes.byref(L)))
+    return S, int(L.value)
 
 
 def conn_fixed_num(seed, n_pre, k, n_post, afferent_ratio=None, device=None):

@@ -135,11 +135,25 @@ BS_API int bs_event_gather_f32(const uint32_t* spk_bits, int32_t n_pre,
 /* ---------------------------------------------------------------- N2c event x dense
  * Replaces `EventArray(spk) @ W` / `spk @ W` of EventLinear
  * (brainstate/nn/_event_linear.py:99-102).  spk [batch, n_in], W [n_in, n_out] row-major,
- * out [batch, n_out].  float_as_event != 0: out[b] = sum of rows W[i] with spk[b,i] != 0,
- * added in ascending i; otherwise out[b] = sum_i spk[b,i] * W[i] (same order). */
+ * out [batch, n_out].  float_as_event != 0: out[b] = sum of rows W[i] with spk[b,i] != 0;
+ * otherwise out[b] = sum_i spk[b,i] * W[i].
+ * Order of the fp32 additions (fixed by the shape alone): the inputs are split into
+ * S = bs_event_dense_chunks(batch, n_in, n_out, &L) chunks of L consecutive rows (L a multiple
+ * of 64; the last chunk may be shorter); P_c = the chunk's terms added in ascending i starting
+ * from 0; out = ((P_0 + P_1) + P_2) + ... + P_{S-1}.  S = 1 is the plain ascending sum.
+ * `workspace` holds bs_event_dense_workspace_size(batch, n_in, n_out) bytes (0 when S = 1,
+ * then it may be NULL).  Its first bs_event_dense_ticket_bytes(batch, n_in, n_out) bytes are
+ * ticket counters: they must be zero on entry and the call leaves them zero; the rest holds
+ * partial sums and needs no initialisation.  A workspace zero-filled once therefore serves any
+ * sequence of calls whose ticket bytes do not grow; before a call whose ticket bytes exceed
+ * the previous call's, zero the difference.  Calls that share a workspace must be ordered on
+ * one stream. */
+BS_API int bs_event_dense_chunks(int32_t batch, int32_t n_in, int32_t n_out, int32_t* chunk_rows);
+BS_API size_t bs_event_dense_workspace_size(int32_t batch, int32_t n_in, int32_t n_out);
+BS_API size_t bs_event_dense_ticket_bytes(int32_t batch, int32_t n_in, int32_t n_out);
 BS_API int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t batch, int32_t n_in,
                        const float* W, int32_t n_out, int32_t float_as_event, float* out,
-                       bs_stream_t stream);
+                       void* workspace, size_t workspace_bytes, bs_stream_t stream);
 
 /* Reverse mode of EventLinear's heterogeneous product (the VJP the reference checks at
  * brainstate/nn/_event_linear_test.py:51-89; its "true gradient" is that of x @ W with the

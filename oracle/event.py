@@ -113,8 +113,13 @@ def gather_post_major(spk, post_indptr, pre_of, w_post, n_post):
     return out
 
 
-def event_linear(spk, W, float_as_event=True, n_out=None):
-    """brainstate/nn/_event_linear.py:75-102 for spk [..., n_in], W [n_in, n_out] or scalar."""
+def event_linear(spk, W, float_as_event=True, n_out=None, chunk_rows=None):
+    """brainstate/nn/_event_linear.py:75-102 for spk [..., n_in], W [n_in, n_out] or scalar.
+
+    Heterogeneous W: each output is a sum of fp32 terms; with ``chunk_rows`` = L the inputs
+    are cut into chunks of L consecutive rows, each chunk summed in ascending order from 0,
+    and the chunk sums added in chunk order (the order the device kernel documents);
+    ``chunk_rows=None`` is the plain ascending sum."""
     spk = np.asarray(spk)
     if np.ndim(W) == 0 or np.size(W) == 1:
         w = F(np.asarray(W).reshape(()))
@@ -126,14 +131,16 @@ def event_linear(spk, W, float_as_event=True, n_out=None):
                 np.asarray(reduced * w, F)[..., None]).astype(F)
     W = np.asarray(W, dtype=F)
     x = spk.reshape(-1, spk.shape[-1])
+    n_in = x.shape[1]
+    L = n_in if chunk_rows is None else int(chunk_rows)
     out = np.zeros((x.shape[0], W.shape[1]), dtype=F)
     for b in range(x.shape[0]):
-        if float_as_event:
-            for i in np.flatnonzero(x[b] != 0):
-                out[b] = (out[b] + W[i]).astype(F)
-        else:
-            for i in np.flatnonzero(x[b] != 0):
-                out[b] = (out[b] + F(x[b, i]) * W[i]).astype(F)
+        for c, lo in enumerate(range(0, max(n_in, 1), max(L, 1))):
+            part = np.zeros(W.shape[1], dtype=F)
+            for i in lo + np.flatnonzero(x[b, lo:lo + L] != 0):
+                term = W[i] if float_as_event else (F(x[b, i]) * W[i]).astype(F)
+                part = (part + term).astype(F)
+            out[b] = part if c == 0 else (out[b] + part).astype(F)
     return out.reshape(spk.shape[:-1] + (W.shape[1],))
 
 

@@ -51,6 +51,38 @@ def test_host_only_calls_without_gpu():
     assert rc == N.BS_ERR_INVALID and b'net is NULL' in lib.bs_last_error()
 
 
+def test_event_dense_chunk_plan_host_only():
+    """The chunk plan of bs_event_dense_f32 is a function of the shape only (no device)."""
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip('library not built')
+    lib = N.load_library()
+    L = ctypes.c_int32(0)
+    # config [4]: 32 column tiles of 128 x 1 batch group -> 8 chunks of 512 rows
+    assert lib.bs_event_dense_chunks(64, 4096, 4096, ctypes.byref(L)) == 8 and L.value == 512
+    # few inputs: one chunk (plain ascending sum), no workspace
+    assert lib.bs_event_dense_chunks(64, 200, 256, ctypes.byref(L)) == 1 and L.value == 256
+    assert lib.bs_event_dense_workspace_size(64, 200, 256) == 0
+    # at most 8 chunks of >= 256 rows; a wide output keeps one chunk
+    assert lib.bs_event_dense_chunks(1, 40000, 64, ctypes.byref(L)) == 8 and L.value == 5056
+    assert lib.bs_event_dense_chunks(64, 512, 256, ctypes.byref(L)) == 2 and L.value == 256
+    assert lib.bs_event_dense_chunks(64, 4096, 1 << 16, ctypes.byref(L)) == 1
+    for b, ni, no in ((64, 4096, 4096), (3, 2500, 66), (130, 1000, 70), (1, 40000, 64)):
+        S = lib.bs_event_dense_chunks(b, ni, no, ctypes.byref(L))
+        assert (S - 1) * L.value < ni <= S * L.value and L.value % 64 == 0
+        tiles, groups = -(-no // 128), -(-b // 64)
+        ws = lib.bs_event_dense_workspace_size(b, ni, no)
+        tick = lib.bs_event_dense_ticket_bytes(b, ni, no)
+        if S == 1:
+            assert ws == 0 and tick == 0
+        else:
+            assert tick == -(-(tiles * groups * 4) // 256) * 256
+            assert ws == tick + S * b * no * 4
+    # a chunked shape without its workspace is refused before any device work
+    rc = lib.bs_event_dense_f32(ctypes.c_void_p(16), 0, 64, 4096, ctypes.c_void_p(16), 4096, 1,
+                                ctypes.c_void_p(16), None, 0, None)
+    assert rc == N.BS_ERR_INVALID and b'workspace' in lib.bs_last_error()
+
+
 def test_struct_layouts_match_header():
     # field counts/order of the ctypes mirrors (sizes of plain C structs on x86-64)
     assert ctypes.sizeof(N.LifParams) == 12 * 4

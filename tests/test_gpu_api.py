@@ -11,6 +11,12 @@ from oracle import event, network, neuron
 pytestmark = pytest.mark.gpu
 
 F = np.float32
+
+
+def ops_chunks(batch, n_in, n_out):
+    """(S, L) of bs_event_dense_f32's summation order for this shape."""
+    from brainstate_amd import ops
+    return ops.event_dense_chunks(batch, n_in, n_out)
 GOLD = os.path.join(os.path.dirname(__file__), 'golden')
 sys.path.insert(0, GOLD)
 import make_golden  # noqa: E402
@@ -107,7 +113,8 @@ def test_event_linear_batched_bit_exact(bs):
     W = rng.normal(0, 0.125, (512, 256)).astype(F)
     m = bs.nn.EventLinear(512, 256, W)
     y = m(torch.tensor(spk, device='cuda')).cpu().numpy()
-    assert np.array_equal(y, event.event_linear(spk, W))
+    _, L = ops_chunks(64, 512, 256)
+    assert np.array_equal(y, event.event_linear(spk, W, chunk_rows=L))
 
 
 class _EINet:

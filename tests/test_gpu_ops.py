@@ -125,18 +125,28 @@ def test_gather_bit_exact(torch_cuda, n_pre, n_post, k, p, het):
 
 @pytest.mark.parametrize('B,n_in,n_out,p,fae,sdt', [
     (1, 20, 40, 0.1, True, 'u8'), (64, 4096, 4096, 0.05, True, 'u8'),
-    (3, 100, 37, 0.3, True, 'f32'), (4, 64, 128, 0.3, False, 'f32'), (2, 10, 8, 0.5, True, 'u8')])
+    (3, 100, 37, 0.3, True, 'f32'), (4, 64, 128, 0.3, False, 'f32'), (2, 10, 8, 0.5, True, 'u8'),
+    (5, 3000, 130, 0.1, True, 'u8'), (3, 2500, 66, 0.2, False, 'f32'),
+    (130, 1000, 70, 0.05, True, 'u8'), (70, 4097, 200, 0.05, False, 'u8'),
+    (1, 40000, 64, 0.01, True, 'u8')])
 def test_event_dense(torch_cuda, B, n_in, n_out, p, fae, sdt):
+    """Bit-exact against the oracle summed in the kernel's documented chunk order."""
     torch = torch_cuda
     from brainstate_amd import ops
-    say('dense', B, n_in, n_out, p, fae, sdt)
+    S, L = ops.event_dense_chunks(B, n_in, n_out)
+    say('dense', B, n_in, n_out, p, fae, sdt, 'chunks', S, L)
     rng = np.random.RandomState(n_in)
     s = rng.rand(B, n_in) < p
     spk = s.astype(np.uint8) if sdt == 'u8' else np.where(s, rng.rand(B, n_in) * 3, 0).astype(F)
     W = rng.normal(0, 0.125, (n_in, n_out)).astype(F)
-    got = ops.event_dense(dev(torch, spk), dev(torch, W), float_as_event=fae).cpu().numpy()
-    ref = event.event_linear(spk, W, float_as_event=fae)
+    ds, dW = dev(torch, spk), dev(torch, W)
+    got = ops.event_dense(ds, dW, float_as_event=fae).cpu().numpy()
+    ref = event.event_linear(spk, W, float_as_event=fae, chunk_rows=L)
     assert np.array_equal(got, ref)
+    # the workspace is left ready: a second call (another spike pattern) is exact too
+    s2 = np.roll(spk, 1, axis=1)
+    got2 = ops.event_dense(dev(torch, s2), dW, float_as_event=fae).cpu().numpy()
+    assert np.array_equal(got2, event.event_linear(s2, W, float_as_event=fae, chunk_rows=L))
 
 
 # ---------------------------------------------------------------- N3 neuron steps

@@ -162,6 +162,28 @@ def test_event_linear_batched_equals_rows():
     assert np.allclose(out, spk.astype(np.float64) @ W.astype(np.float64), atol=1e-5)
 
 
+@pytest.mark.parametrize('L', [64, 128, 192, 1000, 4096])
+def test_event_linear_chunked_order(L):
+    """Chunked sums: integer-valued weights make every order exact, so the chunked oracle must
+    equal the integer product (a row dropped or counted twice at a chunk boundary fails);
+    L >= n_in is the plain ascending sum; real weights stay within fp32 rounding of float64."""
+    rng = np.random.RandomState(L)
+    n_in = 1000
+    spk = rng.rand(6, n_in) < 0.1
+    Wi = rng.randint(-8, 9, (n_in, 24)).astype(F)
+    assert np.array_equal(event.event_linear(spk, Wi, chunk_rows=L),
+                          (spk.astype(np.int64) @ Wi.astype(np.int64)).astype(F))
+    x = np.where(spk, rng.rand(6, n_in) * 3, 0).astype(F)
+    Wf = rng.normal(0, 0.125, (n_in, 24)).astype(F)
+    got = event.event_linear(x, Wf, float_as_event=False, chunk_rows=L)
+    assert np.allclose(got, x.astype(np.float64) @ Wf.astype(np.float64), rtol=1e-5, atol=1e-5)
+    if L >= n_in:
+        assert np.array_equal(got, event.event_linear(x, Wf, float_as_event=False))
+    else:  # a different grouping of the same terms: equal up to rounding, not bit for bit
+        assert not np.array_equal(event.event_linear(spk, Wf, chunk_rows=L),
+                                  event.event_linear(spk, Wf))
+
+
 # ---- derivative restatements: pinned by identities, not by retyping the formulas ----
 
 def _conn(seed, n_pre=40, n_post=30, k=5):
