@@ -129,7 +129,8 @@ def _timed(fn, reps, warm=2):
 
 def bench_sparse(args):
     """event CSR mat-vec 100k x 100k, K=1000, w ~ N(0.5, 0.1), p in {.001,.01,.1}.
-    Scatter (compaction + atomic scatter) and deterministic SELL-64 gather."""
+    Destination-bucketed scatter (LDS atomics, no global atomics), scatter (compaction + atomic
+    scatter), fused atomic mat-vec and deterministic SELL-64 gather."""
     import torch
     from brainstate_amd import ops
     n, k = 100_000, 1000
@@ -140,6 +141,7 @@ def bench_sparse(args):
     d_w = torch.from_numpy(w).cuda()
     indptr = (np.arange(n + 1, dtype=np.int64) * k).astype(np.int32)
     sell = ops.build_sell(indptr, idx.reshape(-1), n, n, w=w, device='cuda')
+    bkt = ops.build_buckets(d_idx, n, w=d_w)
     out = torch.empty(n, device='cuda')
     lines = []
     for p in (0.001, 0.01, 0.1):
@@ -158,12 +160,18 @@ def bench_sparse(args):
         def fused():
             ops.event_matvec(spk, d_idx, d_w, n, out=out)
 
+        def bucket():
+            ops.event_bucket(spk, bkt, out=out)
+
         ts = _timed(scatter, 20)
         tg = _timed(gather, 20)
         tf = _timed(fused, 20)
+        tb = _timed(bucket, 50)
         b_s = n * 1 + E * 8 + n * 4
         b_g = (n + 1) * 4 + sell['padded'] * 4 + E * 4 + n + n * 4
         lines.append({'workload': f'event_matvec_100k_K1000_p{p}', 'events': E,
+                      'bucket_us': tb * 1e6, 'bucket_GSOPs': E / tb / 1e9,
+                      'bucket_alg_GBs': b_s / tb / 1e9, 'bucket_frac': b_s / tb / PEAK_HBM,
                       'fused_matvec_us': tf * 1e6, 'fused_GSOPs': E / tf / 1e9,
                       'scatter_us': ts * 1e6, 'scatter_GSOPs': E / ts / 1e9,
                       'scatter_alg_GBs': b_s / ts / 1e9, 'scatter_frac': b_s / ts / PEAK_HBM,

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, 'csrc')
 LIBDIR = os.path.join(HERE, '_lib')
 LIB = os.path.join(LIBDIR, 'libbsamd.so')
-SOURCES = ['runtime.hip', 'compact.hip', 'event_sparse.hip', 'event_dense.hip',
+SOURCES = ['runtime.hip', 'compact.hip', 'event_sparse.hip', 'event_bucket.hip', 'event_dense.hip',
            'neuron.hip', 'network.hip', 'delay.hip', 'conn.hip']
 ARCH = 'gfx950'
 

@@ -253,6 +253,67 @@ def build_sell(indptr, indices, n_pre, n_post, w=None, w_homo=0.0, device='cuda'
                 padded=total, nnz=nnz)
 
 
+def build_buckets(indices, n_post, w=None, w_homo=0.0, indptr=None, k=None):
+    """Destination-bucketed layout of a fixed-num ([n_pre, k] indices) or CSR connectivity, built
+    on the device (layout contract of ``bs_bucket_build``); ``w`` per synapse or None."""
+    N.require_gpu()
+    dev = indices.device
+    idx = indices.contiguous().to(torch.int32)
+    if indptr is None:
+        if idx.dim() == 2:
+            n_pre, k = idx.shape
+        else:
+            k = int(k)
+            n_pre = idx.numel() // k if k > 0 else 0
+        ip = None
+    else:
+        ip = indptr.contiguous().to(device=dev, dtype=torch.int32)
+        n_pre = ip.numel() - 1
+        k = 0
+    nnz = idx.numel()
+    P = ctypes.c_int32(0)
+    nb = int(N.lib().bs_bucket_plan(int(n_post), ctypes.byref(P)))
+    if nb < 0:
+        N.check(N.BS_ERR_INVALID, 'bs_bucket_plan')
+    seg = torch.empty(max(n_pre * (nb + 1), 1), dtype=torch.int32, device=dev)
+    lidx = torch.empty(max(nnz, 1), dtype=torch.int16, device=dev)
+    lw = qexp = scratch = None
+    if w is not None:
+        wt = torch.as_tensor(w, dtype=torch.float32, device=dev).contiguous().reshape(-1)
+        lw = torch.empty(max(nnz, 1), dtype=torch.float32, device=dev)
+        qexp = torch.zeros(1, dtype=torch.int32, device=dev)
+        scratch = torch.zeros(1, dtype=torch.int32, device=dev)
+    opt = lambda t: N.ptr(t) if t is not None else None
+    N.check(N.lib().bs_bucket_build(int(n_pre), opt(ip), N.ptr(idx), int(k),
+                                    N.ptr(wt) if w is not None else None, int(n_post), nb,
+                                    P.value, N.ptr(seg), N.ptr(lidx), opt(lw), opt(qexp),
+                                    opt(scratch), N.stream_handle(dev)), 'bs_bucket_build')
+    return dict(n_pre=int(n_pre), n_post=int(n_post), nb=nb, P=P.value, seg=seg, lidx=lidx,
+                w=lw, qexp=qexp, w_homo=float(w_homo))
+
+
+def event_bucket(spk, layout, out=None, accumulate=False):
+    """``EventArray(spk) @ conn`` on a destination-bucketed layout (``build_buckets``)."""
+    spk = _spk_view(spk)
+    L = layout
+    dev = L['seg'].device
+    if out is None:
+        out = torch.empty(L['n_post'], dtype=torch.float32, device=dev)
+    nbytes = int(N.lib().bs_event_bucket_workspace_size(L['n_pre'], L['n_post'], L['nb']))
+    key = ('bucket', dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WS_CACHE.get(key)
+    if nbytes > 0 and (ws is None or ws.numel() < nbytes):
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WS_CACHE[key] = ws
+    N.check(N.lib().bs_event_bucket_f32(
+        N.ptr(spk), _spk_dtype(spk), L['n_pre'], L['n_post'], L['nb'], L['P'], N.ptr(L['seg']),
+        N.ptr(L['lidx']), N.ptr(L['w']) if L['w'] is not None else None,
+        N.ptr(L['qexp']) if L['qexp'] is not None else None, L['w_homo'], N.ptr(out),
+        1 if accumulate else 0, N.ptr(ws) if nbytes > 0 else None, nbytes,
+        N.stream_handle(dev)), 'bs_event_bucket_f32')
+    return out
+
+
 def event_dense(spk, W, float_as_event=True, out=None):
     """spk [B, n_in] (or [n_in]) x W [n_in, n_out] -> [B, n_out]."""
     squeeze = spk.dim() == 1

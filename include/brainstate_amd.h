@@ -115,6 +115,41 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
                                    const float* grad_out, float* grad_spk, float* grad_w,
                                    bs_stream_t stream);
 
+/* ---------------------------------------------------------------- N2a, destination-bucketed
+ * Same operator as bs_event_scatter_f32 / bs_event_matvec_f32 (replaces `EventArray(spk) @
+ * FixedPostNumConn` / `@ CSR`, brainstate/nn/_event_fixedprob.py:176-181,192,202-205,249-252)
+ * with no global atomics and no fp32 atomics, on a layout built once per connectivity:
+ *   nb = bs_bucket_plan(n_post, &P): posts are cut into nb buckets of P consecutive posts
+ *        (bucket b holds [b*P, min((b+1)*P, n_post)), P <= 12288, nb <= 1024);
+ *   bs_bucket_build: seg[n_pre][nb+1] (int32), lidx[nnz] (uint16), lw[nnz] (fp32 or NULL)
+ *        and, with per-synapse weights, the fixed-point exponent *qexp (device int32;
+ *        `workspace` = 4 device bytes of scratch).  Row i's synapses stay inside
+ *        [indptr[i], indptr[i+1]) (fixed-num: [i*k, i*k+k)), sorted by bucket with the
+ *        original order kept inside a bucket; bucket b's synapses of row i are
+ *        [seg[i][b], seg[i][b+1]) with lidx = target - b*P; valid synapses end at seg[i][nb]
+ *        (out-of-range targets follow and are never read).  S = *qexp = 60 - e_w - e_n with
+ *        max|w| < 2^e_w and nnz <= 2^e_n (-1000 if a weight is not finite).
+ * bs_event_bucket_f32: out[j] = (accumulate ? out[j] : 0) + v_j, where v_j is
+ *   - per-synapse weights, finite: each weight of an event onto j rounded to a multiple of
+ *     2^-S (round to nearest even), the rounded weights summed exactly (64-bit integers),
+ *     the sum rounded once to fp32 and scaled by 2^-S: deterministic, whatever the order of
+ *     the device's atomics;
+ *   - homogeneous weight (lw == NULL): w_homo added once per event onto j, in one chain
+ *     starting from out[j] (or 0): bit-identical to a sequential scatter;
+ *   - a non-finite per-synapse weight: fp32 sums in an unspecified order.
+ * `workspace`: bs_event_bucket_workspace_size bytes, no initialisation needed. */
+BS_API int bs_bucket_plan(int32_t n_post, int32_t* P_out);
+BS_API int bs_bucket_build(int32_t n_pre, const int32_t* indptr, const int32_t* indices, int32_t k,
+                           const float* w, int32_t n_post, int32_t nb, int32_t P, int32_t* seg,
+                           uint16_t* lidx, float* lw, int32_t* qexp, void* workspace,
+                           bs_stream_t stream);
+BS_API size_t bs_event_bucket_workspace_size(int32_t n_pre, int32_t n_post, int32_t nb);
+BS_API int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n_pre, int32_t n_post,
+                               int32_t nb, int32_t P, const int32_t* seg, const uint16_t* lidx,
+                               const float* lw, const int32_t* qexp, float w_homo, float* out,
+                               int32_t accumulate, void* workspace, size_t workspace_bytes,
+                               bs_stream_t stream);
+
 /* ---------------------------------------------------------------- N2b event gather
  * Same operator as N2a, post-major and deterministic (no atomics).  Spikes come as a
  * bitmap (bs_spike_pack: bit i%32 of word i/32 set <=> spk[i] != 0).  Layout SELL-64x4:

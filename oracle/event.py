@@ -144,6 +144,41 @@ def event_linear(spk, W, float_as_event=True, n_out=None, chunk_rows=None):
     return out.reshape(spk.shape[:-1] + (W.shape[1],))
 
 
+# ---- destination-bucketed operator: exact fixed-point sums ----
+
+def bucket_qexp(w, nnz):
+    """Fixed-point exponent S of the bucketed layout: 60 - e_w - e_n with max|w| < 2^e_w and
+    nnz <= 2^e_n; -1000 if a weight is not finite, 0 if every weight is 0."""
+    w = np.abs(np.asarray(w, dtype=F).reshape(-1))
+    if w.size and not np.all(np.isfinite(w)):
+        return -1000
+    wmax = float(w.max()) if w.size else 0.0
+    if wmax == 0.0:
+        return 0
+    e_w = int(np.frexp(np.float64(wmax))[1])          # wmax = m * 2^e_w, 0.5 <= m < 1
+    e_n = 0
+    while (1 << e_n) < nnz:
+        e_n += 1
+    return 60 - e_w - e_n
+
+
+def scatter_fixed_point(spk, indptr, indices, w, n_post, S):
+    """Event mat-vec with each weight rounded to a multiple of 2^-S (round half to even), the
+    rounded weights of the events onto each output summed exactly, the sum rounded once to
+    fp32 and scaled by 2^-S.  Out-of-range targets contribute nothing."""
+    indptr = np.asarray(indptr, dtype=np.int64)
+    indices = np.asarray(indices, dtype=np.int64)
+    w = np.asarray(w, dtype=F).reshape(-1)
+    acc = np.zeros(n_post, dtype=np.int64)
+    for i in np.flatnonzero(np.asarray(spk) != 0):
+        lo, hi = indptr[i], indptr[i + 1]
+        t = indices[lo:hi]
+        keep = (t >= 0) & (t < n_post)
+        q = np.rint(np.ldexp(w[lo:hi][keep].astype(np.float64), S)).astype(np.int64)
+        np.add.at(acc, t[keep], q)
+    return np.ldexp(acc.astype(F), -S).astype(F)
+
+
 # ---- derivatives (float64) ----
 
 def _rows_of(idx, indptr):

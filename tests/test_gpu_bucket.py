@@ -1,0 +1,193 @@
+"""GPU parity of the destination-bucketed event mat-vec (bs_bucket_build, bs_event_bucket_f32)
+against the oracle's sequential scatter (brainstate/nn/_event_fixedprob.py:202-209,249-252;
+closed form of _event_fixedprob_test.py:247-260)."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import event
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+@pytest.fixture(scope='module')
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail('GPU tests need a ROCm GPU')
+    from brainstate_amd import _native
+    _native.load_library()
+    return torch
+
+
+def say(*a):
+    print('[case]', *a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(t, a):
+    return t.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def expected_layout(indptr, indices, n_post, nb, P):
+    """The layout contract of bs_bucket_build, restated row by row with a stable sort."""
+    n_pre = indptr.size - 1
+    seg = np.zeros((n_pre, nb + 1), np.int64)
+    lidx = np.zeros(indices.size, np.int64)
+    for i in range(n_pre):
+        lo, hi = int(indptr[i]), int(indptr[i + 1])
+        t = indices[lo:hi].astype(np.int64)
+        valid = (t >= 0) & (t < n_post)
+        b = np.where(valid, t // P, nb)
+        order = np.argsort(b, kind='stable')
+        lidx[lo:hi] = np.where(valid, t - b * P, 0)[order]
+        counts = np.bincount(b[valid], minlength=nb)
+        seg[i, :nb] = lo + np.concatenate([[0], np.cumsum(counts)[:-1]])
+        seg[i, nb] = lo + valid.sum()
+    return seg, lidx
+
+
+@pytest.mark.parametrize('n_pre,n_post,k,het', [(300, 1000, 17, True), (70, 5, 9, False),
+                                                (513, 200_003, 40, True)])
+def test_layout_matches_contract(torch_cuda, n_pre, n_post, k, het):
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket layout', n_pre, n_post, k, het)
+    rng = np.random.RandomState(n_pre)
+    idx = rng.randint(-2, n_post + 2, (n_pre, k)).astype(np.int32)  # some out of range
+    w = rng.rand(n_pre, k).astype(F) if het else None
+    L = ops.build_buckets(dev(torch, idx), n_post, w=w, w_homo=0.5)
+    nb, P = L['nb'], L['P']
+    assert nb * P >= n_post > (nb - 1) * P and P <= 16384
+    indptr = np.arange(n_pre + 1, dtype=np.int64) * k
+    seg, lidx = expected_layout(indptr, idx.reshape(-1), n_post, nb, P)
+    got_seg = L['seg'][:n_pre * (nb + 1)].cpu().numpy().reshape(n_pre, nb + 1)
+    assert np.array_equal(got_seg, seg)
+    got = L['lidx'].cpu().numpy().view(np.uint16).astype(np.int64)[:idx.size]
+    for i in range(n_pre):  # valid synapses (out-of-range ones follow, never read)
+        lo, hi = seg[i, 0], seg[i, nb]
+        assert np.array_equal(got[lo:hi], lidx[lo:hi])
+    if het:
+        # weights travel with their synapse: the bucketed sums reproduce the row sums
+        got_w = L['w'].cpu().numpy()[:idx.size]
+        for i in range(0, n_pre, 37):
+            lo, hi = seg[i, 0], seg[i, nb]
+            row = idx[i]
+            valid = (row >= 0) & (row < n_post)
+            assert np.isclose(got_w[lo:hi].astype(np.float64).sum(),
+                              w[i][valid].astype(np.float64).sum(), rtol=1e-6)
+
+
+@pytest.mark.parametrize('n_pre,n_post,k,p,het,sdt', [
+    (2000, 3000, 50, 0.1, True, 'u8'), (2000, 3000, 50, 0.1, False, 'u8'),
+    (20_000, 100_000, 200, 0.01, True, 'u8'), (20_000, 100_000, 200, 0.1, False, 'u8'),
+    (5000, 150_000, 100, 0.05, True, 'f32'), (64, 10, 3, 0.5, True, 'u8'),
+    (1000, 1000, 10, 0.0, True, 'u8'), (100_000, 100_000, 1000, 0.001, True, 'u8')])
+def test_bucket_matvec_matches_oracle(torch_cuda, n_pre, n_post, k, p, het, sdt):
+    """Per-synapse weights: bit-exact against the oracle's fixed-point restatement and within
+    rtol 1e-5 / atol 1e-6 of the sequential fp32 scatter; homogeneous weights bit-exact
+    against the sequential scatter (counted events, one chain of additions)."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket matvec', n_pre, n_post, k, p, het, sdt)
+    rng = np.random.RandomState(k + n_pre)
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F) if het else F(0.6)
+    s = rng.rand(n_pre) < p
+    spk = s.astype(np.uint8) if sdt == 'u8' else np.where(s, rng.rand(n_pre) + 0.5, 0).astype(F)
+    L = ops.build_buckets(dev(torch, idx), n_post, w=w if het else None, w_homo=0.6)
+    got = ops.event_bucket(dev(torch, spk), L).cpu().numpy()
+    ref = event.scatter_fixed(spk, idx, w, n_post)
+    if het:
+        S = int(L['qexp'].item())
+        assert S == event.bucket_qexp(w, idx.size)
+        indptr = np.arange(n_pre + 1, dtype=np.int64) * k
+        exact = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, n_post, S)
+        assert np.array_equal(got, exact)                      # the documented arithmetic
+        assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)     # the sequential fp32 scatter
+        again = ops.event_bucket(dev(torch, spk), L).cpu().numpy()
+        assert np.array_equal(got, again)                      # deterministic
+    else:
+        assert np.array_equal(got, ref)
+    # accumulate adds onto what is there
+    base = rng.rand(n_post).astype(F)
+    acc = ops.event_bucket(dev(torch, spk), L, out=dev(torch, base.copy()), accumulate=True)
+    assert np.allclose(acc.cpu().numpy(), base + ref, rtol=1e-5, atol=1e-5)
+
+
+def test_bucket_csr_ragged_and_out_of_range(torch_cuda):
+    """CSR rows of varying length (some empty) with out-of-range targets, which contribute
+    nothing (as in the scatter)."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket csr')
+    rng = np.random.RandomState(5)
+    n_pre, n_post = 3000, 40_000
+    lens = rng.randint(0, 90, n_pre)
+    lens[::17] = 0
+    indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    indices = rng.randint(-5, n_post + 5, indptr[-1]).astype(np.int32)
+    w = rng.rand(indptr[-1]).astype(F)
+    spk = (rng.rand(n_pre) < 0.2).astype(np.uint8)
+    L = ops.build_buckets(dev(torch, indices), n_post, w=w, indptr=dev(torch, indptr))
+    got = ops.event_bucket(dev(torch, spk), L).cpu().numpy()
+    keep = (indices >= 0) & (indices < n_post)
+    ref = event.scatter_csr(spk, indptr, np.where(keep, indices, 0), np.where(keep, w, 0), n_post)
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)
+    S = int(L['qexp'].item())
+    assert S == event.bucket_qexp(w[keep], indices.size)  # max over the valid synapses
+    assert np.array_equal(got, event.scatter_fixed_point(spk, indptr, indices, w, n_post, S))
+
+
+def test_bucket_non_finite_weight_falls_back(torch_cuda):
+    """A non-finite per-synapse weight cannot be held in fixed point: the sums fall back to
+    fp32 and the inf / nan reach exactly the outputs the scatter sends them to."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket non-finite')
+    rng = np.random.RandomState(9)
+    n_pre, n_post, k = 500, 2000, 20
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.rand(n_pre, k).astype(F)
+    w[3, 4] = np.inf
+    w[7, 1] = np.nan
+    spk = (rng.rand(n_pre) < 0.5).astype(np.uint8)
+    spk[3] = spk[7] = 1
+    L = ops.build_buckets(dev(torch, idx), n_post, w=w)
+    assert int(L['qexp'].item()) == -1000
+    got = ops.event_bucket(dev(torch, spk), L).cpu().numpy()
+    ref = event.scatter_fixed(spk, idx, w, n_post)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(np.isinf(got), np.isinf(ref))
+    fin = np.isfinite(ref)
+    assert np.allclose(got[fin], ref[fin], rtol=1e-5, atol=1e-6)
+
+
+def test_bucket_config2_full_size_properties(torch_cuda):
+    """Config [2] at full size (100k x 100k, K = 1000, p = 0.1): homogeneous weights equal the
+    fused atomic mat-vec bit for bit (a chain of one repeated value is order-free); per-synapse
+    weights are deterministic, conserve the total mass and match the atomic mat-vec within
+    the atomic-path tolerance."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket config2 full size')
+    n, k = 100_000, 1000
+    rng = np.random.RandomState(7)
+    d_idx = dev(torch, rng.randint(0, n, size=(n, k)).astype(np.int32))
+    d_w = dev(torch, rng.normal(0.5, 0.1, (n, k)).astype(F))
+    spk = (np.random.RandomState(1000).rand(n) < 0.1).astype(np.uint8)
+    d_spk = dev(torch, spk)
+    Lh = ops.build_buckets(d_idx, n, w=None, w_homo=0.6)
+    gh = ops.event_bucket(d_spk, Lh).cpu().numpy()
+    assert np.array_equal(gh, ops.event_matvec(d_spk, d_idx, 0.6, n).cpu().numpy())
+    del Lh
+    L = ops.build_buckets(d_idx, n, w=d_w)
+    got = ops.event_bucket(d_spk, L).cpu().numpy().astype(np.float64)
+    assert np.array_equal(got, ops.event_bucket(d_spk, L).cpu().numpy())  # deterministic
+    act = torch.from_numpy(spk.astype(bool)).cuda()
+    mass = float(d_w[act].double().sum().item())
+    assert np.isclose(got.sum(), mass, rtol=1e-5)
+    ref = ops.event_matvec(d_spk, d_idx, d_w, n).cpu().numpy()
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-4)

@@ -184,6 +184,57 @@ def test_event_linear_chunked_order(L):
                                   event.event_linear(spk, Wf))
 
 
+# ---- bucketed operator: fixed-point exponent and exact sums ----
+
+def test_bucket_qexp_bounds_every_sum():
+    """S keeps nnz * max|w| below 2^60 units and is as large as that allows (one more bit
+    would break the bound for some nnz / max|w|)."""
+    rng = np.random.RandomState(3)
+    for _ in range(200):
+        nnz = int(rng.randint(1, 10**8))
+        wmax = F(rng.lognormal(0, 8))
+        S = event.bucket_qexp(np.array([wmax, -wmax / 2], F), nnz)
+        assert nnz * float(wmax) * 2.0 ** S < 2.0 ** 60
+        assert nnz * float(wmax) * 2.0 ** (S + 2) >= 2.0 ** 60 or nnz == 1
+    assert event.bucket_qexp(np.zeros(5, F), 5) == 0
+    assert event.bucket_qexp(np.array([1.0, np.inf], F), 2) == -1000
+    assert event.bucket_qexp(np.array([np.nan], F), 1) == -1000
+    assert event.bucket_qexp(np.array([0.75], F), 1) == 60       # 0.75 < 2^0, nnz = 2^0
+
+
+def test_fixed_point_scatter_is_the_rounded_exact_sum():
+    """Weights that are multiples of 2^-S are exact, so the result is the exact sum rounded
+    once (checked through float64, exact here); any event order gives the same bits; real
+    weights stay within fp32 rounding of the float64 sum and of the sequential oracle."""
+    rng = np.random.RandomState(11)
+    n_pre, n_post, k = 400, 300, 30
+    idx = rng.randint(0, n_post, (n_pre, k))
+    indptr = np.arange(n_pre + 1) * k
+    spk = rng.rand(n_pre) < 0.3
+    S = event.bucket_qexp(np.ones(1, F), n_pre * k)
+    wq = (rng.randint(-2**20, 2**20, n_pre * k) * 2.0 ** -18).astype(F)  # multiples of 2^-18
+    got = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), wq, n_post, S)
+    exact = np.zeros(n_post)
+    act = np.repeat(spk, k)
+    np.add.at(exact, idx.reshape(-1)[act], wq[act].astype(np.float64))
+    assert np.array_equal(got, exact.astype(F))
+    perm = rng.permutation(k)  # reorder every row's synapses
+    got2 = event.scatter_fixed_point(spk, indptr, idx[:, perm].reshape(-1),
+                                     wq.reshape(n_pre, k)[:, perm].reshape(-1), n_post, S)
+    assert np.array_equal(got, got2)
+    w = rng.normal(0.5, 0.1, n_pre * k).astype(F)
+    Sw = event.bucket_qexp(w, n_pre * k)
+    gw = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, n_post, Sw)
+    ref64 = np.zeros(n_post)
+    np.add.at(ref64, idx.reshape(-1)[act], w[act].astype(np.float64))
+    assert np.allclose(gw, ref64, rtol=2e-7, atol=1e-12)
+    seq = event.scatter_csr(spk, indptr, idx.reshape(-1), w, n_post)
+    assert np.allclose(gw, seq, rtol=1e-5, atol=1e-6)
+    # a scale off by one bit would be caught
+    assert not np.allclose(event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, n_post,
+                                                     Sw) * 2, ref64, rtol=1e-3)
+
+
 # ---- derivative restatements: pinned by identities, not by retyping the formulas ----
 
 def _conn(seed, n_pre=40, n_post=30, k=5):
