@@ -95,6 +95,9 @@ __global__ __launch_bounds__(kBB) void k_bucket_place(int32_t n_pre, const int32
   for (int b = lane; b <= nb; b += BS_WAVE) run[b] = b < nb ? sr[b] : sr[nb];
   const int64_t beg = indptr ? indptr[i] : i * (int64_t)k;
   const int64_t end = indptr ? indptr[i + 1] : beg + k;
+  // max |w| over the row's valid synapses (the bit pattern of a non-negative float orders like
+  // its value; NaN sorts above +inf): lane maxima, a wave maximum, one atomic per row
+  uint32_t amax = 0u;
   // 64 synapses at a time; each distinct bucket of the chunk is ranked with one ballot, so
   // synapses keep their original order inside a bucket
   for (int64_t s0 = beg; s0 < end; s0 += BS_WAVE) {
@@ -102,6 +105,10 @@ __global__ __launch_bounds__(kBB) void k_bucket_place(int32_t n_pre, const int32
     const bool live = s < end;
     int32_t t = live ? indices[s] : 0;
     const int b = !live ? -1 : ((uint32_t)t < (uint32_t)n_post ? t / P : nb);
+    if (lw && live && b < nb) {
+      const uint32_t aw = __float_as_uint(w[s]) & 0x7FFFFFFFu;
+      amax = aw > amax ? aw : amax;
+    }
     uint64_t left = bs_ballot(live);
     while (left) {
       const int leader = __builtin_ctzll(left);
@@ -113,13 +120,17 @@ __global__ __launch_bounds__(kBB) void k_bucket_place(int32_t n_pre, const int32
         lidx[pos] = (uint16_t)(bl < nb ? t - bl * P : 0);
         if (lw) lw[pos] = w[s];
       }
-      if (lw && b == bl && bl < nb) {
-        const uint32_t aw = __float_as_uint(w[s]) & 0x7FFFFFFFu;  // |w|, NaN above +inf
-        atomicMax(wmax, aw);
-      }
+
       if (lane == leader) run[bl] = base + (int32_t)__popcll(m);
       left &= ~m;
     }
+  }
+  if (lw) {
+    for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+      const uint32_t x = (uint32_t)__shfl_xor((int)amax, o);
+      amax = x > amax ? x : amax;
+    }
+    if (lane == 0 && amax) atomicMax(wmax, amax);
   }
 }
 
