@@ -6,6 +6,10 @@
   fused HIP spike-vector event mat-vec (C ABI ``bs_event_matvec_f32``: per-workgroup
   compaction of the spike vector, then the pre-major scatter of the active rows) instead of
   brainevent's kernel.
+  With ``event_kernel='bucket'`` (or ``'auto'`` for outputs wider than 16,384 neurons), the
+  event path of inference runs the destination-bucketed operator instead
+  (``bs_event_bucket_f32``: no global or fp32 atomics, exact fixed-point sums, deterministic)
+  on a layout built on first use and rebuilt when the weight value changes.
 * ``EventLinear`` -- brainstate/nn/_event_linear.py:32-102, on ``bs_event_dense_f32``.
 
 Both are differentiable (torch autograd, reverse and forward mode) with the gradients the
@@ -98,6 +102,21 @@ class _EventMatvecFn(torch.autograd.Function):
         return t
 
 
+def _no_autodiff(*ts):
+    """True when no operand takes part in reverse or forward mode autodiff."""
+    from torch.autograd import forward_ad
+    for t in ts:
+        if torch.is_tensor(t):
+            if t.requires_grad and torch.is_grad_enabled():
+                return False
+            if forward_ad.unpack_dual(t).tangent is not None:
+                return False
+    return True
+
+
+_BUCKET_AUTO_POSTS = 16384   # 'auto': bucketed above this many outputs (one LDS accumulator)
+
+
 def _wants_grad(*ts):
     """Route through the autograd Functions whenever autodiff may be recording: grad mode on
     and a tensor operand (forward-mode dual tensors do not set requires_grad).  Under
@@ -172,8 +191,12 @@ class FixedNumConn(Module):
 
     def __init__(self, in_size, out_size, conn_num, conn_weight, efferent_target='post',
                  afferent_ratio=1., allow_multi_conn=True, seed=None, name=None,
-                 conn_init='vmap', param_type=ParamState):
+                 conn_init='vmap', param_type=ParamState, event_kernel='auto'):
         super().__init__(name=name)
+        if event_kernel not in ('auto', 'atomic', 'bucket'):
+            raise ValueError(f"event_kernel must be 'auto', 'atomic' or 'bucket', not {event_kernel!r}")
+        self.event_kernel = event_kernel
+        self._bucket = None       # (key of the weight value, layout)
         self.in_size = init.to_size(in_size)
         self.out_size = init.to_size(out_size)
         self.efferent_target = efferent_target
@@ -260,11 +283,40 @@ class FixedNumConn(Module):
             lead = tuple(x.shape[:-1]) if torch.is_tensor(x) else ()
             return torch.zeros(lead + (self.out_size[-1],), dtype=torch.float32,
                                device=_device())
-        conn = self.conn.with_data(_weight_for_kernel(self.weight.value))
+        w = _weight_for_kernel(self.weight.value)
         x = x if torch.is_tensor(x) else _to_dev(x, torch.float32)
         if x.device.type != 'cuda':
             x = x.to(_device())
+        if not value and x.dim() == 1 and self._bucketed() and _no_autodiff(x, w):
+            return ops.event_bucket(x, self._bucket_layout(w))
+        conn = self.conn.with_data(w)
         return conn.matvec_events(x, value)   # [..., n_pre] -> [..., n_post], one launch
+
+    def _bucketed(self):
+        if self.event_kernel == 'bucket':
+            return True
+        return self.event_kernel == 'auto' and self.out_size[-1] > _BUCKET_AUTO_POSTS
+
+    def _bucket_layout(self, w):
+        """Destination-bucketed layout of the current connectivity and weight; rebuilt when the
+        weight State is assigned a new value or its tensor is modified in place."""
+        v = self.weight.value
+        key = (id(v), v._version if torch.is_tensor(v) else None,
+               float(v) if init._is_scalar(v) else None)
+        if self._bucket is None or self._bucket[0] != key:
+            homo = w.numel() == 1
+            conn = self.conn
+            indptr = getattr(conn, 'indptr', None)
+            wt = None
+            if not homo:
+                wt = w.detach()
+                if indptr is None and wt.shape != conn.indices.shape:
+                    wt = wt.expand(conn.indices.shape)
+            layout = ops.build_buckets(conn.indices, self.out_size[-1], w=wt,
+                                       w_homo=float(w.reshape(())) if homo else 0.0,
+                                       indptr=indptr)
+            self._bucket = (key, layout)
+        return self._bucket[1]
 
     def update(self, x):
         """``x @ conn`` (:202-209): bool spikes are events; any other dtype is a

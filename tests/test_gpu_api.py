@@ -199,3 +199,39 @@ def test_hh_module_step_matches_oracle(bs):
         V, m, h, nn_, ge, gi, spk = neuron.hh_step(V, m, h, nn_, ge, gi, z, z, p)
         assert np.array_equal(out[t], spk)
     assert np.array_equal(hh.V.value.cpu().numpy(), V)
+
+
+@pytest.mark.parametrize('het,ratio', [(True, 1.0), (False, 1.0), (True, 0.6)])
+def test_event_fixed_prob_bucketed_path(bs, het, ratio):
+    """event_kernel='auto' on a wide output (> 16,384 posts) runs the bucketed operator; it
+    matches the atomic path (bit for bit for a homogeneous weight, within the atomic-path
+    tolerance otherwise), follows a new weight value, and autodiff still goes through the
+    differentiable path."""
+    import torch
+    print('[case] event fixed prob bucketed', het, ratio, flush=True)
+    n_pre, n_post = 3000, 40_000
+    w = bs.nn.init.Normal(0.5, 0.1) if het else 0.6
+    kw = dict(conn_num=0.002, conn_weight=w, seed=42, afferent_ratio=ratio)
+    torch.manual_seed(0)
+    auto = bs.nn.EventFixedProb(n_pre, n_post, **kw)
+    atomic = bs.nn.EventFixedProb(n_pre, n_post, event_kernel='atomic', **kw)
+    atomic.weight.value = auto.weight.value
+    spk = torch.from_numpy(np.random.RandomState(3).rand(n_pre) < 0.2).cuda()
+    a = auto(spk).cpu().numpy()
+    assert auto._bucket is not None and atomic._bucket is None
+    b = atomic(spk).cpu().numpy()
+    if het:
+        assert np.allclose(a, b, rtol=1e-5, atol=1e-6)
+    else:
+        assert np.array_equal(a, b)
+    if het:  # a new weight value rebuilds the layout
+        auto.weight.value = auto.weight.value * 2
+        atomic.weight.value = auto.weight.value
+        assert np.allclose(auto(spk).cpu().numpy(), atomic(spk).cpu().numpy(), rtol=1e-5,
+                           atol=1e-6)
+        wv = torch.as_tensor(np.asarray(auto.weight.value), dtype=torch.float32,
+                             device='cuda').clone().requires_grad_(True)
+        auto.weight.value = wv
+        y = auto(spk.to(torch.float32))   # float spikes: value path, differentiable
+        y.sum().backward()
+        assert wv.grad is not None and torch.isfinite(wv.grad).all()
