@@ -126,6 +126,8 @@ struct LifModel {
     s.gi[j] = r.gi;
     s.ref[j] = r.ref;
   }
+  static constexpr bool kPrepare = false;  // every operation of the step needs the input
+  __device__ static void prepare(const Params&, Regs&) {}
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
     return bs_lif_update(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
   }
@@ -144,9 +146,17 @@ struct HhModel {
   using State = bs_hh_state;
   struct Regs {
     float V, m, h, n, ge, gi;
+    bs_hh_pre pre;  // input-independent part of the coming step
   };
   __device__ static Regs load(const State& s, int64_t j) {
-    return Regs{s.V[j], s.m[j], s.h[j], s.n[j], s.ge[j], s.gi[j]};
+    Regs r;
+    r.V = s.V[j];
+    r.m = s.m[j];
+    r.h = s.h[j];
+    r.n = s.n[j];
+    r.ge = s.ge[j];
+    r.gi = s.gi[j];
+    return r;
   }
   __device__ static void store(const State& s, int64_t j, const Regs& r) {
     s.V[j] = r.V;
@@ -156,8 +166,14 @@ struct HhModel {
     s.ge[j] = r.ge;
     s.gi[j] = r.gi;
   }
+  // The gate updates and channel conductances need only the previous state, so they run
+  // before the step's inputs are awaited; the rest of the step follows once they are in.
+  static constexpr bool kPrepare = true;
+  __device__ static void prepare(const Params& p, Regs& r) {
+    r.pre = bs_hh_prepare(p, r.V, r.m, r.h, r.n);
+  }
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
-    return bs_hh_update(p, r.V, r.m, r.h, r.n, r.ge, r.gi, in_e, in_i);
+    return bs_hh_finish(p, r.pre, r.V, r.m, r.h, r.n, r.ge, r.gi, in_e, in_i);
   }
   // No row prefetch for HH: its spikes are rarer and its update is VALU-heavy, and on the
   // 1M-neuron net prefetching the rows of neurons on the upstroke (V within 10-60 mV below
@@ -274,14 +290,24 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // ---- A: inputs produced by step ta-1-D ----
     // tps threads per source: all poll the source's count word (one transaction per
     // wave), then each reads every tps-th entry, up to kBatch loads in flight per thread.
+    // The first look at each count word is issued before the input-independent part of the
+    // update (Model::prepare), which runs while those loads are in flight.
+    const uint64_t* cin = cnt + ((int64_t)slot_rd * nb + me) * nb;
+    uint64_t v_first = 0;
+    if (Model::kPrepare) {
+      if (ta > dly && (int)threadIdx.x < nb * tps) v_first = ld_dev64(cin + threadIdx.x / tps);
+#pragma unroll
+      for (int q = 0; q < NPT; ++q) {
+        if (base + q * kBlock + threadIdx.x < n) Model::prepare(p, r[q]);
+      }
+    }
     if (ta > dly) {
-      const uint64_t* cin = cnt + ((int64_t)slot_rd * nb + me) * nb;
       const uint32_t want = (uint32_t)(ta - dly);  // step u publishes tag u + 1
       const char* ib = inbox + (size_t)slot_rd * buf_bytes;
       for (int x = threadIdx.x; x < nb * tps; x += kBlock) {
         const int s = x / tps;
         const uint32_t sub = (uint32_t)(x - s * tps);
-        uint64_t v = ld_dev64(cin + s);
+        uint64_t v = (Model::kPrepare && x == (int)threadIdx.x) ? v_first : ld_dev64(cin + s);
         uint64_t spins = 0;
         while ((uint32_t)(v >> 32) != want) {
           if (++spins > kSpinLimit) {

@@ -65,33 +65,56 @@ __device__ __forceinline__ float bs_hh_gate(float x, float a, float b, float dt)
   return bs_fma(dt * phi, f, x);
 }
 
+// The part of one HH step that does not depend on this step's synaptic input: the gate
+// updates (rates of the previous V, exp-Euler per gate) and the channel conductances of the
+// previous m, h, n.  Same operations as inline, so splitting the step changes no bit.
+struct bs_hh_pre {
+  float mn, hn, nn;  // gates after the step
+  float gna, gk;     // gNa m^3 h and gK n^4 of the previous gates
+};
+
+__device__ __forceinline__ bs_hh_pre bs_hh_prepare(const bs_hh_params& p, float V, float m,
+                                                   float h, float n) {
+  const bs_hh_rates r = bs_hh_rate(V);
+  bs_hh_pre q;
+  q.gna = p.gNa * m * m * m * h;
+  const float n2 = n * n;
+  q.gk = p.gK * n2 * n2;
+  q.mn = bs_hh_gate(m, r.am, r.bm, p.dt);
+  q.hn = bs_hh_gate(h, r.ah, r.bh, p.dt);
+  q.nn = bs_hh_gate(n, r.an, r.bn, p.dt);
+  return q;
+}
+
+// The rest of the step: Expon + COBA conductances from this step's input and the
+// exp-Euler step of V (examples/100_hh_neuron_model.py:72-93).
+__device__ __forceinline__ bool bs_hh_finish(const bs_hh_params& p, const bs_hh_pre& q, float& V,
+                                             float& m, float& h, float& n, float& ge,
+                                             float& gi, float in_e, float in_i) {
+  ge = bs_fma(ge, p.decay_e, in_e);
+  gi = bs_fma(gi, p.decay_i, in_i);
+  float I = bs_fma(ge, p.E_e - V, p.I_ext);
+  I = bs_fma(gi, p.E_i - V, I);
+  // (I - INa - IK - IL) / C, each channel current folded in with one fused multiply-add
+  float acc = bs_fma(-q.gna, V - p.ENa, I);
+  acc = bs_fma(-q.gk, V - p.EK, acc);
+  acc = bs_fma(-p.gL, V - p.EL, acc);
+  const float f = acc * p.inv_C;
+  const float J = ((((-q.gna) - q.gk) - p.gL) - (ge + gi)) * p.inv_C;
+  const float phi = bs_exprel(p.dt * J);
+  const float Vn = bs_fma(p.dt * phi, f, V);
+  const bool spk = (V < p.V_th) && (Vn >= p.V_th);
+  V = Vn;
+  m = q.mn;
+  h = q.hn;
+  n = q.nn;
+  return spk;
+}
+
 // Expon + COBA + HH exp-Euler for one neuron (examples/100_hh_neuron_model.py:72-93).
 __device__ __forceinline__ bool bs_hh_update(const bs_hh_params& p, float& V, float& m, float& h,
                                              float& n, float& ge, float& gi, float in_e,
                                              float in_i) {
-  ge = bs_fma(ge, p.decay_e, in_e);
-  gi = bs_fma(gi, p.decay_i, in_i);
-  const bs_hh_rates r = bs_hh_rate(V);
-  float I = bs_fma(ge, p.E_e - V, p.I_ext);
-  I = bs_fma(gi, p.E_i - V, I);
-  const float gna = p.gNa * m * m * m * h;
-  const float n2 = n * n;
-  const float gk = p.gK * n2 * n2;
-  // (I - INa - IK - IL) / C, each channel current folded in with one fused multiply-add
-  float acc = bs_fma(-gna, V - p.ENa, I);
-  acc = bs_fma(-gk, V - p.EK, acc);
-  acc = bs_fma(-p.gL, V - p.EL, acc);
-  const float f = acc * p.inv_C;
-  const float J = ((((-gna) - gk) - p.gL) - (ge + gi)) * p.inv_C;
-  const float phi = bs_exprel(p.dt * J);
-  const float Vn = bs_fma(p.dt * phi, f, V);
-  const float mn = bs_hh_gate(m, r.am, r.bm, p.dt);
-  const float hn = bs_hh_gate(h, r.ah, r.bh, p.dt);
-  const float nn = bs_hh_gate(n, r.an, r.bn, p.dt);
-  const bool spk = (V < p.V_th) && (Vn >= p.V_th);
-  V = Vn;
-  m = mn;
-  h = hn;
-  n = nn;
-  return spk;
+  const bs_hh_pre q = bs_hh_prepare(p, V, m, h, n);
+  return bs_hh_finish(p, q, V, m, h, n, ge, gi, in_e, in_i);
 }
