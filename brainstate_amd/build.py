@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, 'csrc')
 LIBDIR = os.path.join(HERE, '_lib')
 LIB = os.path.join(LIBDIR, 'libbsamd.so')
 SOURCES = ['runtime.hip', 'compact.hip', 'event_sparse.hip', 'event_bucket.hip', 'event_dense.hip',
-           'neuron.hip', 'network.hip', 'delay.hip', 'conn.hip']
+           'event_dense_packed.hip', 'neuron.hip', 'network.hip', 'delay.hip', 'conn.hip']
 ARCH = 'gfx950'
 
 

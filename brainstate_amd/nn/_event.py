@@ -103,13 +103,16 @@ class _EventMatvecFn(torch.autograd.Function):
 
 
 def _no_autodiff(*ts):
-    """True when no operand takes part in reverse or forward mode autodiff."""
+    """True when no operand takes part in reverse or forward mode autodiff (including the
+    wrapped tensors of torch.func transforms)."""
     from torch.autograd import forward_ad
     for t in ts:
         if torch.is_tensor(t):
             if t.requires_grad and torch.is_grad_enabled():
                 return False
             if forward_ad.unpack_dual(t).tangent is not None:
+                return False
+            if torch._C._functorch.is_functorch_wrapped_tensor(t):
                 return False
     return True
 
@@ -415,18 +418,50 @@ class _HomoLinearFn(torch.autograd.Function):
 
 
 class EventLinear(Module):
-    """brainstate/nn/_event_linear.py:32-102."""
+    """brainstate/nn/_event_linear.py:32-102.
+
+    ``event_kernel`` picks the kernel of the heterogeneous event product: ``'packed'`` (and
+    ``'auto'``, for event inputs, i.e. ``float_as_event=True``, and up to 65536 inputs) packs
+    the weight once per value (ops.pack_dense; repacked when the weight State is assigned or
+    modified in place) and runs the matrix-core form, exact in fixed point per column;
+    ``'stream'`` streams W through the fp32 event kernel in its documented chunk order (also
+    used for value inputs, for weights holding inf or NaN, and whenever autodiff records the
+    spikes or the weight).  Packing reads W twice and
+    writes ~1.25x its size, so the packed form pays from the second call with one weight."""
     __module__ = 'brainstate_amd.nn'
 
     def __init__(self, in_size, out_size, weight, float_as_event=True, block_size=64,
-                 name=None, param_type=ParamState):
+                 name=None, param_type=ParamState, event_kernel='auto'):
         super().__init__(name=name)
+        if event_kernel not in ('auto', 'packed', 'stream'):
+            raise ValueError(f'event_kernel must be auto, packed or stream, got {event_kernel!r}')
         self.in_size = init.to_size(in_size)
         self.out_size = init.to_size(out_size)
         self.float_as_event = float_as_event
         self.block_size = block_size
+        self.event_kernel = event_kernel
         w = init.param(weight, (self.in_size[-1], self.out_size[-1]), allow_none=False)
         self.weight = param_type(w)
+        self._packed = None
+
+    def _packed_weight(self, W):
+        """ops.pack_dense of the current weight; None when the packed form does not apply.
+        A torch weight is packed once per value (cached on the tensor's identity, storage and
+        version counter, which in-place changes bump); a numpy weight, which carries no
+        version, is packed on every call."""
+        if self.event_kernel == 'stream' or not self.float_as_event:
+            return None
+        if ops.dense_digits(W.shape[0]) == 0:
+            return None
+        v = self.weight.value
+        if not torch.is_tensor(v):
+            P = ops.pack_dense(W.detach())
+            return P if P['finite'] else None
+        key = (id(v), v.data_ptr(), v._version)
+        if self._packed is None or self._packed[0] != key:
+            self._packed = (key, ops.pack_dense(W.detach()))
+        P = self._packed[1]
+        return P if P['finite'] else None
 
     def update(self, spk):
         w = self.weight.value
@@ -442,6 +477,10 @@ class EventLinear(Module):
         W = W.expand(self.in_size[-1], self.out_size[-1]).contiguous()
         if x.dtype not in (torch.bool, torch.uint8, torch.float32):
             x = x.to(torch.float32)
+        if _no_autodiff(x, W):
+            P = self._packed_weight(W)
+            if P is not None:
+                return ops.event_dense_packed(x, P)
         if _wants_grad(x, W):
             return _EventDenseFn.apply(x, W, self.float_as_event)
         return ops.event_dense(x, W, float_as_event=self.float_as_event)

@@ -344,6 +344,47 @@ def event_dense(spk, W, float_as_event=True, out=None):
     return out[0] if squeeze else out
 
 
+
+def dense_digits(n_in):
+    """Signed 8-bit digits per weight of the packed EventLinear form (0: n_in not packable)."""
+    return int(N.lib().bs_event_dense_digits(int(n_in)))
+
+
+def pack_dense(W):
+    """Pack W [n_in, n_out] fp32 for ``event_dense_packed`` (bs_event_dense_pack): per-column
+    fixed-point digits in the matrix-core operand order.  Returns a dict with the packed
+    buffer and ``finite`` (False when a weight is inf or NaN: the packed product then returns
+    NaN everywhere).  Reading the status synchronises the stream once per packing."""
+    W = W.contiguous()
+    n_in, n_out = int(W.shape[0]), int(W.shape[1])
+    nbytes = int(N.lib().bs_event_dense_packed_bytes(n_in, n_out))
+    if nbytes <= 0:
+        raise ValueError(f'pack_dense: n_in = {n_in} exceeds the packed form (65536 inputs)')
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=W.device)   # 256-byte aligned
+    N.check(N.lib().bs_event_dense_pack(N.ptr(W), n_in, n_out, N.ptr(buf), nbytes,
+                                        N.stream_handle(W.device)), 'bs_event_dense_pack')
+    finite = int(buf[:4].view(torch.int32).item()) == 0
+    return {'packed': buf, 'n_in': n_in, 'n_out': n_out, 'L': dense_digits(n_in),
+            'finite': finite}
+
+
+def event_dense_packed(spk, P, out=None):
+    """spk [B, n_in] (or [n_in]; any nonzero value is an event) x the packed W -> [B, n_out]
+    fp32: exact fixed-point sums, one rounding (bs_event_dense_packed_f32)."""
+    squeeze = spk.dim() == 1
+    s2 = _spk_view(spk.reshape(1, -1) if squeeze else spk)
+    B, n_in = s2.shape
+    if n_in != P['n_in']:
+        raise ValueError(f'event_dense_packed: spikes have {n_in} inputs, W has {P["n_in"]}')
+    buf = P['packed']
+    if out is None:
+        out = torch.empty(B, P['n_out'], dtype=torch.float32, device=buf.device)
+    N.check(N.lib().bs_event_dense_packed_f32(N.ptr(s2), _spk_dtype(s2), B, n_in, N.ptr(buf),
+                                              P['n_out'], N.ptr(out),
+                                              N.stream_handle(buf.device)),
+            'bs_event_dense_packed_f32')
+    return out[0] if squeeze else out
+
 def event_dense_chunks(batch, n_in, n_out):
     """(S, L): the chunk plan that fixes the order of bs_event_dense_f32's additions."""
     L = ctypes.c_int32(0)

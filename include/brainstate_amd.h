@@ -190,6 +190,31 @@ BS_API int bs_event_dense_f32(const void* spk, int32_t spk_dtype, int32_t batch,
                        const float* W, int32_t n_out, int32_t float_as_event, float* out,
                        void* workspace, size_t workspace_bytes, bs_stream_t stream);
 
+/* Packed form of the same product for byte / event spikes (float_as_event semantics: any
+ * nonzero spike is an event), for a W that is reused across calls.  Exact in fixed point:
+ * column j is scaled by 2^S_j, S_j = D - e_j, D = 8 L - 2, where max_i |W[i,j]| = f * 2^e_j with
+ * f in [0.5, 1) and L = bs_event_dense_digits(n_in) (4, 5 or 6: the smallest with
+ * D >= 24 + ceil(log2 n_in); 0 when n_in > 65536, which the packed form does not take).
+ * q[i,j] = rint(W[i,j] * 2^S_j) (ties to even); out[b,j] = ldexp((float) sum of q[i,j] over
+ * the inputs with spk[b,i] != 0, -S_j): one rounding of an exact integer sum, so the result
+ * does not depend on any order, and the weight rounding moves a sum by at most
+ * 2^-24 * max_i |W[i,j]|.  A column of zeros gives +0.
+ * bs_event_dense_pack(W, ...) fills `packed` (bs_event_dense_packed_bytes(n_in, n_out) bytes,
+ * 256-byte aligned): a header whose first uint32 is the status (1 when a weight is inf or
+ * NaN: then every output of bs_event_dense_packed_f32 is NaN; use bs_event_dense_f32), the
+ * column maxima and the digits (layout in csrc/event_dense_packed.hip).  It must be redone
+ * after W changes.  bs_event_dense_packed_f32 reads it (n_in, n_out as packed), spk u8 or
+ * f32 [batch, n_in], and writes out [batch, n_out]; no workspace.  Replaces the same call
+ * as bs_event_dense_f32 (brainstate/nn/_event_linear.py:99-100) when one W serves many calls
+ * (recurrent loops over time, inference). */
+BS_API int32_t bs_event_dense_digits(int32_t n_in);
+BS_API int64_t bs_event_dense_packed_bytes(int32_t n_in, int32_t n_out);
+BS_API int bs_event_dense_pack(const float* W, int32_t n_in, int32_t n_out, void* packed,
+                               int64_t packed_bytes, bs_stream_t stream);
+BS_API int bs_event_dense_packed_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                     int32_t n_in, const void* packed, int32_t n_out, float* out,
+                                     bs_stream_t stream);
+
 /* Reverse mode of EventLinear's heterogeneous product (the VJP the reference checks at
  * brainstate/nn/_event_linear_test.py:51-89; its "true gradient" is that of x @ W with the
  * spike values x, 0/1 for byte spikes, in both float_as_event modes):

@@ -179,6 +179,64 @@ def scatter_fixed_point(spk, indptr, indices, w, n_post, S):
     return np.ldexp(acc.astype(F), -S).astype(F)
 
 
+
+# ---- packed EventLinear: exact fixed-point sums per column ----
+
+def dense_digits(n_in):
+    """Signed 8-bit digits L of the packed EventLinear form: the smallest L in 4..6 with
+    8 L - 2 >= 24 + ceil(log2 n_in); 0 when n_in > 65536 (not packable)."""
+    n_in = int(n_in)
+    if n_in < 0 or n_in > 65536:
+        return 0
+    c = 0
+    while (1 << c) < max(n_in, 1):
+        c += 1
+    for L in (4, 5, 6):
+        if 8 * L - 2 >= 24 + c:
+            return L
+    return 0
+
+
+def dense_column_shifts(W):
+    """S_j = D - e_j with D = 8 L - 2 and max_i |W[i, j]| = f * 2^e_j (f in [0.5, 1)); 0 for a
+    column of zeros.  Returns (S int32 [n_out], zero-column mask)."""
+    W = np.asarray(W, dtype=F)
+    n_in, n_out = W.shape
+    D = 8 * dense_digits(n_in) - 2
+    m = np.abs(W).max(axis=0) if n_in else np.zeros(n_out, F)
+    e = np.frexp(m.astype(np.float64))[1].astype(np.int64)
+    zero = m == 0
+    return np.where(zero, 0, D - e).astype(np.int32), zero
+
+
+def _exact_int_matmul(a01, q):
+    """a01 (0/1 int) @ q (int64, |q| <= 2^46, n_in <= 65536) exactly, through float64 BLAS on
+    24-bit halves: every partial sum stays below 2^53, so each float64 sum is exact."""
+    hi = q >> 24
+    lo = q - (hi << 24)                       # in [0, 2^24)
+    a = a01.astype(np.float64)
+    s_hi = (a @ hi.astype(np.float64)).astype(np.int64)
+    s_lo = (a @ lo.astype(np.float64)).astype(np.int64)
+    return (s_hi << 24) + s_lo
+
+
+def event_dense_fixed_point(spk, W):
+    """Packed EventLinear (event spikes: any nonzero is an event): each weight rounded to a
+    multiple of 2^-S_j of its column (round half to even), the rounded weights selected by
+    each batch row summed exactly, the sum rounded once to fp32 and scaled by 2^-S_j; a
+    column of zeros gives +0.  Any non-finite weight: every output NaN."""
+    W = np.asarray(W, dtype=F)
+    spk = np.asarray(spk)
+    x = spk.reshape(-1, W.shape[0])
+    if not np.all(np.isfinite(W)):
+        return np.full(spk.shape[:-1] + (W.shape[1],), np.nan, F)
+    S, zero = dense_column_shifts(W)
+    q = np.rint(np.ldexp(W.astype(np.float64), S[None, :].astype(np.int64))).astype(np.int64)
+    tot = _exact_int_matmul((x != 0).astype(np.int8), q)
+    out = np.ldexp(tot.astype(F), (-S)[None, :]).astype(F)
+    out[:, zero] = F(0.0)
+    return out.reshape(spk.shape[:-1] + (W.shape[1],))
+
 # ---- derivatives (float64) ----
 
 def _rows_of(idx, indptr):

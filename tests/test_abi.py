@@ -83,6 +83,29 @@ def test_event_dense_chunk_plan_host_only():
     assert rc == N.BS_ERR_INVALID and b'workspace' in lib.bs_last_error()
 
 
+
+def test_event_dense_packed_sizes_host_only():
+    """Digits per weight and the packed size (header, column maxima, 1 KiB digit blocks per
+    (16-column tile, 64-input block, digit)) are host-side functions of the shape; argument
+    checks fail before any device work."""
+    if not os.path.exists(N.LIB_PATH):
+        pytest.skip('library not built')
+    from oracle import event
+    lib = N.load_library()
+    for n in (0, 1, 64, 65, 4096, 16384, 16385, 65536, 65537, -3):
+        assert lib.bs_event_dense_digits(n) == event.dense_digits(n)
+    for n_in, n_out in [(4096, 4096), (1, 1), (100, 33), (65536, 17), (0, 5)]:
+        L = event.dense_digits(n_in)
+        kb, nt = -(-n_in // 64), -(-n_out // 16)
+        bits = -(-(nt * 16 * 4) // 256) * 256
+        assert lib.bs_event_dense_packed_bytes(n_in, n_out) == 256 + bits + nt * kb * L * 1024
+    assert lib.bs_event_dense_packed_bytes(65537, 4) == 0
+    assert lib.bs_event_dense_packed_bytes(4, -1) == 0
+    rc = lib.bs_event_dense_pack(None, 70000, 4, None, 0, None)
+    assert rc == N.BS_ERR_INVALID and b'exceeds' in lib.bs_last_error()
+    rc = lib.bs_event_dense_packed_f32(None, 0, 1, 64, None, 16, None, None)
+    assert rc == N.BS_ERR_INVALID and b'aligned' in lib.bs_last_error()
+
 def test_struct_layouts_match_header():
     # field counts/order of the ctypes mirrors (sizes of plain C structs on x86-64)
     assert ctypes.sizeof(N.LifParams) == 12 * 4

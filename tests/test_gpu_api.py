@@ -111,10 +111,13 @@ def test_event_linear_batched_bit_exact(bs):
     rng = np.random.RandomState(7)
     spk = rng.rand(64, 512) < 0.05
     W = rng.normal(0, 0.125, (512, 256)).astype(F)
-    m = bs.nn.EventLinear(512, 256, W)
+    m = bs.nn.EventLinear(512, 256, W, event_kernel='stream')
     y = m(torch.tensor(spk, device='cuda')).cpu().numpy()
     _, L = ops_chunks(64, 512, 256)
     assert np.array_equal(y, event.event_linear(spk, W, chunk_rows=L))
+    p = bs.nn.EventLinear(512, 256, W)   # 'auto': packed, exact per-column fixed point
+    assert np.array_equal(p(torch.tensor(spk, device='cuda')).cpu().numpy(),
+                          event.event_dense_fixed_point(spk, W))
 
 
 class _EINet:

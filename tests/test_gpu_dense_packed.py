@@ -1,0 +1,177 @@
+"""GPU parity of the packed EventLinear product (bs_event_dense_pack, bs_event_dense_packed_f32)
+against the oracle's per-column fixed-point restatement (bit-exact) and the sequential fp32
+sum of brainstate/nn/_event_linear.py:99-100 (rtol 1e-5, atol 1e-6 scaled by the largest
+weight)."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import event
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+@pytest.fixture(scope='module')
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail('GPU tests need a ROCm GPU')
+    from brainstate_amd import _native
+    _native.load_library()
+    return torch
+
+
+def say(*a):
+    print('[case]', *a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(t, a):
+    return t.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run(torch, spk, W):
+    from brainstate_amd import ops
+    P = ops.pack_dense(dev(torch, W))
+    return P, ops.event_dense_packed(dev(torch, spk), P).cpu().numpy()
+
+
+@pytest.mark.parametrize('B,n_in,n_out,p,sdt', [
+    (1, 64, 16, 0.3, 'u8'), (3, 17, 5, 0.5, 'u8'), (64, 4096, 4096, 0.05, 'u8'),
+    (65, 100, 33, 0.2, 'u8'), (130, 1000, 257, 0.05, 'bool'), (5, 20000, 70, 0.02, 'u8'),
+    (7, 96, 40, 0.4, 'f32'), (64, 512, 256, 0.05, 'f32'), (2, 65536, 16, 0.01, 'u8'),
+    (16, 1, 3, 0.9, 'u8')])
+def test_packed_matches_oracle(torch_cuda, B, n_in, n_out, p, sdt):
+    """Bit-exact against the fixed-point restatement; within tolerance of the sequential
+    fp32 sum.  Byte spikes hold values other than 1 and float spikes arbitrary nonzero
+    values: any nonzero is one event."""
+    torch = torch_cuda
+    say('packed', B, n_in, n_out, p, sdt)
+    rng = np.random.RandomState(B + n_in + n_out)
+    W = rng.normal(0, 0.125, (n_in, n_out)).astype(F)
+    s = rng.rand(B, n_in) < p
+    if sdt == 'u8':
+        spk = s.astype(np.uint8) * rng.randint(1, 256, (B, n_in)).astype(np.uint8)
+    elif sdt == 'bool':
+        spk = s
+    else:
+        spk = np.where(s, rng.normal(0, 2, (B, n_in)), 0).astype(F)
+        spk[s & (spk == 0)] = 1.0
+    P, got = run(torch, spk, W)
+    assert P['finite'] and P['L'] == event.dense_digits(n_in)
+    want = event.event_dense_fixed_point(spk, W)
+    assert np.array_equal(got, want)
+    if n_in * B <= 200_000:
+        seq = event.event_linear(spk != 0, W)
+        assert np.allclose(got, seq, rtol=1e-5, atol=1e-6 * float(np.abs(W).max()))
+
+
+def test_packed_unaligned_spikes_and_repack(torch_cuda):
+    """A spike view that starts one byte into its buffer (byte-load path) gives the same
+    bits; packing a second W into the same buffer leaves nothing of the first behind."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('packed unaligned + repack')
+    rng = np.random.RandomState(3)
+    B, n_in, n_out = 9, 640, 48
+    W1 = rng.normal(0, 1, (n_in, n_out)).astype(F)
+    W2 = (rng.normal(0, 1e-3, (n_in, n_out)) * (rng.rand(n_in, n_out) < 0.5)).astype(F)
+    spk = (rng.rand(B, n_in) < 0.2).astype(np.uint8)
+    raw = torch.zeros(B * n_in + 1, dtype=torch.uint8, device='cuda')
+    raw[1:] = dev(torch, spk.reshape(-1))
+    view = raw[1:].view(B, n_in)
+    P = ops.pack_dense(dev(torch, W1))
+    got1 = ops.event_dense_packed(view, P).cpu().numpy()
+    assert np.array_equal(got1, event.event_dense_fixed_point(spk, W1))
+    buf = P['packed']
+    from brainstate_amd import _native as N
+    N.check(N.lib().bs_event_dense_pack(N.ptr(dev(torch, W2)), n_in, n_out, N.ptr(buf),
+                                        buf.numel(), N.stream_handle(buf.device)), 'pack')
+    got2 = ops.event_dense_packed(dev(torch, spk), P).cpu().numpy()
+    assert np.array_equal(got2, event.event_dense_fixed_point(spk, W2))
+    again = ops.event_dense_packed(dev(torch, spk), P).cpu().numpy()
+    assert np.array_equal(got2, again)
+
+
+def test_packed_column_scales_zero_columns_and_ties(torch_cuda):
+    """Columns 2^60 apart keep their own scale; a column of zeros gives +0; the half-way
+    weights of the oracle's tie pins round to even on the device too."""
+    torch = torch_cuda
+    say('packed scales')
+    rng = np.random.RandomState(8)
+    n_in, n_out, B = 64, 20, 6
+    W = rng.normal(0, 1, (n_in, n_out)).astype(F)
+    W[:, 1] *= F(2.0 ** -60)
+    W[:, 2] *= F(2.0 ** 60)
+    W[:, 3] = 0
+    W[:, 4] = 0
+    W[:4, 4] = [1.0, 2.0 ** -30, 3 * 2.0 ** -30, 5 * 2.0 ** -30]
+    W[:, 5] = rng.normal(0, 1, n_in).astype(F) * F(1e-40)  # subnormal column
+    spk = (rng.rand(B, n_in) < 0.5).astype(np.uint8)
+    spk[0, :4] = [0, 1, 0, 0]
+    spk[1, :4] = [0, 0, 1, 0]
+    spk[2, :4] = [0, 0, 0, 1]
+    _, got = run(torch, spk, W)
+    want = event.event_dense_fixed_point(spk, W)
+    assert np.array_equal(got, want)
+    assert np.all(got[:, 3] == 0) and not np.any(np.signbit(got[:, 3]))
+    assert got[0, 4] == 0.0 and got[1, 4] == F(2.0 ** -28) and got[2, 4] == F(2.0 ** -28)
+
+
+def test_packed_non_finite_weight_flags(torch_cuda):
+    """A weight that is inf or NaN sets the status word; every output is then NaN."""
+    torch = torch_cuda
+    say('packed non-finite')
+    rng = np.random.RandomState(2)
+    W = rng.normal(0, 1, (128, 32)).astype(F)
+    W[5, 7] = np.inf
+    spk = (rng.rand(4, 128) < 0.3).astype(np.uint8)
+    P, got = run(torch, spk, W)
+    assert not P['finite'] and np.all(np.isnan(got))
+
+
+def test_packed_empty_shapes(torch_cuda):
+    """n_in = 0 gives zeros; batch 0 writes nothing."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('packed empty')
+    P = ops.pack_dense(torch.zeros(0, 7, device='cuda'))
+    out = ops.event_dense_packed(torch.zeros(3, 0, dtype=torch.uint8, device='cuda'), P)
+    assert out.shape == (3, 7) and torch.all(out == 0)
+    P = ops.pack_dense(dev(torch, np.ones((32, 16), F)))
+    out = ops.event_dense_packed(torch.zeros(0, 32, dtype=torch.uint8, device='cuda'), P)
+    assert out.shape == (0, 16)
+
+
+def test_event_linear_module_routes(torch_cuda):
+    """nn.EventLinear ('auto') uses the packed form for event inputs without autodiff,
+    repacks when a torch weight changes in place, and streams value inputs or on request."""
+    torch = torch_cuda
+    import brainstate_amd as bs
+    say('EventLinear routes')
+    rng = np.random.RandomState(12)
+    W = rng.normal(0, 0.125, (512, 256)).astype(F)
+    spk = rng.rand(64, 512) < 0.05
+    m = bs.nn.EventLinear(512, 256, dev(torch, W))
+    x = torch.tensor(spk, device='cuda')
+    with torch.no_grad():
+        y = m(x).cpu().numpy()
+    assert np.array_equal(y, event.event_dense_fixed_point(spk, W))
+    with torch.no_grad():
+        m.weight.value.mul_(2.0)   # in place: version bump -> repack
+        y2 = m(x).cpu().numpy()
+    assert np.array_equal(y2, event.event_dense_fixed_point(spk, W * 2))
+    s = bs.nn.EventLinear(512, 256, W, event_kernel='stream')
+    with torch.no_grad():
+        ys = s(x).cpu().numpy()
+    from brainstate_amd import ops
+    _, L = ops.event_dense_chunks(64, 512, 256)
+    assert np.array_equal(ys, event.event_linear(spk, W, chunk_rows=L))
+    v = bs.nn.EventLinear(512, 256, W, float_as_event=False)
+    xf = np.where(spk, 0.5, 0).astype(F)
+    with torch.no_grad():
+        yv = v(dev(torch, xf)).cpu().numpy()
+    assert np.array_equal(yv, event.event_linear(xf, W, float_as_event=False, chunk_rows=L))

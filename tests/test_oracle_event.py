@@ -235,6 +235,60 @@ def test_fixed_point_scatter_is_the_rounded_exact_sum():
                                                      Sw) * 2, ref64, rtol=1e-3)
 
 
+
+# ---- packed EventLinear: per-column fixed point ----
+
+def test_dense_digits_table():
+    """Smallest L with 8 L - 2 >= 24 + ceil(log2 n_in), at the boundaries of each L."""
+    got = [event.dense_digits(n) for n in (0, 1, 64, 65, 16384, 16385, 65536, 65537, -1)]
+    assert got == [4, 4, 4, 5, 5, 6, 6, 0, 0]
+
+
+def test_dense_fixed_point_dyadic_weights_are_exact():
+    """Weights with few significant bits relative to their column maximum are held exactly,
+    so every output is the exact sum rounded once (float64 is exact here); the per-column
+    scale is exercised by columns 2^40 apart."""
+    rng = np.random.RandomState(21)
+    n_in, n_out, B = 300, 40, 9
+    W = (rng.randint(-2**10, 2**10, (n_in, n_out)) * 2.0 ** -12).astype(F)
+    W[:, 5] *= F(2.0 ** -40)
+    W[:, 6] *= F(2.0 ** 40)
+    W[:, 7] = 0
+    spk = (rng.rand(B, n_in) < 0.3).astype(np.uint8) * rng.randint(1, 4, (B, n_in)).astype(np.uint8)
+    got = event.event_dense_fixed_point(spk, W)
+    exact = ((spk != 0).astype(np.float64) @ W.astype(np.float64)).astype(F)
+    assert np.array_equal(got, exact)
+    assert np.all(got[:, 7] == 0) and not np.any(np.signbit(got[:, 7]))
+
+
+def test_dense_fixed_point_ties_to_even_and_bound():
+    """q = rint(w 2^S) rounds halves to even: with max|w| = 1 (e = 1) and n_in <= 64 (L = 4,
+    D = 30, S = 29), 2^-30 becomes 0, 3 * 2^-30 becomes 2 * 2^-29 and 5 * 2^-30 becomes
+    2 * 2^-29 (round half up would give 2^-29, 2 * 2^-29 and 3 * 2^-29).  On random weights each sum stays within 2^-24 max|W[:, j]|
+    plus half an ulp of the exact sum, and within the tolerance of the sequential oracle."""
+    W = np.zeros((4, 2), F)
+    W[:, 0] = [1.0, 2.0 ** -30, 3 * 2.0 ** -30, 5 * 2.0 ** -30]
+    W[:, 1] = [0.5, 0.25, -2.0 ** -31, 0.0]
+    spk = np.array([[0, 1, 0, 0], [0, 0, 1, 0], [0, 0, 0, 1], [0, 1, 1, 1]], np.uint8)
+    got = event.event_dense_fixed_point(spk, W)
+    assert got[0, 0] == 0.0 and got[1, 0] == F(2.0 ** -28) and got[2, 0] == F(2.0 ** -28)
+    assert got[3, 0] == F(4 * 2.0 ** -29)            # 0 + 2 + 2 units of 2^-29
+    assert got[1, 1] == 0.0                          # -2^-31 * 2^30 = -0.5 -> 0 (even)
+    rng = np.random.RandomState(5)
+    for n_in, n_out, B in [(64, 33, 5), (1000, 50, 7), (20000, 8, 3)]:
+        W = rng.normal(0, 0.125, (n_in, n_out)).astype(F)
+        W[:, 0] *= F(1e-20)
+        spk = rng.rand(B, n_in) < 0.1
+        got = event.event_dense_fixed_point(spk, W).astype(np.float64)
+        exact = spk.astype(np.float64) @ W.astype(np.float64)
+        m = np.abs(W).max(axis=0).astype(np.float64)
+        ulp = np.spacing(np.abs(exact).astype(F)).astype(np.float64)
+        assert np.all(np.abs(got - exact) <= 2.0 ** -24 * m + 0.5 * ulp + 1e-300)
+        seq = event.event_linear(spk, W)
+        assert np.allclose(got, seq, rtol=1e-5, atol=1e-6 * m.max())
+    assert np.all(np.isnan(event.event_dense_fixed_point(
+        np.ones((2, 3), np.uint8), np.array([[1, 2], [np.inf, 0], [0, 1]], F))))
+
 # ---- derivative restatements: pinned by identities, not by retyping the formulas ----
 
 def _conn(seed, n_pre=40, n_post=30, k=5):
