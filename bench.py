@@ -182,7 +182,10 @@ def bench_sparse(args):
 
 def bench_event_linear(args):
     """spikes [64, 4096] @ 5 % x W [4096, 4096] N(0, 1/64), 100 recurrent steps,
-    LIF state [64, 4096] (fused update with the EventLinear output as conductance input)."""
+    LIF state [64, 4096] (COBA-LIF update with the EventLinear output as conductance input).
+    The step runs the packed EventLinear with the LIF update fused into it (W packed once per
+    run, inside the timed region); the unfused pair and the streamed fp32 kernel are timed
+    beside it."""
     import torch
     from brainstate_amd import ops
     B, n, T = 64, 4096, 100
@@ -196,25 +199,50 @@ def bench_event_linear(args):
     cur = torch.empty(B, n, device='cuda')
     p = ops.lif_params()
 
-    def dense_only():
+    P = ops.pack_dense(W)
+
+    def stream_only():
         for t in range(T):
             ops.event_dense(spk[t], W, out=cur)
+
+    def packed_only():
+        for t in range(T):
+            ops.event_dense_packed(spk[t], P, out=cur)
+
+    def pack_only():
+        ops.pack_dense(W)
+
+    spk_out = torch.empty(B, n, dtype=torch.uint8, device='cuda')
 
     def step_all():
+        # one run of T steps with one W: pack it (status read included), then T launches of
+        # the packed EventLinear with the COBA-LIF update fused into its epilogue
+        Pr = ops.pack_dense(W)
         for t in range(T):
-            ops.event_dense(spk[t], W, out=cur)
-            ops.coba_lif_step(V, ge, gi, ref, cur.view(-1), None, p)
+            ops.event_dense_packed_lif_step(spk[t], Pr, V, ge, gi, ref, p, spk_out=spk_out)
 
-    td = _timed(dense_only, 3, 1) / T
+    def step_unfused():
+        Pr = ops.pack_dense(W)
+        for t in range(T):
+            ops.event_dense_packed(spk[t], Pr, out=cur)
+            ops.coba_lif_step(V, ge, gi, ref, cur.view(-1), None, p, spk_out=spk_out)
+
+    ts = _timed(stream_only, 3, 1) / T
+    tp = _timed(packed_only, 3, 1) / T
+    tk = _timed(pack_only, 3, 1)
+    tu = _timed(step_unfused, 3, 1) / T
     tall = _timed(step_all, 3, 1) / T
     act = spk.float().sum(1)
     pairs = float(spk.float().sum()) / T
     U = float((act > 0).float().sum()) / T
     b_alg = B * n * 1 + U * n * 4 + B * n * 4 + B * n * 9
+    dig = int(P['packed'].numel())
     return [{'workload': 'event_linear_64x4096_p0.05', 'events_per_step': pairs * n,
-             'dense_kernel_us': td * 1e6, 'step_us': tall * 1e6,
-             'GSOPs': pairs * n / tall / 1e9, 'alg_GBs': b_alg / tall / 1e9,
-             'frac': b_alg / tall / PEAK_HBM}]
+             'dense_kernel_us': tp * 1e6, 'stream_kernel_us': ts * 1e6, 'pack_us': tk * 1e6,
+             'packed_bytes': dig, 'packed_read_GBs': dig / tp / 1e9,
+             'step_us': tall * 1e6, 'step_unfused_us': tu * 1e6,
+             'GSOPs': pairs * n / tall / 1e9,
+             'alg_GBs': b_alg / tall / 1e9, 'frac': b_alg / tall / PEAK_HBM}]
 
 
 def bench_hh(args):

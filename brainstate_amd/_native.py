@@ -94,6 +94,10 @@ SIGNATURES = {
     'bs_event_dense_pack': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, ctypes.c_int64, c_vp]),
     'bs_event_dense_packed_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_vp,
                                                  c_vp]),
+    'bs_event_dense_packed_lif_step': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32,
+                                                      c_i32, c_vp, c_vp, c_vp, c_vp,
+                                                      ctypes.POINTER(LifParams), c_vp, c_vp,
+                                                      c_vp]),
     'bs_coba_lif_step': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                         ctypes.POINTER(LifParams), c_vp, c_vp]),
     'bs_hh_init': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),

@@ -35,6 +35,7 @@
 // and wave w rounds and stores row tile w.
 #include "bs_math.h"
 #include "common.h"
+#include "neuron_dev.h"
 
 namespace {
 
@@ -45,7 +46,7 @@ constexpr int kBlkIn = 64;      // inputs per instruction (K)
 constexpr int kTileN = 16;      // columns per tile (N)
 constexpr int kRowTiles = 4;    // row tiles of 16 per workgroup
 constexpr int kGroupB = 16 * kRowTiles;   // batch rows per workgroup
-constexpr int kPW = kRowTiles;  // waves per workgroup (wave w stores row tile w)
+constexpr int kPW = kRowTiles;  // waves per workgroup (waves 0..3 store row tiles 0..3)
 constexpr int kPB = kPW * BS_WAVE;
 constexpr int kGroup = 2;       // input blocks per pipeline stage
 constexpr int32_t kMaxIn = 65536;
@@ -226,13 +227,24 @@ __device__ __forceinline__ v4i load_spk(const T* __restrict__ spk, int32_t batch
   return a;
 }
 
-template <typename T, int L, bool kVec>
+// COBA-LIF state of the fused step (bs_event_dense_packed_lif_step); unused otherwise.
+struct LifOut {
+  float* V;
+  float* ge;
+  float* gi;
+  int32_t* ref;
+  uint8_t* spk;
+  int32_t inh;  // the product drives g_i (1) or g_e (0)
+  bs_lif_params p;
+};
+
+template <typename T, int L, bool kVec, bool kLif>
 __global__ __launch_bounds__(kPB) void k_event_dense_packed(
     const T* __restrict__ spk, int32_t batch, int32_t n_in, const uint8_t* __restrict__ dig,
     const uint32_t* __restrict__ bits, const uint32_t* __restrict__ status, int32_t n_out,
-    int32_t KB, float* __restrict__ out) {
+    int32_t KB, float* __restrict__ out, LifOut lif) {
   constexpr int D = 8 * L - 2;
-  __shared__ int64_t s_sum[kPW][kRowTiles][4][BS_WAVE];  // 32 KiB
+  __shared__ int64_t s_sum[kPW][kRowTiles][4][BS_WAVE];  // 8 KiB per wave
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int64_t t = blockIdx.x;
@@ -248,6 +260,24 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
   for (int mt = 0; mt < kRowTiles; ++mt)
 #pragma unroll
     for (int l = 0; l < L; ++l) acc[mt][l] = v4i{0, 0, 0, 0};
+
+  // fused step: the neuron state of the outputs this lane will finish is loaded now, so
+  // its latency passes while the digits stream
+  float sV[4], sge[4], sgi[4];
+  int32_t sref[4];
+  if constexpr (kLif) {
+    const int64_t jj = t * kTileN + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t b = b0 + 16 * wid + 4 * (lane >> 4) + r;
+      const bool v = wid < kRowTiles && b < batch && jj < n_out;
+      const int64_t o = v ? (int64_t)b * n_out + jj : 0;
+      sV[r] = v ? lif.V[o] : 0.0f;
+      sge[r] = v ? lif.ge[o] : 0.0f;
+      sgi[r] = v ? lif.gi[o] : 0.0f;
+      sref[r] = v ? lif.ref[o] : 0;
+    }
+  }
 
   // one pipeline stage: kGroup input blocks (blocks past k_hi load the wave's last block
   // again with zero spikes, so every load is in bounds and adds nothing).  Byte spikes on
@@ -320,7 +350,7 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
   __syncthreads();
   const int mt = wid;
   const int64_t j = t * kTileN + (lane & 15);
-  if (j >= n_out) return;
+  if (mt >= kRowTiles || j >= n_out) return;
   const uint32_t mb = bits[j];
   const bool bad = *status != 0u;
   const int S = mb ? D - frexp_exp_bits(mb) : 0;
@@ -328,27 +358,80 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
   for (int r = 0; r < 4; ++r) {
     const int32_t b = b0 + 16 * mt + 4 * (lane >> 4) + r;
     if (b >= batch) continue;
-    const int64_t tot = s_sum[0][mt][r][lane] + s_sum[1][mt][r][lane] +
-                        s_sum[2][mt][r][lane] + s_sum[3][mt][r][lane];
+    int64_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kPW; ++w) tot += s_sum[w][mt][r][lane];
     float v = mb ? ldexpf((float)tot, -S) : 0.0f;
     if (bad) v = __builtin_nanf("");
-    out[(int64_t)b * n_out + j] = v;
+    const int64_t o = (int64_t)b * n_out + j;
+    if (!kLif || out != nullptr) out[o] = v;
+    if constexpr (kLif) {
+      // the update of bs_coba_lif_step with this output as its conductance input
+      float V = sV[r], ge = sge[r], gi = sgi[r];
+      int32_t rf = sref[r];
+      const bool sp =
+          bs_lif_update(lif.p, V, ge, gi, rf, lif.inh ? 0.0f : v, lif.inh ? v : 0.0f);
+      lif.V[o] = V;
+      lif.ge[o] = ge;
+      lif.gi[o] = gi;
+      lif.ref[o] = rf;
+      if (lif.spk != nullptr) lif.spk[o] = sp ? 1 : 0;
+    }
   }
 }
 
 template <typename T, int L>
 void launch_packed(const T* spk, int32_t batch, int32_t n_in, const PackDims& d,
-                   const uint8_t* packed, int32_t n_out, float* out, bool vec, hipStream_t s) {
+                   const uint8_t* packed, int32_t n_out, float* out, bool vec,
+                   const LifOut* lif, hipStream_t s) {
   const dim3 grid(d.NT, (batch + kGroupB - 1) / kGroupB);
   const uint8_t* dig = packed + d.dig_off;
   const uint32_t* bits = (const uint32_t*)(packed + d.bits_off);
   const uint32_t* status = (const uint32_t*)packed;
-  if (vec)
-    k_event_dense_packed<T, L, true><<<grid, kPB, 0, s>>>(spk, batch, n_in, dig, bits, status,
-                                                          n_out, d.KB, out);
-  else
-    k_event_dense_packed<T, L, false><<<grid, kPB, 0, s>>>(spk, batch, n_in, dig, bits,
-                                                           status, n_out, d.KB, out);
+  const LifOut none{};
+#define BS_PK(V, F)                                                                        \
+  k_event_dense_packed<T, L, V, F><<<grid, kPB, 0, s>>>(spk, batch, n_in, dig, bits, status, \
+                                                        n_out, d.KB, out, F ? *lif : none)
+  if (lif) { if (vec) BS_PK(true, true); else BS_PK(false, true); }
+  else { if (vec) BS_PK(true, false); else BS_PK(false, false); }
+#undef BS_PK
+}
+
+// Checks shared by the two product entry points; dispatch on the spike type and L.
+int packed_product(const char* fn, const void* spk, int32_t spk_dtype, int32_t batch,
+                   int32_t n_in, const void* packed, int32_t n_out, float* out,
+                   const LifOut* lif, hipStream_t s) {
+  BS_CHECK_ARG(batch >= 0 && n_in >= 0 && n_out >= 0, "%s: negative size", fn);
+  BS_CHECK_ARG(n_in <= kMaxIn, "%s: n_in = %d exceeds %d", fn, n_in, kMaxIn);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "%s: unknown spike dtype %d", fn, spk_dtype);
+  BS_CHECK_ARG(packed != nullptr && ((uintptr_t)packed & 255) == 0,
+               "%s: packed buffer must be non-NULL and 256-byte aligned", fn);
+  BS_CHECK_ARG((batch + kGroupB - 1) / kGroupB <= 65535, "%s: batch %d too large", fn, batch);
+  if ((int64_t)batch * n_out == 0) return BS_OK;
+  BS_CHECK_ARG(out != nullptr || lif != nullptr, "%s: out is NULL", fn);
+  BS_CHECK_ARG(spk != nullptr || n_in == 0, "%s: spk is NULL", fn);
+  const PackDims d = pack_dims(n_in, n_out);
+  const uint8_t* pk = (const uint8_t*)packed;
+  const size_t es = spk_dtype == BS_SPK_U8 ? 1 : 4;
+  const bool vec = n_in % 16 == 0 && ((uintptr_t)spk & 15) == 0 && (n_in * es) % 16 == 0;
+  if (spk_dtype == BS_SPK_U8) {
+    const uint8_t* p = (const uint8_t*)spk;
+    switch (d.L) {
+      case 4: launch_packed<uint8_t, 4>(p, batch, n_in, d, pk, n_out, out, vec, lif, s); break;
+      case 5: launch_packed<uint8_t, 5>(p, batch, n_in, d, pk, n_out, out, vec, lif, s); break;
+      default: launch_packed<uint8_t, 6>(p, batch, n_in, d, pk, n_out, out, vec, lif, s); break;
+    }
+  } else {
+    const float* p = (const float*)spk;
+    switch (d.L) {
+      case 4: launch_packed<float, 4>(p, batch, n_in, d, pk, n_out, out, vec, lif, s); break;
+      case 5: launch_packed<float, 5>(p, batch, n_in, d, pk, n_out, out, vec, lif, s); break;
+      default: launch_packed<float, 6>(p, batch, n_in, d, pk, n_out, out, vec, lif, s); break;
+    }
+  }
+  BS_CHECK_LAUNCH();
+  return BS_OK;
 }
 
 }  // namespace
@@ -403,37 +486,22 @@ extern "C" int bs_event_dense_packed_f32(const void* spk, int32_t spk_dtype, int
                                          int32_t n_in, const void* packed, int32_t n_out,
                                          float* out, bs_stream_t stream) {
   bs_clear_error();
-  BS_CHECK_ARG(batch >= 0 && n_in >= 0 && n_out >= 0, "bs_event_dense_packed_f32: negative size");
-  BS_CHECK_ARG(n_in <= kMaxIn, "bs_event_dense_packed_f32: n_in = %d exceeds %d", n_in, kMaxIn);
-  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
-               "bs_event_dense_packed_f32: unknown spike dtype %d", spk_dtype);
-  BS_CHECK_ARG(packed != nullptr && ((uintptr_t)packed & 255) == 0,
-               "bs_event_dense_packed_f32: packed buffer must be non-NULL and 256-byte aligned");
-  BS_CHECK_ARG((batch + kGroupB - 1) / kGroupB <= 65535,
-               "bs_event_dense_packed_f32: batch %d too large", batch);
-  if ((int64_t)batch * n_out == 0) return BS_OK;
-  BS_CHECK_ARG(out != nullptr, "bs_event_dense_packed_f32: out is NULL");
-  BS_CHECK_ARG(spk != nullptr || n_in == 0, "bs_event_dense_packed_f32: spk is NULL");
-  const PackDims d = pack_dims(n_in, n_out);
-  hipStream_t s = bs_stream(stream);
-  const uint8_t* pk = (const uint8_t*)packed;
-  const size_t es = spk_dtype == BS_SPK_U8 ? 1 : 4;
-  const bool vec = n_in % 16 == 0 && ((uintptr_t)spk & 15) == 0 && (n_in * es) % 16 == 0;
-  if (spk_dtype == BS_SPK_U8) {
-    const uint8_t* p = (const uint8_t*)spk;
-    switch (d.L) {
-      case 4: launch_packed<uint8_t, 4>(p, batch, n_in, d, pk, n_out, out, vec, s); break;
-      case 5: launch_packed<uint8_t, 5>(p, batch, n_in, d, pk, n_out, out, vec, s); break;
-      default: launch_packed<uint8_t, 6>(p, batch, n_in, d, pk, n_out, out, vec, s); break;
-    }
-  } else {
-    const float* p = (const float*)spk;
-    switch (d.L) {
-      case 4: launch_packed<float, 4>(p, batch, n_in, d, pk, n_out, out, vec, s); break;
-      case 5: launch_packed<float, 5>(p, batch, n_in, d, pk, n_out, out, vec, s); break;
-      default: launch_packed<float, 6>(p, batch, n_in, d, pk, n_out, out, vec, s); break;
-    }
-  }
-  BS_CHECK_LAUNCH();
-  return BS_OK;
+  return packed_product("bs_event_dense_packed_f32", spk, spk_dtype, batch, n_in, packed, n_out,
+                        out, nullptr, bs_stream(stream));
+}
+
+extern "C" int bs_event_dense_packed_lif_step(const void* spk, int32_t spk_dtype, int32_t batch,
+                                              int32_t n_in, const void* packed, int32_t n_out,
+                                              int32_t inh, float* V, float* ge, float* gi,
+                                              int32_t* ref, const bs_lif_params* p,
+                                              float* cur_out, uint8_t* spk_out,
+                                              bs_stream_t stream) {
+  bs_clear_error();
+  const char* fn = "bs_event_dense_packed_lif_step";
+  BS_CHECK_ARG(p != nullptr, "%s: params are NULL", fn);
+  BS_CHECK_ARG((int64_t)batch * n_out <= 0 || (V && ge && gi && ref), "%s: NULL state pointer",
+               fn);
+  LifOut lif{V, ge, gi, ref, spk_out, inh ? 1 : 0, *p};
+  return packed_product(fn, spk, spk_dtype, batch, n_in, packed, n_out, cur_out, &lif,
+                        bs_stream(stream));
 }

@@ -385,6 +385,30 @@ def event_dense_packed(spk, P, out=None):
             'bs_event_dense_packed_f32')
     return out[0] if squeeze else out
 
+
+def event_dense_packed_lif_step(spk, P, V, ge, gi, ref, params, inh=False, cur_out=None,
+                                spk_out=None):
+    """One launch: cur = event_dense_packed(spk, P), then coba_lif_step on the [B, n_out]
+    state (flattened or 2-D) with cur as the excitatory (or, ``inh``, inhibitory) input.
+    Bit-identical to the two calls; returns spk_out (0/1 bytes) when given, else None."""
+    s2 = _spk_view(spk.reshape(1, -1) if spk.dim() == 1 else spk)
+    B, n_in = s2.shape
+    if n_in != P['n_in']:
+        raise ValueError(f'event_dense_packed_lif_step: spikes have {n_in} inputs, W has '
+                         f'{P["n_in"]}')
+    n = B * P['n_out']
+    for name, t, dt in (('V', V, torch.float32), ('ge', ge, torch.float32),
+                        ('gi', gi, torch.float32), ('ref', ref, torch.int32)):
+        if t.numel() != n or not t.is_contiguous() or t.dtype != dt:
+            raise ValueError(f'event_dense_packed_lif_step: {name} must be contiguous {dt} '
+                             f'with {n} elements')
+    buf = P['packed']
+    N.check(N.lib().bs_event_dense_packed_lif_step(
+        N.ptr(s2), _spk_dtype(s2), B, n_in, N.ptr(buf), P['n_out'], 1 if inh else 0, N.ptr(V),
+        N.ptr(ge), N.ptr(gi), N.ptr(ref), ctypes_ref(params), N.ptr(cur_out), N.ptr(spk_out),
+        N.stream_handle(buf.device)), 'bs_event_dense_packed_lif_step')
+    return spk_out
+
 def event_dense_chunks(batch, n_in, n_out):
     """(S, L): the chunk plan that fixes the order of bs_event_dense_f32's additions."""
     L = ctypes.c_int32(0)

@@ -247,6 +247,19 @@ BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* 
                      const float* in_e, const float* in_i, const bs_lif_params* p,
                      uint8_t* spk_out, bs_stream_t stream);
 
+/* One recurrent step of a packed EventLinear driving COBA-LIF neurons, in one launch:
+ * cur = the bs_event_dense_packed_f32 product of spk [batch, n_in] with `packed`, then the
+ * bs_coba_lif_step update of the [batch, n_out] state (V, ge, gi, ref) with in_e = cur,
+ * in_i = 0 (inh = 0) or in_e = 0, in_i = cur (inh != 0).  The bits equal those two calls in
+ * sequence.  cur_out (nullable) receives cur; spk_out (nullable) the spikes as 0/1 bytes.
+ * Replaces EventLinear (brainstate/nn/_event_linear.py:99-100) followed by the Expon + COBA +
+ * LIFRef update it feeds (brainstate/nn/_exp_euler.py:226-249). */
+BS_API int bs_event_dense_packed_lif_step(const void* spk, int32_t spk_dtype, int32_t batch,
+                                          int32_t n_in, const void* packed, int32_t n_out,
+                                          int32_t inh, float* V, float* ge, float* gi,
+                                          int32_t* ref, const bs_lif_params* p, float* cur_out,
+                                          uint8_t* spk_out, bs_stream_t stream);
+
 /* Hodgkin-Huxley with Expon synapses and COBA output (examples/100_hh_neuron_model.py:25-93):
  * rates from the old V; V, m, h, n each by exp-Euler; spike = (V < V_th) & (V' >= V_th). */
 typedef struct {

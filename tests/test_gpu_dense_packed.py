@@ -175,3 +175,53 @@ def test_event_linear_module_routes(torch_cuda):
     with torch.no_grad():
         yv = v(dev(torch, xf)).cpu().numpy()
     assert np.array_equal(yv, event.event_linear(xf, W, float_as_event=False, chunk_rows=L))
+
+
+@pytest.mark.parametrize('inh', [False, True])
+def test_fused_lif_step_recurrent(torch_cuda, inh):
+    """Four recurrent steps (the spikes of one step are the next step's input) of the fused
+    packed EventLinear + COBA-LIF launch equal, bit for bit, the oracle's fixed-point product
+    followed by its COBA-LIF step, and the unfused pair of device calls."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    from oracle import neuron
+    say('fused lif step', inh)
+    rng = np.random.RandomState(31 + inh)
+    B, n = 70, 512
+    W = rng.normal(0.4 if not inh else 0.8, 0.3, (n, n)).astype(F)
+    spk = rng.rand(B, n) < 0.1
+    V = rng.uniform(-60, -50, (B, n)).astype(F).reshape(-1)
+    ge = np.zeros(B * n, F)
+    gi = np.zeros(B * n, F)
+    ref = rng.choice([0, 0, 0, 2], B * n).astype(np.int32)
+    p = neuron.LIFParams()
+    P = ops.pack_dense(dev(torch, W))
+    dV, dge, dgi, dref = (dev(torch, a) for a in (V, ge, gi, ref))
+    uV, uge, ugi, uref = (dev(torch, a) for a in (V, ge, gi, ref))
+    x = dev(torch, spk.astype(np.uint8))
+    ux = x.clone()
+    fired = 0
+    for step in range(4):
+        cur = event.event_dense_fixed_point(spk, W).reshape(-1)
+        z = np.zeros_like(cur)
+        V, ge, gi, ref, s_new = neuron.coba_lif_step(V, ge, gi, ref, z if inh else cur,
+                                                     cur if inh else z, p)
+        cur_d = torch.empty(B, n, device='cuda')
+        spk_d = torch.empty(B, n, dtype=torch.uint8, device='cuda')
+        ops.event_dense_packed_lif_step(x, P, dV, dge, dgi, dref, ops.lif_params(), inh=inh,
+                                        cur_out=cur_d, spk_out=spk_d)
+        ucur = ops.event_dense_packed(ux, P)
+        zero = torch.zeros_like(ucur)
+        us = ops.coba_lif_step(uV, uge, ugi, uref, (zero if inh else ucur).view(-1),
+                               (ucur if inh else zero).view(-1), ops.lif_params())
+        assert np.array_equal(cur_d.cpu().numpy().reshape(-1), cur)
+        for d, e in ((dV, V), (dge, ge), (dgi, gi), (dref, ref)):
+            assert np.array_equal(d.cpu().numpy(), e)
+        for d, u in ((dV, uV), (dge, uge), (dgi, ugi), (dref, uref)):
+            assert torch.equal(d, u)
+        assert np.array_equal(spk_d.cpu().numpy().reshape(-1).astype(bool), s_new)
+        assert torch.equal(spk_d.view(-1), us)
+        spk = s_new.reshape(B, n)
+        x, ux = spk_d, us.view(B, n)
+        fired += int(s_new.sum())
+    assert fired > 100 or inh
