@@ -21,7 +21,7 @@
 // (0, or 1 when a weight is not finite), then the bit patterns of m_j for the NT * 16 padded
 // columns (uint32; NT = ceil(n_out / 16); rounded up to 256 bytes), then the digits in
 // 1024-byte blocks, one per (column tile t, input block k of 64 inputs, digit l), at
-// ((t * KB + k) * L + l) * 1024.  Byte 16 m + u of a block is digit l of
+// ((t * KB + k) * L + l) * 1024, KB = ceil(n_in / 64) rounded up to a multiple of 8.  Byte 16 m + u of a block is digit l of
 // W[64 k + 16 (m / 16) + u, 16 t + m % 16]: lane m of the instruction's B operand holds
 // column m % 16, and the spike operand puts batch row m % 16 and the same 16 inputs in lane
 // m, so both operands agree on which input each byte is (the instruction sums over all 64
@@ -75,7 +75,9 @@ struct PackDims {
 PackDims pack_dims(int32_t n_in, int32_t n_out) {
   PackDims d;
   d.L = digits_for(n_in);
-  d.KB = (n_in + kBlkIn - 1) / kBlkIn;
+  // input blocks, padded with zero digits to whole pipeline stages of every wave
+  constexpr int kStageBlocks = kPW * kGroup;
+  d.KB = ((n_in + kBlkIn - 1) / kBlkIn + kStageBlocks - 1) / kStageBlocks * kStageBlocks;
   d.NT = (n_out + kTileN - 1) / kTileN;
   d.bits_off = kHeader;
   d.dig_off = kHeader + ((int64_t)d.NT * kTileN * 4 + 255) / 256 * 256;
@@ -194,9 +196,9 @@ __device__ __forceinline__ uint32_t nz_bytes(uint32_t x) {
 // 64 k + 16 (lane / 16) + [0, 16) as 0/1 bytes.
 template <typename T, bool kVec>
 __device__ __forceinline__ v4i load_spk(const T* __restrict__ spk, int32_t batch, int32_t n_in,
-                                        int32_t b, int64_t i0, bool ok) {
+                                        int32_t b, int64_t i0) {
   v4i a = {0, 0, 0, 0};
-  if (!ok || b >= batch || i0 >= n_in) return a;
+  if (b >= batch || i0 >= n_in) return a;
   const T* p = spk + (int64_t)b * n_in + i0;
   if constexpr (sizeof(T) == 1) {
     if (kVec) {  // n_in % 16 == 0 and 16-byte aligned rows: i0 + 16 <= n_in
@@ -283,13 +285,15 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
   // again with zero spikes, so every load is in bounds and adds nothing).  Byte spikes on
   // the 16-byte path are loaded from an in-bounds address whatever the lane's row, kept raw
   // and masked when multiplied, so no load waits for another before the stage's products.
+  // Every wave's block range is whole stages (KB is a multiple of kPW * kGroup), so no stage
+  // reaches past it.  Byte spikes on the 16-byte path are loaded from clamped addresses: rows
+  // past `batch` repeat the last row (their sums are never stored) and inputs past n_in repeat
+  // the last 16 (their digits are zero), so the loads need no masks and no branches.
   constexpr bool kRaw = sizeof(T) == 1 && kVec;
-  auto load = [&](int32_t k, v4i (&a)[kGroup][kRowTiles], uint32_t (&am)[kGroup][kRowTiles],
-                  v4i (&bv)[kGroup][L]) {
+  auto load = [&](int32_t k, v4i (&a)[kGroup][kRowTiles], v4i (&bv)[kGroup][L]) {
 #pragma unroll
     for (int s = 0; s < kGroup; ++s) {
-      const bool ok = k + s < k_hi;
-      const int64_t kk = ok ? k + s : (k_hi > 0 ? k_hi - 1 : 0);
+      const int64_t kk = k + s;
 #pragma unroll
       for (int l = 0; l < L; ++l) bv[s][l] = *(const v4i*)(dp + (kk * L + l) * 1024);
       const int64_t i0 = kk * kBlkIn + iq;
@@ -297,19 +301,16 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
       for (int mt = 0; mt < kRowTiles; ++mt) {
         const int32_t b = brow + 16 * mt;
         if constexpr (kRaw) {
-          const bool v = ok && b < batch && i0 < n_in;
-          const int64_t off = v ? (int64_t)b * n_in + i0 : 0;
+          const int64_t off = (int64_t)(b < batch ? b : batch - 1) * n_in +
+                              (i0 < n_in ? i0 : (int64_t)n_in - 16);
           a[s][mt] = *(const v4i*)((const uint8_t*)spk + off);
-          am[s][mt] = v ? 0x01010101u : 0u;
         } else {
-          a[s][mt] = load_spk<T, kVec>(spk, batch, n_in, b, i0, ok);
-          am[s][mt] = 0x01010101u;
+          a[s][mt] = load_spk<T, kVec>(spk, batch, n_in, b, i0);
         }
       }
     }
   };
-  auto mult = [&](const v4i (&a)[kGroup][kRowTiles], const uint32_t (&am)[kGroup][kRowTiles],
-                  const v4i (&bv)[kGroup][L]) {
+  auto mult = [&](const v4i (&a)[kGroup][kRowTiles], const v4i (&bv)[kGroup][L]) {
 #pragma unroll
     for (int s = 0; s < kGroup; ++s)
 #pragma unroll
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
         v4i x = a[s][mt];
         if constexpr (kRaw) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) x[q] = (int32_t)(nz_bytes((uint32_t)x[q]) & am[s][mt]);
+          for (int q = 0; q < 4; ++q) x[q] = (int32_t)nz_bytes((uint32_t)x[q]);
         }
 #pragma unroll
         for (int l = 0; l < L; ++l)
@@ -325,15 +326,24 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
       }
   };
   if (k_lo < k_hi) {
+    // the steady-state body always has the next stage's loads in flight while it multiplies,
+    // and every path into its first multiply has issued the same loads, so the waits before
+    // each product count only the stage it needs; the last one or two stages follow it
     v4i a0[kGroup][kRowTiles], b0v[kGroup][L], a1[kGroup][kRowTiles], b1v[kGroup][L];
-    uint32_t m0[kGroup][kRowTiles], m1[kGroup][kRowTiles];
-    load(k_lo, a0, m0, b0v);
-    for (int32_t k = k_lo; k < k_hi; k += 2 * kGroup) {
-      if (k + kGroup < k_hi) load(k + kGroup, a1, m1, b1v);
-      mult(a0, m0, b0v);
-      if (k + kGroup >= k_hi) break;
-      if (k + 2 * kGroup < k_hi) load(k + 2 * kGroup, a0, m0, b0v);
-      mult(a1, m1, b1v);
+    load(k_lo, a0, b0v);
+    int32_t k = k_lo;
+    for (; k + 2 * kGroup < k_hi; k += 2 * kGroup) {
+      load(k + kGroup, a1, b1v);
+      mult(a0, b0v);
+      load(k + 2 * kGroup, a0, b0v);
+      mult(a1, b1v);
+    }
+    if (k + kGroup < k_hi) {
+      load(k + kGroup, a1, b1v);
+      mult(a0, b0v);
+      mult(a1, b1v);
+    } else {
+      mult(a0, b0v);
     }
   }
 
