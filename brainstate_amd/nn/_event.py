@@ -302,11 +302,14 @@ class FixedNumConn(Module):
 
     def _bucket_layout(self, w):
         """Destination-bucketed layout of the current connectivity and weight; rebuilt when the
-        weight State is assigned a new value or its tensor is modified in place."""
+        weight State is assigned a new value (another object, or another scalar value) or its
+        tensor is modified in place (version counter).  The cache holds the weight object it
+        was built from, so a freed weight's identity cannot be recycled by a new one; a numpy
+        weight changed in place is not seen (it carries no version)."""
         v = self.weight.value
-        key = (id(v), v._version if torch.is_tensor(v) else None,
+        key = (v._version if torch.is_tensor(v) else None,
                float(v) if init._is_scalar(v) else None)
-        if self._bucket is None or self._bucket[0] != key:
+        if self._bucket is None or self._bucket[0] is not v or self._bucket[1] != key:
             homo = w.numel() == 1
             conn = self.conn
             indptr = getattr(conn, 'indptr', None)
@@ -318,8 +321,8 @@ class FixedNumConn(Module):
             layout = ops.build_buckets(conn.indices, self.out_size[-1], w=wt,
                                        w_homo=float(w.reshape(())) if homo else 0.0,
                                        indptr=indptr)
-            self._bucket = (key, layout)
-        return self._bucket[1]
+            self._bucket = (v, key, layout)
+        return self._bucket[2]
 
     def update(self, x):
         """``x @ conn`` (:202-209): bool spikes are events; any other dtype is a
@@ -446,8 +449,8 @@ class EventLinear(Module):
 
     def _packed_weight(self, W):
         """ops.pack_dense of the current weight; None when the packed form does not apply.
-        A torch weight is packed once per value (cached on the tensor's identity, storage and
-        version counter, which in-place changes bump); a numpy weight, which carries no
+        A torch weight is packed once per value (cached on the tensor object, its storage and
+        its version counter, which in-place changes bump); a numpy weight, which carries no
         version, is packed on every call."""
         if self.event_kernel == 'stream' or not self.float_as_event:
             return None
@@ -457,10 +460,12 @@ class EventLinear(Module):
         if not torch.is_tensor(v):
             P = ops.pack_dense(W.detach())
             return P if P['finite'] else None
-        key = (id(v), v.data_ptr(), v._version)
-        if self._packed is None or self._packed[0] != key:
-            self._packed = (key, ops.pack_dense(W.detach()))
-        P = self._packed[1]
+        # the cache holds the weight tensor it packed, so a freed weight's identity and
+        # storage cannot be recycled by a new tensor while the packed form is kept
+        key = (v.data_ptr(), v._version)
+        if self._packed is None or self._packed[0] is not v or self._packed[1] != key:
+            self._packed = (v, key, ops.pack_dense(W.detach()))
+        P = self._packed[2]
         return P if P['finite'] else None
 
     def update(self, spk):

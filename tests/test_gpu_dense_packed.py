@@ -164,6 +164,11 @@ def test_event_linear_module_routes(torch_cuda):
         m.weight.value.mul_(2.0)   # in place: version bump -> repack
         y2 = m(x).cpu().numpy()
     assert np.array_equal(y2, event.event_dense_fixed_point(spk, W * 2))
+    for it in range(3):   # a new tensor each time, the previous one released
+        m.weight.value = dev(torch, W * F(it + 3))
+        with torch.no_grad():
+            y3 = m(x).cpu().numpy()
+        assert np.array_equal(y3, event.event_dense_fixed_point(spk, W * F(it + 3)))
     s = bs.nn.EventLinear(512, 256, W, event_kernel='stream')
     with torch.no_grad():
         ys = s(x).cpu().numpy()
