@@ -379,8 +379,9 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
       // the update of bs_coba_lif_step with this output as its conductance input
       float V = sV[r], ge = sge[r], gi = sgi[r];
       int32_t rf = sref[r];
-      const bool sp =
-          bs_lif_update(lif.p, V, ge, gi, rf, lif.inh ? 0.0f : v, lif.inh ? v : 0.0f);
+      const float in_e = lif.inh ? 0.0f : v, in_i = lif.inh ? v : 0.0f;
+      const bool sp = lif.p.cuba ? bs_lif_update<true>(lif.p, V, ge, gi, rf, in_e, in_i)
+                                 : bs_lif_update<false>(lif.p, V, ge, gi, rf, in_e, in_i);
       lif.V[o] = V;
       lif.ge[o] = ge;
       lif.gi[o] = gi;

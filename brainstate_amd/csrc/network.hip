@@ -110,6 +110,7 @@ struct NetArgs {
 
 // ---- neuron models: register-resident state, one fused update per neuron-step ----
 
+template <bool kCuba>
 struct LifModel {
   using Params = bs_lif_params;
   using State = bs_lif_state;
@@ -129,13 +130,15 @@ struct LifModel {
   static constexpr bool kPrepare = false;  // every operation of the step needs the input
   __device__ static void prepare(const Params&, Regs&) {}
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
-    return bs_lif_update(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
+    return bs_lif_update<kCuba>(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
   }
   // Whether the neuron may spike this step: a zero-input forward-Euler estimate of the next
   // V within 15 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
   // estimate never decides a spike.
   __device__ static bool near(const Params& p, const Regs& r) {
-    const float I = p.I_ext + r.ge * p.decay_e * (p.E_e - r.V) + r.gi * p.decay_i * (p.E_i - r.V);
+    const float I = kCuba ? p.I_ext + r.ge * p.decay_e * p.scale_e + r.gi * p.decay_i * p.scale_i
+                          : p.I_ext + r.ge * p.decay_e * (p.E_e - r.V) +
+                                r.gi * p.decay_i * (p.E_i - r.V);
     const float vp = r.V + p.dt * p.inv_tau * ((p.V_rest - r.V) + p.R * I);
     return r.ref <= 0 && vp >= p.V_th - 0.15f * (p.V_th - p.V_reset);
   }
@@ -826,8 +829,11 @@ extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const 
     BS_CHECK_ARG(st->V && st->ge && st->gi && st->ref, "bs_coba_lif_run: NULL state pointer");
   }
   if (p) BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_run: inv_tau is NaN");
-  return run<LifModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
-                       stream, "bs_coba_lif_run");
+  if (p && p->cuba)
+    return run<LifModel<true>>(net, st, p, t0, steps, counts_out, hash_out, raster_out,
+                               workspace, stream, "bs_coba_lif_run");
+  return run<LifModel<false>>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
+                              stream, "bs_coba_lif_run");
 }
 
 extern "C" int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,

@@ -9,6 +9,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
+template <bool kCuba>
 __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restrict__ V,
                                                      float* __restrict__ ge,
                                                      float* __restrict__ gi,
@@ -21,7 +22,8 @@ __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restric
        j += (int64_t)gridDim.x * kBlock) {
     float v = V[j], e = ge[j], i = gi[j];
     int32_t r = ref[j];
-    const bool s = bs_lif_update(p, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
+    const bool s =
+        bs_lif_update<kCuba>(p, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
     V[j] = v;
     ge[j] = e;
     gi[j] = i;
@@ -82,8 +84,12 @@ extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32
   BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_step: inv_tau is NaN");
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
-  k_lif_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i, *p,
-                                                         spk_out);
+  if (p->cuba)
+    k_lif_step<true><<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i,
+                                                               *p, spk_out);
+  else
+    k_lif_step<false><<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i,
+                                                                *p, spk_out);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

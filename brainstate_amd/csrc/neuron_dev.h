@@ -11,16 +11,25 @@
 #include "bs_math.h"
 #include "common.h"
 
-// brainpy.state Expon + COBA + LIFRef for one neuron; see bs_lif_params in the header.
-// Returns the spike; updates V, ge, gi, ref in place.
+// brainpy.state Expon + COBA (kCuba: CUBA) + LIFRef for one neuron; see bs_lif_params in the
+// header.  Returns the spike; updates V, ge, gi, ref in place.  The CUBA current does not
+// depend on V, so the exp-Euler Jacobian is -1 * inv_tau.
+template <bool kCuba = false>
 __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, float& ge,
                                               float& gi, int32_t& ref, float in_e, float in_i) {
   ge = bs_fma(ge, p.decay_e, in_e);
   gi = bs_fma(gi, p.decay_i, in_i);
-  float I = bs_fma(ge, p.E_e - V, p.I_ext);
-  I = bs_fma(gi, p.E_i - V, I);
+  float I, J;
+  if constexpr (kCuba) {
+    I = bs_fma(ge, p.scale_e, p.I_ext);
+    I = bs_fma(gi, p.scale_i, I);
+    J = -1.0f * p.inv_tau;
+  } else {
+    I = bs_fma(ge, p.E_e - V, p.I_ext);
+    I = bs_fma(gi, p.E_i - V, I);
+    J = bs_fma(-p.R, ge + gi, -1.0f) * p.inv_tau;
+  }
   const float f = bs_fma(p.R, I, p.V_rest - V) * p.inv_tau;
-  const float J = bs_fma(-p.R, ge + gi, -1.0f) * p.inv_tau;
   const float phi = bs_exprel(p.dt * J);
   float Vn = bs_fma(p.dt * phi, f, V);
   bool spk = false;

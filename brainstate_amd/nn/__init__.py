@@ -6,10 +6,10 @@ from ._delay import (Delay, DelayAccess, InterpolationRegistry, OutputDelayAt, P
 from ._event import EventFixedNumConn, EventFixedProb, EventLinear, FixedNumConn
 from ._fuse import fuse
 from ._module import Dynamics, Module, init_all_states
-from ._neurons import COBA, HH, LIF, AlignPostProj, Expon, LIFRef
+from ._neurons import COBA, CUBA, HH, LIF, AlignPostProj, Expon, LIFRef
 
 __all__ = ['init', 'Module', 'Dynamics', 'init_all_states', 'FixedNumConn', 'EventFixedNumConn',
-           'EventFixedProb', 'EventLinear', 'Expon', 'COBA', 'AlignPostProj', 'LIF', 'LIFRef',
-           'HH', 'fuse', 'Delay', 'DelayAccess', 'StateWithDelay', 'InterpolationRegistry',
+           'EventFixedProb', 'EventLinear', 'Expon', 'COBA', 'CUBA', 'AlignPostProj', 'LIF',
+           'LIFRef', 'HH', 'fuse', 'Delay', 'DelayAccess', 'StateWithDelay', 'InterpolationRegistry',
            'Prefetch', 'PrefetchDelay', 'PrefetchDelayAt', 'OutputDelayAt',
            'receive_update_output', 'not_receive_update_output']

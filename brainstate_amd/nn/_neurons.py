@@ -10,8 +10,9 @@ registers a conductance channel on the post-synaptic neuron; calling the project
 spikes runs ``comm`` (the event mat-vec) and queues its output as the channel's delta
 input; calling the neuron advances every channel's Expon conductance and the membrane in
 one fused kernel (``bs_coba_lif_step`` / ``bs_coba_hh_step``): g' = g*exp(-dt/tau) + delta,
-COBA current g*(E - V), exp-Euler membrane, spike.  Up to two conductance channels per
-neuron (E and I) map onto the kernel's two; more raise NotImplementedError.
+COBA current g*(E - V) (or, with ``out=CUBA``, g*scale), exp-Euler membrane, spike.  Up to
+two channels per neuron (E and I) map onto the kernel's two; more raise NotImplementedError,
+and the channels of one LIF neuron are all COBA or all CUBA.
 
 Units: plain floats in mV, ms, mS (per cm^2 for HH); brainunit is not used.
 """
@@ -24,7 +25,7 @@ from .._state import HiddenState, ShortTermState
 from . import init
 from ._module import Dynamics, Module
 
-__all__ = ['Expon', 'COBA', 'AlignPostProj', 'LIF', 'LIFRef', 'HH']
+__all__ = ['Expon', 'COBA', 'CUBA', 'AlignPostProj', 'LIF', 'LIFRef', 'HH']
 
 
 class _Desc:
@@ -83,6 +84,16 @@ class COBA(Module, _Describable):
         self.E = float(E)
 
 
+class CUBA(Module, _Describable):
+    """Current-based output: I = g * scale (brainpy.state CUBA; examples/400_CUBA_2005_bpu.py
+    uses scale = 1 V, i.e. 1.0 with g in mS and currents in mA)."""
+    __module__ = 'brainstate_amd.nn'
+
+    def __init__(self, scale=1.0, name=None):
+        super().__init__(name=name)
+        self.scale = float(scale)
+
+
 class AlignPostProj(Module):
     """Projection with post-aligned synapse (brainpy.state AlignPostProj)."""
     __module__ = 'brainstate_amd.nn'
@@ -94,9 +105,9 @@ class AlignPostProj(Module):
         self.comm = comm
         self.syn = syn() if isinstance(syn, _Desc) else syn
         self.out = out() if isinstance(out, _Desc) else out
-        if not isinstance(self.syn, Expon) or not isinstance(self.out, COBA):
+        if not isinstance(self.syn, Expon) or not isinstance(self.out, (COBA, CUBA)):
             raise NotImplementedError('the fused kernels implement Expon synapses with COBA '
-                                      'output')
+                                      'or CUBA output')
         self.post = post
         post._add_channel(self)
 
@@ -115,7 +126,12 @@ class _COBANeuron(Dynamics):
         if len(self._channels) >= 2:
             raise NotImplementedError('the fused step kernels take at most two conductance '
                                       'channels (E and I)')
+        if self._channels and isinstance(proj.out, CUBA) != self._cuba():
+            raise NotImplementedError('the channels of one neuron must all be COBA or all CUBA')
         self._channels.append(proj)
+
+    def _cuba(self):
+        return bool(self._channels) and isinstance(self._channels[0].out, CUBA)
 
     def _channel_args(self):
         zeros = torch.zeros_like(self.V.value)
@@ -123,7 +139,7 @@ class _COBANeuron(Dynamics):
         for ch in self._channels:
             g.append(ch.syn.g.value)
             ins.append(ch.syn.delta)
-            E.append(ch.out.E)
+            E.append(ch.out.scale if isinstance(ch.out, CUBA) else ch.out.E)
             tau.append(ch.syn.tau)
         while len(g) < 2:
             g.append(zeros.clone())
@@ -184,7 +200,12 @@ class LIFRef(_COBANeuron, _Describable):
         self.spike = ShortTermState(torch.zeros(shape, dtype=torch.bool, device=_dev()))
 
     def params(self, I_ext=0.0):
-        _, _, E, tau = self._channel_args()
+        _, _, E, tau = self._channel_args()   # E holds the CUBA scales for CUBA channels
+        if self._cuba():
+            return ops.lif_params(V_rest=self.V_rest, V_th=self.V_th, V_reset=self.V_reset,
+                                  tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
+                                  tau_e=tau[0], tau_i=tau[1], dt=environ.get_dt(),
+                                  out='cuba', scale_e=E[0], scale_i=E[1])
         return ops.lif_params(V_rest=self.V_rest, V_th=self.V_th, V_reset=self.V_reset,
                               tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
                               E_e=E[0], E_i=E[1], tau_e=tau[0], tau_i=tau[1],
@@ -231,6 +252,8 @@ class HH(_COBANeuron, _Describable):
         self.spike = ShortTermState(torch.zeros(shape, dtype=torch.bool, device=dev))
 
     def params(self, I_ext=0.0):
+        if self._cuba():
+            raise NotImplementedError('the HH kernels implement COBA channels only')
         _, _, E, tau = self._channel_args()
         return ops.hh_params(ENa=self.ENa, gNa=self.gNa, EK=self.EK, gK=self.gK, EL=self.EL,
                              gL=self.gL, C=self.C, V_th=self.V_th, I_ext=I_ext, E_e=E[0],

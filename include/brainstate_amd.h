@@ -241,6 +241,11 @@ BS_API int bs_event_dense_vjp_f32(const void* spk, int32_t spk_dtype, int32_t ba
 typedef struct {
   float V_rest, V_th, V_reset, inv_tau, R, I_ext, E_e, E_i, dt, decay_e, decay_i;
   int32_t ref_steps;
+  /* cuba != 0: current-based output (brainpy.state CUBA, used by
+   * examples/400_CUBA_2005_bpu.py:42-58): I = I_ext + g_e*scale_e + g_i*scale_i (one fused
+   * multiply-add each), J = -inv_tau; E_e / E_i are then unused.  cuba == 0: COBA as above. */
+  int32_t cuba;
+  float scale_e, scale_i;
 } bs_lif_params;
 
 BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,

@@ -61,8 +61,14 @@ def ref_steps(tau_ref, dt):
 
 
 class LIFParams:
+    """``out='cuba'``: current-based synaptic output I += g * scale (brainpy.state CUBA, used
+    by examples/400_CUBA_2005_bpu.py:42-58) instead of g * (E - V)."""
+
     def __init__(self, V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5.,
-                 I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1):
+                 I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba',
+                 scale_e=1., scale_i=1.):
+        self.cuba = out == 'cuba'
+        self.scale_e, self.scale_i = F(scale_e), F(scale_i)
         self.V_rest, self.V_th, self.V_reset = F(V_rest), F(V_th), F(V_reset)
         self.tau, self.R, self.I_ext = F(tau), F(R), F(I_ext)
         self.inv_tau = F(F(1.0) / F(tau))
@@ -74,12 +80,18 @@ class LIFParams:
 
 
 def lif_membrane(V, ge, gi, p):
-    """One exp-Euler step of the COBA LIF membrane (no refractoriness, no reset)."""
+    """One exp-Euler step of the COBA (or, p.cuba, CUBA) LIF membrane (no refractoriness, no
+    reset).  CUBA: the current does not depend on V, so the Jacobian is -1/tau."""
     V, ge, gi = (np.asarray(x, F) for x in (V, ge, gi))
-    I = fma32(ge, (p.E_e - V).astype(F), p.I_ext)
-    I = fma32(gi, (p.E_i - V).astype(F), I)
+    if getattr(p, 'cuba', False):
+        I = fma32(ge, np.full_like(V, p.scale_e), p.I_ext)
+        I = fma32(gi, np.full_like(V, p.scale_i), I)
+        J = np.full_like(V, (F(-1.0) * p.inv_tau).astype(F))
+    else:
+        I = fma32(ge, (p.E_e - V).astype(F), p.I_ext)
+        I = fma32(gi, (p.E_i - V).astype(F), I)
+        J = (fma32(-p.R, (ge + gi).astype(F), F(-1.0)) * p.inv_tau).astype(F)
     f = (fma32(p.R, I, (p.V_rest - V).astype(F)) * p.inv_tau).astype(F)
-    J = (fma32(-p.R, (ge + gi).astype(F), F(-1.0)) * p.inv_tau).astype(F)
     phi = exprel((p.dt * J).astype(F))
     return fma32((p.dt * phi).astype(F), f, V)
 

@@ -7,6 +7,7 @@
   used by the parity configs (brainstate/nn/_event_fixedprob.py:165-171).
 * coba_lif_4000.json -- config [1]: 4000-neuron COBA E/I net, 1000 steps; per-step spike
   counts, per-step order-free spike digests and SHA-256 of the raster / final state.
+* cuba_lif_4000.json -- examples/400_CUBA_2005_bpu.py's CUBA E/I net, 1000 steps, same records.
 * coba_hh_2000.json -- a 2000-neuron COBA-HH net, 600 steps, same records.
 The reference itself is not imported (it needs JAX, brainevent and brainunit, which are
 absent); these fixtures freeze the oracle so that any drift in it is caught.
@@ -25,6 +26,10 @@ from oracle import conn, neuron, network  # noqa: E402
 
 CONFIG1 = dict(n=4000, n_exc=3200, p=0.02, w_e=0.6, w_i=6.7, seed_e=1, seed_i=2, seed_v=3,
                steps=1000)
+# examples/400_CUBA_2005_bpu.py:36-66 (V0 ~ N(-55, 2) drawn with numpy; 1000 of its steps)
+CUBA_NET = dict(n=4000, n_exc=3200, p=0.02, w_e=1.62, w_i=-9.0, seed_e=21, seed_i=22,
+                seed_v=23, steps=1000, V_rest=-49., V_th=-50., V_reset=-60., tau=20.,
+                tau_ref=5., I_ext=20.)
 HH_NET = dict(n=2000, n_exc=1600, k=80, w_e=0.05, w_i=0.3, seed_e=11, seed_i=12, seed_v=13,
               steps=600, I_ext=6.5)
 
@@ -39,6 +44,16 @@ def config1_net():
     pi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=c['seed_i'])
     V0 = np.random.RandomState(c['seed_v']).uniform(-60., -50., c['n']).astype(np.float32)
     return pe, pi, V0, neuron.LIFParams()
+
+
+def cuba_net():
+    c = CUBA_NET
+    pe = network.Projection(0, c['n_exc'], c['n'], c['p'], c['w_e'], seed=c['seed_e'])
+    pi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=c['seed_i'])
+    V0 = np.random.RandomState(c['seed_v']).normal(-55., 2., c['n']).astype(np.float32)
+    p = neuron.LIFParams(V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'],
+                         tau=c['tau'], tau_ref=c['tau_ref'], I_ext=c['I_ext'], out='cuba')
+    return pe, pi, V0, p
 
 
 def hh_net():
@@ -71,6 +86,13 @@ def main():
     with open(os.path.join(HERE, 'coba_lif_4000.json'), 'w') as f:
         json.dump(rec, f)
     print('coba_lif_4000: total spikes', int(res['counts'].sum()))
+
+    pe, pi, V0, p = cuba_net()
+    res = network.run_coba_lif(V0, pe, pi, p, CUBA_NET['n_exc'], CUBA_NET['steps'])
+    rec = dict(config=CUBA_NET, **run_records(res))
+    with open(os.path.join(HERE, 'cuba_lif_4000.json'), 'w') as f:
+        json.dump(rec, f)
+    print('cuba_lif_4000: total spikes', int(res['counts'].sum()))
 
     pe, pi, V0, p = hh_net()
     res = network.run_coba_hh(V0, pe, pi, p, HH_NET['n_exc'], HH_NET['steps'])

@@ -107,10 +107,37 @@ def test_event_dense_packed_sizes_host_only():
     rc = lib.bs_event_dense_packed_f32(None, 0, 1, 64, None, 16, None, None)
     assert rc == N.BS_ERR_INVALID and b'aligned' in lib.bs_last_error()
 
+
 def test_struct_layouts_match_header():
     # field counts/order of the ctypes mirrors (sizes of plain C structs on x86-64)
-    assert ctypes.sizeof(N.LifParams) == 12 * 4
+    assert ctypes.sizeof(N.LifParams) == 15 * 4
+    assert [f[0] for f in N.LifParams._fields_][11:] == ['ref_steps', 'cuba', 'scale_e',
+                                                         'scale_i']
     assert ctypes.sizeof(N.HhParams) == 14 * 4
     assert ctypes.sizeof(N.LifState) == 4 * 8
     assert ctypes.sizeof(N.HhState) == 6 * 8
     assert [f[0] for f in N.Net._fields_][:4] == ['n', 'n_exc', 'k_e', 'k_i']
+
+
+def test_lif_params_offsets_match_the_compiled_header(tmp_path):
+    """The header compiled by the host compiler puts bs_lif_params' fields where the ctypes
+    mirror reads them."""
+    import shutil
+    import subprocess
+    cc = shutil.which('gcc')
+    if cc is None:
+        pytest.skip('no host C compiler')
+    src = tmp_path / 'off.c'
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "brainstate_amd.h"\n'
+                   'int main(void) { printf("%zu %zu %zu %zu %zu\\n", sizeof(bs_lif_params), '
+                   'offsetof(bs_lif_params, ref_steps), offsetof(bs_lif_params, cuba), '
+                   'offsetof(bs_lif_params, scale_e), offsetof(bs_lif_params, scale_i)); '
+                   'return 0; }\n')
+    exe = tmp_path / 'off'
+    subprocess.run([cc, '-I', os.path.join(ROOT, 'include'), str(src), '-o', str(exe)],
+                   check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True,
+                                          check=True).stdout.split()]
+    L = N.LifParams
+    assert got == [ctypes.sizeof(L), L.ref_steps.offset, L.cuba.offset, L.scale_e.offset,
+                   L.scale_i.offset]

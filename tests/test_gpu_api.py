@@ -182,6 +182,75 @@ def test_fused_network_continues_eager_state(bs):
     assert np.array_equal(net.E.syn.g.value.cpu().numpy(), ref['ge'])
 
 
+
+class _CUBANet:
+    """examples/400_CUBA_2005_bpu.py:36-66: LIFRef with Expon synapses and CUBA outputs
+    (scale 1 V), signed weights 1.62 / -9.0, external input 20."""
+
+    def __init__(self, bs):
+        c = make_golden.CUBA_NET
+        self.bs = bs
+        self.n_exc, self.num = c['n_exc'], c['n']
+        V0 = np.random.RandomState(c['seed_v']).normal(-55., 2., c['n']).astype(F)
+        self.N = bs.nn.LIFRef(self.num, V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'],
+                              tau=c['tau'], tau_ref=c['tau_ref'], V_initializer=lambda s: V0)
+        self.E = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=c['p'],
+                                      conn_weight=c['w_e'], seed=c['seed_e']),
+            syn=bs.nn.Expon.desc(self.num, tau=5.), out=bs.nn.CUBA.desc(scale=1.0), post=self.N)
+        self.I = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(self.num - self.n_exc, self.num, conn_num=c['p'],
+                                      conn_weight=c['w_i'], seed=c['seed_i']),
+            syn=bs.nn.Expon.desc(self.num, tau=10.), out=bs.nn.CUBA.desc(scale=1.0), post=self.N)
+        for m in (self.E.syn, self.I.syn, self.N):
+            m.init_state()
+
+    def update(self, t):
+        with self.bs.environ.context(t=t):
+            spk = self.N.get_spike() != 0.
+            self.E(spk[:self.n_exc])
+            self.I(spk[self.n_exc:])
+            self.N(make_golden.CUBA_NET['I_ext'])
+            return self.N.get_spike()
+
+
+def test_cuba_module_network_eager_and_fused(bs):
+    """The reference's CUBA example through the module API: stepped eagerly (200 steps), and
+    a fresh copy handed to the persistent runner with fuse() (500 steps).  Rasters and final
+    states equal the oracle's."""
+    import torch
+    print('[case] module CUBA net eager + fused', flush=True)
+    pe, pi, V0, p = make_golden.cuba_net()
+    ref = network.run_coba_lif(V0, pe, pi, p, make_golden.CUBA_NET['n_exc'], 500)
+    assert ref['counts'].sum() > 100
+    with bs.environ.context(dt=0.1):
+        net = _CUBANet(bs)
+        spikes = bs.transform.for_loop(net.update, torch.arange(200) * 0.1)
+    assert np.array_equal(spikes.cpu().numpy(), ref['raster'][:200])
+    with bs.environ.context(dt=0.1):
+        net = _CUBANet(bs)
+        r = bs.nn.fuse(net.N, net.E, net.I, n_exc=net.n_exc, inp=make_golden.CUBA_NET['I_ext'])
+        raster = torch.zeros(500, net.num, dtype=torch.uint8, device='cuda')
+        r.run(500, raster=raster)
+        r.check()
+        r.write_back()
+    assert np.array_equal(raster.cpu().numpy().astype(bool), ref['raster'])
+    assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+    assert np.array_equal(net.I.syn.g.value.cpu().numpy(), ref['gi'])
+
+
+def test_cuba_and_coba_channels_do_not_mix(bs):
+    with bs.environ.context(dt=0.1):
+        N = bs.nn.LIFRef(10)
+        bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(10, 10, conn_num=2, conn_weight=1.0,
+                                                      seed=1),
+                            syn=bs.nn.Expon.desc(10, tau=5.), out=bs.nn.CUBA.desc(), post=N)
+        with pytest.raises(NotImplementedError):
+            bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(10, 10, conn_num=2, conn_weight=1.0,
+                                                          seed=2),
+                                syn=bs.nn.Expon.desc(10, tau=5.), out=bs.nn.COBA.desc(E=0.),
+                                post=N)
+
 def test_hh_module_step_matches_oracle(bs):
     import torch
     print('[case] HH module', flush=True)

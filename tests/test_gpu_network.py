@@ -152,6 +152,33 @@ def test_coba_lif_4000_raster_bit_exact(torch_cuda, het, chunks):
     assert make_golden.sha(r.state['V'].cpu().numpy()) == gold['final_V_sha256']
 
 
+
+@pytest.mark.parametrize('het', [False, True])
+def test_cuba_lif_4000_raster_bit_exact(torch_cuda, het):
+    """examples/400_CUBA_2005_bpu.py's net (CUBA outputs, signed weights) in the persistent
+    runner: raster, counts and final V equal the oracle's golden run."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    say('cuba lif 4000', het)
+    with open(os.path.join(GOLD, 'cuba_lif_4000.json')) as f:
+        gold = json.load(f)
+    c = make_golden.CUBA_NET
+    pe, pi, V0, _ = make_golden.cuba_net()
+    p = ops.lif_params(V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'], tau=c['tau'],
+                       tau_ref=c['tau_ref'], I_ext=c['I_ext'], out='cuba')
+    r = EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx,
+                    np.full(pe.idx.shape, F(c['w_e'])) if het else c['w_e'],
+                    np.full(pi.idx.shape, F(c['w_i'])) if het else c['w_i'], p, V0)
+    T = c['steps']
+    raster = torch.zeros(T, c['n'], dtype=torch.uint8, device='cuda')
+    counts = torch.zeros(T, dtype=torch.int32, device='cuda')
+    r.run(T, counts=counts, raster=raster)
+    r.check()
+    assert counts.cpu().numpy().tolist() == gold['counts']
+    assert make_golden.sha(np.packbits(raster.cpu().numpy().astype(bool))) == gold['raster_sha256']
+    assert make_golden.sha(r.state['V'].cpu().numpy()) == gold['final_V_sha256']
+
 def test_coba_lif_state_matches_oracle_midway(torch_cuda):
     torch = torch_cuda
     say('coba lif state')

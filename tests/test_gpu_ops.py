@@ -175,6 +175,33 @@ def test_lif_step_bit_exact(torch_cuda):
     assert espk.sum() > 100
 
 
+
+def test_cuba_lif_step_bit_exact(torch_cuda):
+    """bs_coba_lif_step with CUBA output (cuba = 1, signed conductances) equals the oracle."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('cuba lif step')
+    n = 100_003
+    rng = np.random.RandomState(2)
+    V = rng.uniform(-62, -48, n).astype(F)
+    ge = rng.exponential(0.5, n).astype(F)
+    gi = -rng.exponential(2.0, n).astype(F)
+    ref_c = rng.choice([0, 0, 0, 1, 7, 49], n).astype(np.int32)
+    in_e = (rng.rand(n) < 0.1).astype(F) * F(1.62)
+    in_i = (rng.rand(n) < 0.05).astype(F) * F(-9.0)
+    p = neuron.LIFParams(V_rest=-49., V_th=-50., V_reset=-60., tau=20., I_ext=20., out='cuba',
+                         scale_e=1.0, scale_i=0.75)
+    eV, ege, egi, eref, espk = neuron.coba_lif_step(V, ge, gi, ref_c, in_e, in_i, p)
+    tV, tge, tgi, tref = (dev(torch, a) for a in (V, ge, gi, ref_c))
+    spk = ops.coba_lif_step(tV, tge, tgi, tref, dev(torch, in_e), dev(torch, in_i),
+                            ops.lif_params(V_rest=-49., V_th=-50., V_reset=-60., tau=20.,
+                                           I_ext=20., out='cuba', scale_e=1.0, scale_i=0.75))
+    assert np.array_equal(tV.cpu().numpy(), eV)
+    assert np.array_equal(tge.cpu().numpy(), ege) and np.array_equal(tgi.cpu().numpy(), egi)
+    assert np.array_equal(tref.cpu().numpy(), eref)
+    assert np.array_equal(spk.cpu().numpy().astype(bool), espk)
+    assert espk.sum() > 100
+
 def test_lif_reference_kat_on_gpu(torch_cuda):
     """docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cell 5: -59.84079742 mV."""
     torch = torch_cuda

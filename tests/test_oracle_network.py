@@ -42,6 +42,33 @@ def test_lif_refractory_and_reset():
     assert ref[0] == 0
 
 
+def test_cuba_membrane_is_the_exact_linear_solution():
+    """CUBA (brainpy.state CUBA, examples/400_CUBA_2005_bpu.py:42-58): the current does not
+    depend on V, so dV/dt = (V_rest - V + R I) / tau is linear and exp-Euler is its exact
+    solution V' = V_inf + (V - V_inf) exp(-dt / tau), V_inf = V_rest + R I, with
+    I = I_ext + g_e s_e + g_i s_i (signed weights: g_i < 0 lowers I).  A Jacobian that kept
+    a conductance term, or a wrong sign or scale, moves V' by far more than these few ulp."""
+    rng = np.random.RandomState(4)
+    n = 2000
+    p = neuron.LIFParams(V_rest=-49., V_th=-50., V_reset=-60., tau=20., I_ext=20., out='cuba',
+                         scale_e=1.0, scale_i=0.5)
+    V = rng.uniform(-70, -40, n).astype(F)
+    ge = rng.uniform(0, 3, n).astype(F)
+    gi = -rng.uniform(0, 5, n).astype(F)
+    got = neuron.lif_membrane(V, ge, gi, p).astype(np.float64)
+    I = 20.0 + ge.astype(np.float64) * 1.0 + gi.astype(np.float64) * 0.5
+    Vinf = -49.0 + I
+    exact = Vinf + (V.astype(np.float64) - Vinf) * np.exp(-0.1 / 20.0)
+    ulp = np.spacing(np.abs(exact).astype(F)).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 8 * ulp)
+    # zero conductances: CUBA and COBA are the same equation, bit for bit
+    pc = neuron.LIFParams(V_rest=-49., V_th=-50., V_reset=-60., tau=20., I_ext=20.)
+    z = np.zeros(n, F)
+    assert np.array_equal(neuron.lif_membrane(V, z, z, p), neuron.lif_membrane(V, z, z, pc))
+    # and with conductances they differ (the COBA current depends on V)
+    assert not np.allclose(neuron.lif_membrane(V, ge, -gi, pc), got, atol=1e-3)
+
+
 def test_hh_matches_float64_equations():
     """examples/100_hh_neuron_model.py:49-86 in float64 (libm exp) vs the fp32 oracle."""
     V = np.linspace(-90, 50, 2001)
@@ -107,6 +134,18 @@ def test_coba_hh_2000_matches_golden():
     res = network.run_coba_hh(V0, pe, pi, p, make_golden.HH_NET['n_exc'], gold['config']['steps'])
     assert res['counts'].tolist() == gold['counts']
     assert make_golden.sha(res['V']) == gold['final_V_sha256']
+
+
+def test_cuba_lif_4000_matches_golden():
+    """examples/400_CUBA_2005_bpu.py's E/I net (CUBA outputs, signed weights), 1000 steps."""
+    gold = json.load(open(os.path.join(GOLD, 'cuba_lif_4000.json')))
+    pe, pi, V0, p = make_golden.cuba_net()
+    res = network.run_coba_lif(V0, pe, pi, p, make_golden.CUBA_NET['n_exc'],
+                               make_golden.CUBA_NET['steps'])
+    assert res['counts'].tolist() == gold['counts']
+    assert make_golden.sha(np.packbits(res['raster'])) == gold['raster_sha256']
+    assert make_golden.sha(res['V']) == gold['final_V_sha256']
+    assert 0 < sum(gold['counts'])
 
 
 @pytest.mark.parametrize('nthreads', [1, 4])
