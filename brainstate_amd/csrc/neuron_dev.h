@@ -39,7 +39,7 @@ __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, 
   } else {
     spk = Vn >= p.V_th;
     if (spk) {
-      Vn = p.V_reset;
+      Vn = p.soft_reset ? Vn - (p.V_th - p.V_reset) : p.V_reset;
       ref = p.ref_steps;
     } else {
       ref = 0;

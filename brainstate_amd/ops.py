@@ -468,18 +468,22 @@ def conn_fixed_num_unique(seed, n_pre, k, n_post, device=None):
 
 def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., I_ext=20.,
                E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba', scale_e=1.,
-               scale_i=1.):
+               scale_i=1., spk_reset='hard'):
     """bs_lif_params.  ``out='coba'``: synaptic current g * (E - V); ``out='cuba'``: g * scale
-    (brainpy.state CUBA; E_e / E_i unused)."""
+    (brainpy.state CUBA; E_e / E_i unused).  ``spk_reset='soft'``: a spike subtracts
+    V_th - V_reset from V instead of setting V_reset."""
     if out not in ('coba', 'cuba'):
         raise ValueError(f"out must be 'coba' or 'cuba', got {out!r}")
+    if spk_reset not in ('hard', 'soft'):
+        raise ValueError(f"spk_reset must be 'hard' or 'soft', got {spk_reset!r}")
     q = float(tau_ref) / float(dt)
     ref_steps = max(int(np.ceil(q - 1e-9)) - 1, 0)
     inv_tau = float(np.float32(1.0) / np.float32(tau))   # fp32 reciprocal of the constant
     return N.LifParams(V_rest, V_th, V_reset, inv_tau, R, I_ext, E_e, E_i, dt,
                        float(np.float32(np.exp(-dt / tau_e))),
                        float(np.float32(np.exp(-dt / tau_i))), ref_steps,
-                       1 if out == 'cuba' else 0, scale_e, scale_i)
+                       1 if out == 'cuba' else 0, scale_e, scale_i,
+                       1 if spk_reset == 'soft' else 0)
 
 
 def hh_params(ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03, C=1.0, V_th=20.,

@@ -246,6 +246,10 @@ typedef struct {
    * multiply-add each), J = -inv_tau; E_e / E_i are then unused.  cuba == 0: COBA as above. */
   int32_t cuba;
   float scale_e, scale_i;
+  /* soft_reset != 0 (brainpy.state LIF spk_reset='soft', used by
+   * docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cells 5, 11): a spike subtracts
+   * (V_th - V_reset) from V' instead of setting V' = V_reset. */
+  int32_t soft_reset;
 } bs_lif_params;
 
 BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,

@@ -62,12 +62,15 @@ def ref_steps(tau_ref, dt):
 
 class LIFParams:
     """``out='cuba'``: current-based synaptic output I += g * scale (brainpy.state CUBA, used
-    by examples/400_CUBA_2005_bpu.py:42-58) instead of g * (E - V)."""
+    by examples/400_CUBA_2005_bpu.py:42-58) instead of g * (E - V).  ``spk_reset='soft'``
+    (docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cells 5, 11): a spike subtracts
+    V_th - V_reset from V' instead of setting V_reset."""
 
     def __init__(self, V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5.,
                  I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba',
-                 scale_e=1., scale_i=1.):
+                 scale_e=1., scale_i=1., spk_reset='hard'):
         self.cuba = out == 'cuba'
+        self.soft_reset = spk_reset == 'soft'
         self.scale_e, self.scale_i = F(scale_e), F(scale_i)
         self.V_rest, self.V_th, self.V_reset = F(V_rest), F(V_th), F(V_reset)
         self.tau, self.R, self.I_ext = F(tau), F(R), F(I_ext)
@@ -104,7 +107,10 @@ def coba_lif_step(V, ge, gi, ref, in_e, in_i, p):
     refr = ref > 0
     Vn = np.where(refr, V, Vn).astype(F)
     spk = (~refr) & (Vn >= p.V_th)
-    Vn = np.where(spk, p.V_reset, Vn).astype(F)
+    if getattr(p, 'soft_reset', False):   # subtractive reset: V' - (V_th - V_reset)
+        Vn = np.where(spk, (Vn - (p.V_th - p.V_reset).astype(F)).astype(F), Vn).astype(F)
+    else:
+        Vn = np.where(spk, p.V_reset, Vn).astype(F)
     ref = np.where(spk, p.ref_steps, np.where(refr, ref - 1, 0)).astype(I32)
     return Vn, ge, gi, ref, spk
 

@@ -8,6 +8,7 @@
 * coba_lif_4000.json -- config [1]: 4000-neuron COBA E/I net, 1000 steps; per-step spike
   counts, per-step order-free spike digests and SHA-256 of the raster / final state.
 * cuba_lif_4000.json -- examples/400_CUBA_2005_bpu.py's CUBA E/I net, 1000 steps, same records.
+* tut_lif_soft_500.json -- the SNN tutorial's E/I net (LIF, soft reset, CUBA), 2000 steps.
 * coba_hh_2000.json -- a 2000-neuron COBA-HH net, 600 steps, same records.
 The reference itself is not imported (it needs JAX, brainevent and brainunit, which are
 absent); these fixtures freeze the oracle so that any drift in it is caught.
@@ -30,6 +31,13 @@ CONFIG1 = dict(n=4000, n_exc=3200, p=0.02, w_e=0.6, w_i=6.7, seed_e=1, seed_i=2,
 CUBA_NET = dict(n=4000, n_exc=3200, p=0.02, w_e=1.62, w_i=-9.0, seed_e=21, seed_i=22,
                 seed_v=23, steps=1000, V_rest=-49., V_th=-50., V_reset=-60., tau=20.,
                 tau_ref=5., I_ext=20.)
+# docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cells 11-14: LIF (no refractory
+# period, soft reset) with CUBA outputs, balanced weights +-1/sqrt(p N), input 3 (V0 drawn
+# with numpy)
+TUT_NET = dict(n=500, n_exc=400, p=0.1, w_e=float(np.float32(1.0 / np.sqrt(40.0))),
+               w_i=float(np.float32(-1.0 / np.sqrt(10.0))), seed_e=31, seed_i=32, seed_v=33,
+               steps=2000, V_rest=-52., V_th=-50., V_reset=-60., tau=10., tau_e=2., tau_i=2.,
+               I_ext=3.)
 HH_NET = dict(n=2000, n_exc=1600, k=80, w_e=0.05, w_i=0.3, seed_e=11, seed_i=12, seed_v=13,
               steps=600, I_ext=6.5)
 
@@ -53,6 +61,17 @@ def cuba_net():
     V0 = np.random.RandomState(c['seed_v']).normal(-55., 2., c['n']).astype(np.float32)
     p = neuron.LIFParams(V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'],
                          tau=c['tau'], tau_ref=c['tau_ref'], I_ext=c['I_ext'], out='cuba')
+    return pe, pi, V0, p
+
+
+def tut_net():
+    c = TUT_NET
+    pe = network.Projection(0, c['n_exc'], c['n'], c['p'], c['w_e'], seed=c['seed_e'])
+    pi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=c['seed_i'])
+    V0 = np.random.RandomState(c['seed_v']).normal(-60., 10., c['n']).astype(np.float32)
+    p = neuron.LIFParams(V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'],
+                         tau=c['tau'], tau_ref=0., tau_e=c['tau_e'], tau_i=c['tau_i'],
+                         I_ext=c['I_ext'], out='cuba', spk_reset='soft')
     return pe, pi, V0, p
 
 
@@ -93,6 +112,13 @@ def main():
     with open(os.path.join(HERE, 'cuba_lif_4000.json'), 'w') as f:
         json.dump(rec, f)
     print('cuba_lif_4000: total spikes', int(res['counts'].sum()))
+
+    pe, pi, V0, p = tut_net()
+    res = network.run_coba_lif(V0, pe, pi, p, TUT_NET['n_exc'], TUT_NET['steps'])
+    rec = dict(config=TUT_NET, **run_records(res))
+    with open(os.path.join(HERE, 'tut_lif_soft_500.json'), 'w') as f:
+        json.dump(rec, f)
+    print('tut_lif_soft_500: total spikes', int(res['counts'].sum()))
 
     pe, pi, V0, p = hh_net()
     res = network.run_coba_hh(V0, pe, pi, p, HH_NET['n_exc'], HH_NET['steps'])

@@ -239,6 +239,52 @@ def test_cuba_module_network_eager_and_fused(bs):
     assert np.array_equal(net.I.syn.g.value.cpu().numpy(), ref['gi'])
 
 
+def test_tutorial_network_modules_soft_reset(bs):
+    """docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cells 11-14 through the module
+    API: LIF(spk_reset='soft') with Expon + CUBA projections, stepped eagerly (300 steps) and
+    fused (the whole 2000 steps); both equal the oracle."""
+    import torch
+    print('[case] tutorial net modules', flush=True)
+    c = make_golden.TUT_NET
+    pe, pi, V0, p = make_golden.tut_net()
+    ref = network.run_coba_lif(V0, pe, pi, p, c['n_exc'], c['steps'])
+
+    def build():
+        N = bs.nn.LIF(c['n'], V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'],
+                      tau=c['tau'], V_initializer=lambda s: V0, spk_reset='soft')
+        E = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n_exc'], c['n'], c['p'], c['w_e'], seed=c['seed_e']),
+            syn=bs.nn.Expon.desc(c['n'], tau=c['tau_e']), out=bs.nn.CUBA.desc(), post=N)
+        I = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n'] - c['n_exc'], c['n'], c['p'], c['w_i'],
+                                      seed=c['seed_i']),
+            syn=bs.nn.Expon.desc(c['n'], tau=c['tau_i']), out=bs.nn.CUBA.desc(), post=N)
+        for m in (E.syn, I.syn, N):
+            m.init_state()
+        return N, E, I
+
+    with bs.environ.context(dt=0.1):
+        N, E, I = build()
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            E(spk[:c['n_exc']])
+            I(spk[c['n_exc']:])
+            return N(c['I_ext'])
+
+        spikes = bs.transform.for_loop(step, torch.arange(300) * 0.1)
+    assert np.array_equal(spikes.cpu().numpy(), ref['raster'][:300])
+    with bs.environ.context(dt=0.1):
+        N, E, I = build()
+        r = bs.nn.fuse(N, E, I, n_exc=c['n_exc'], inp=c['I_ext'])
+        raster = torch.zeros(c['steps'], c['n'], dtype=torch.uint8, device='cuda')
+        r.run(c['steps'], raster=raster)
+        r.check()
+        r.write_back()
+    assert np.array_equal(raster.cpu().numpy().astype(bool), ref['raster'])
+    assert np.array_equal(N.V.value.cpu().numpy(), ref['V'])
+
+
 def test_cuba_and_coba_channels_do_not_mix(bs):
     with bs.environ.context(dt=0.1):
         N = bs.nn.LIFRef(10)

@@ -179,6 +179,29 @@ def test_cuba_lif_4000_raster_bit_exact(torch_cuda, het):
     assert make_golden.sha(np.packbits(raster.cpu().numpy().astype(bool))) == gold['raster_sha256']
     assert make_golden.sha(r.state['V'].cpu().numpy()) == gold['final_V_sha256']
 
+
+def test_tutorial_soft_reset_net_in_runner(torch_cuda):
+    """04_building_an_snn.ipynb's E/I net (LIF without refractory period, soft reset, CUBA)
+    in the persistent runner: counts and final V equal the oracle's golden run."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    say('tutorial soft-reset net')
+    with open(os.path.join(GOLD, 'tut_lif_soft_500.json')) as f:
+        gold = json.load(f)
+    c = make_golden.TUT_NET
+    pe, pi, V0, _ = make_golden.tut_net()
+    p = ops.lif_params(V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'], tau=c['tau'],
+                       tau_ref=0., tau_e=c['tau_e'], tau_i=c['tau_i'], I_ext=c['I_ext'],
+                       out='cuba', spk_reset='soft')
+    r = EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx, c['w_e'], c['w_i'], p, V0)
+    counts = torch.zeros(c['steps'], dtype=torch.int32, device='cuda')
+    r.run(c['steps'], counts=counts)
+    r.check()
+    assert counts.cpu().numpy().tolist() == gold['counts']
+    assert make_golden.sha(r.state['V'].cpu().numpy()) == gold['final_V_sha256']
+
+
 def test_coba_lif_state_matches_oracle_midway(torch_cuda):
     torch = torch_cuda
     say('coba lif state')

@@ -176,11 +176,13 @@ def test_lif_step_bit_exact(torch_cuda):
 
 
 
-def test_cuba_lif_step_bit_exact(torch_cuda):
-    """bs_coba_lif_step with CUBA output (cuba = 1, signed conductances) equals the oracle."""
+@pytest.mark.parametrize('reset', ['hard', 'soft'])
+def test_cuba_lif_step_bit_exact(torch_cuda, reset):
+    """bs_coba_lif_step with CUBA output (cuba = 1, signed conductances), hard or soft reset,
+    equals the oracle."""
     torch = torch_cuda
     from brainstate_amd import ops
-    say('cuba lif step')
+    say('cuba lif step', reset)
     n = 100_003
     rng = np.random.RandomState(2)
     V = rng.uniform(-62, -48, n).astype(F)
@@ -190,12 +192,13 @@ def test_cuba_lif_step_bit_exact(torch_cuda):
     in_e = (rng.rand(n) < 0.1).astype(F) * F(1.62)
     in_i = (rng.rand(n) < 0.05).astype(F) * F(-9.0)
     p = neuron.LIFParams(V_rest=-49., V_th=-50., V_reset=-60., tau=20., I_ext=20., out='cuba',
-                         scale_e=1.0, scale_i=0.75)
+                         scale_e=1.0, scale_i=0.75, spk_reset=reset)
     eV, ege, egi, eref, espk = neuron.coba_lif_step(V, ge, gi, ref_c, in_e, in_i, p)
     tV, tge, tgi, tref = (dev(torch, a) for a in (V, ge, gi, ref_c))
     spk = ops.coba_lif_step(tV, tge, tgi, tref, dev(torch, in_e), dev(torch, in_i),
                             ops.lif_params(V_rest=-49., V_th=-50., V_reset=-60., tau=20.,
-                                           I_ext=20., out='cuba', scale_e=1.0, scale_i=0.75))
+                                           I_ext=20., out='cuba', scale_e=1.0, scale_i=0.75,
+                                           spk_reset=reset))
     assert np.array_equal(tV.cpu().numpy(), eV)
     assert np.array_equal(tge.cpu().numpy(), ege) and np.array_equal(tgi.cpu().numpy(), egi)
     assert np.array_equal(tref.cpu().numpy(), eref)

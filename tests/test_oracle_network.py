@@ -69,6 +69,36 @@ def test_cuba_membrane_is_the_exact_linear_solution():
     assert not np.allclose(neuron.lif_membrane(V, ge, -gi, pc), got, atol=1e-3)
 
 
+def test_soft_reset_subtracts_the_threshold_gap():
+    """spk_reset='soft' (04_building_an_snn.ipynb cells 5, 11): a spiking neuron keeps its
+    overshoot, V = V' - (V_th - V_reset); hard reset sets V_reset; below threshold both are
+    the plain membrane step."""
+    p_s = neuron.LIFParams(V_rest=-52., V_th=-50., V_reset=-60., tau=10., tau_ref=0.,
+                           I_ext=30., out='cuba', spk_reset='soft')
+    p_h = neuron.LIFParams(V_rest=-52., V_th=-50., V_reset=-60., tau=10., tau_ref=0.,
+                           I_ext=30., out='cuba')
+    V = np.array([-50.5, -49.0, -58.0, -45.0], F)
+    z = np.zeros(4, F)
+    r0 = np.zeros(4, np.int32)
+    Vm = neuron.lif_membrane(V, z, z, p_s)
+    Vs, _, _, rs, ss = neuron.coba_lif_step(V, z, z, r0, z, z, p_s)
+    Vh, _, _, rh, sh = neuron.coba_lif_step(V, z, z, r0, z, z, p_h)
+    assert np.array_equal(ss, Vm >= F(-50.)) and np.array_equal(ss, sh) and ss.sum() >= 2
+    assert np.array_equal(Vs[ss], (Vm[ss] - F(10.)).astype(F))
+    assert np.all(Vh[sh] == F(-60.)) and np.array_equal(Vs[~ss], Vm[~ss])
+    assert np.all(rs == 0) and np.all(rh == 0)   # no refractory period (tau_ref = 0)
+
+
+def test_tutorial_soft_reset_net_matches_golden():
+    gold = json.load(open(os.path.join(GOLD, 'tut_lif_soft_500.json')))
+    pe, pi, V0, p = make_golden.tut_net()
+    res = network.run_coba_lif(V0, pe, pi, p, make_golden.TUT_NET['n_exc'],
+                               make_golden.TUT_NET['steps'])
+    assert res['counts'].tolist() == gold['counts']
+    assert make_golden.sha(res['V']) == gold['final_V_sha256']
+    assert 0 < sum(gold['counts'])
+
+
 def test_hh_matches_float64_equations():
     """examples/100_hh_neuron_model.py:49-86 in float64 (libm exp) vs the fp32 oracle."""
     V = np.linspace(-90, 50, 2001)
