@@ -380,8 +380,7 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
       float V = sV[r], ge = sge[r], gi = sgi[r];
       int32_t rf = sref[r];
       const float in_e = lif.inh ? 0.0f : v, in_i = lif.inh ? v : 0.0f;
-      const bool sp = lif.p.cuba ? bs_lif_update<true>(lif.p, V, ge, gi, rf, in_e, in_i)
-                                 : bs_lif_update<false>(lif.p, V, ge, gi, rf, in_e, in_i);
+      const bool sp = bs_lif_update_p(lif.p, V, ge, gi, rf, in_e, in_i);
       lif.V[o] = V;
       lif.ge[o] = ge;
       lif.gi[o] = gi;

@@ -110,7 +110,7 @@ struct NetArgs {
 
 // ---- neuron models: register-resident state, one fused update per neuron-step ----
 
-template <bool kCuba>
+template <bool kCuba, bool kSoft>
 struct LifModel {
   using Params = bs_lif_params;
   using State = bs_lif_state;
@@ -130,7 +130,7 @@ struct LifModel {
   static constexpr bool kPrepare = false;  // every operation of the step needs the input
   __device__ static void prepare(const Params&, Regs&) {}
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
-    return bs_lif_update<kCuba>(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
+    return bs_lif_update<kCuba, kSoft>(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
   }
   // Whether the neuron may spike this step: a zero-input forward-Euler estimate of the next
   // V within 15 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
@@ -829,11 +829,14 @@ extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const 
     BS_CHECK_ARG(st->V && st->ge && st->gi && st->ref, "bs_coba_lif_run: NULL state pointer");
   }
   if (p) BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_run: inv_tau is NaN");
-  if (p && p->cuba)
-    return run<LifModel<true>>(net, st, p, t0, steps, counts_out, hash_out, raster_out,
-                               workspace, stream, "bs_coba_lif_run");
-  return run<LifModel<false>>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
-                              stream, "bs_coba_lif_run");
+#define BS_RUN(C, S)                                                                    \
+  return run<LifModel<C, S>>(net, st, p, t0, steps, counts_out, hash_out, raster_out,      \
+                             workspace, stream, "bs_coba_lif_run")
+  const bool cuba = p && p->cuba, soft = p && p->soft_reset;
+  if (cuba) { if (soft) BS_RUN(true, true); else BS_RUN(true, false); }
+  if (soft) BS_RUN(false, true);
+  BS_RUN(false, false);
+#undef BS_RUN
 }
 
 extern "C" int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,

@@ -9,7 +9,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
-template <bool kCuba>
+template <bool kCuba, bool kSoft>
 __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restrict__ V,
                                                      float* __restrict__ ge,
                                                      float* __restrict__ gi,
@@ -23,7 +23,7 @@ __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restric
     float v = V[j], e = ge[j], i = gi[j];
     int32_t r = ref[j];
     const bool s =
-        bs_lif_update<kCuba>(p, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
+        bs_lif_update<kCuba, kSoft>(p, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
     V[j] = v;
     ge[j] = e;
     gi[j] = i;
@@ -84,12 +84,12 @@ extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32
   BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_step: inv_tau is NaN");
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
-  if (p->cuba)
-    k_lif_step<true><<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i,
-                                                               *p, spk_out);
-  else
-    k_lif_step<false><<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, ge, gi, ref, in_e, in_i,
-                                                                *p, spk_out);
+  hipStream_t s = bs_stream(stream);
+#define BS_LIF(C, S) \
+  k_lif_step<C, S><<<grid(n), kBlock, 0, s>>>(n, V, ge, gi, ref, in_e, in_i, *p, spk_out)
+  if (p->cuba) { if (p->soft_reset) BS_LIF(true, true); else BS_LIF(true, false); }
+  else { if (p->soft_reset) BS_LIF(false, true); else BS_LIF(false, false); }
+#undef BS_LIF
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

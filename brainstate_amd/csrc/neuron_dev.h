@@ -13,8 +13,10 @@
 
 // brainpy.state Expon + COBA (kCuba: CUBA) + LIFRef for one neuron; see bs_lif_params in the
 // header.  Returns the spike; updates V, ge, gi, ref in place.  The CUBA current does not
-// depend on V, so the exp-Euler Jacobian is -1 * inv_tau.
-template <bool kCuba = false>
+// depend on V, so the exp-Euler Jacobian is -1 * inv_tau.  kSoft: a spike subtracts
+// V_th - V_reset from V' (p.soft_reset) instead of setting V_reset.  Both are compile-time
+// choices so that the persistent runner's update carries no per-neuron selects.
+template <bool kCuba = false, bool kSoft = false>
 __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, float& ge,
                                               float& gi, int32_t& ref, float in_e, float in_i) {
   ge = bs_fma(ge, p.decay_e, in_e);
@@ -39,7 +41,7 @@ __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, 
   } else {
     spk = Vn >= p.V_th;
     if (spk) {
-      Vn = p.soft_reset ? Vn - (p.V_th - p.V_reset) : p.V_reset;
+      Vn = kSoft ? Vn - (p.V_th - p.V_reset) : p.V_reset;
       ref = p.ref_steps;
     } else {
       ref = 0;
@@ -47,6 +49,17 @@ __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, 
   }
   V = Vn;
   return spk;
+}
+
+// bs_lif_update with the output kind and reset taken from p at run time (uniform branch).
+__device__ __forceinline__ bool bs_lif_update_p(const bs_lif_params& p, float& V, float& ge,
+                                                float& gi, int32_t& ref, float in_e,
+                                                float in_i) {
+  if (p.cuba)
+    return p.soft_reset ? bs_lif_update<true, true>(p, V, ge, gi, ref, in_e, in_i)
+                        : bs_lif_update<true, false>(p, V, ge, gi, ref, in_e, in_i);
+  return p.soft_reset ? bs_lif_update<false, true>(p, V, ge, gi, ref, in_e, in_i)
+                      : bs_lif_update<false, false>(p, V, ge, gi, ref, in_e, in_i);
 }
 
 struct bs_hh_rates {
