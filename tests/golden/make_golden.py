@@ -10,6 +10,10 @@
 * cuba_lif_4000.json -- examples/400_CUBA_2005_bpu.py's CUBA E/I net, 1000 steps, same records.
 * tut_lif_soft_500.json -- the SNN tutorial's E/I net (LIF, soft reset, CUBA), 2000 steps.
 * coba_hh_2000.json -- a 2000-neuron COBA-HH net, 600 steps, same records.
+* hh_single_trace.json -- examples/100_hh_neuron_model.py's neuron (dt 0.01 ms, 10,000 steps,
+  random input per step): SHA-256 of the V trace, its spike steps, V every 1000 steps.
+* matvec_2000.json -- config [2] at 2000 x 2000, K = 100: SHA-256 of the homogeneous sums
+  (order-free), of the sequential per-synapse sums and of the fixed-point sums, per density.
 The reference itself is not imported (it needs JAX, brainevent and brainunit, which are
 absent); these fixtures freeze the oracle so that any drift in it is caught.
 """
@@ -23,7 +27,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
-from oracle import conn, neuron, network  # noqa: E402
+from oracle import conn, event, neuron, network  # noqa: E402
 
 CONFIG1 = dict(n=4000, n_exc=3200, p=0.02, w_e=0.6, w_i=6.7, seed_e=1, seed_i=2, seed_v=3,
                steps=1000)
@@ -38,6 +42,12 @@ TUT_NET = dict(n=500, n_exc=400, p=0.1, w_e=float(np.float32(1.0 / np.sqrt(40.0)
                w_i=float(np.float32(-1.0 / np.sqrt(10.0))), seed_e=31, seed_i=32, seed_v=33,
                steps=2000, V_rest=-52., V_th=-50., V_reset=-60., tau=10., tau_e=2., tau_i=2.,
                I_ext=3.)
+# examples/100_hh_neuron_model.py:96-112: 10 HH neurons, dt = 0.01 ms, 100 ms, input
+# uniform(1, 10) per step (drawn with numpy)
+HH_SINGLE = dict(n=10, dt=0.01, steps=10000, seed_in=7, V0=-65.)
+# config [2] at reduced size: 2000 x 2000, K = 100, w ~ N(0.5, 0.1), spikes at three densities
+MATVEC = dict(n_pre=2000, n_post=2000, k=100, seed_idx=41, seed_w=42, seed_spk=43,
+              p=[0.001, 0.01, 0.1], w_homo=0.6)
 HH_NET = dict(n=2000, n_exc=1600, k=80, w_e=0.05, w_i=0.3, seed_e=11, seed_i=12, seed_v=13,
               steps=600, I_ext=6.5)
 
@@ -83,6 +93,35 @@ def hh_net():
     return pe, pi, V0, neuron.HHParams(I_ext=c['I_ext'])
 
 
+def hh_single_trace():
+    """V of neuron 0 after every step, and the steps at which it spikes."""
+    c = HH_SINGLE
+    inp = np.random.RandomState(c['seed_in']).uniform(1., 10., c['steps']).astype(np.float32)
+    V = np.full(c['n'], c['V0'], np.float32)
+    m, h, ng = neuron.hh_init(V)
+    z = np.zeros(c['n'], np.float32)
+    ge, gi = z.copy(), z.copy()
+    trace = np.zeros(c['steps'], np.float32)
+    spikes = []
+    for t in range(c['steps']):
+        p = neuron.HHParams(I_ext=float(inp[t]), dt=c['dt'])
+        V, m, h, ng, ge, gi, spk = neuron.hh_step(V, m, h, ng, ge, gi, z, z, p)
+        trace[t] = V[0]
+        if spk[0]:
+            spikes.append(t)
+    return inp, trace, spikes
+
+
+def matvec_case(p_spk):
+    """(spk, idx, w) of the reduced config-[2] mat-vec at spike density p_spk."""
+    c = MATVEC
+    idx = np.random.RandomState(c['seed_idx']).randint(0, c['n_post'], (c['n_pre'], c['k']))
+    w = np.random.RandomState(c['seed_w']).normal(0.5, 0.1, idx.shape).astype(np.float32)
+    rs = np.random.RandomState(c['seed_spk'] + int(round(p_spk * 1000)))
+    spk = (rs.rand(c['n_pre']) < p_spk).astype(np.uint8)
+    return spk, idx.astype(np.int32), w
+
+
 def run_records(res):
     return dict(counts=res['counts'].tolist(),
                 hashes=[network.spike_hash(r) for r in res['raster']],
@@ -119,6 +158,28 @@ def main():
     with open(os.path.join(HERE, 'tut_lif_soft_500.json'), 'w') as f:
         json.dump(rec, f)
     print('tut_lif_soft_500: total spikes', int(res['counts'].sum()))
+
+    inp, trace, spikes = hh_single_trace()
+    rec = dict(config=HH_SINGLE, trace_sha256=sha(trace), spikes=spikes,
+               V_every_1000=[float(v) for v in trace[999::1000]])
+    with open(os.path.join(HERE, 'hh_single_trace.json'), 'w') as f:
+        json.dump(rec, f)
+    print('hh_single_trace: spikes', len(spikes))
+
+    cases = []
+    for p_spk in MATVEC['p']:
+        spk, idx, w = matvec_case(p_spk)
+        homo = event.scatter_fixed(spk, idx, np.float32(MATVEC['w_homo']), MATVEC['n_post'])
+        het = event.scatter_fixed(spk, idx, w, MATVEC['n_post'])
+        S = event.bucket_qexp(w, idx.size)
+        indptr = np.arange(MATVEC['n_pre'] + 1, dtype=np.int64) * MATVEC['k']
+        fixed = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, MATVEC['n_post'], S)
+        cases.append(dict(p=p_spk, active=int(spk.sum()), homo_sha256=sha(homo),
+                          het_sequential_sha256=sha(het), fixed_point_S=S,
+                          fixed_point_sha256=sha(fixed)))
+    with open(os.path.join(HERE, 'matvec_2000.json'), 'w') as f:
+        json.dump(dict(config=MATVEC, cases=cases), f, indent=1)
+    print('matvec_2000:', [c['active'] for c in cases])
 
     pe, pi, V0, p = hh_net()
     res = network.run_coba_hh(V0, pe, pi, p, HH_NET['n_exc'], HH_NET['steps'])

@@ -319,6 +319,30 @@ def test_hh_module_step_matches_oracle(bs):
     assert np.array_equal(hh.V.value.cpu().numpy(), V)
 
 
+def test_hh_single_neuron_trace_matches_fixture(bs):
+    """examples/100_hh_neuron_model.py through the module API: 10 HH neurons, dt = 0.01 ms,
+    10,000 steps of random input; the V trace and spike steps equal the committed fixture."""
+    import hashlib
+    import json
+    import os
+    import torch
+    print('[case] HH single-neuron trace', flush=True)
+    gold = json.load(open(os.path.join(GOLD, 'hh_single_trace.json')))
+    c = gold['config']
+    inp = np.random.RandomState(c['seed_in']).uniform(1., 10., c['steps']).astype(F)
+    Vs, spk = [], []
+    with bs.environ.context(dt=c['dt']):
+        hh = bs.nn.HH(c['n'], V_initializer=c['V0'])
+        hh.init_state()
+        for t in range(c['steps']):
+            spk.append(hh(float(inp[t]))[0].clone())
+            Vs.append(hh.V.value[0].clone())   # the state tensor is updated in place
+    trace = torch.stack(Vs).cpu().numpy()
+    assert hashlib.sha256(trace.tobytes()).hexdigest() == gold['trace_sha256']
+    assert np.flatnonzero(torch.stack(spk).cpu().numpy()).tolist() == gold['spikes']
+    assert [float(v) for v in trace[999::1000]] == gold['V_every_1000']
+
+
 @pytest.mark.parametrize('het,ratio', [(True, 1.0), (False, 1.0), (True, 0.6)])
 def test_event_fixed_prob_bucketed_path(bs, het, ratio):
     """event_kernel='auto' on a wide output (> 16,384 posts) runs the bucketed operator; it

@@ -191,3 +191,34 @@ def test_bucket_config2_full_size_properties(torch_cuda):
     assert np.isclose(got.sum(), mass, rtol=1e-5)
     ref = ops.event_matvec(d_spk, d_idx, d_w, n).cpu().numpy()
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-4)
+
+
+def test_matvec_2000_fixture_on_every_path(torch_cuda):
+    """The committed reduced config-[2] digests: the bucketed path gives the fixed-point sums,
+    the SELL gather the sequential per-synapse sums, and every path the homogeneous sums."""
+    import hashlib
+    import json
+    import os
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('matvec 2000 fixture')
+    gdir = os.path.join(os.path.dirname(__file__), 'golden')
+    sys.path.insert(0, gdir)
+    import make_golden
+    gold = json.load(open(os.path.join(gdir, 'matvec_2000.json')))
+    c = gold['config']
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    spk, idx, w = make_golden.matvec_case(c['p'][0])
+    d_idx, d_w = dev(torch, idx), dev(torch, w)
+    L = ops.build_buckets(d_idx, c['n_post'], w=d_w)
+    Lh = ops.build_buckets(d_idx, c['n_post'], w=None, w_homo=c['w_homo'])
+    indptr = np.arange(c['n_pre'] + 1, dtype=np.int64) * c['k']
+    sell = ops.build_sell(indptr, idx.reshape(-1), c['n_pre'], c['n_post'], w=w.reshape(-1))
+    for case in gold['cases']:
+        spk, _, _ = make_golden.matvec_case(case['p'])
+        d_spk = dev(torch, spk)
+        assert sha(ops.event_bucket(d_spk, L).cpu().numpy()) == case['fixed_point_sha256']
+        assert sha(ops.event_bucket(d_spk, Lh).cpu().numpy()) == case['homo_sha256']
+        assert sha(ops.event_matvec(d_spk, d_idx, c['w_homo'], c['n_post']).cpu().numpy()) \
+            == case['homo_sha256']
+        assert sha(ops.event_gather(d_spk, sell).cpu().numpy()) == case['het_sequential_sha256']

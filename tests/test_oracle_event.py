@@ -346,3 +346,29 @@ def test_dense_vjp_adjoint_identity():
     v, U = rs.randn(3, 7), rs.randn(7, 5)
     assert np.isclose(np.sum(g * (v @ W)), np.sum(gx * v))
     assert np.isclose(np.sum(g * (x @ U)), np.sum(gW * U))
+
+
+def test_matvec_2000_matches_golden():
+    """Config [2] at reduced size: the committed digests of the homogeneous, sequential
+    per-synapse and fixed-point sums are what the oracle computes."""
+    import hashlib
+    import json
+    import os
+    import sys
+    gdir = os.path.join(os.path.dirname(__file__), 'golden')
+    sys.path.insert(0, gdir)
+    import make_golden
+    gold = json.load(open(os.path.join(gdir, 'matvec_2000.json')))
+    c = gold['config']
+    sha = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    for case in gold['cases']:
+        spk, idx, w = make_golden.matvec_case(case['p'])
+        assert int(spk.sum()) == case['active']
+        assert sha(event.scatter_fixed(spk, idx, F(c['w_homo']), c['n_post'])) == \
+            case['homo_sha256']
+        assert sha(event.scatter_fixed(spk, idx, w, c['n_post'])) == case['het_sequential_sha256']
+        S = event.bucket_qexp(w, idx.size)
+        indptr = np.arange(c['n_pre'] + 1, dtype=np.int64) * c['k']
+        assert S == case['fixed_point_S']
+        assert sha(event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, c['n_post'], S)) \
+            == case['fixed_point_sha256']

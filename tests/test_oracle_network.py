@@ -178,6 +178,14 @@ def test_cuba_lif_4000_matches_golden():
     assert 0 < sum(gold['counts'])
 
 
+def test_hh_single_trace_matches_golden():
+    """examples/100_hh_neuron_model.py's neuron over 10,000 steps of random input."""
+    gold = json.load(open(os.path.join(GOLD, 'hh_single_trace.json')))
+    _, trace, spikes = make_golden.hh_single_trace()
+    assert make_golden.sha(trace) == gold['trace_sha256'] and spikes == gold['spikes']
+    assert len(spikes) > 0
+
+
 @pytest.mark.parametrize('nthreads', [1, 4])
 def test_c_restatement_equals_numpy_oracle(nthreads):
     with open(os.path.join(GOLD, 'coba_lif_4000.json')) as f:
