@@ -29,7 +29,8 @@
 // digits.
 //
 // Forward tiling: a workgroup owns one column tile of 16 columns and 64 batch rows (4 MFMA
-// row tiles); its 4 waves split the input blocks into 4 consecutive ranges and stream their
+// row tiles; tiles ordered so that neighbours share an XCD); its 4 waves split the input
+// blocks into 4 consecutive ranges and stream their
 // digit blocks (16 bytes per lane per digit, 1 KiB per wave-load) with the next group of
 // blocks in flight while the current one is multiplied.  The waves' int64 sums meet in LDS
 // and wave w rounds and stores row tile w.
@@ -249,7 +250,13 @@ __global__ __launch_bounds__(kPB) void k_event_dense_packed(
   __shared__ int64_t s_sum[kPW][kRowTiles][4][BS_WAVE];  // 8 KiB per wave
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int64_t t = blockIdx.x;
+  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin; consecutive tiles
+  // share an XCD (and its L2), so the two 64-byte halves of each 128-byte line of the
+  // outputs and neuron state meet in one L2 (fused step 19.2 -> 18.5 us at config [4])
+  const int64_t nt = gridDim.x, per = (nt + 7) / 8;
+  const int64_t bx = blockIdx.x, xcd = bx % 8, slot = bx / 8;
+  const int64_t full = nt % 8 == 0 ? 8 : nt % 8;  // XCDs that hold `per` tiles
+  const int64_t t = xcd < full ? xcd * per + slot : full * per + (xcd - full) * (per - 1) + slot;
   const int32_t b0 = (int32_t)blockIdx.y * kGroupB;
   const int32_t k_lo = (int32_t)((int64_t)KB * wid / kPW);
   const int32_t k_hi = (int32_t)((int64_t)KB * (wid + 1) / kPW);
