@@ -53,43 +53,52 @@ def load_traffic():
     return None
 
 
-def cpu_baseline(idx_e, idx_i, V0, n_exc, k, budget_s):
-    """C/OpenMP restatement on the host cores; warm 200 steps, then time >= budget_s."""
-    from oracle import cbuild, neuron
-    n = V0.size
-    F = np.float32
-    p = neuron.LIFParams()
-    we = np.full(idx_e.shape, F(0.6))
-    wi = np.full(idx_i.shape, F(6.7))
-    st = dict(V=V0.copy(), ge=np.zeros(n, F), gi=np.zeros(n, F), ref=np.zeros(n, np.int32),
-              spk=np.zeros(n, np.uint8), in_e=np.zeros(n, F), in_i=np.zeros(n, F))
-    threads = min(16, os.cpu_count() or 1)
-    cbuild.coba_lif_run(st, idx_e, idx_i, we, wi, p, n_exc, 200, nthreads=threads)
-    chunk = 100
-    total_spk = 0
-    steps = 0
-    t0 = time.perf_counter()
-    while True:
-        total_spk += cbuild.coba_lif_run(st, idx_e, idx_i, we, wi, p, n_exc, chunk,
-                                         nthreads=threads)
-        steps += chunk
-        el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 20000:
-            break
-    cpu = 'unknown'
+def _cpu_model():
     try:
         with open('/proc/cpuinfo') as f:
             for line in f:
                 if line.startswith('model name'):
-                    cpu = line.split(':', 1)[1].strip()
-                    break
+                    return line.split(':', 1)[1].strip()
     except OSError:
         pass
-    return {'value': total_spk * k / el / 1e9, 'unit': 'GSOP/s', 'cores': threads,
-            'kind': 'port',
+    return 'unknown'
+
+
+def cpu_baseline(idx_e, idx_i, V0, n_exc, k, budget_s, single_s=4.0):
+    """C/OpenMP restatement on every core this process may run on (os.sched_getaffinity),
+    warm 200 steps, then time >= budget_s; then the same on one thread for >= single_s."""
+    from oracle import cbuild, neuron
+    F = np.float32
+    p = neuron.LIFParams()
+    we = np.full(idx_e.shape, F(0.6))
+    wi = np.full(idx_i.shape, F(6.7))
+    cores = len(os.sched_getaffinity(0))
+    st = cbuild.lif_state(V0)
+
+    def timed(threads, budget, max_steps):
+        chunk = 100 if threads > 1 else 20
+        spk = steps = 0
+        t0 = time.perf_counter()
+        while True:
+            spk += cbuild.coba_lif_run(st, idx_e, idx_i, we, wi, p, n_exc, chunk,
+                                       nthreads=threads)
+            steps += chunk
+            el = time.perf_counter() - t0
+            if el >= budget or steps >= max_steps:
+                return spk, steps, el
+
+    cbuild.coba_lif_run(st, idx_e, idx_i, we, wi, p, n_exc, 200, nthreads=cores)
+    spk, steps, el = timed(cores, budget_s, 20000)
+    spk1, steps1, el1 = timed(1, single_s, 2000)
+    return {'value': spk * k / el / 1e9, 'unit': 'GSOP/s', 'cores': cores, 'kind': 'port',
             'sample': f'{steps} steps of the same 1M-neuron net after 200 warm-up steps '
-                      f'({el:.1f} s, {total_spk} spikes), oracle/c/coba_cpu.c, {cpu}',
-            'ms_per_sim_step': el / steps * 1e3}
+                      f'({el:.1f} s, {spk} spikes) on {cores} threads, oracle/c/coba_cpu.c '
+                      f'(OpenMP, same fixed-point input sums), {_cpu_model()}',
+            'nproc': os.cpu_count(), 'cpu_model': _cpu_model(),
+            'ms_per_sim_step': el / steps * 1e3,
+            'single_thread': {'value': spk1 * k / el1 / 1e9, 'unit': 'GSOP/s',
+                              'steps': steps1, 'seconds': el1,
+                              'ms_per_sim_step': el1 / steps1 * 1e3}}
 
 
 def summarize_rocpd(path):
@@ -258,7 +267,7 @@ def bench_hh(args):
     r = EINetRunner('hh', n, n_exc, idx_e, idx_i, we, wi, ops.hh_params(I_ext=6.5), V0)
     c = torch.zeros(T, dtype=torch.int32, device='cuda')
     r.run(T, counts=c)
-    torch.cuda.synchronize()
+    r.check()
     t = _timed(lambda: r.run(T, counts=c), 1, 0)
     r.check()
     spikes = int(c.sum().item())
@@ -406,7 +415,7 @@ def main():
     wcounts = torch.zeros(T, dtype=torch.int32, device='cuda')
     for _ in range(args.warmup):
         runner.run(T, counts=wcounts)
-    torch.cuda.synchronize()
+    runner.check()   # raises if a count-word wait hit its spin limit (results invalid)
     print(f'[bench] warm-up done: {int(wcounts.sum().item())} spikes in last warm-up launch',
           file=sys.stderr, flush=True)
 
@@ -421,6 +430,7 @@ def main():
         ev[s][1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    runner.check()
     kern_ms = [a.elapsed_time(b) for a, b in ev]
     cnt = counts[:args.steps].cpu().numpy()
     spikes = int(cnt.sum())

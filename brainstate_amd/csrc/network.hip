@@ -16,13 +16,23 @@
 // Per step t, workgroup d:
 //   A. waits until every workgroup s has published its step t-1-D count word for d (tagged
 //      with the step; D = synaptic delay in steps, 0 by default) and adds the entries of
-//      that inbox into LDS inputs with LDS atomics -- point-to-point dependencies, no grid
-//      barrier;
+//      that inbox into one 64-bit LDS word per neuron with integer LDS atomics --
+//      point-to-point dependencies, no grid barrier;
 //   B. runs the fused Expon + COBA + neuron update from those inputs;
 //   C. compacts its spikes into an LDS list (one ballot per neuron slot, one LDS prefix);
 //   D. expands its spikes into (local target | inh flag, weight) entries, written with
 //      device-scope stores at slots taken from per-destination LDS cursors, waits for its
 //      stores to complete, then publishes one tagged count word per destination.
+//
+// Input sums are integers, so they do not depend on the order in which entries arrive:
+//   * one weight per projection (homogeneous): the word counts events, E in bits 0-31 and
+//     I in bits 32-63; the input is w added c times in one fp32 chain (c = count), which is
+//     what a sequential scatter of one repeated value gives in any order;
+//   * per-synapse weights: each weight is rounded to a multiple of 2^-S (S per projection,
+//     fixed at prepare from the largest |w| and the largest in-degree so that no sum can
+//     leave int32), the E and I sums are kept as two's-complement 32-bit fields of the word
+//     (E = low half read as int32, I = the rest shifted down), and the input is the sum
+//     converted to fp32 (one rounding) times 2^-S.
 // Cross-workgroup data is only touched with device-scope loads/stores (emitted with the
 // device-coherence bit), so no L2 writeback/invalidate is ever needed (each costs ~5 us).
 // Deadlock freedom: every workgroup publishes step t's counts unconditionally after
@@ -64,14 +74,18 @@ struct NetLayout {
   uint64_t off_cap;    // uint32 [nb src][nb dst]      capacities
   uint64_t off_ofs;    // uint64 [nb dst][nb src] + 1  inbox entry offsets (dst-major)
   uint64_t off_part;   // uint32 [2][kRunSteps][nb]  per-workgroup spike counts / hashes
+  uint64_t off_deg;    // uint32 [2][n]  in-degree per kind (prepare, per-synapse weights)
   uint64_t off_inbox;  // entries [R][total]
   uint64_t bytes;
 };
 
 struct WsHeader {
-  uint32_t error;      // nonzero: a wait hit the spin limit
-  uint32_t pad[63];
+  uint32_t error;      // 1: a wait hit the spin limit; 2: a per-synapse weight is not finite
+  int32_t qexp[2];     // fixed-point exponents S_e, S_i of per-synapse weights (prepare)
+  uint32_t wbits[2];   // bit patterns of max |w| per kind (prepare)
+  uint32_t pad[59];
 };
+static_assert(sizeof(WsHeader) == 256, "workspace header is 256 bytes");
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -200,6 +214,28 @@ __device__ __forceinline__ Row row_of(const NetArgs& a, int32_t i) {
   return Row{a.idx_i + r, a.w_i ? a.w_i + r : nullptr, a.k_i, true};
 }
 
+// E / I fields of a neuron's 64-bit input word (see the header comment).
+constexpr int kTab = 256;  // repeated-sum table entries per kind (homogeneous weights)
+
+__device__ __forceinline__ int32_t acc_lo(uint64_t acc) { return (int32_t)(uint32_t)acc; }
+__device__ __forceinline__ int32_t acc_hi(uint64_t acc) {
+  return (int32_t)((acc - (uint64_t)(int64_t)acc_lo(acc)) >> 32);
+}
+
+// w added c times in one fp32 chain, from a table of the first kTab partial sums.
+__device__ __forceinline__ float repeated_sum(const float* tab, float w, uint32_t c) {
+  if (c < (uint32_t)kTab) return tab[c];
+  float s = tab[kTab - 1];
+  for (uint32_t i = kTab - 1; i < c; ++i) s = s + w;
+  return s;
+}
+
+// Fixed-point value of a per-synapse weight: rint(w * 2^S) (|w| * 2^S < 2^30 by the choice
+// of S, so the conversion is exact).
+__device__ __forceinline__ int32_t quantize(float w, float scale) {
+  return (int32_t)bs_rint(w * scale);
+}
+
 template <class Model, int NPT, bool kHet>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
                                                 typename Model::Params p) {
@@ -207,7 +243,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   constexpr int kBatch = 4;                   // phase A: entry loads in flight per thread
   constexpr int kChunks = 4;                  // phase D: 64-synapse chunks per wave and round
   constexpr int kSlots = NPT >= 8 ? 8 : 16;   // phase D: LDS slots per destination and round
-  __shared__ float s_in[2 * kChunk];          // (E, I) inputs of this workgroup's neurons
+  __shared__ uint64_t s_acc[kChunk];          // input word per neuron: E bits 0-31, I 32-63
+  __shared__ float s_tab[2][kTab];            // homogeneous: repeated sums of w_e, w_i
   __shared__ uint32_t s_pos[kMaxBlocks];      // next inbox entry per destination (d <- me)
   __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
   __shared__ uint32_t s_ofs_out[kMaxBlocks];  // first inbox entry of (d <- me)
@@ -237,7 +274,26 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     s_pos[s] = s_ofs_out[s];
     s_rcnt[s] = 0;
   }
-  for (int i = threadIdx.x; i < 2 * kChunk; i += kBlock) s_in[i] = 0.0f;
+  for (int i = threadIdx.x; i < kChunk; i += kBlock) s_acc[i] = 0ull;
+  // per-synapse weights: 2^S and 2^-S per kind; homogeneous: the repeated-sum tables
+  float qscale[2] = {1.0f, 1.0f}, qinv[2] = {1.0f, 1.0f};
+  if (kHet) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int S = __builtin_amdgcn_readfirstlane(hdr->qexp[k]);
+      qscale[k] = bs_pow2i(S);
+      qinv[k] = bs_pow2i(-S);
+    }
+  } else if (threadIdx.x == 0 || threadIdx.x == BS_WAVE) {
+    const int k = threadIdx.x == 0 ? 0 : 1;
+    const float w = k ? a.w_i_homo : a.w_e_homo;
+    float s = 0.0f;
+    s_tab[k][0] = 0.0f;
+    for (int c = 1; c < kTab; ++c) {
+      s = s + w;
+      s_tab[k][c] = s;
+    }
+  }
 
   typename Model::Regs r[NPT];
 #pragma unroll
@@ -338,11 +394,16 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           for (int u = 0; u < kBatch; ++u) {
             if (e0 + u * tps < c) {
               const uint32_t tgt = (uint32_t)ent[u];
-              const float w = kHet ? __uint_as_float((uint32_t)(ent[u] >> 32))
-                                   : ((tgt & kInhFlag) ? a.w_i_homo : a.w_e_homo);
+              const bool inh = (tgt & kInhFlag) != 0;
+              // per-synapse: the signed fixed-point weight into the E field (sign-extended,
+              // so a negative E sum borrows from the I field and is read back exactly) or
+              // the I field; homogeneous: one event count
+              const uint64_t add =
+                  kHet ? (inh ? (ent[u] & 0xFFFFFFFF00000000ull)
+                              : (uint64_t)(int64_t)(int32_t)(uint32_t)(ent[u] >> 32))
+                       : (inh ? (1ull << 32) : 1ull);
               const uint32_t loc = tgt & ~kInhFlag;
-              if (loc < (uint32_t)kChunk)
-                atomicAdd(&s_in[2 * loc + ((tgt & kInhFlag) ? 1 : 0)], w);
+              if (loc < (uint32_t)kChunk) atomicAdd(&s_acc[loc], add);
             }
           }
         }
@@ -358,9 +419,17 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       const int loc = q * kBlock + threadIdx.x;
       last[q] = false;
       if (j < n) {
-        const float2 in = *(float2*)&s_in[2 * loc];
-        *(float2*)&s_in[2 * loc] = make_float2(0.0f, 0.0f);
-        last[q] = Model::update(p, r[q], in.x, in.y);
+        const uint64_t acc = s_acc[loc];
+        s_acc[loc] = 0ull;
+        float in_e, in_i;
+        if (kHet) {
+          in_e = (float)acc_lo(acc) * qinv[0];
+          in_i = (float)acc_hi(acc) * qinv[1];
+        } else {
+          in_e = repeated_sum(s_tab[0], a.w_e_homo, (uint32_t)acc);
+          in_i = repeated_sum(s_tab[1], a.w_i_homo, (uint32_t)(acc >> 32));
+        }
+        last[q] = Model::update(p, r[q], in_e, in_i);
         if (last[q]) h += bs_mix32((uint32_t)j);
         if (a.raster) a.raster[(int64_t)t * n + j] = last[q] ? 1 : 0;
       }
@@ -404,6 +473,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     if (threadIdx.x == 0) {  // per-workgroup partials, summed over workgroups after the launch
       if (a.counts) a.counts[(int64_t)t * nb + me] = nsp2[0] + nsp2[1];
       if (a.hash) a.hash[(int64_t)t * nb + me] = s_hash;
+      // s_hash's last reader; the next adds come after this step's final barrier
+      s_hash = 0;
     }
 
     // ---- D: expand spikes into the destinations' inboxes ----
@@ -423,12 +494,12 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     const uint32_t rounds = (G + kPer - 1) / kPer;
     for (uint32_t rnd = 0; rnd < rounds; ++rnd) {
       int32_t tgt[kChunks];
-      float wv[kChunks];
+      int32_t wq[kChunks];  // fixed-point weights (per-synapse weights only)
       bool inh[kChunks];
 #pragma unroll
       for (int u = 0; u < kChunks; ++u) {
         tgt[u] = -1;
-        wv[u] = 0.0f;
+        wq[u] = 0;
         inh[u] = false;
         const uint32_t g = rnd * kPer + (uint32_t)(u * kWaves + wid);
         if (g < G) {
@@ -447,7 +518,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           const int32_t tt = (int32_t)(c * BS_WAVE) + lane;
           if (tt < rw.k) {
             tgt[u] = rw.idx[tt];
-            if (kHet) wv[u] = rw.w[tt];
+            if (kHet) wq[u] = quantize(rw.w[tt], rw.inh ? qscale[1] : qscale[0]);
             inh[u] = rw.inh;
           }
         }
@@ -459,7 +530,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           const uint32_t rk = atomicAdd(&s_rcnt[d], 1u);
           const uint32_t loc = (uint32_t)(tgt[u] & (kChunk - 1)) | (inh[u] ? kInhFlag : 0u);
           const uint64_t ent =
-              kHet ? (((uint64_t)__float_as_uint(wv[u]) << 32) | loc) : (uint64_t)loc;
+              kHet ? (((uint64_t)(uint32_t)wq[u] << 32) | loc) : (uint64_t)loc;
           if (rk < (uint32_t)kSlots) {
             s_stage[d * kSlots + rk] = ent;
           } else {  // slots full: store this one directly
@@ -497,10 +568,13 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - s_ofs_out[d]));
         s_pos[d] = s_ofs_out[d];
       }
+      // Clear the counters this step used: every read of them came before the barrier
+      // above, and their next user is step ta+2, whose adds follow step ta+1's final
+      // barrier.  (Clearing the other parity here would race with step ta+1's adds when
+      // phase A has no barrier, i.e. while ta+1 <= D.)
       if (threadIdx.x == 0) {
-        s_nsp[(ta + 1) & 1][0] = 0;
-        s_nsp[(ta + 1) & 1][1] = 0;
-        s_hash = 0;
+        s_nsp[ta & 1][0] = 0;
+        s_nsp[ta & 1][1] = 0;
       }
     }
     slot_rd = slot_rd + 1 == ring ? 0 : slot_rd + 1;
@@ -569,6 +643,70 @@ __global__ __launch_bounds__(kBlock) void k_offsets(int nb, const uint32_t* cap,
     const int64_t d = x / nb, s = x - d * nb;
     ofs[x] = acc;
     acc += cap[s * nb + d];
+  }
+}
+
+// Per-synapse weights: in-degree of every neuron per kind (valid targets) and the bit
+// pattern of max |w| per kind (all weights of the kind).
+__global__ __launch_bounds__(256) void k_indeg(NetArgs a, uint32_t* deg, WsHeader* hdr) {
+  const int64_t tot_e = (int64_t)a.n_exc * a.k_e;
+  const int64_t tot = tot_e + (int64_t)(a.n - a.n_exc) * a.k_i;
+  uint32_t wb[2] = {0u, 0u};
+  for (int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; s < tot;
+       s += (int64_t)gridDim.x * blockDim.x) {
+    const int k = s >= tot_e ? 1 : 0;
+    const int64_t o = k ? s - tot_e : s;
+    const int32_t tgt = k ? a.idx_i[o] : a.idx_e[o];
+    const uint32_t b = __float_as_uint(k ? a.w_i[o] : a.w_e[o]) & 0x7FFFFFFFu;
+    wb[k] = b > wb[k] ? b : wb[k];
+    if ((uint32_t)tgt < (uint32_t)a.n) atomicAdd(&deg[(int64_t)k * a.n + tgt], 1u);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    uint32_t m = wb[k];
+    for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+      const uint32_t v = __shfl_xor(m, o);
+      m = v > m ? v : m;
+    }
+    if (bs_lane() == 0 && m) atomicMax(&hdr->wbits[k], m);
+  }
+}
+
+// S per kind from D = max in-degree and W = max |w|: with W < 2^e_w and D <= 2^e_d,
+// S = 30 - e_w - e_d (at most 100) keeps |sum of rounded weights| < 2^30 + D/2 < 2^31.
+// A weight that is not finite, or S < -100, sets error 2.  One workgroup.
+__global__ __launch_bounds__(kBlock) void k_qexp(int32_t n, const uint32_t* deg, WsHeader* hdr) {
+  __shared__ uint32_t s_max[2][kWaves];
+  uint32_t m[2] = {0u, 0u};
+  for (int64_t j = threadIdx.x; j < n; j += kBlock) {
+    const uint32_t de = deg[j], di = deg[(int64_t)n + j];
+    m[0] = de > m[0] ? de : m[0];
+    m[1] = di > m[1] ? di : m[1];
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+      const uint32_t v = __shfl_xor(m[k], o);
+      m[k] = v > m[k] ? v : m[k];
+    }
+    if (bs_lane() == 0) s_max[k][threadIdx.x / BS_WAVE] = m[k];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 0; k < 2; ++k) {
+      uint32_t D = 0;
+      for (int w = 0; w < kWaves; ++w) D = s_max[k][w] > D ? s_max[k][w] : D;
+      const uint32_t wb = hdr->wbits[k];
+      const int e_w = (wb >> 23) ? (int)(wb >> 23) - 126 : -126;
+      const int e_d = D <= 1 ? 0 : 32 - __clz(D - 1);
+      int S = 30 - e_w - e_d;
+      if (S > 100) S = 100;
+      if (wb >= 0x7F800000u || S < -100) {
+        hdr->error = 2u;
+        S = 0;
+      }
+      hdr->qexp[k] = S;
+    }
   }
 }
 
@@ -646,6 +784,8 @@ int plan(const bs_net* net, NetLayout* L) {
   o = align256(o + (size_t)(nb * nb + 1) * sizeof(uint64_t));
   L->off_part = o;
   o = align256(o + (size_t)2 * kRunSteps * nb * sizeof(uint32_t));
+  L->off_deg = o;
+  if (net->w_e) o = align256(o + (size_t)2 * net->n * sizeof(uint32_t));
   L->off_inbox = o;
   o = align256(o + (size_t)L->ring * L->total * L->entry);
   L->bytes = o;
@@ -808,9 +948,17 @@ extern "C" int bs_net_prepare(const bs_net* net, void* workspace, bs_stream_t st
   hipStream_t s = bs_stream(stream);
   char* ws = (char*)workspace;
   NetArgs a = make_args(net, L, workspace);
-  // header, tagged counts, capacities and offsets are cleared; inboxes need no clearing
-  k_zero_u64<<<64, 256, 0, s>>>((uint64_t*)ws, (int64_t)(L.off_inbox / 8));
+  // header, tagged counts, capacities, offsets and in-degrees are cleared; inboxes need no
+  // clearing
+  k_zero_u64<<<256, 256, 0, s>>>((uint64_t*)ws, (int64_t)(L.off_inbox / 8));
   BS_CHECK_LAUNCH();
+  if (net->w_e) {  // fixed-point exponents of the per-synapse weights
+    uint32_t* deg = (uint32_t*)(ws + L.off_deg);
+    k_indeg<<<2048, 256, 0, s>>>(a, deg, (WsHeader*)ws);
+    BS_CHECK_LAUNCH();
+    k_qexp<<<1, kBlock, 0, s>>>(net->n, deg, (WsHeader*)ws);
+    BS_CHECK_LAUNCH();
+  }
   k_caps<<<L.nb, kBlock, 0, s>>>(a, (uint32_t*)(ws + L.off_cap));
   BS_CHECK_LAUNCH();
   uint64_t* ofs = (uint64_t*)(ws + L.off_ofs);
@@ -860,5 +1008,11 @@ extern "C" int bs_net_error(const void* workspace, bs_stream_t stream) {
   BS_CHECK_HIP(hipMemcpyAsync(&e, workspace, sizeof(e), hipMemcpyDeviceToHost,
                               bs_stream(stream)));
   BS_CHECK_HIP(hipStreamSynchronize(bs_stream(stream)));
+  if (e == 2u) {
+    bs_set_error("runner: a per-synapse weight is not finite (or too large for the fixed-point "
+                 "input sums)");
+    return -2;
+  }
+  if (e) bs_set_error("runner: a wait for a count word hit its spin limit");
   return e ? -1 : 0;
 }

@@ -19,6 +19,10 @@ class EINetRunner:
 
     ``model`` is 'lif' (Expon + COBA + LIFRef) or 'hh' (Expon + COBA + Hodgkin-Huxley).
     ``w_e``/``w_i`` are scalars (homogeneous) or [n_pre, K] arrays (heterogeneous).
+    A step's input sums are exact integer sums, whatever the order in which events arrive:
+    event counts turned into w added c times (homogeneous), or per-synapse weights rounded
+    to multiples of 2^-S with one exponent S per projection (the largest that keeps every
+    sum inside int32), summed exactly, then rounded once to fp32.
     ``delay_steps`` D: step t's synaptic inputs come from the spikes of step t-1-D (the
     reference's ``N.prefetch_delay('spike', D*dt)``; no spikes before the first step).
     """
@@ -41,8 +45,13 @@ class EINetRunner:
         self.idx_i = torch.from_numpy(idx_i).to(dev)
         het = np.ndim(w_e) > 0 or np.ndim(w_i) > 0
         if het:
-            we = np.broadcast_to(np.asarray(w_e, np.float32), idx_e.shape)
-            wi = np.broadcast_to(np.asarray(w_i, np.float32), idx_i.shape)
+            we, wi = (np.asarray(w, np.float32) for w in (w_e, w_i))
+            if we.shape != idx_e.shape or not we.flags.writeable:
+                we = np.array(np.broadcast_to(we, idx_e.shape))
+            if wi.shape != idx_i.shape or not wi.flags.writeable:
+                wi = np.array(np.broadcast_to(wi, idx_i.shape))
+            if not (np.isfinite(we).all() and np.isfinite(wi).all()):
+                raise ValueError('per-synapse weights must be finite')
             self.w_e = torch.from_numpy(np.ascontiguousarray(we)).to(dev)
             self.w_i = torch.from_numpy(np.ascontiguousarray(wi)).to(dev)
             self.w_e_homo = self.w_i_homo = 0.0
@@ -106,7 +115,8 @@ class EINetRunner:
         self.t += int(steps)
 
     def check(self):
-        """Synchronise and raise if a run's wait hit its spin limit."""
+        """Synchronise and raise if a run's wait hit its spin limit or the per-synapse weights
+        could not be given a fixed-point exponent (a weight is not finite)."""
         rc = N.lib().bs_net_error(N.ptr(self.ws), N.stream_handle(self.device))
         if rc != 0:
             raise N.NativeError(f'runner error {rc}: '

@@ -325,7 +325,8 @@ BS_API int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_
 /* Workgroups the runners use for this net on the current device (-1 on error). */
 BS_API int bs_net_grid_blocks(const bs_net* net);
 /* Synchronises `stream`; returns 0 if every wait of the runs so far completed, -1 if one
- * hit its spin limit (results invalid), or a positive status on a call failure. */
+ * hit its spin limit (results invalid), -2 if bs_net_prepare found a per-synapse weight that
+ * is not finite (results invalid), or a positive status on a call failure. */
 BS_API int bs_net_error(const void* workspace, bs_stream_t stream);
 
 /* ---------------------------------------------------------------- connectivity on the device

@@ -27,7 +27,15 @@ def build(verbose=False):
 class _LifParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_float) for n in ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'I_ext',
                                                 'E_e', 'E_i', 'dt', 'decay_e', 'decay_i')] + \
-               [('ref_steps', ctypes.c_int32)]
+               [('ref_steps', ctypes.c_int32), ('cuba', ctypes.c_int32),
+                ('scale_e', ctypes.c_float), ('scale_i', ctypes.c_float),
+                ('soft_reset', ctypes.c_int32)]
+
+
+class _HhParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_float) for n in ('ENa', 'gNa', 'EK', 'gK', 'EL', 'gL', 'inv_C',
+                                                'V_th', 'I_ext', 'E_e', 'E_i', 'dt', 'decay_e',
+                                                'decay_i')]
 
 
 _lib = None
@@ -40,7 +48,9 @@ def lib():
             build()
         L = ctypes.CDLL(LIB)
         L.bso_coba_lif_run.restype = ctypes.c_longlong
+        L.bso_coba_hh_run.restype = ctypes.c_longlong
         L.bso_max_threads.restype = ctypes.c_int
+        L.bso_net_qexp.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -48,7 +58,55 @@ def lib():
 def lif_params(p):
     """From an oracle.neuron.LIFParams."""
     return _LifParams(p.V_rest, p.V_th, p.V_reset, p.inv_tau, p.R, p.I_ext, p.E_e, p.E_i, p.dt,
-                      p.de, p.di, int(p.ref_steps))
+                      p.de, p.di, int(p.ref_steps), int(bool(getattr(p, 'cuba', False))),
+                      float(getattr(p, 'scale_e', 1.0)), float(getattr(p, 'scale_i', 1.0)),
+                      int(bool(getattr(p, 'soft_reset', False))))
+
+
+def hh_params(p):
+    """From an oracle.neuron.HHParams."""
+    return _HhParams(p.ENa, p.gNa, p.EK, p.gK, p.EL, p.gL, p.inv_C, p.V_th, p.I_ext, p.E_e,
+                     p.E_i, p.dt, p.de, p.di)
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def net_qexp(idx_e, w_e, idx_i, w_i, n):
+    """Fixed-point exponents (S_e, S_i) of per-synapse weights, as the runner fixes them."""
+    import numpy as np
+    q = np.zeros(2, np.int32)
+    idx_e = np.ascontiguousarray(idx_e, np.int32)
+    idx_i = np.ascontiguousarray(idx_i, np.int32)
+    w_e = np.ascontiguousarray(np.broadcast_to(np.asarray(w_e, np.float32), idx_e.shape))
+    w_i = np.ascontiguousarray(np.broadcast_to(np.asarray(w_i, np.float32), idx_i.shape))
+    rc = lib().bso_net_qexp(ctypes.c_int(n), ctypes.c_int(idx_e.shape[0]),
+                            ctypes.c_int(idx_e.shape[1]), ctypes.c_int(idx_i.shape[1]),
+                            _ptr(idx_e), _ptr(w_e), _ptr(idx_i), _ptr(w_i), _ptr(q))
+    if rc:
+        raise ValueError('a per-synapse weight is not finite (or too large)')
+    return int(q[0]), int(q[1])
+
+
+def _common(state, idx_e, idx_i, w_e, w_i, delay):
+    import numpy as np
+    het = np.ndim(w_e) > 0
+    n = state['V'].size
+    for key in ('in_e', 'in_i'):
+        if state[key].size != (delay + 1) * n or state[key].itemsize != 4:
+            raise ValueError(f'{key} must hold (delay + 1) * n = {(delay + 1) * n} 4-byte values')
+    qexp = None
+    if het:
+        if 'qexp' not in state:
+            state['qexp'] = np.array(net_qexp(idx_e, w_e, idx_i, w_i, n), np.int32)
+        qexp = state['qexp']
+    t0 = int(state.get('t', 0))
+    ctf = ctypes.c_float
+    args = [ctypes.c_int(n), None, ctypes.c_int(idx_e.shape[1]), ctypes.c_int(idx_i.shape[1]),
+            _ptr(idx_e), _ptr(w_e) if het else None, ctf(0.0 if het else float(w_e)),
+            _ptr(idx_i), _ptr(w_i) if het else None, ctf(0.0 if het else float(w_i))]
+    return args, qexp, t0
 
 
 def coba_lif_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, counts=None,
@@ -56,22 +114,61 @@ def coba_lif_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, cou
     """Advance ``state`` (dict of numpy arrays V, ge, gi, ref, spk, in_e, in_i) in place.
 
     With ``delay`` D > 0, in_e / in_i are rings of D+1 input slots ([(D+1) * n]) and
-    ``state['t']`` (absolute index of the next step, default 0) is advanced."""
-    import numpy as np
-    P = ctypes.c_void_p
-    f = lambda a: a.ctypes.data_as(P) if a is not None else None
-    het = np.ndim(w_e) > 0
-    n = state['V'].size
-    for key in ('in_e', 'in_i'):
-        if state[key].size != (delay + 1) * n:
-            raise ValueError(f'{key} must hold (delay + 1) * n = {(delay + 1) * n} floats')
-    t0 = int(state.get('t', 0))
+    ``state['t']`` (absolute index of the next step, default 0) is advanced.  With
+    per-synapse weights the rings hold int32 fixed-point sums (start them at zero) and
+    ``state['qexp']`` caches the exponents."""
+    args, qexp, t0 = _common(state, idx_e, idx_i, w_e, w_i, delay)
+    args[1] = ctypes.c_int(n_exc)
     state['t'] = t0 + int(steps)
     return lib().bso_coba_lif_run(
-        ctypes.c_int(n), ctypes.c_int(n_exc), ctypes.c_int(idx_e.shape[1]),
-        ctypes.c_int(idx_i.shape[1]), f(idx_e), f(w_e) if het else None,
-        ctypes.c_float(0.0 if het else float(w_e)), f(idx_i), f(w_i) if het else None,
-        ctypes.c_float(0.0 if het else float(w_i)), ctypes.byref(lif_params(p)),
-        f(state['V']), f(state['ge']), f(state['gi']), f(state['ref']), f(state['spk']),
-        f(state['in_e']), f(state['in_i']), ctypes.c_int(steps), f(counts), f(hashes),
-        ctypes.c_int(nthreads), ctypes.c_int(delay), ctypes.c_longlong(t0))
+        *args, ctypes.byref(lif_params(p)),
+        _ptr(state['V']), _ptr(state['ge']), _ptr(state['gi']), _ptr(state['ref']),
+        _ptr(state['spk']), _ptr(state['in_e']), _ptr(state['in_i']), ctypes.c_int(steps),
+        _ptr(counts), _ptr(hashes), ctypes.c_int(nthreads), ctypes.c_int(delay),
+        ctypes.c_longlong(t0), _ptr(qexp))
+
+
+def coba_hh_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, counts=None,
+                hashes=None, delay=0):
+    """HH network (state: V, m, h, n, ge, gi, spk, in_e, in_i), as coba_lif_run."""
+    args, qexp, t0 = _common(state, idx_e, idx_i, w_e, w_i, delay)
+    args[1] = ctypes.c_int(n_exc)
+    state['t'] = t0 + int(steps)
+    return lib().bso_coba_hh_run(
+        *args, ctypes.byref(hh_params(p)),
+        _ptr(state['V']), _ptr(state['m']), _ptr(state['h']), _ptr(state['n']),
+        _ptr(state['ge']), _ptr(state['gi']), _ptr(state['spk']), _ptr(state['in_e']),
+        _ptr(state['in_i']), ctypes.c_int(steps), _ptr(counts), _ptr(hashes),
+        ctypes.c_int(nthreads), ctypes.c_int(delay), ctypes.c_longlong(t0), _ptr(qexp))
+
+
+def hh_init(V):
+    """Steady-state gates (m, h, n) at V."""
+    import numpy as np
+    V = np.ascontiguousarray(V, np.float32)
+    m, h, n = (np.empty_like(V) for _ in range(3))
+    lib().bso_hh_init(ctypes.c_int(V.size), _ptr(V), _ptr(m), _ptr(h), _ptr(n))
+    return m, h, n
+
+
+def lif_state(V0, delay=0):
+    """Fresh LIF state for coba_lif_run (rings zero; they are reinterpreted as int32 sums
+    with per-synapse weights)."""
+    import numpy as np
+    F = np.float32
+    n = V0.size
+    return dict(V=np.array(V0, F), ge=np.zeros(n, F), gi=np.zeros(n, F),
+                ref=np.zeros(n, np.int32), spk=np.zeros(n, np.uint8),
+                in_e=np.zeros((delay + 1) * n, F), in_i=np.zeros((delay + 1) * n, F))
+
+
+def hh_state(V0, delay=0):
+    """Fresh HH state for coba_hh_run, gates at steady state."""
+    import numpy as np
+    F = np.float32
+    n = V0.size
+    V = np.array(V0, F)
+    m, h, ng = hh_init(V)
+    return dict(V=V, m=m, h=h, n=ng, ge=np.zeros(n, F), gi=np.zeros(n, F),
+                spk=np.zeros(n, np.uint8), in_e=np.zeros((delay + 1) * n, F),
+                in_i=np.zeros((delay + 1) * n, F))

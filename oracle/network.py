@@ -34,19 +34,70 @@ def repeated_sum_table(w, max_count):
     return t
 
 
-class Projection:
-    """One fixed-num projection (pre block of the neuron vector -> all N)."""
+def runner_qexp(idx, w, n_post):
+    """Fixed-point exponent S of one projection's per-synapse weights, as the persistent
+    runner fixes it: with D = the largest number of the projection's synapses onto one
+    neuron (valid targets) and W = max |w| < 2^e_w (e_w from W's exponent field; -126 for a
+    zero or subnormal W), D <= 2^e_d, S = min(30 - e_w - e_d, 100).  Every neuron's sum of
+    rint(w * 2^S) then has magnitude < 2^30 + D/2 < 2^31."""
+    idx = np.asarray(idx)
+    w = np.ascontiguousarray(np.broadcast_to(np.asarray(w, F), idx.shape))
+    t = idx.reshape(-1)
+    t = t[(t >= 0) & (t < n_post)]
+    D = int(np.bincount(t, minlength=n_post).max()) if t.size else 0
+    wb = int((w.view(np.uint32) & np.uint32(0x7FFFFFFF)).max()) if w.size else 0
+    if wb >= 0x7F800000:
+        raise ValueError('a per-synapse weight is not finite')
+    e_w = (wb >> 23) - 126 if (wb >> 23) else -126
+    e_d = (D - 1).bit_length() if D > 1 else 0
+    S = min(30 - e_w - e_d, 100)
+    if S < -100:
+        raise ValueError('per-synapse weights too large for the fixed-point input sums')
+    return S
 
-    def __init__(self, pre_lo, pre_hi, n_post, conn_num, w, seed, het=False):
+
+def fixed_point_input(spk_pre, idx, w, S, n_post):
+    """The runner's input of one projection with per-synapse weights: every weight of an
+    event onto j rounded to a multiple of 2^-S (round half to even), the rounded weights
+    summed exactly, the sum converted to fp32 once and scaled by 2^-S."""
+    act = np.flatnonzero(spk_pre)
+    q = np.rint(np.asarray(w, F)[act] * F(2.0 ** S)).astype(np.int64).reshape(-1)
+    t = np.asarray(idx)[act].reshape(-1)
+    ok = (t >= 0) & (t < n_post)
+    acc = np.zeros(n_post, np.int64)
+    np.add.at(acc, t[ok], q[ok])
+    assert np.abs(acc).max(initial=0) < 2 ** 31
+    return (acc.astype(F) * F(2.0 ** -S)).astype(F)
+
+
+class Projection:
+    """One fixed-num projection (pre block of the neuron vector -> all N).
+
+    ``w``: one value (homogeneous; ``het=True`` stores it per synapse) or an array of
+    per-synapse weights of the connectivity's shape.  ``fixed=True`` sums per-synapse weights
+    as the persistent runner does (``fixed_point_input``); otherwise in the sequential
+    (pre, k) order of a plain scatter.  Sums of one repeated value use the repeated-sum table
+    either way (order-free)."""
+
+    def __init__(self, pre_lo, pre_hi, n_post, conn_num, w, seed, het=False, fixed=False):
         self.pre_lo, self.pre_hi, self.n_post = pre_lo, pre_hi, n_post
         self.k = _conn.conn_num_from(conn_num, n_post)
         self.idx, _ = _conn.fixed_num_indices(pre_hi - pre_lo, n_post, self.k, seed)
-        self.w_scalar = F(w)
-        self.het = het
-        self.w = np.full(self.idx.shape, F(w), F) if het else F(w)
+        if np.ndim(w) > 0:
+            self.w = np.ascontiguousarray(np.broadcast_to(np.asarray(w, F), self.idx.shape))
+            self.w_scalar = self.w.reshape(-1)[0] if self.w.size else F(0)
+            self.het = True
+        else:
+            self.w_scalar = F(w)
+            self.het = het
+            self.w = np.full(self.idx.shape, F(w), F) if het else F(w)
+        self.fixed = fixed
+        self.S = runner_qexp(self.idx, self.w, n_post) if (self.het and fixed) else None
         self._table = None
 
     def __call__(self, spk_pre):
+        if self.het and self.fixed:
+            return fixed_point_input(spk_pre, self.idx, self.w, self.S, self.n_post)
         if not self.het or np.all(self.w == self.w_scalar):
             # one repeated weight value: counts + repeated-sum table (exact, order-free)
             act = np.flatnonzero(spk_pre)

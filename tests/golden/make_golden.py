@@ -7,6 +7,8 @@
   used by the parity configs (brainstate/nn/_event_fixedprob.py:165-171).
 * coba_lif_4000.json -- config [1]: 4000-neuron COBA E/I net, 1000 steps; per-step spike
   counts, per-step order-free spike digests and SHA-256 of the raster / final state.
+* coba_lif_4000_het.json -- the same net with random per-synapse weights summed in the
+  persistent runner's fixed-point arithmetic (the exponents S_e, S_i recorded too).
 * cuba_lif_4000.json -- examples/400_CUBA_2005_bpu.py's CUBA E/I net, 1000 steps, same records.
 * tut_lif_soft_500.json -- the SNN tutorial's E/I net (LIF, soft reset, CUBA), 2000 steps.
 * coba_hh_2000.json -- a 2000-neuron COBA-HH net, 600 steps, same records.
@@ -50,6 +52,9 @@ MATVEC = dict(n_pre=2000, n_post=2000, k=100, seed_idx=41, seed_w=42, seed_spk=4
               p=[0.001, 0.01, 0.1], w_homo=0.6)
 HH_NET = dict(n=2000, n_exc=1600, k=80, w_e=0.05, w_i=0.3, seed_e=11, seed_i=12, seed_v=13,
               steps=600, I_ext=6.5)
+# config [1] with per-synapse weights w_e ~ N(0.6, 0.06), w_i ~ N(6.7, 0.67) (numpy seeds),
+# summed as the persistent runner sums them (fixed point, oracle.network.fixed_point_input)
+CONFIG1_HET = dict(CONFIG1, seed_we=4, seed_wi=5, sd_e=0.06, sd_i=0.67)
 
 
 def sha(a):
@@ -62,6 +67,23 @@ def config1_net():
     pi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=c['seed_i'])
     V0 = np.random.RandomState(c['seed_v']).uniform(-60., -50., c['n']).astype(np.float32)
     return pe, pi, V0, neuron.LIFParams()
+
+
+def config1_het_weights(shape_e, shape_i):
+    c = CONFIG1_HET
+    we = np.random.RandomState(c['seed_we']).normal(c['w_e'], c['sd_e'], shape_e)
+    wi = np.random.RandomState(c['seed_wi']).normal(c['w_i'], c['sd_i'], shape_i)
+    return we.astype(np.float32), wi.astype(np.float32)
+
+
+def config1_het_net():
+    """Config [1] with random per-synapse weights, runner (fixed-point) sums."""
+    c = CONFIG1_HET
+    pe0, pi0, V0, p = config1_net()
+    we, wi = config1_het_weights(pe0.idx.shape, pi0.idx.shape)
+    pe = network.Projection(0, c['n_exc'], c['n'], c['p'], we, seed=c['seed_e'], fixed=True)
+    pi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'], wi, seed=c['seed_i'], fixed=True)
+    return pe, pi, V0, p
 
 
 def cuba_net():
@@ -144,6 +166,13 @@ def main():
     with open(os.path.join(HERE, 'coba_lif_4000.json'), 'w') as f:
         json.dump(rec, f)
     print('coba_lif_4000: total spikes', int(res['counts'].sum()))
+
+    pe, pi, V0, p = config1_het_net()
+    res = network.run_coba_lif(V0, pe, pi, p, CONFIG1_HET['n_exc'], CONFIG1_HET['steps'])
+    rec = dict(config=CONFIG1_HET, qexp=[pe.S, pi.S], **run_records(res))
+    with open(os.path.join(HERE, 'coba_lif_4000_het.json'), 'w') as f:
+        json.dump(rec, f)
+    print('coba_lif_4000_het: total spikes', int(res['counts'].sum()))
 
     pe, pi, V0, p = cuba_net()
     res = network.run_coba_lif(V0, pe, pi, p, CUBA_NET['n_exc'], CUBA_NET['steps'])

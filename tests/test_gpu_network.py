@@ -43,15 +43,45 @@ def _lif_runner(torch, het, blocks_per_cu=0, delay_steps=0):
 def _c_lif(idx_e, idx_i, w_e, w_i, p, n_exc, V0, T, D, nthreads=8):
     """C restatement with a D-step synaptic delay: per-step counts, hashes, final state."""
     from oracle import cbuild
-    n = V0.size
-    st = dict(V=V0.copy(), ge=np.zeros(n, F), gi=np.zeros(n, F), ref=np.zeros(n, np.int32),
-              spk=np.zeros(n, np.uint8), in_e=np.zeros((D + 1) * n, F),
-              in_i=np.zeros((D + 1) * n, F))
+    st = cbuild.lif_state(V0, delay=D)
     c = np.zeros(T, np.int32)
     h = np.zeros(T, np.uint32)
     cbuild.coba_lif_run(st, idx_e, idx_i, w_e, w_i, p, n_exc, T, nthreads=nthreads, counts=c,
                         hashes=h, delay=D)
     return c, h, st
+
+
+def _c_hh(idx_e, idx_i, w_e, w_i, p, n_exc, V0, T, D=0, nthreads=16):
+    from oracle import cbuild
+    st = cbuild.hh_state(V0, delay=D)
+    c = np.zeros(T, np.int32)
+    h = np.zeros(T, np.uint32)
+    cbuild.coba_hh_run(st, idx_e, idx_i, w_e, w_i, p, n_exc, T, nthreads=nthreads, counts=c,
+                       hashes=h, delay=D)
+    return c, h, st
+
+
+def _host_threads():
+    import os
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def _big_net(n, k, seed, weights):
+    """Config [3]-shaped net: 80 % E, K fixed-num targets per neuron (numpy MT19937), V0 ~
+    U(-60, -50).  weights: 'homo' (0.6 / 6.7), 'const' (0.6 / 6.7 stored per synapse, as
+    bench.py) or 'normal' (N(0.6, 0.06) / N(6.7, 0.67) per synapse)."""
+    n_exc = n * 4 // 5
+    idx_e = np.random.RandomState(seed + 1).randint(0, n, size=(n_exc, k)).astype(np.int32)
+    idx_i = np.random.RandomState(seed + 2).randint(0, n, size=(n - n_exc, k)).astype(np.int32)
+    V0 = np.random.RandomState(seed + 3).uniform(-60., -50., n).astype(F)
+    if weights == 'homo':
+        w_e, w_i = 0.6, 6.7
+    elif weights == 'const':
+        w_e, w_i = np.full(idx_e.shape, F(0.6)), np.full(idx_i.shape, F(6.7))
+    else:
+        w_e = np.random.RandomState(seed + 4).normal(0.6, 0.06, idx_e.shape).astype(F)
+        w_i = np.random.RandomState(seed + 5).normal(6.7, 0.67, idx_i.shape).astype(F)
+    return n_exc, idx_e, idx_i, w_e, w_i, V0
 
 
 def _run_chunks(torch, r, T, chunks):
@@ -128,7 +158,133 @@ def test_coba_hh_delay_matches_oracle(torch_cuda):
     assert np.array_equal(r.state['V'].cpu().numpy(), ref['V'])
 
 
-@pytest.mark.parametrize('het,chunks', [(False, [1000]), (True, [1000]), (False, [1, 9, 90, 900])])
+@pytest.mark.parametrize('n,steps,weights,D', [
+    (1_000_000, 1000, 'normal', 0),   # the bench's instantiation: 4 neurons per thread
+    (1_000_000, 1000, 'const', 0),    # the bench's own weights
+    (1_000_000, 600, 'homo', 0),      # event counts at the same instantiation
+    (400_000, 1000, 'normal', 0),     # 2 neurons per thread
+    (1_500_000, 600, 'normal', 0),    # 8 neurons per thread
+    (1_000_000, 600, 'normal', 2),    # ring of inbox slots at the bench's instantiation
+])
+def test_coba_lif_large_matches_c(torch_cuda, n, steps, weights, D):
+    """Config [3]-shaped nets (K = 100) at every neurons-per-thread instantiation of the
+    persistent runner, including the one bench.py times: per-step spike counts and hashes, and
+    the final V, g_e, g_i and refractory counters equal the C restatement's (same integer input
+    sums, any thread schedule)."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    torch = torch_cuda
+    say('coba lif large', n, steps, weights, D)
+    n_exc, idx_e, idx_i, w_e, w_i, V0 = _big_net(n, 100, 100, weights)
+    r = EINetRunner('lif', n, n_exc, idx_e, idx_i, w_e, w_i, ops.lif_params(), V0,
+                    delay_steps=D)
+    nb = r.grid_blocks
+    npt = -(-n // (nb * 1024))
+    assert {400_000: 2, 1_000_000: 4, 1_500_000: 8}[n] == 1 << (npt - 1).bit_length()
+    counts, hashes = _run_chunks(torch, r, steps, [steps // 3, steps - steps // 3])
+    say('  gpu done, running the C restatement on', _host_threads(), 'threads')
+    c_ref, h_ref, st = _c_lif(idx_e, idx_i, w_e, w_i, neuron.LIFParams(), n_exc, V0, steps, D,
+                              nthreads=_host_threads())
+    assert c_ref.sum() > steps * n // 2000   # > 0.05 % of the neurons fire per step
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    for key in ('V', 'ge', 'gi', 'ref'):
+        assert np.array_equal(r.state[key].cpu().numpy(), st[key]), key
+    assert np.array_equal(r.spk.cpu().numpy(), st['spk'])
+
+
+@pytest.mark.parametrize('weights', ['const', 'normal'])
+def test_coba_hh_1m_matches_c(torch_cuda, weights):
+    """Config [5]: 1M COBA-HH neurons, K = 80 (4 neurons per thread), bench.py's drive (I_ext
+    6.5, V0 ~ U(-70, -50), weights 0.05 / 0.3 or N(0.05, 0.005) / N(0.3, 0.03) per synapse):
+    counts, hashes and the final V, m, h, n equal the C restatement's over 300 steps."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    torch = torch_cuda
+    n, k, T = 1_000_000, 80, 300
+    say('coba hh 1m', weights, T)
+    n_exc = n * 4 // 5
+    idx_e = np.random.RandomState(201).randint(0, n, size=(n_exc, k)).astype(np.int32)
+    idx_i = np.random.RandomState(202).randint(0, n, size=(n - n_exc, k)).astype(np.int32)
+    V0 = np.random.RandomState(203).uniform(-70., -50., n).astype(F)
+    if weights == 'const':
+        w_e, w_i = np.full(idx_e.shape, F(0.05)), np.full(idx_i.shape, F(0.3))
+    else:
+        w_e = np.random.RandomState(204).normal(0.05, 0.005, idx_e.shape).astype(F)
+        w_i = np.random.RandomState(205).normal(0.3, 0.03, idx_i.shape).astype(F)
+    r = EINetRunner('hh', n, n_exc, idx_e, idx_i, w_e, w_i, ops.hh_params(I_ext=6.5), V0)
+    counts, hashes = _run_chunks(torch, r, T, [T])
+    say('  gpu done, running the C restatement on', _host_threads(), 'threads')
+    c_ref, h_ref, st = _c_hh(idx_e, idx_i, w_e, w_i, neuron.HHParams(I_ext=6.5), n_exc, V0, T,
+                             nthreads=_host_threads())
+    assert c_ref.sum() > 1000
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    for key in ('V', 'm', 'h', 'n', 'ge', 'gi'):
+        assert np.array_equal(r.state[key].cpu().numpy(), st[key]), key
+
+
+@pytest.mark.parametrize('chunks', [[1000], [1, 9, 90, 900]])
+def test_coba_lif_4000_het_golden(torch_cuda, chunks):
+    """Config [1] with random per-synapse weights N(0.6, 0.06) / N(6.7, 0.67): raster, counts,
+    hashes and final V equal the oracle's golden run of the runner's fixed-point sums."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    torch = torch_cuda
+    say('coba lif 4000 het', chunks)
+    with open(os.path.join(GOLD, 'coba_lif_4000_het.json')) as f:
+        gold = json.load(f)
+    pe, pi, V0, _ = make_golden.config1_het_net()
+    c = make_golden.CONFIG1_HET
+    r = EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx, pe.w, pi.w, ops.lif_params(), V0)
+    T, n = c['steps'], c['n']
+    raster = torch.zeros(T, n, dtype=torch.uint8, device='cuda')
+    counts = torch.zeros(T, dtype=torch.int32, device='cuda')
+    hashes = torch.zeros(T, dtype=torch.int32, device='cuda')
+    t0 = 0
+    for ch in chunks:
+        r.run(ch, counts=counts[t0:t0 + ch], hashes=hashes[t0:t0 + ch], raster=raster[t0:t0 + ch])
+        t0 += ch
+    r.check()
+    assert counts.cpu().numpy().tolist() == gold['counts']
+    assert [int(h) & 0xFFFFFFFF for h in hashes.cpu().numpy()] == gold['hashes']
+    assert make_golden.sha(np.packbits(raster.cpu().numpy().astype(bool))) == gold['raster_sha256']
+    assert make_golden.sha(r.state['V'].cpu().numpy()) == gold['final_V_sha256']
+
+
+@pytest.mark.parametrize('D', [1, 5])
+def test_coba_lif_het_delay_matches_oracle(torch_cuda, D):
+    """Random per-synapse weights with a synaptic delay: the numpy oracle's spike-history
+    Delay with fixed-point sums, split runs."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    torch = torch_cuda
+    say('coba lif het delay', D)
+    pe, pi, V0, p = make_golden.config1_het_net()
+    T = 400
+    ref = network.run_coba_lif(V0, pe, pi, p, 3200, T, record_raster=False, delay_steps=D)
+    r = EINetRunner('lif', 4000, 3200, pe.idx, pi.idx, pe.w, pi.w, ops.lif_params(), V0,
+                    delay_steps=D)
+    counts, _ = _run_chunks(torch, r, T, [D, T - D])
+    assert ref['counts'].sum() > 500
+    assert counts.tolist() == ref['counts'].tolist()
+    assert np.array_equal(r.state['V'].cpu().numpy(), ref['V'])
+
+
+def test_runner_rejects_non_finite_weights(torch_cuda):
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    idx_e = np.zeros((8, 4), np.int32)
+    w = np.ones((8, 4), F)
+    w[3, 1] = np.nan
+    with pytest.raises(ValueError):
+        EINetRunner('lif', 10, 8, idx_e, np.zeros((2, 4), np.int32), w, np.ones((2, 4), F),
+                    ops.lif_params(), np.zeros(10, F))
+
+
+@pytest.mark.parametrize('het,chunks', [(False, [1000]), (False, [1, 9, 90, 900])])
 def test_coba_lif_4000_raster_bit_exact(torch_cuda, het, chunks):
     """Config [1]: 4000-neuron COBA net, 1000 steps; raster equal to the oracle's."""
     torch = torch_cuda
@@ -156,7 +312,9 @@ def test_coba_lif_4000_raster_bit_exact(torch_cuda, het, chunks):
 @pytest.mark.parametrize('het', [False, True])
 def test_cuba_lif_4000_raster_bit_exact(torch_cuda, het):
     """examples/400_CUBA_2005_bpu.py's net (CUBA outputs, signed weights) in the persistent
-    runner: raster, counts and final V equal the oracle's golden run."""
+    runner: raster, counts and final V equal the oracle's golden run (one weight per
+    projection), or the oracle's run of the fixed-point sums of the same weights stored per
+    synapse (the negative I weights exercise the signed I field)."""
     torch = torch_cuda
     from brainstate_amd import ops
     from brainstate_amd.runner import EINetRunner
@@ -171,6 +329,14 @@ def test_cuba_lif_4000_raster_bit_exact(torch_cuda, het):
                     np.full(pe.idx.shape, F(c['w_e'])) if het else c['w_e'],
                     np.full(pi.idx.shape, F(c['w_i'])) if het else c['w_i'], p, V0)
     T = c['steps']
+    if het:
+        ope = network.Projection(0, c['n_exc'], c['n'], c['p'], np.full(pe.idx.shape, F(c['w_e'])),
+                                 seed=c['seed_e'], fixed=True)
+        opi = network.Projection(c['n_exc'], c['n'], c['n'], c['p'],
+                                 np.full(pi.idx.shape, F(c['w_i'])), seed=c['seed_i'], fixed=True)
+        res = network.run_coba_lif(V0, ope, opi, make_golden.cuba_net()[3], c['n_exc'], T)
+        gold = make_golden.run_records(res)
+        assert opi.S is not None and res['counts'].sum() > 1000
     raster = torch.zeros(T, c['n'], dtype=torch.uint8, device='cuda')
     counts = torch.zeros(T, dtype=torch.int32, device='cuda')
     r.run(T, counts=counts, raster=raster)

@@ -216,3 +216,152 @@ def test_spike_hash_matches_mix32_definition():
         x ^= x >> 16
         return x
     assert network.spike_hash(spk) == (mix(3) + mix(50)) & 0xFFFFFFFF
+
+
+# ---- the persistent runner's fixed-point input sums (per-synapse weights) ----
+
+@pytest.mark.parametrize('seed', range(6))
+def test_runner_qexp_bounds_and_tightness(seed):
+    """S never lets a neuron's sum of rint(w * 2^S) leave int32, even when every presynaptic
+    neuron fires, and it is within a factor 4 of the largest S with D * W * 2^S <= 2^30 (a
+    wrong exponent offset either overflows or wastes bits); the C restatement agrees."""
+    rs = np.random.RandomState(seed)
+    n = int(rs.randint(5, 300))                # neurons: E rows [0, n_exc), I rows the rest
+    n_exc = int(rs.randint(1, n))
+    k = int(rs.randint(1, 40))
+    Ss = []
+    for rows in (n_exc, n - n_exc):
+        idx = rs.randint(0, n, (rows, k)).astype(np.int32)
+        idx[rs.rand(rows, k) < 0.3] = 0   # a hub: large in-degree of neuron 0
+        scale = float(2.0 ** rs.randint(-20, 20))
+        w = (rs.standard_normal((rows, k)) * scale).astype(F)
+        S = network.runner_qexp(idx, w, n)
+        D = int(np.bincount(idx.reshape(-1), minlength=n).max())
+        W = float(np.abs(w).max())
+        q = np.rint(w.astype(np.float64) * 2.0 ** S)
+        worst = np.zeros(n)
+        np.add.at(worst, idx.reshape(-1), np.abs(q).reshape(-1))
+        assert worst.max() < 2 ** 31
+        assert D * W * 2.0 ** S <= 2 ** 30
+        assert D * W * 2.0 ** (S + 2) > 2 ** 30
+        Ss.append((S, idx, w))
+    (Se, ie, we), (Si, ii, wi) = Ss
+    assert cbuild.net_qexp(ie, we, ii, wi, n) == (Se, Si)
+
+
+def test_runner_qexp_special_cases():
+    idx = np.array([[0, 0, 1]], np.int32)               # D = 2 onto neuron 0
+    assert network.runner_qexp(idx, np.full((1, 3), 0.6, F), 3) == 29     # W < 1, 2 <= 2^1
+    assert network.runner_qexp(idx, np.full((1, 3), 1.0, F), 3) == 28     # W = 1 < 2^1
+    assert network.runner_qexp(idx, np.zeros((1, 3), F), 3) == 100        # capped
+    assert network.runner_qexp(np.array([[7]], np.int32), np.ones((1, 1), F), 3) == 29  # D = 0
+    for bad in (np.inf, np.nan):
+        with pytest.raises(ValueError):
+            network.runner_qexp(idx, np.array([[1.0, bad, 1.0]], F), 3)
+        with pytest.raises(ValueError):
+            cbuild.net_qexp(idx, np.array([[1.0, bad, 1.0]], F), idx, np.ones((1, 3), F), 3)
+
+
+def test_fixed_point_input_is_exact_on_representable_weights():
+    """Weights that are multiples of 2^-S: the sum is the exact (float64) sum rounded once to
+    fp32; random weights: within the rounding of each weight to 2^-S plus half an ulp."""
+    rs = np.random.RandomState(3)
+    n_post, n_pre, k = 50, 400, 30
+    idx = rs.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    spk = rs.rand(n_pre) < 0.3
+    w = (rs.randint(-3000, 3000, (n_pre, k)) * 2.0 ** -10).astype(F)
+    S = network.runner_qexp(idx, w, n_post)
+    assert S >= 10
+    exact = np.zeros(n_post)
+    np.add.at(exact, idx[spk].reshape(-1), w[spk].astype(np.float64).reshape(-1))
+    got = network.fixed_point_input(spk, idx, w, S, n_post)
+    assert np.array_equal(got, exact.astype(F))
+    w = rs.standard_normal((n_pre, k)).astype(F)
+    S = network.runner_qexp(idx, w, n_post)
+    exact = np.zeros(n_post)
+    cnt = np.bincount(idx[spk].reshape(-1), minlength=n_post)
+    np.add.at(exact, idx[spk].reshape(-1), w[spk].astype(np.float64).reshape(-1))
+    got = network.fixed_point_input(spk, idx, w, S, n_post).astype(np.float64)
+    bound = cnt * 2.0 ** -(S + 1) + np.spacing(np.abs(exact).astype(F)).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= bound)
+    # same-sign weights (a conductance projection, config [3]'s N(0.6, 0.06) at its in-degree
+    # ~100): within the north_star tolerance of the atomic path, rel 1e-5 / abs 1e-6
+    n_post, n_pre, k = 200, 400, 50
+    idx = rs.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    spk = rs.rand(n_pre) < 0.05
+    w = rs.normal(0.6, 0.06, (n_pre, k)).astype(F)
+    S = network.runner_qexp(idx, w, n_post)
+    exact = np.zeros(n_post)
+    np.add.at(exact, idx[spk].reshape(-1), w[spk].astype(np.float64).reshape(-1))
+    got = network.fixed_point_input(spk, idx, w, S, n_post).astype(np.float64)
+    assert np.allclose(got, exact, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize('nthreads', [1, 4])
+def test_c_restatement_het_equals_golden(nthreads):
+    """Config [1] with random per-synapse weights: the C restatement's integer sums (any
+    thread schedule) equal the numpy oracle's golden run bit for bit."""
+    with open(os.path.join(GOLD, 'coba_lif_4000_het.json')) as f:
+        gold = json.load(f)
+    pe, pi, V0, p = make_golden.config1_het_net()
+    assert [pe.S, pi.S] == gold['qexp']
+    st = cbuild.lif_state(V0)
+    T = gold['config']['steps']
+    counts = np.zeros(T, np.int32)
+    hashes = np.zeros(T, np.uint32)
+    cbuild.coba_lif_run(st, pe.idx, pi.idx, pe.w, pi.w, p, 3200, T, nthreads=nthreads,
+                        counts=counts, hashes=hashes)
+    assert st['qexp'].tolist() == gold['qexp']
+    assert counts.tolist() == gold['counts']
+    assert hashes.tolist() == gold['hashes']
+    assert make_golden.sha(st['V']) == gold['final_V_sha256']
+
+
+def test_het_golden_matches_its_own_oracle_run():
+    with open(os.path.join(GOLD, 'coba_lif_4000_het.json')) as f:
+        gold = json.load(f)
+    pe, pi, V0, p = make_golden.config1_het_net()
+    res = network.run_coba_lif(V0, pe, pi, p, 3200, gold['config']['steps'])
+    assert make_golden.run_records(res)['raster_sha256'] == gold['raster_sha256']
+
+
+@pytest.mark.parametrize('nthreads', [1, 4])
+def test_c_hh_restatement_equals_golden(nthreads):
+    """The C HH network (steady-state init, exp-Euler gates, COBA) reproduces the numpy
+    oracle's golden 2000-neuron HH run."""
+    with open(os.path.join(GOLD, 'coba_hh_2000.json')) as f:
+        gold = json.load(f)
+    c = make_golden.HH_NET
+    pe, pi, V0, p = make_golden.hh_net()
+    st = cbuild.hh_state(V0)
+    m, h, n = neuron.hh_init(V0)
+    assert np.array_equal(st['m'], m) and np.array_equal(st['h'], h) and \
+        np.array_equal(st['n'], n)
+    counts = np.zeros(c['steps'], np.int32)
+    cbuild.coba_hh_run(st, pe.idx, pi.idx, pe.w_scalar, pi.w_scalar, p, c['n_exc'], c['steps'],
+                       nthreads=nthreads, counts=counts)
+    assert counts.tolist() == gold['counts']
+    assert make_golden.sha(st['V']) == gold['final_V_sha256']
+
+
+def test_c_hh_het_delay_equals_numpy_oracle():
+    """HH net with per-synapse weights and a 3-step delay: the C input ring of int32 sums
+    equals the numpy oracle's spike-history Delay with fixed-point sums."""
+    c = make_golden.HH_NET
+    pe0, pi0, V0, p = make_golden.hh_net()
+    rs = np.random.RandomState(9)
+    we = rs.normal(c['w_e'], 0.01, pe0.idx.shape).astype(F)
+    wi = rs.normal(c['w_i'], 0.05, pi0.idx.shape).astype(F)
+    pe = network.Projection(0, c['n_exc'], c['n'], c['k'], we, seed=c['seed_e'], fixed=True)
+    pi = network.Projection(c['n_exc'], c['n'], c['n'], c['k'], wi, seed=c['seed_i'], fixed=True)
+    D, T = 3, 300
+    ref = network.run_coba_hh(V0, pe, pi, p, c['n_exc'], T, record_raster=False, delay_steps=D)
+    st = cbuild.hh_state(V0, delay=D)
+    counts = np.zeros(T, np.int32)
+    cbuild.coba_hh_run(st, pe.idx, pi.idx, we, wi, p, c['n_exc'], 100, nthreads=4,
+                       counts=counts[:100], delay=D)
+    cbuild.coba_hh_run(st, pe.idx, pi.idx, we, wi, p, c['n_exc'], T - 100, nthreads=4,
+                       counts=counts[100:], delay=D)
+    assert ref['counts'].sum() > 50
+    assert counts.tolist() == ref['counts'].tolist()
+    assert np.array_equal(st['V'], ref['V'])
