@@ -67,6 +67,7 @@ SIGNATURES = {
     'bs_version': (ctypes.c_int, []),
     'bs_spike_compact_workspace_size': (c_size, [c_i32]),
     'bs_spike_compact': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
+    'bs_spike_compact_noalloc': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp]),
     'bs_event_scatter_f32': (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,
                                             c_i32, c_vp, c_i32, c_vp]),
     'bs_event_matvec_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,

@@ -6,6 +6,8 @@
 // tiles with smaller tickets and writes the list out coalesced.
 #include "common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -105,6 +107,47 @@ __global__ __launch_bounds__(kBlock) void k_compact(const T* __restrict__ spk, i
 
 __global__ void k_set_i32(int32_t* p, int32_t v) { *p = v; }
 
+__global__ void k_zero_u64(uint64_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0ull;
+}
+
+// ---- bs_spike_compact_noalloc: the scan workspace in a file-scope device array ----
+// The scan header and one status word per 4096-spike tile, for up to kNoAllocTiles tiles.
+// Each device holds its own copy; host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device (the array's name is a host-side
+// stand-in, not a device address).
+constexpr int64_t kNoAllocTiles = 16384;  // n <= 16384 * 4096 = 67,108,864 spikes
+constexpr size_t kScratchBytes = BS_SCAN_WS_HEADER + (size_t)kNoAllocTiles * sizeof(uint64_t);
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];  // device address of `scratch`, per device (null: not yet)
+
+// Device address of this device's scratch.  The first call on a device looks it up with that
+// device current and clears it with a kernel on `s` (the scan counters must start at zero;
+// every later call leaves them at rest again).
+int scratch_for_current_device(hipStream_t s, void** out) {
+  int dev = -1;
+  BS_CHECK_HIP(hipGetDevice(&dev));
+  BS_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "bs_spike_compact_noalloc: device %d beyond %d",
+               dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    BS_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    BS_CHECK_ARG(p != nullptr, "bs_spike_compact_noalloc: no device address for the scratch");
+    k_zero_u64<<<64, 256, 0, s>>>((uint64_t*)p, (int64_t)(kScratchBytes / sizeof(uint64_t)));
+    BS_CHECK_LAUNCH();
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return BS_OK;
+}
+
 }  // namespace
 
 extern "C" size_t bs_spike_compact_workspace_size(int32_t n) {
@@ -132,6 +175,38 @@ extern "C" int bs_spike_compact(const void* spk, int32_t spk_dtype, int32_t n, i
     k_compact<uint8_t><<<nb, kBlock, 0, s>>>((const uint8_t*)spk, n, idx_out, count_out, ws, nb);
   else
     k_compact<float><<<nb, kBlock, 0, s>>>((const float*)spk, n, idx_out, count_out, ws, nb);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_spike_compact_noalloc(const void* spk, int32_t spk_dtype, int32_t n,
+                                        int32_t* idx_out, int32_t* count_out,
+                                        bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0 && n <= kNoAllocTiles * kTile,
+               "bs_spike_compact_noalloc: n=%d exceeds the maximum %lld (a static scratch of "
+               "%zu bytes per device); use bs_spike_compact with a workspace",
+               n, (long long)(kNoAllocTiles * kTile), kScratchBytes);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_spike_compact_noalloc: unknown spike dtype %d", spk_dtype);
+  BS_CHECK_ARG(count_out != nullptr, "bs_spike_compact_noalloc: count_out is NULL");
+  hipStream_t s = bs_stream(stream);
+  if (n == 0) {
+    k_set_i32<<<1, 1, 0, s>>>(count_out, 0);
+    BS_CHECK_LAUNCH();
+    return BS_OK;
+  }
+  BS_CHECK_ARG(spk && idx_out, "bs_spike_compact_noalloc: NULL pointer");
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(s, &ws);
+  if (rc) return rc;
+  const uint32_t nb = (uint32_t)(((int64_t)n + kTile - 1) / kTile);
+  if (spk_dtype == BS_SPK_U8)
+    k_compact<uint8_t><<<nb, kBlock, 0, s>>>((const uint8_t*)spk, n, idx_out, count_out,
+                                             (bs_scan_ws*)ws, nb);
+  else
+    k_compact<float><<<nb, kBlock, 0, s>>>((const float*)spk, n, idx_out, count_out,
+                                           (bs_scan_ws*)ws, nb);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

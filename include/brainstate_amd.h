@@ -56,6 +56,17 @@ BS_API size_t bs_spike_compact_workspace_size(int32_t n);
 BS_API int bs_spike_compact(const void* spk, int32_t spk_dtype, int32_t n, int32_t* idx_out,
                      int32_t* count_out, void* workspace, bs_stream_t stream);
 
+/* bs_spike_compact without a workspace and without allocating: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The scan state lives in a static
+ * device array of 131,328 bytes that each device holds until the process ends, so
+ * n <= 67,108,864 (larger n: BS_ERR_INVALID; use bs_spike_compact).  The first call on a
+ * device clears that array with a kernel on `stream`; every call leaves it ready for the
+ * next.  All calls on one device share the array: calls that overlap in time on one device
+ * (different streams or threads without ordering) race and give wrong results. */
+BS_API int bs_spike_compact_noalloc(const void* spk, int32_t spk_dtype, int32_t n,
+                                    int32_t* idx_out, int32_t* count_out, bs_stream_t stream);
+
 /* ---------------------------------------------------------------- N2a event scatter
  * Replaces `EventArray(spk) @ FixedPostNumConn((w, idx))` and `... @ CSR((w, idx, indptr))`
  * (brainstate/nn/_event_fixedprob.py:176-181,192,202-205,249-252).
