@@ -68,18 +68,21 @@ BS_HD inline float bs_expf(float x) {
 // exprel(z) = (e^z - 1) / z, with exprel(0) = 1.  For |z| < 1/2 the degree-7 Taylor
 // series of exprel is used (truncation < 1.1e-8); elsewhere (e^z - 1) / z has no
 // harmful cancellation.
+// The series branch of bs_exprel (|z| < 1/2).
+BS_HD inline float bs_exprel_series(float z) {
+  float p = (float)(1.0 / 40320.0);
+  p = bs_fma(p, z, (float)(1.0 / 5040.0));
+  p = bs_fma(p, z, (float)(1.0 / 720.0));
+  p = bs_fma(p, z, (float)(1.0 / 120.0));
+  p = bs_fma(p, z, (float)(1.0 / 24.0));
+  p = bs_fma(p, z, (float)(1.0 / 6.0));
+  p = bs_fma(p, z, 0.5f);
+  p = bs_fma(p, z, 1.0f);
+  return p;
+}
+
 BS_HD inline float bs_exprel(float z) {
   float az = z < 0.0f ? -z : z;
-  if (az < BS_EXPREL_SERIES) {
-    float p = (float)(1.0 / 40320.0);
-    p = bs_fma(p, z, (float)(1.0 / 5040.0));
-    p = bs_fma(p, z, (float)(1.0 / 720.0));
-    p = bs_fma(p, z, (float)(1.0 / 120.0));
-    p = bs_fma(p, z, (float)(1.0 / 24.0));
-    p = bs_fma(p, z, (float)(1.0 / 6.0));
-    p = bs_fma(p, z, 0.5f);
-    p = bs_fma(p, z, 1.0f);
-    return p;
-  }
+  if (az < BS_EXPREL_SERIES) return bs_exprel_series(z);
   return (bs_expf(z) - 1.0f) / z;
 }

@@ -16,22 +16,22 @@
 // Per step t, workgroup d:
 //   A. waits until every workgroup s has published its step t-1-D count word for d (tagged
 //      with the step; D = synaptic delay in steps, 0 by default) and adds the entries of
-//      that inbox into one 64-bit LDS word per neuron with integer LDS atomics --
+//      that inbox into two 32-bit LDS words per neuron (E, I) with integer LDS atomics --
 //      point-to-point dependencies, no grid barrier;
 //   B. runs the fused Expon + COBA + neuron update from those inputs;
 //   C. compacts its spikes into an LDS list (one ballot per neuron slot, one LDS prefix);
 //   D. expands its spikes into (local target | inh flag, weight) entries, written with
-//      device-scope stores at slots taken from per-destination LDS cursors, waits for its
-//      stores to complete, then publishes one tagged count word per destination.
+//      device-scope stores at slots taken from per-destination LDS cursors; each wave waits
+//      for its own stores to complete and publishes the tagged count words of the
+//      destinations it wrote (all waves' stores first when an entry overflowed the slots).
 //
 // Input sums are integers, so they do not depend on the order in which entries arrive:
-//   * one weight per projection (homogeneous): the word counts events, E in bits 0-31 and
-//     I in bits 32-63; the input is w added c times in one fp32 chain (c = count), which is
-//     what a sequential scatter of one repeated value gives in any order;
+//   * one weight per projection (homogeneous): the words count events; the input is w added
+//     c times in one fp32 chain (c = count), which is what a sequential scatter of one
+//     repeated value gives in any order;
 //   * per-synapse weights: each weight is rounded to a multiple of 2^-S (S per projection,
 //     fixed at prepare from the largest |w| and the largest in-degree so that no sum can
-//     leave int32), the E and I sums are kept as two's-complement 32-bit fields of the word
-//     (E = low half read as int32, I = the rest shifted down), and the input is the sum
+//     leave int32), the words hold the two's-complement int32 sums, and the input is the sum
 //     converted to fp32 (one rounding) times 2^-S.
 // Cross-workgroup data is only touched with device-scope loads/stores (emitted with the
 // device-coherence bit), so no L2 writeback/invalidate is ever needed (each costs ~5 us).
@@ -214,13 +214,7 @@ __device__ __forceinline__ Row row_of(const NetArgs& a, int32_t i) {
   return Row{a.idx_i + r, a.w_i ? a.w_i + r : nullptr, a.k_i, true};
 }
 
-// E / I fields of a neuron's 64-bit input word (see the header comment).
 constexpr int kTab = 256;  // repeated-sum table entries per kind (homogeneous weights)
-
-__device__ __forceinline__ int32_t acc_lo(uint64_t acc) { return (int32_t)(uint32_t)acc; }
-__device__ __forceinline__ int32_t acc_hi(uint64_t acc) {
-  return (int32_t)((acc - (uint64_t)(int64_t)acc_lo(acc)) >> 32);
-}
 
 // w added c times in one fp32 chain, from a table of the first kTab partial sums.
 __device__ __forceinline__ float repeated_sum(const float* tab, float w, uint32_t c) {
@@ -238,12 +232,21 @@ __device__ __forceinline__ int32_t quantize(float w, float scale) {
 
 template <class Model, int NPT, bool kHet>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
-                                                typename Model::Params p) {
+                                                typename Model::Params p_arg) {
+  // The parameters live in VGPRs (uniform values, one register each): the update reads them
+  // as vector operands, so they take no scalar registers in a loop that is short of them.
+  typename Model::Params p = p_arg;
+  {
+    static_assert(sizeof(p) % 4 == 0, "parameters are 32-bit words");
+    uint32_t* pw = reinterpret_cast<uint32_t*>(&p);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(p) / 4); ++i) asm volatile("" : "+v"(pw[i]));
+  }
   constexpr int kChunk = NPT * kBlock;
   constexpr int kBatch = 4;                   // phase A: entry loads in flight per thread
   constexpr int kChunks = 4;                  // phase D: 64-synapse chunks per wave and round
   constexpr int kSlots = NPT >= 8 ? 8 : 16;   // phase D: LDS slots per destination and round
-  __shared__ uint64_t s_acc[kChunk];          // input word per neuron: E bits 0-31, I 32-63
+  __shared__ uint32_t s_acc[2 * kChunk];      // input words per neuron: [2 loc] E, [2 loc + 1] I
   __shared__ float s_tab[2][kTab];            // homogeneous: repeated sums of w_e, w_i
   __shared__ uint32_t s_pos[kMaxBlocks];      // next inbox entry per destination (d <- me)
   __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
@@ -251,6 +254,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   __shared__ int32_t s_list[kChunk];          // this step's spikes: E from the front, I from the back
   __shared__ uint32_t s_nsp[2][2];            // (E, I) spike counts, by step parity
   __shared__ uint32_t s_hash;
+  __shared__ uint32_t s_ovf;                  // an entry of this step was stored past the slots
   __shared__ uint32_t s_junk[BS_WAVE];        // destination of the row prefetches (never read)
   __shared__ uint32_t s_rcnt[kMaxBlocks];     // expand round: entries per destination
   __shared__ uint64_t s_stage[kMaxBlocks * kSlots];  // expand round: per-destination slots
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     s_pos[s] = s_ofs_out[s];
     s_rcnt[s] = 0;
   }
-  for (int i = threadIdx.x; i < kChunk; i += kBlock) s_acc[i] = 0ull;
+  for (int i = threadIdx.x; i < 2 * kChunk; i += kBlock) s_acc[i] = 0u;
   // per-synapse weights: 2^S and 2^-S per kind; homogeneous: the repeated-sum tables
   float qscale[2] = {1.0f, 1.0f}, qinv[2] = {1.0f, 1.0f};
   if (kHet) {
@@ -283,6 +287,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       const int S = __builtin_amdgcn_readfirstlane(hdr->qexp[k]);
       qscale[k] = bs_pow2i(S);
       qinv[k] = bs_pow2i(-S);
+      asm volatile("" : "+v"(qscale[k]), "+v"(qinv[k]));
     }
   } else if (threadIdx.x == 0 || threadIdx.x == BS_WAVE) {
     const int k = threadIdx.x == 0 ? 0 : 1;
@@ -308,8 +313,12 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   int lgE = 0, lgI = 0;
   while ((BS_WAVE << lgE) < a.k_e) ++lgE;
   while ((BS_WAVE << lgI) < a.k_i) ++lgI;
+  // values used only in vector arithmetic and addresses: VGPRs, like the parameters
+  asm volatile("" : "+v"(a.idx_e), "+v"(a.w_e), "+v"(a.idx_i), "+v"(a.w_i));
+  asm volatile("" : "+v"(a.n_exc), "+v"(a.k_e), "+v"(a.k_i), "+v"(a.w_e_homo), "+v"(a.w_i_homo));
   if (threadIdx.x == 0) {
     s_nsp[0][0] = s_nsp[0][1] = s_nsp[1][0] = s_nsp[1][1] = 0;
+    s_ovf = 0u;
     s_hash = 0;
   }
   int tps = 1;  // threads per source in phase A (power of two, tps * nb <= kBlock)
@@ -394,16 +403,11 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           for (int u = 0; u < kBatch; ++u) {
             if (e0 + u * tps < c) {
               const uint32_t tgt = (uint32_t)ent[u];
-              const bool inh = (tgt & kInhFlag) != 0;
-              // per-synapse: the signed fixed-point weight into the E field (sign-extended,
-              // so a negative E sum borrows from the I field and is read back exactly) or
-              // the I field; homogeneous: one event count
-              const uint64_t add =
-                  kHet ? (inh ? (ent[u] & 0xFFFFFFFF00000000ull)
-                              : (uint64_t)(int64_t)(int32_t)(uint32_t)(ent[u] >> 32))
-                       : (inh ? (1ull << 32) : 1ull);
+              // per-synapse: the fixed-point weight (two's complement); homogeneous: one event
+              const uint32_t add = kHet ? (uint32_t)(ent[u] >> 32) : 1u;
               const uint32_t loc = tgt & ~kInhFlag;
-              if (loc < (uint32_t)kChunk) atomicAdd(&s_acc[loc], add);
+              if (loc < (uint32_t)kChunk)
+                atomicAdd(&s_acc[2 * loc + ((tgt & kInhFlag) ? 1 : 0)], add);
             }
           }
         }
@@ -419,15 +423,15 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       const int loc = q * kBlock + threadIdx.x;
       last[q] = false;
       if (j < n) {
-        const uint64_t acc = s_acc[loc];
-        s_acc[loc] = 0ull;
+        const uint2 acc = *(uint2*)&s_acc[2 * loc];
+        *(uint2*)&s_acc[2 * loc] = make_uint2(0u, 0u);
         float in_e, in_i;
         if (kHet) {
-          in_e = (float)acc_lo(acc) * qinv[0];
-          in_i = (float)acc_hi(acc) * qinv[1];
+          in_e = (float)(int32_t)acc.x * qinv[0];
+          in_i = (float)(int32_t)acc.y * qinv[1];
         } else {
-          in_e = repeated_sum(s_tab[0], a.w_e_homo, (uint32_t)acc);
-          in_i = repeated_sum(s_tab[1], a.w_i_homo, (uint32_t)(acc >> 32));
+          in_e = repeated_sum(s_tab[0], a.w_e_homo, acc.x);
+          in_i = repeated_sum(s_tab[1], a.w_i_homo, acc.y);
         }
         last[q] = Model::update(p, r[q], in_e, in_i);
         if (last[q]) h += bs_mix32((uint32_t)j);
@@ -534,6 +538,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           if (rk < (uint32_t)kSlots) {
             s_stage[d * kSlots + rk] = ent;
           } else {  // slots full: store this one directly
+            s_ovf = 1u;
             const uint32_t pos = s_pos[d] + rk;
             if (kHet) st_dev64((uint64_t*)ob + pos, ent);
             else st_dev32((uint32_t*)ob + pos, (uint32_t)ent);
@@ -560,13 +565,24 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       if (rnd + 1 < rounds) __syncthreads();  // slots and round counts are reused
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
-    __syncthreads();
+    // Destination d's staged entries were all written by the wave of write-out slots
+    // [d*kSlots, (d+1)*kSlots), so that wave alone publishes d once its own stores are
+    // complete -- unless an entry went past the slots (stored by another wave): then every
+    // wave's stores are awaited first.
+    const bool ovf = rounds > 0 && s_ovf != 0u;   // uniform: set before the round barrier
+    if (ovf) __syncthreads();
     {
       uint64_t* cout = cnt + (int64_t)slot_wr * nb * nb;
       const uint64_t tag = (uint64_t)(uint32_t)(ta + 1) << 32;
-      for (int d = threadIdx.x; d < nb; d += kBlock) {
+      for (int x = threadIdx.x; x < nb * kSlots; x += kBlock) {
+        if (x % kSlots) continue;
+        const int d = x / kSlots;
         st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - s_ofs_out[d]));
         s_pos[d] = s_ofs_out[d];
+      }
+      if (ovf) {
+        __syncthreads();
+        if (threadIdx.x == 0) s_ovf = 0u;
       }
       // Clear the counters this step used: every read of them came before the barrier
       // above, and their next user is step ta+2, whose adds follow step ta+1's final
