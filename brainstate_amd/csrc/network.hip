@@ -49,7 +49,7 @@ namespace {
 
 constexpr int kBlock = 1024;
 constexpr int kWaves = kBlock / BS_WAVE;
-constexpr int kMaxBlocks = 512;
+constexpr int kMaxBlocks = 256;
 constexpr int kMaxNpt = 8;
 constexpr uint32_t kInhFlag = 0x80000000u;
 constexpr uint64_t kSpinLimit = 1ull << 24;
@@ -197,6 +197,14 @@ struct HhModel {
   // threshold) made the step slower, not faster.
   __device__ static bool near(const Params&, const Regs&) { return false; }
 };
+
+// Load through a global-memory pointer.  The row pointers are held in VGPRs through an
+// empty asm statement, after which the compiler no longer knows their address space and
+// would emit flat loads.
+template <class T>
+__device__ __forceinline__ T ld_global(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
 
 // Synapse row of neuron i (global index) in the E or I connectivity.
 struct Row {
@@ -497,13 +505,14 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     constexpr uint32_t kPer = kWaves * kChunks;
     const uint32_t rounds = (G + kPer - 1) / kPer;
     for (uint32_t rnd = 0; rnd < rounds; ++rnd) {
+      // all chunk loads of the round are issued before any of them is used
       int32_t tgt[kChunks];
-      int32_t wq[kChunks];  // fixed-point weights (per-synapse weights only)
+      float wraw[kChunks];  // per-synapse weights only
       bool inh[kChunks];
 #pragma unroll
       for (int u = 0; u < kChunks; ++u) {
         tgt[u] = -1;
-        wq[u] = 0;
+        wraw[u] = 0.0f;
         inh[u] = false;
         const uint32_t g = rnd * kPer + (uint32_t)(u * kWaves + wid);
         if (g < G) {
@@ -521,12 +530,16 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           const Row rw = row_of(a, jw);
           const int32_t tt = (int32_t)(c * BS_WAVE) + lane;
           if (tt < rw.k) {
-            tgt[u] = rw.idx[tt];
-            if (kHet) wq[u] = quantize(rw.w[tt], rw.inh ? qscale[1] : qscale[0]);
+            tgt[u] = ld_global(rw.idx + tt);
+            if (kHet) wraw[u] = ld_global(rw.w + tt);
             inh[u] = rw.inh;
           }
         }
       }
+      int32_t wq[kChunks];  // fixed-point weights
+#pragma unroll
+      for (int u = 0; u < kChunks; ++u)
+        wq[u] = kHet ? quantize(wraw[u], inh[u] ? qscale[1] : qscale[0]) : 0;
 #pragma unroll
       for (int u = 0; u < kChunks; ++u) {
         if ((uint32_t)tgt[u] < (uint32_t)n) {
