@@ -68,6 +68,9 @@ SIGNATURES = {
     'bs_spike_compact_workspace_size': (c_size, [c_i32]),
     'bs_spike_compact': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]),
     'bs_spike_compact_noalloc': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    'bs_exp_euler_f32': (ctypes.c_int, [ctypes.c_int64, c_vp, c_vp, c_vp, c_f32, c_vp, c_vp]),
+    'bs_exp_euler_f64': (ctypes.c_int, [ctypes.c_int64, c_vp, c_vp, c_vp, ctypes.c_double, c_vp,
+                                        c_vp]),
     'bs_event_scatter_f32': (ctypes.c_int, [c_vp, c_vp, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,
                                             c_i32, c_vp, c_i32, c_vp]),
     'bs_event_matvec_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp, c_i32, c_vp, c_f32,

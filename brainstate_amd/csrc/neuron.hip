@@ -67,6 +67,38 @@ __global__ __launch_bounds__(kBlock) void k_hh_step(int32_t n, float* __restrict
   }
 }
 
+// Exponential Euler of a general drift (brainstate/nn/_exp_euler.py:226-249):
+//   out = x + (dt * exprel(dt * J)) * f,  one fused multiply-add, as the fused updates write
+// it, so a drift and Jacobian that equal theirs give their bits.
+__global__ __launch_bounds__(kBlock) void k_exp_euler_f32(int64_t n, const float* __restrict__ x,
+                                                         const float* __restrict__ f,
+                                                         const float* __restrict__ jac, float dt,
+                                                         float* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kBlock) {
+    const float phi = bs_exprel(dt * jac[i]);
+    out[i] = bs_fma(dt * phi, f[i], x[i]);
+  }
+}
+
+// Double-precision exprel: series below 1e-3 (truncation < 1e-13 relative), expm1(z) / z
+// elsewhere.
+__device__ __forceinline__ double exprel_f64(double z) {
+  if (fabs(z) < 1e-3) return 1.0 + z * (0.5 + z * (1.0 / 6.0 + z * (1.0 / 24.0 + z / 120.0)));
+  return expm1(z) / z;
+}
+
+__global__ __launch_bounds__(kBlock) void k_exp_euler_f64(int64_t n, const double* __restrict__ x,
+                                                         const double* __restrict__ f,
+                                                         const double* __restrict__ jac,
+                                                         double dt, double* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kBlock) {
+    const double phi = exprel_f64(dt * jac[i]);
+    out[i] = fma(dt * phi, f[i], x[i]);
+  }
+}
+
 int grid(int32_t n) {
   int64_t b = ((int64_t)n + kBlock - 1) / kBlock;
   const int64_t cap = (int64_t)bs_num_cus() * 16;
@@ -116,6 +148,32 @@ extern "C" int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* n
   BS_CHECK_ARG(V && m && h && ng && ge && gi, "bs_coba_hh_step: NULL state pointer");
   k_hh_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng, ge, gi, in_e, in_i, *p,
                                                         spk_out);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_exp_euler_f32(int64_t n, const float* x, const float* drift, const float* jac,
+                                float dt, float* out, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0 && n < ((int64_t)1 << 40), "bs_exp_euler_f32: n=%lld out of range",
+               (long long)n);
+  if (n == 0) return BS_OK;
+  BS_CHECK_ARG(x && drift && jac && out, "bs_exp_euler_f32: NULL pointer");
+  const int g = grid((int32_t)(n < (1 << 30) ? n : (1 << 30)));
+  k_exp_euler_f32<<<g, kBlock, 0, bs_stream(stream)>>>(n, x, drift, jac, dt, out);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_exp_euler_f64(int64_t n, const double* x, const double* drift,
+                                const double* jac, double dt, double* out, bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(n >= 0 && n < ((int64_t)1 << 40), "bs_exp_euler_f64: n=%lld out of range",
+               (long long)n);
+  if (n == 0) return BS_OK;
+  BS_CHECK_ARG(x && drift && jac && out, "bs_exp_euler_f64: NULL pointer");
+  const int g = grid((int32_t)(n < (1 << 30) ? n : (1 << 30)));
+  k_exp_euler_f64<<<g, kBlock, 0, bs_stream(stream)>>>(n, x, drift, jac, dt, out);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

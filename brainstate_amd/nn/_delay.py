@@ -296,8 +296,46 @@ class DelayAccess(Module):
         return self.delay.at(self._delay_entry)
 
 
+def _interpolation_of(interpolation, interp_method):
+    """The interpolation a Delay reads with: ``interpolation`` when given, else the deprecated
+    ``interp_method`` spelled through its alias; a registered method name or a callable."""
+    choice = interpolation
+    if choice is None:
+        choice = INTERP_ALIAS_MAP.get(interp_method, interp_method)
+    if callable(choice):
+        return choice
+    if not isinstance(choice, str):
+        raise TypeError(f'interpolation must be str or callable, got {type(choice)}')
+    methods = InterpolationRegistry.list_methods()
+    if choice not in methods:
+        raise ValueError(f'Unknown interpolation method: {choice}. '
+                         f'Available methods: {methods}')
+    return choice
+
+
+def _valid_init(init):
+    """History before the first update: None (zeros), a number, an array or a callable."""
+    if init is None or callable(init) or \
+            isinstance(init, (numbers.Number, np.ndarray, torch.Tensor)):
+        return init
+    raise TypeError(f'init should be Array, Callable, or None. But got {init}')
+
+
+def _slots_every(update_every, dt):
+    """(update_every, steps per history slot): a slot per step unless update_every is set."""
+    if update_every is None:
+        return None, 1
+    if update_every < dt:
+        raise ValueError(f'update_every must be >= dt ({dt}), got {update_every}')
+    return update_every, int(update_every / dt)
+
+
 class Delay(Module):
-    """Delay variable for short-term history (:399-957); history resident in device memory."""
+    """Delay variable for short-term history (:399-957); history resident in device memory.
+
+    ``delay_method`` is accepted for compatibility only ('concat' warns): every history is one
+    ring of ``max_length`` slots.  A registered read (``register_entry`` / ``register_delay``)
+    widens the ring to cover it and is answered from the slot it names."""
     __module__ = 'brainstate_amd.nn'
     _init_last = True
 
@@ -305,52 +343,31 @@ class Delay(Module):
                  take_aware_unit=False, update_every=None, delay_method=_DELAY_ROTATE,
                  interp_method=_INTERP_LINEAR):
         super().__init__()
-        self.target_info = None if target_info is None else _tree_map(_info_of, target_info)
-        if delay_method is None:
-            delay_method = _DELAY_ROTATE
         if delay_method == _DELAY_CONCAT:
             warnings.warn("delay_method='concat' is deprecated. The unified ring buffer "
                           "implementation now uses rotation for all delays, providing better "
                           "performance.", DeprecationWarning, stacklevel=2)
         self.delay_method = _DELAY_ROTATE
-        if interpolation is None:
-            interpolation = INTERP_ALIAS_MAP.get(interp_method, interp_method)
-        if isinstance(interpolation, str):
-            if interpolation not in InterpolationRegistry.list_methods():
-                raise ValueError(f'Unknown interpolation method: {interpolation}. '
-                                 f'Available methods: {InterpolationRegistry.list_methods()}')
-            self.interp_method = interpolation
-        elif callable(interpolation):
-            self.interp_method = interpolation
-        else:
-            raise TypeError(f'interpolation must be str or callable, got {type(interpolation)}')
-        dt = environ.get_dt()
-        self.max_time, length = _get_delay(time, dt if update_every is None else update_every)
-        self.max_length = length + 1
-        if init is not None and not isinstance(init, (numbers.Number, np.ndarray, torch.Tensor)) \
-                and not callable(init):
-            raise TypeError(f'init should be Array, Callable, or None. But got {init}')
-        self._init = init
-        self.take_aware_unit = take_aware_unit
+        self.interp_method = _interpolation_of(interpolation, interp_method)
+        self._init = _valid_init(init)
+        self.update_every, self.update_every_step = _slots_every(update_every,
+                                                                 environ.get_dt())
+        self.target_info = None if target_info is None else _tree_map(_info_of, target_info)
+        self.max_time, steps = _get_delay(time, self._slot_dt())
+        self.max_length = steps + 1
+        self.take_aware_unit = take_aware_unit   # units are not modelled here
         self._unit = None
-        if update_every is not None:
-            if update_every < dt:
-                raise ValueError(f'update_every must be >= dt ({dt}), got {update_every}')
-            self.update_every = update_every
-            self.update_every_step = int(update_every / dt)
-        else:
-            self.update_every = None
-            self.update_every_step = 1
-        self._registered_entries = dict()
-        self._reads = dict()
+        self._registered_entries = {}
+        self._reads = {}
         self.history = None
         self.write_ptr = None
-        if entries is not None:
-            for entry, time_and_idx in entries.items():
-                if isinstance(time_and_idx, (tuple, list)):
-                    self.register_entry(entry, *time_and_idx)
-                else:
-                    self.register_entry(entry, time_and_idx)
+        for entry, spec in (entries or {}).items():
+            self.register_entry(entry, *(tuple(spec) if isinstance(spec, (tuple, list))
+                                         else (spec,)))
+
+    def _slot_dt(self):
+        """Time between history slots."""
+        return environ.get_dt() if self.update_every is None else self.update_every
 
     # -- state
     def _f_to_init(self, info, batch_size, length):
@@ -379,29 +396,30 @@ class Delay(Module):
 
     # -- registration
     def register_delay(self, *time_and_idx):
+        """A read ``time`` back (then integer indices into the delayed value): grows the ring
+        to hold it and returns the ``(steps, *indices)`` that ``retrieve_at_step`` takes, or
+        None for a read of the latest value (time None)."""
         assert len(time_and_idx) >= 1, 'You should provide at least one delay time.'
-        for d in time_and_idx[1:]:
-            assert _is_integer(d), f'The index should be integer. But got {d}.'
-        if time_and_idx[0] is None:
+        time, *indices = time_and_idx
+        for i in indices:
+            assert _is_integer(i), f'The index should be integer. But got {i}.'
+        if time is None:
             return None
-        time, delay_step = _get_delay(time_and_idx[0], environ.get_dt()
-                                      if self.update_every is None else self.update_every)
-        max_delay_step = int(np.max(delay_step))
-        self.max_time = max(float(self.max_time), float(np.max(_index_array(time))))
-        if self.max_length <= max_delay_step + 1:
-            self.max_length = int(max_delay_step + 1)
-        return (delay_step, *time_and_idx[1:])
+        when, steps = _get_delay(time, self._slot_dt())
+        self.max_time = max(float(self.max_time), float(np.max(_index_array(when))))
+        self.max_length = max(self.max_length, int(np.max(steps)) + 1)
+        return (steps, *indices)
 
     def register_entry(self, entry, *time_and_idx):
-        if entry in self._registered_entries:
+        """Name a read for ``at(entry)``; one read per name."""
+        known = self._registered_entries
+        if entry in known:
             raise KeyError(f'Entry {entry} has been registered. '
-                           f'The existing delay for the key {entry} is '
-                           f'{self._registered_entries[entry]}. '
+                           f'The existing delay for the key {entry} is {known[entry]}. '
                            f'The new delay for the key {entry} is {time_and_idx}. '
                            f'You can use another key. ')
-        delay_info = self.register_delay(*time_and_idx)
-        self._registered_entries[entry] = delay_info
-        return delay_info
+        known[entry] = self.register_delay(*time_and_idx)
+        return known[entry]
 
     def access(self, entry, *time_and_idx):
         return DelayAccess(self, *time_and_idx, entry=entry)
@@ -563,12 +581,32 @@ def not_receive_update_output(obj):
     return obj
 
 
-def _prefetch_item(target):
-    item = getattr(target.module, target.item, None)
-    if item is None:
-        raise AttributeError(f'The target {target.module} should have an `{target.item}` '
-                             f'attribute.')
-    return item
+def _attr_of(module, item):
+    """``module.<item>``: a State or a plain attribute (missing or None raises)."""
+    obj = getattr(module, item, None)
+    if obj is None:
+        raise AttributeError(f'The target {module} should have an `{item}` attribute.')
+    return obj
+
+
+def _require_dynamics(module):
+    if not isinstance(module, Dynamics):
+        raise AssertionError('The module should be an instance of Dynamics.')
+
+
+def _shared_hook(module, key, build):
+    """The after-update hook ``key`` of ``module``; ``build()`` makes and registers it on the
+    first request, so every delayed read of one source shares one history."""
+    if not module.has_after_update(key):
+        module.add_after_update(key, build())
+    return module.get_after_update(key)
+
+
+def _read_spec(args):
+    """Delay arguments as ``(time, *indices)``, given flat or as one tuple / list."""
+    if len(args) == 1 and isinstance(args[0], (tuple, list)):
+        return tuple(args[0])
+    return tuple(args)
 
 
 class Prefetch(Module):
@@ -580,81 +618,76 @@ class Prefetch(Module):
         self.module = module
         self.item = item
 
+    def get_item(self):
+        return _attr_of(self.module, self.item)
+
+    def get_item_value(self):
+        obj = self.get_item()
+        return obj.value if isinstance(obj, State) else obj
+
+    def __call__(self, *args, **kwargs):
+        return self.get_item_value()
+
     @property
     def delay(self):
         return PrefetchDelay(self.module, self.item)
 
-    def __call__(self, *args, **kwargs):
-        item = _prefetch_item(self)
-        return item.value if isinstance(item, State) else item
 
-    def get_item_value(self):
-        return self()
-
-    def get_item(self):
-        return _prefetch_item(self)
-
-
-class PrefetchDelay(Module):
+class PrefetchDelay(Prefetch):
     """``prefetch(item).delay``; ``.at(time)`` registers a delayed read (:608-653)."""
     __module__ = 'brainstate_amd.nn'
-
-    def __init__(self, module, item):
-        super().__init__()
-        self.module = module
-        self.item = item
 
     def at(self, *delay_time):
         return PrefetchDelayAt(self.module, self.item, delay_time)
 
 
 class PrefetchDelayAt(Module):
-    """A module state read ``time`` ago through a StateWithDelay after-update hook
-    (:655-745)."""
+    """``module.<item>`` read ``time`` ago (:655-745).  The values are recorded by one
+    StateWithDelay per (item, update_every), an after-update hook of the module that records
+    after every update; with no time the read is the current value."""
     __module__ = 'brainstate_amd.nn'
 
     def __init__(self, module, item, *time_and_index, delay_init=None, interpolation=None,
                  update_every=None, **kwargs):
         super().__init__()
-        assert isinstance(module, Dynamics), 'The module should be an instance of Dynamics.'
+        _require_dynamics(module)
         self.module = module
         self.item = item
-        if len(time_and_index) == 1 and isinstance(time_and_index[0], (tuple, list)):
-            time_and_index = time_and_index[0]
-        if not isinstance(time_and_index, (tuple, list)):
-            time_and_index = (time_and_index,)
-        self.delay_time = time_and_index
-        if len(time_and_index) > 0:
-            key = f'{item}-prefetch-delay-{update_every}'
-            if not module.has_after_update(key):
-                delay = StateWithDelay(module, item, init=delay_init, interpolation=interpolation,
-                                       update_every=update_every, **kwargs)
-                module.add_after_update(key, not_receive_update_output(delay))
-            self.state_delay = module.get_after_update(key)
-            self.delay_info = self.state_delay.register_delay(*time_and_index)
+        self.delay_time = _read_spec(time_and_index)
+        self.state_delay = None
+        self.delay_info = None
+        if self.delay_time:
+            def build():
+                return not_receive_update_output(StateWithDelay(
+                    module, item, init=delay_init, interpolation=interpolation,
+                    update_every=update_every, **kwargs))
+            self.state_delay = _shared_hook(module, f'{item}-prefetch-delay-{update_every}',
+                                            build)
+            self.delay_info = self.state_delay.register_delay(*self.delay_time)
 
     def __call__(self, *args, **kwargs):
-        if len(self.delay_time) == 0:
-            return _prefetch_item(self).value
+        if self.state_delay is None:
+            return _attr_of(self.module, self.item).value
         return self.state_delay.retrieve_at_step(*self.delay_info)
 
 
 class OutputDelayAt(Module):
-    """The module's update output read ``time`` ago (:748-800)."""
+    """The module's update output read ``time`` ago (:748-800): one Delay per update_every,
+    an after-update hook that receives each update's return value."""
     __module__ = 'brainstate_amd.nn'
 
     def __init__(self, module, *delay_time, delay_init=None, interpolation=None,
                  update_every=None, **kwargs):
         super().__init__()
-        assert isinstance(module, Dynamics), 'The module should be an instance of Dynamics.'
+        _require_dynamics(module)
         self.module = module
-        key = f'output-delay-{update_every}'
-        if not module.has_after_update(key):
-            delay = Delay(ShapeDtype(tuple(module.out_size), torch.float32), take_aware_unit=True,
-                          init=delay_init, interpolation=interpolation, update_every=update_every,
-                          **kwargs)
-            module.add_after_update(key, receive_update_output(delay))
-        self.out_delay = module.get_after_update(key)
+
+        def build():
+            return receive_update_output(Delay(
+                ShapeDtype(tuple(module.out_size), torch.float32), take_aware_unit=True,
+                init=delay_init, interpolation=interpolation, update_every=update_every,
+                **kwargs))
+        self.out_delay = _shared_hook(module, f'output-delay-{update_every}', build)
         self.delay_info = self.out_delay.register_delay(*delay_time)
 
     def __call__(self, *args, **kwargs):

@@ -286,6 +286,17 @@ typedef struct {
   float ENa, gNa, EK, gK, EL, gL, inv_C, V_th, I_ext, E_e, E_i, dt, decay_e, decay_i;
 } bs_hh_params;   /* inv_C = fp32(1/C) */
 
+/* One exponential-Euler step of a general drift, elementwise over n values:
+ *   out = x + (dt * exprel(dt * jac)) * drift     (one fused multiply-add; exprel as above)
+ * drift = f(x, ...) and jac = the vector-Jacobian product of f with ones (the diagonal of
+ * df/dx for an elementwise f), both computed by the caller.  Replaces the arithmetic of
+ * brainstate.nn.exp_euler_step (brainstate/nn/_exp_euler.py:206-249).  out may alias x.
+ * The f64 form uses exprel(z) = expm1(z) / z (series below |z| = 1e-3). */
+BS_API int bs_exp_euler_f32(int64_t n, const float* x, const float* drift, const float* jac,
+                            float dt, float* out, bs_stream_t stream);
+BS_API int bs_exp_euler_f64(int64_t n, const double* x, const double* drift, const double* jac,
+                            double dt, double* out, bs_stream_t stream);
+
 /* Gates at steady state for V (examples/100_hh_neuron_model.py:66-70). */
 BS_API int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng, bs_stream_t stream);
 BS_API int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge, float* gi,

@@ -122,3 +122,13 @@ def test_module_tree_and_init_order():
     net = Net()
     bs.nn.init_all_states(net)
     assert log[0] is net.b[0] and log[1] is net.a
+
+
+def test_exp_euler_operand_check_rejects_host_tensors():
+    """exp_euler_step's kernel launch is preceded by a host check: a host tensor (or a size
+    or layout mismatch) raises instead of reaching the kernel as a host pointer."""
+    import torch
+    from brainstate_amd.nn import _exp_euler
+    x = torch.zeros(4)
+    with pytest.raises(ValueError, match='on a GPU'):
+        _exp_euler._check_operands((x, x, x, x), 4)
