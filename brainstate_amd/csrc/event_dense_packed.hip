@@ -518,6 +518,22 @@ extern "C" int bs_event_dense_packed_lif_step(const void* spk, int32_t spk_dtype
   BS_CHECK_ARG(p != nullptr, "%s: params are NULL", fn);
   BS_CHECK_ARG((int64_t)batch * n_out <= 0 || (V && ge && gi && ref), "%s: NULL state pointer",
                fn);
+  // Workgroups of other column tiles read the spikes of a batch row while one writes that
+  // row's outputs, so no output may share memory with the spike input (a recurrent caller
+  // passing one buffer as both would read spikes of this step).
+  if ((int64_t)batch * n_in > 0 && (int64_t)batch * n_out > 0 && spk != nullptr) {
+    const uintptr_t s0 = (uintptr_t)spk;
+    const uintptr_t s1 = s0 + (uintptr_t)batch * n_in * (spk_dtype == BS_SPK_F32 ? 4 : 1);
+    const uintptr_t no = (uintptr_t)batch * n_out;
+    auto overlaps = [&](const void* q, uintptr_t bytes) {
+      const uintptr_t q0 = (uintptr_t)q;
+      return q != nullptr && q0 < s1 && s0 < q0 + bytes;
+    };
+    BS_CHECK_ARG(!overlaps(spk_out, no) && !overlaps(cur_out, 4 * no) && !overlaps(V, 4 * no) &&
+                     !overlaps(ge, 4 * no) && !overlaps(gi, 4 * no) && !overlaps(ref, 4 * no),
+                 "%s: an output (spk_out, cur_out or the neuron state) overlaps the spike input",
+                 fn);
+  }
   LifOut lif{V, ge, gi, ref, spk_out, inh ? 1 : 0, *p};
   return packed_product(fn, spk, spk_dtype, batch, n_in, packed, n_out, cur_out, &lif,
                         bs_stream(stream));

@@ -182,15 +182,20 @@ def _ext_input(x):
 
 class LIFRef(_COBANeuron, _Describable):
     """Leaky integrate-and-fire with refractory period; ``spk_reset='hard'`` sets V_reset after
-    a spike, ``'soft'`` subtracts V_th - V_reset."""
+    a spike, ``'soft'`` subtracts V_th - V_reset.  ``ref_rule`` fixes how many steps tau_ref
+    holds a neuron after its spike step: ``'open'`` those with k*dt < tau_ref, ``'closed'``
+    those with k*dt <= tau_ref (one more when tau_ref is a multiple of dt)."""
     __module__ = 'brainstate_amd.nn'
 
     def __init__(self, in_size, R=1., tau=5., tau_ref=5., V_th=1., V_reset=0., V_rest=0.,
-                 V_initializer=0., spk_reset='hard', name=None):
+                 V_initializer=0., spk_reset='hard', ref_rule='open', name=None):
         super().__init__(in_size, name=name)
         if spk_reset not in ('hard', 'soft'):
             raise ValueError(f"spk_reset must be 'hard' or 'soft', got {spk_reset!r}")
+        if ref_rule not in ('open', 'closed'):
+            raise ValueError(f"ref_rule must be 'open' or 'closed', got {ref_rule!r}")
         self.spk_reset = spk_reset
+        self.ref_rule = ref_rule
         self.R, self.tau, self.tau_ref = float(R), float(tau), float(tau_ref)
         self.V_th, self.V_reset, self.V_rest = float(V_th), float(V_reset), float(V_rest)
         self.V_initializer = V_initializer
@@ -208,11 +213,12 @@ class LIFRef(_COBANeuron, _Describable):
                                   tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
                                   tau_e=tau[0], tau_i=tau[1], dt=environ.get_dt(),
                                   out='cuba', scale_e=E[0], scale_i=E[1],
-                                  spk_reset=self.spk_reset)
+                                  spk_reset=self.spk_reset, ref_rule=self.ref_rule)
         return ops.lif_params(V_rest=self.V_rest, V_th=self.V_th, V_reset=self.V_reset,
                               tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
                               E_e=E[0], E_i=E[1], tau_e=tau[0], tau_i=tau[1],
-                              dt=environ.get_dt(), spk_reset=self.spk_reset)
+                              dt=environ.get_dt(), spk_reset=self.spk_reset,
+                              ref_rule=self.ref_rule)
 
     def update(self, x=0.):
         g, ins, E, tau = self._channel_args()

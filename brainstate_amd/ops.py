@@ -402,6 +402,11 @@ def event_dense_packed_lif_step(spk, P, V, ge, gi, ref, params, inh=False, cur_o
         if t.numel() != n or not t.is_contiguous() or t.dtype != dt:
             raise ValueError(f'event_dense_packed_lif_step: {name} must be contiguous {dt} '
                              f'with {n} elements')
+    lo, hi = s2.data_ptr(), s2.data_ptr() + s2.numel() * s2.element_size()
+    for name, t in (('spk_out', spk_out), ('cur_out', cur_out)):
+        if t is not None and t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * t.element_size():
+            raise ValueError(f'event_dense_packed_lif_step: {name} overlaps the spike input '
+                             f'(double-buffer the spikes of a recurrent step)')
     buf = P['packed']
     N.check(N.lib().bs_event_dense_packed_lif_step(
         N.ptr(s2), _spk_dtype(s2), B, n_in, N.ptr(buf), P['n_out'], 1 if inh else 0, N.ptr(V),
@@ -466,18 +471,28 @@ def conn_fixed_num_unique(seed, n_pre, k, n_post, device=None):
     return idx
 
 
+def refractory_steps(tau_ref, dt, rule='open'):
+    """Steps a neuron is held after its spike step: those k >= 1 with k*dt < tau_ref
+    (``rule='open'``, 49 at 5 ms / 0.1 ms) or k*dt <= tau_ref (``'closed'``, 50: the
+    ``t - t_last <= tau_ref`` test of BrainPy's LifRef taken on the exact dt grid)."""
+    if rule not in ('open', 'closed'):
+        raise ValueError(f"ref_rule must be 'open' or 'closed', got {rule!r}")
+    q = float(tau_ref) / float(dt)
+    n = int(np.ceil(q - 1e-9)) - 1 if rule == 'open' else int(np.floor(q + 1e-9))
+    return max(n, 0)
+
+
 def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., I_ext=20.,
                E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba', scale_e=1.,
-               scale_i=1., spk_reset='hard'):
+               scale_i=1., spk_reset='hard', ref_rule='open'):
     """bs_lif_params.  ``out='coba'``: synaptic current g * (E - V); ``out='cuba'``: g * scale
     (brainpy.state CUBA; E_e / E_i unused).  ``spk_reset='soft'``: a spike subtracts
-    V_th - V_reset from V instead of setting V_reset."""
+    V_th - V_reset from V instead of setting V_reset.  ``ref_rule``: refractory_steps."""
     if out not in ('coba', 'cuba'):
         raise ValueError(f"out must be 'coba' or 'cuba', got {out!r}")
     if spk_reset not in ('hard', 'soft'):
         raise ValueError(f"spk_reset must be 'hard' or 'soft', got {spk_reset!r}")
-    q = float(tau_ref) / float(dt)
-    ref_steps = max(int(np.ceil(q - 1e-9)) - 1, 0)
+    ref_steps = refractory_steps(tau_ref, dt, ref_rule)
     inv_tau = float(np.float32(1.0) / np.float32(tau))   # fp32 reciprocal of the constant
     return N.LifParams(V_rest, V_th, V_reset, inv_tau, R, I_ext, E_e, E_i, dt,
                        float(np.float32(np.exp(-dt / tau_e))),

@@ -272,6 +272,8 @@ BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* 
  * bs_coba_lif_step update of the [batch, n_out] state (V, ge, gi, ref) with in_e = cur,
  * in_i = 0 (inh = 0) or in_e = 0, in_i = cur (inh != 0).  The bits equal those two calls in
  * sequence.  cur_out (nullable) receives cur; spk_out (nullable) the spikes as 0/1 bytes.
+ * No output (spk_out, cur_out, V, ge, gi, ref) may overlap the spike input -- a recurrent
+ * caller double-buffers the spikes; an overlap is rejected with BS_ERR_INVALID.
  * Replaces EventLinear (brainstate/nn/_event_linear.py:99-100) followed by the Expon + COBA +
  * LIFRef update it feeds (brainstate/nn/_exp_euler.py:226-249). */
 BS_API int bs_event_dense_packed_lif_step(const void* spk, int32_t spk_dtype, int32_t batch,

@@ -23,7 +23,10 @@ from the equations and are **parity unpinned** beyond the checks above:
     multiplication, XLA's algebraic simplifier rewriting ``A / Const`` into
     ``A * InvertConstant(Const)``; the same holds for ``/ C`` and the HH rate scales.
   * LIFRef: a neuron is refractory for ``ref_steps`` steps after the spike step
-    (the steps with 0 < t - t_spike < tau_ref on the dt grid); V is held there.
+    (the steps with 0 < t - t_spike < tau_ref on the dt grid, or <= tau_ref with
+    ``ref_rule='closed'``); V is held there.  Which one brainpy.state uses is not pinned
+    (its ``t - t_last <= tau_ref`` in float32 gives 49, 50 or 51 steps at 5 ms / 0.1 ms
+    depending on how the absolute times round).
     Spike when V' >= V_th; hard reset V' = V_reset.
 HH (examples/100_hh_neuron_model.py:49-93, reference-held): rates from the old V, V
 and the gates each by exp-Euler from the old state, spike = (V < V_th) & (V' >= V_th).
@@ -53,10 +56,11 @@ def decay_factor(dt, tau):
     return F(np.exp(-float(dt) / float(tau)))
 
 
-def ref_steps(tau_ref, dt):
-    """Number of steps after a spike step with 0 < k*dt < tau_ref."""
+def ref_steps(tau_ref, dt, rule='open'):
+    """Number of steps after a spike step with 0 < k*dt < tau_ref (``'open'``) or
+    0 < k*dt <= tau_ref (``'closed'``, BrainPy's ``t - t_last <= tau_ref`` on the exact grid)."""
     q = float(tau_ref) / float(dt)
-    n = int(np.ceil(q - 1e-9)) - 1
+    n = int(np.ceil(q - 1e-9)) - 1 if rule == 'open' else int(np.floor(q + 1e-9))
     return max(n, 0)
 
 
@@ -68,7 +72,7 @@ class LIFParams:
 
     def __init__(self, V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5.,
                  I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba',
-                 scale_e=1., scale_i=1., spk_reset='hard'):
+                 scale_e=1., scale_i=1., spk_reset='hard', ref_rule='open'):
         self.cuba = out == 'cuba'
         self.soft_reset = spk_reset == 'soft'
         self.scale_e, self.scale_i = F(scale_e), F(scale_i)
@@ -79,7 +83,7 @@ class LIFParams:
         self.dt = F(dt)
         self.de = decay_factor(dt, tau_e)
         self.di = decay_factor(dt, tau_i)
-        self.ref_steps = I32(ref_steps(tau_ref, dt))
+        self.ref_steps = I32(ref_steps(tau_ref, dt, ref_rule))
 
 
 def lif_membrane(V, ge, gi, p):

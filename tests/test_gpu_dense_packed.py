@@ -230,3 +230,46 @@ def test_fused_lif_step_recurrent(torch_cuda, inh):
         x, ux = spk_d, us.view(B, n)
         fired += int(s_new.sum())
     assert fired > 100 or inh
+
+
+def test_packed_config4_against_float64_sum(torch_cuda):
+    """Config [4] (spikes [64, 4096] at 5 %, W [4096, 4096] ~ N(0, 1/64)): every output within
+    abs 1e-6 + rel 1e-5 of the float64 sum (the north_star tolerance, fixed, not scaled by
+    max|W|), and within the packed form's own bound 2^-24 max|W[:, j]| + half an ulp."""
+    torch = torch_cuda
+    say('packed config [4] vs float64')
+    rng = np.random.RandomState(11)
+    W = rng.normal(0, 0.125, (4096, 4096)).astype(F)
+    spk = (rng.rand(64, 4096) < 0.05).astype(np.uint8)
+    _, got = run(torch, spk, W)
+    exact = (spk != 0).astype(np.float64) @ W.astype(np.float64)
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.all(err <= 1e-6 + 1e-5 * np.abs(exact))
+    bound = 2.0 ** -24 * np.abs(W).max(0)[None, :] + 0.5 * np.spacing(np.abs(exact).astype(F))
+    assert np.all(err <= bound)
+
+
+def test_packed_lif_step_rejects_overlapping_outputs(torch_cuda):
+    """An output that shares memory with the spike input is refused by the wrapper and by
+    the C entry point (workgroups would read spikes another one already overwrote)."""
+    torch = torch_cuda
+    from brainstate_amd import _native as N
+    from brainstate_amd import ops
+    say('packed lif step overlap')
+    B, n = 4, 64
+    W = torch.from_numpy(np.random.RandomState(2).normal(0, 0.1, (n, n)).astype(F)).cuda()
+    P = ops.pack_dense(W)
+    buf = torch.zeros(B, n, dtype=torch.uint8, device='cuda')
+    V = torch.full((B * n,), -60.0, device='cuda')
+    ge, gi = torch.zeros(B * n, device='cuda'), torch.zeros(B * n, device='cuda')
+    ref = torch.zeros(B * n, dtype=torch.int32, device='cuda')
+    with pytest.raises(ValueError):
+        ops.event_dense_packed_lif_step(buf, P, V, ge, gi, ref, ops.lif_params(), spk_out=buf)
+    rc = N.lib().bs_event_dense_packed_lif_step(
+        N.ptr(buf), N.BS_SPK_U8, B, n, N.ptr(P['packed']), n, 0, N.ptr(V), N.ptr(ge), N.ptr(gi),
+        N.ptr(ref), ops.ctypes_ref(ops.lif_params()), None, N.ptr(buf),
+        N.stream_handle(buf.device))
+    assert rc == N.BS_ERR_INVALID and b'overlaps' in N.lib().bs_last_error()
+    out = torch.empty(B, n, dtype=torch.uint8, device='cuda')
+    ops.event_dense_packed_lif_step(buf, P, V, ge, gi, ref, ops.lif_params(), spk_out=out)
+    torch.cuda.synchronize()

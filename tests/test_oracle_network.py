@@ -26,6 +26,26 @@ def test_refractory_counts_steps_on_dt_grid():
     assert neuron.ref_steps(5.0, 0.1) == 49      # 0 < k*dt < 5 ms -> k = 1..49
     assert neuron.ref_steps(0.0, 0.1) == 0
     assert neuron.ref_steps(0.25, 0.1) == 2
+    assert neuron.ref_steps(5.0, 0.1, 'closed') == 50   # 0 < k*dt <= 5 ms -> k = 1..50
+    assert neuron.ref_steps(0.25, 0.1, 'closed') == 2
+    assert neuron.ref_steps(0.0, 0.1, 'closed') == 0
+
+
+def test_refractory_rules_against_exact_grid_counts():
+    """Both rules count k >= 1 with k*dt (<, <=) tau_ref in exact decimal arithmetic, for the
+    library's parameter builder and the oracle alike."""
+    from fractions import Fraction
+    from brainstate_amd import ops
+    for tau_ref, dt in [(5.0, 0.1), (2.0, 0.05), (0.3, 0.1), (1.0, 0.3), (3.0, 0.01),
+                        (0.0, 0.1), (0.05, 0.1), (10.0, 0.25)]:
+        T, D = Fraction(str(tau_ref)), Fraction(str(dt))
+        open_n = sum(1 for k in range(1, 100000) if k * D < T)
+        closed_n = sum(1 for k in range(1, 100000) if k * D <= T)
+        assert neuron.ref_steps(tau_ref, dt) == ops.refractory_steps(tau_ref, dt) == open_n
+        assert neuron.ref_steps(tau_ref, dt, 'closed') == \
+            ops.refractory_steps(tau_ref, dt, 'closed') == closed_n
+    with pytest.raises(ValueError):
+        ops.refractory_steps(5.0, 0.1, 'half-open')
 
 
 def test_lif_refractory_and_reset():
@@ -365,3 +385,46 @@ def test_c_hh_het_delay_equals_numpy_oracle():
     assert ref['counts'].sum() > 50
     assert counts.tolist() == ref['counts'].tolist()
     assert np.array_equal(st['V'], ref['V'])
+
+
+def _tut_params():
+    c = make_golden.TUT_NET
+    return neuron.LIFParams(V_rest=c['V_rest'], V_th=c['V_th'], V_reset=c['V_reset'],
+                            tau=c['tau'], tau_ref=0., tau_e=c['tau_e'], tau_i=c['tau_i'],
+                            I_ext=c['I_ext'], out='cuba', spk_reset='soft')
+
+
+def test_c_restatement_cuba_soft_reset_equals_golden():
+    """The tutorial net (CUBA outputs, soft reset, no refractory period) in the C
+    restatement equals the numpy oracle's golden run."""
+    with open(os.path.join(GOLD, 'tut_lif_soft_500.json')) as f:
+        gold = json.load(f)
+    c = make_golden.TUT_NET
+    pe, pi, V0, _ = make_golden.tut_net()
+    st = cbuild.lif_state(V0)
+    counts = np.zeros(c['steps'], np.int32)
+    cbuild.coba_lif_run(st, pe.idx, pi.idx, pe.w_scalar, pi.w_scalar, _tut_params(), c['n_exc'],
+                        c['steps'], nthreads=2, counts=counts)
+    assert counts.tolist() == gold['counts']
+    assert make_golden.sha(st['V']) == gold['final_V_sha256']
+
+
+def test_tutorial_spike_total_within_seed_spread():
+    """docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cell 14 prints 'total spikes:
+    4356' for its 400 E / 100 I soft-reset CUBA net over 200 ms.  Its connectivity (global
+    numpy stream, unseeded) and V0 (braintools / JAX stream) cannot be reproduced, so the
+    same net is run for 20 seeds: the printed total must lie within 3 standard deviations of
+    their mean (observed here: mean 4451.75, sd 46.3, range 4336-4531)."""
+    from oracle import network as onet
+    c = make_golden.TUT_NET
+    totals = []
+    for seed in range(20):
+        pe = onet.Projection(0, c['n_exc'], c['n'], c['p'], c['w_e'], seed=1000 + seed)
+        pi = onet.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=2000 + seed)
+        V0 = np.random.RandomState(3000 + seed).normal(-60., 10., c['n']).astype(F)
+        st = cbuild.lif_state(V0)
+        totals.append(cbuild.coba_lif_run(st, pe.idx, pi.idx, pe.w_scalar, pi.w_scalar,
+                                          _tut_params(), c['n_exc'], c['steps'], nthreads=1))
+    mean, sd = float(np.mean(totals)), float(np.std(totals, ddof=1))
+    assert abs(mean - 4451.75) < 1e-9 and abs(sd - 46.263) < 1e-3
+    assert abs(4356 - mean) < 3 * sd
