@@ -119,6 +119,7 @@ SIGNATURES = {
                                       c_vp, c_vp, c_vp, c_vp]),
     'bs_net_grid_blocks': (ctypes.c_int, [ctypes.POINTER(Net)]),
     'bs_net_error': (ctypes.c_int, [c_vp, c_vp]),
+    'bs_net_seed_spikes': (ctypes.c_int, [c_vp, c_vp, ctypes.c_int64, c_vp, c_vp]),
 }
 
 _lib = None

@@ -620,6 +620,59 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   }
 }
 
+// ---- seeding: a spike vector published as the events of step t0 - 1 ----
+// For a run that starts from a state with pending spikes (a loop handed over after some
+// steps elsewhere): workgroup s expands the spikes of its slice into its inboxes of ring
+// slot a.slot_wr, exactly as phase D of k_run would, and publishes every destination's count
+// word with the tag of step t0 - 1.  Synaptic delay 0 only.  Workgroups do not wait on one
+// another: plain launch.
+template <bool kHet>
+__global__ __launch_bounds__(kBlock) void k_seed(NetArgs a, const uint8_t* spk0, uint32_t tag) {
+  __shared__ uint32_t s_cnt[kMaxBlocks];
+  const NetLayout& L = a.L;
+  const int nb = L.nb;
+  const int me = blockIdx.x;
+  const int lane = bs_lane();
+  const int wid = threadIdx.x / BS_WAVE;
+  const WsHeader* hdr = (const WsHeader*)a.ws;
+  uint64_t* cnt = (uint64_t*)(a.ws + L.off_cnt);
+  const uint64_t* ofs = (const uint64_t*)(a.ws + L.off_ofs);
+  char* ob = a.ws + L.off_inbox + (size_t)a.slot_wr * (size_t)L.total * L.entry;
+  for (int d = threadIdx.x; d < nb; d += kBlock) s_cnt[d] = 0u;
+  float qscale[2] = {1.0f, 1.0f};
+  if (kHet) {
+    qscale[0] = bs_pow2i(hdr->qexp[0]);
+    qscale[1] = bs_pow2i(hdr->qexp[1]);
+  }
+  __syncthreads();
+  const int64_t chunk = (int64_t)1 << L.shift;
+  const int64_t lo = (int64_t)me * chunk;
+  const int64_t hi = lo + chunk < a.n ? lo + chunk : a.n;
+  for (int64_t i = lo + wid; i < hi; i += kWaves) {  // one row per wave and iteration
+    if (spk0[i] == 0) continue;
+    const Row rw = row_of(a, (int32_t)i);
+    for (int tt = lane; tt < rw.k; tt += BS_WAVE) {
+      const int32_t tgt = rw.idx[tt];
+      if ((uint32_t)tgt >= (uint32_t)a.n) continue;
+      const int d = tgt >> L.shift;
+      const uint32_t rk = atomicAdd(&s_cnt[d], 1u);
+      const uint32_t loc = (uint32_t)(tgt & (chunk - 1)) | (rw.inh ? kInhFlag : 0u);
+      const uint32_t pos = (uint32_t)ofs[(int64_t)d * nb + me] + rk;
+      if (kHet)
+        st_dev64((uint64_t*)ob + pos,
+                 ((uint64_t)(uint32_t)quantize(rw.w[tt], rw.inh ? qscale[1] : qscale[0]) << 32) |
+                     loc);
+      else
+        st_dev32((uint32_t*)ob + pos, loc);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
+  __syncthreads();
+  uint64_t* cout = cnt + (int64_t)a.slot_wr * nb * nb;
+  for (int d = threadIdx.x; d < nb; d += kBlock)
+    st_dev64(cout + (int64_t)d * nb + me, ((uint64_t)tag << 32) | s_cnt[d]);
+}
+
 // ---- setup: per-(source, destination) capacities and inbox offsets ----
 
 __global__ __launch_bounds__(kBlock) void k_caps(NetArgs a, uint32_t* cap) {
@@ -993,6 +1046,33 @@ extern "C" int bs_net_prepare(const bs_net* net, void* workspace, bs_stream_t st
   uint64_t* ofs = (uint64_t*)(ws + L.off_ofs);
   k_offsets<<<1, kBlock, 0, s>>>(L.nb, (const uint32_t*)(ws + L.off_cap), ofs,
                                  ofs + (int64_t)L.nb * L.nb);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+extern "C" int bs_net_seed_spikes(const bs_net* net, const uint8_t* spk, int64_t t0,
+                                  void* workspace, bs_stream_t stream) {
+  bs_clear_error();
+  int rc = check_net(net, "bs_net_seed_spikes");
+  if (rc) return rc;
+  BS_CHECK_ARG(spk != nullptr && workspace != nullptr, "bs_net_seed_spikes: NULL pointer");
+  BS_CHECK_ARG(net->delay_steps == 0,
+               "bs_net_seed_spikes: pending spikes can be seeded with synaptic delay 0 only "
+               "(delay_steps=%d)", net->delay_steps);
+  BS_CHECK_ARG(t0 >= 1 && t0 < ((int64_t)1 << 32) - 1, "bs_net_seed_spikes: t0=%lld outside "
+               "[1, 2^32 - 1)", (long long)t0);
+  NetLayout L;
+  if (plan(net, &L)) {
+    bs_set_error("bs_net_seed_spikes: n=%d too large for the grid", net->n);
+    return BS_ERR_UNSUPPORTED;
+  }
+  NetArgs a = make_args(net, L, workspace);
+  a.slot_wr = (int32_t)((t0 - 1) % L.ring);
+  hipStream_t s = bs_stream(stream);
+  if (net->w_e)
+    k_seed<true><<<L.nb, kBlock, 0, s>>>(a, spk, (uint32_t)t0);
+  else
+    k_seed<false><<<L.nb, kBlock, 0, s>>>(a, spk, (uint32_t)t0);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

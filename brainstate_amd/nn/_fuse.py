@@ -4,7 +4,9 @@
 (examples/105_COBA_HH_2007_braincell.py:54-82: ``N``, ``E`` fed by ``spk[:n_exc]``, ``I`` fed
 by ``spk[n_exc:]``) and returns an ``EINetRunner`` that advances the same network many steps
 per launch, with the constant external input ``inp`` the script passes as ``N(inp)``.
-``delay`` (ms) is the synaptic delay of a net whose projections read
+Spikes of the last step that the neurons hold (a loop stepped eagerly so far) become the
+runner's first inputs (synaptic delay 0).  ``delay`` (ms) is the synaptic delay of a net whose
+projections read
 ``N.prefetch_delay('spike', delay)()`` instead of the previous step's spikes; it becomes
 ceil(delay / dt) steps as brainstate's Delay computes them.  A net initialised with
 ``init_all_states(..., batch_size=B)`` ([B, n] states, the replicas sharing connectivity)
@@ -47,9 +49,13 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     if len(neuron._channels) != 2 or neuron._channels[0] is not proj_e or \
             neuron._channels[1] is not proj_i:
         raise ValueError('proj_e and proj_i must be the two projections onto neuron, in order')
-    if bool(neuron.spike.value.any()) or proj_e.syn.delta is not None or \
-            proj_i.syn.delta is not None:
-        raise NotImplementedError('fuse() starts from a state without pending spikes')
+    if proj_e.syn.delta is not None or proj_i.syn.delta is not None:
+        raise NotImplementedError('fuse() starts between steps (a synapse holds an input of a '
+                                  'step in progress)')
+    pending = bool(neuron.spike.value.any())
+    if pending and delay is not None:
+        raise NotImplementedError('fuse() with a synaptic delay starts from a state without '
+                                  'pending spikes')
     for hook in neuron.after_updates.values():   # spike histories of prefetch_delay readers
         hist = getattr(hook, 'history', None)
         if hist is not None and any(bool(h.any()) for h in _leaves(hist.value)):
@@ -110,6 +116,9 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
             neuron.m.value = from_runner(r.state['m'])
             neuron.h.value = from_runner(r.state['h'])
             neuron.n.value = from_runner(r.state['n'])
+
+    if pending:   # the spikes of the last step drive the runner's first step
+        r.seed(to_runner(neuron.spike.value.to(torch.uint8)), 1)
 
     r.write_back = write_back
     r.replica_index = perm   # runner neuron of (replica b, neuron j), for rasters

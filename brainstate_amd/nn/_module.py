@@ -6,9 +6,26 @@ before-update hooks run ahead of ``update`` and after-update hooks run after it
 synapses projecting onto it, the second how delays record a state after every step
 (``prefetch_delay`` / ``output_delay``, :222-298).
 """
+import contextlib
+import threading
 from collections import OrderedDict
 
 import numpy as np
+
+_calls = threading.local()
+
+
+@contextlib.contextmanager
+def record_calls():
+    """Record the outermost module calls made inside the block, as (module, args, kwargs)
+    in call order (calls a module makes of other modules are not listed)."""
+    log = []
+    prev = getattr(_calls, 'log', None), getattr(_calls, 'depth', 0)
+    _calls.log, _calls.depth = log, 0
+    try:
+        yield log
+    finally:
+        _calls.log, _calls.depth = prev
 
 
 def _size(x):
@@ -24,6 +41,18 @@ class Module:
         self.name = name
 
     def __call__(self, *args, **kwargs):
+        log = getattr(_calls, 'log', None)
+        if log is None:
+            return self._run(*args, **kwargs)
+        if _calls.depth == 0:
+            log.append((self, args, kwargs))
+        _calls.depth += 1
+        try:
+            return self._run(*args, **kwargs)
+        finally:
+            _calls.depth -= 1
+
+    def _run(self, *args, **kwargs):
         return self.update(*args, **kwargs)
 
     def update(self, *args, **kwargs):
@@ -133,7 +162,7 @@ class Dynamics(Module):
             if isinstance(fn, Module):
                 yield fn
 
-    def __call__(self, *args, **kwargs):
+    def _run(self, *args, **kwargs):
         for fn in self._before_updates.values():
             if hasattr(fn, '_receive_update_input'):
                 fn(*args, **kwargs)

@@ -87,6 +87,19 @@ class EINetRunner:
         N.check(N.lib().bs_net_prepare(ctypes.byref(self._net), N.ptr(self.ws),
                                        N.stream_handle(dev)), 'bs_net_prepare')
 
+    def seed(self, spk, t0=1):
+        """Take ``spk`` ([n], nonzero = spike) as the spikes of step t0 - 1, so that the next
+        run starts at step t0 >= 1 with their inputs (synaptic delay 0)."""
+        spk = torch.as_tensor(spk, device=self.device).reshape(-1)
+        if spk.numel() != self.n:
+            raise ValueError(f'seed: {spk.numel()} spikes for {self.n} neurons')
+        spk = (spk != 0).to(torch.uint8).contiguous()
+        N.check(N.lib().bs_net_seed_spikes(ctypes.byref(self._net), N.ptr(spk), int(t0),
+                                           N.ptr(self.ws), N.stream_handle(self.device)),
+                'bs_net_seed_spikes')
+        self.spk.copy_(spk)
+        self.t = int(t0)
+
     @property
     def grid_blocks(self):
         return int(N.lib().bs_net_grid_blocks(ctypes.byref(self._net)))

@@ -2,9 +2,10 @@
 
 The reference traces the step function once and runs it as an XLA While loop
 (brainstate/transform/_loop_collect_return.py:487-572).  Here each step launches the HIP
-kernels directly (no tracing); a network that fits the persistent runner runs whole loops
-in one launch via ``brainstate_amd.nn.fuse``.
+kernels directly; ``for_loop`` recognises the E/I network step from the module calls of its
+first two steps and runs the rest of the loop in the persistent runner (one launch).
 """
+import numpy as np
 import torch
 
 
@@ -23,13 +24,119 @@ def _stack(outs):
     return outs
 
 
+fuse_loops = True   # False: for_loop always steps eagerly
+last_loop = None    # how the last for_loop ran: 'fused' (persistent runner) or 'eager'
+
+
+def _ei_step(log, spk_before=None):
+    """The E/I step the persistent runner runs, read off the module calls one step made:
+    ``(neuron, proj_e, proj_i, n_exc, inp)`` when they were exactly the two projections onto
+    one LIFRef / HH population, each given spikes of the population's shape (E: its first
+    n_exc neurons, I: the rest) -- equal to ``spk_before``, its spikes before the step, when
+    given -- then that population with one constant input; else None."""
+    from .nn._event import FixedPostNumConn
+    from .nn._neurons import HH, AlignPostProj, LIFRef
+    if len(log) != 3:
+        return None
+    (pa, aa, ka), (pb, ab, kb), (neuron, an, kn) = log
+    if not isinstance(neuron, (LIFRef, HH)) or ka or kb or kn or len(an) > 1:
+        return None
+    chans = getattr(neuron, '_channels', [])
+    if len(chans) != 2 or {id(pa), id(pb)} != {id(c) for c in chans}:
+        return None
+    proj_e, proj_i = chans
+    if not (isinstance(proj_e, AlignPostProj) and isinstance(proj_i, AlignPostProj)):
+        return None
+    conns = [getattr(p.comm, 'conn', None) for p in chans]
+    if not all(isinstance(c, FixedPostNumConn) for c in conns):
+        return None
+    n, n_exc = neuron.num, conns[0].shape[0]
+    if conns[0].shape != (n_exc, n) or conns[1].shape != (n - n_exc, n):
+        return None
+    shape = tuple(neuron.spike.value.shape)
+    given = {id(pa): aa, id(pb): ab}
+    for proj, lo, hi in ((proj_e, 0, n_exc), (proj_i, n_exc, n)):
+        args = given[id(proj)]
+        if len(args) != 1 or not torch.is_tensor(args[0]) or \
+                tuple(args[0].shape) != shape[:-1] + (hi - lo,):
+            return None
+        if spk_before is not None and not torch.equal(args[0] != 0, spk_before[..., lo:hi] != 0):
+            return None
+    inp = an[0] if an else 0.0
+    if torch.is_tensor(inp):
+        if inp.numel() != 1:
+            return None
+        inp = inp.item()
+    if not isinstance(inp, (int, float, np.floating, np.integer)):
+        return None
+    return neuron, proj_e, proj_i, n_exc, float(inp)
+
+
+def _fused_loop(f, xs, length):
+    """for_loop through the persistent runner.  Steps 0 and 1 run eagerly while their module
+    calls are recorded; when both are the same E/I step (``_ei_step``; step 1 checked against
+    the population's spikes before it), with the same constant input and with the
+    population's spikes (or nothing) as the step's output, the runner advances the other
+    steps in one launch from the state the eager steps left -- pending spikes included -- and
+    writes the final state back.  Returns (outputs of the eager steps, the stacked output of
+    all steps or None when the loop must go on eagerly)."""
+    from .nn import _module
+    from .nn._fuse import fuse
+    outs, steps = [], []
+    for i in range(2):
+        before = steps[0][0].spike.value.clone() if steps else None
+        with _module.record_calls() as log:
+            out = f(*[x[i] for x in xs])
+        outs.append(out)
+        step = _ei_step(log, before)
+        if step is None:
+            return outs, None
+        spk = step[0].spike.value
+        if out is not None and not (torch.is_tensor(out) and out.shape == spk.shape and
+                                    torch.equal(out != 0, spk != 0)):
+            return outs, None
+        steps.append(step)
+    if any(a is not b for a, b in zip(steps[0][:3], steps[1][:3])) or steps[0][3:] != steps[1][3:]:
+        return outs, None
+    neuron, proj_e, proj_i, n_exc, inp = steps[1]
+    r = fuse(neuron, proj_e, proj_i, n_exc, inp)
+    T = length - 2
+    want = outs[0] is not None
+    raster = torch.zeros(T, r.n, dtype=torch.uint8, device=r.device) if want else None
+    r.run(T, raster=raster)
+    r.check()
+    r.write_back()
+    if not want:
+        return outs, [None] * length
+    perm = torch.as_tensor(np.asarray(r.replica_index).reshape(-1), device=raster.device)
+    rest = raster[:, perm].reshape((T,) + tuple(outs[0].shape)).to(outs[0].dtype)
+    return outs, torch.cat([torch.stack(outs), rest])
+
+
 def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
     """Call ``f(*x_t)`` for t along the leading axis of ``xs`` and stack the outputs
-    (brainstate/transform/_loop_collect_return.py:487-572)."""
+    (brainstate/transform/_loop_collect_return.py:487-572).
+
+    The reference traces ``f`` once and runs the whole loop as one compiled scan.  Here a
+    step function that is the E/I network step (the two event projections of one LIFRef or
+    HH population fed its spikes, then the population with a constant input -- the update
+    of examples/105_COBA_HH_2007_braincell.py and of the SNN tutorial) is recognised from the
+    module calls of its first two steps, which run eagerly, and every later step runs in
+    the persistent runner, one launch; the state is written back at the end.  Any other step
+    function runs eagerly step by step."""
+    global last_loop
     if length is None:
         if not xs:
             raise ValueError('for_loop needs xs or length')
         length = len(xs[0])
+    last_loop = 'eager'
+    if fuse_loops and not reverse and length >= 3:
+        done, stacked = _fused_loop(f, xs, length)
+        if stacked is not None:
+            last_loop = 'fused'
+            return stacked if torch.is_tensor(stacked) else _stack(stacked)
+        outs = done + [f(*[x[i] for x in xs]) for i in range(len(done), length)]
+        return _stack(outs)
     order = range(length - 1, -1, -1) if reverse else range(length)
     outs = [f(*[x[i] for x in xs]) for i in order]
     if reverse:

@@ -346,6 +346,13 @@ BS_API int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_
                           int64_t t0, int32_t steps, int32_t* counts_out, uint32_t* hash_out,
                           uint8_t* raster_out, void* workspace, bs_stream_t stream);
 
+/* Pending spikes for a run that starts at step t0 >= 1 (synaptic delay 0): spk [n] (nonzero
+ * = spike) are taken as the spikes of step t0 - 1, so step t0's inputs come from them, as
+ * when the loop was advanced step by step elsewhere (brainstate.transform.for_loop handing
+ * over after its first steps).  Call after bs_net_prepare, before the run from t0. */
+BS_API int bs_net_seed_spikes(const bs_net* net, const uint8_t* spk, int64_t t0,
+                              void* workspace, bs_stream_t stream);
+
 /* Workgroups the runners use for this net on the current device (-1 on error). */
 BS_API int bs_net_grid_blocks(const bs_net* net);
 /* Synchronises `stream`; returns 0 if every wait of the runs so far completed, -1 if one

@@ -1,5 +1,6 @@
 """GPU tests of the brainstate-compatible layer: the reference's own layer tests, and an
 E/I network built from modules, stepped eagerly and fused, against the oracle."""
+import json
 import os
 import sys
 
@@ -150,18 +151,103 @@ class _EINet:
             return self.N.get_spike()
 
 
-def test_module_ei_network_matches_oracle(bs):
-    """The reference's E/I script shape, stepped eagerly through the module API."""
+def _for_loop_paths(bs, make_step, T, dt=0.1):
+    """for_loop(step, times) on a fresh net twice: stepped eagerly, then the default that
+    hands the loop to the persistent runner after two recorded steps.  Returns
+    [(raster, net), ...] and checks which path each took."""
     import torch
-    print('[case] module E/I net eager', flush=True)
-    T = 200
+    res = []
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=dt):
+                step, net = make_step()
+                res.append((bs.transform.for_loop(step, torch.arange(T) * dt), net))
+        finally:
+            bs.transform.fuse_loops = True
+        assert bs.transform.last_loop == ('fused' if fused else 'eager')
+    return res
+
+
+def test_module_ei_network_matches_oracle(bs):
+    """The reference's E/I script shape (examples/105_COBA_HH_2007_braincell.py:76-91):
+    for_loop(net.update, times) stepped eagerly and through the persistent runner; both
+    rasters and final states equal the oracle's."""
+    print('[case] module E/I net for_loop eager + fused', flush=True)
+    T = 300
     pe, pi, V0, p = make_golden.config1_net()
     ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
-    with bs.environ.context(dt=0.1):
+
+    def make():
         net = _EINet(bs)
-        spikes = bs.transform.for_loop(net.update, torch.arange(T) * 0.1)
-    assert np.array_equal(spikes.cpu().numpy(), ref['raster'])
-    assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+        return net.update, net
+    for spikes, net in _for_loop_paths(bs, make, T):
+        assert spikes.dtype == net.N.get_spike().dtype and spikes.shape == (T, 4000)
+        assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'])
+        assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+        assert np.array_equal(net.E.syn.g.value.cpu().numpy(), ref['ge'])
+        assert np.array_equal(net.N.ref.value.cpu().numpy(), ref['ref'])
+        assert np.array_equal(net.N.spike.value.cpu().numpy(), ref['spk'])
+
+
+def test_hh_module_network_for_loop(bs):
+    """A COBA-HH E/I net (the shape of examples/105_COBA_HH_2007_braincell.py) built from the
+    modules: for_loop eagerly and through the runner, both equal to the oracle's golden run."""
+    print('[case] HH module net for_loop', flush=True)
+    c = make_golden.HH_NET
+    with open(os.path.join(GOLD, 'coba_hh_2000.json')) as f:
+        gold = json.load(f)
+    V0 = np.random.RandomState(c['seed_v']).uniform(-70., -50., c['n']).astype(F)
+
+    def make():
+        N = bs.nn.HH(c['n'], V_initializer=lambda s: V0)
+        E = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n_exc'], c['n'], c['k'], c['w_e'], seed=c['seed_e']),
+            syn=bs.nn.Expon.desc(c['n'], tau=5.), out=bs.nn.COBA.desc(E=0.), post=N)
+        I = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n'] - c['n_exc'], c['n'], c['k'], c['w_i'],
+                                      seed=c['seed_i']),
+            syn=bs.nn.Expon.desc(c['n'], tau=10.), out=bs.nn.COBA.desc(E=-80.), post=N)
+        bs.nn.init_all_states(N)
+        for m in (E.syn, I.syn):
+            m.init_state()
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            E(spk[:c['n_exc']])
+            I(spk[c['n_exc']:])
+            return N(c['I_ext'])
+        return step, N
+    for spikes, N in _for_loop_paths(bs, make, c['steps'], dt=0.05):
+        ras = spikes.cpu().numpy() != 0
+        assert ras.sum(1).tolist() == gold['counts']
+        assert make_golden.sha(np.packbits(ras)) == gold['raster_sha256']
+        assert make_golden.sha(N.V.value.cpu().numpy()) == gold['final_V_sha256']
+
+
+def test_for_loop_stays_eager_for_other_steps(bs):
+    """A step whose input changes with time is not the runner's step: after its two recorded
+    steps the loop goes on eagerly, and equals the loop stepped eagerly from the start."""
+    import torch
+    print('[case] for_loop time-varying input', flush=True)
+    outs = []
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                net = _EINet(bs)
+
+                def step(t):
+                    spk = net.N.get_spike() != 0.
+                    net.E(spk[:net.n_exc])
+                    net.I(spk[net.n_exc:])
+                    return net.N(20. + float(t))
+
+                outs.append(bs.transform.for_loop(step, torch.arange(50) * 0.1))
+        finally:
+            bs.transform.fuse_loops = True
+        assert bs.transform.last_loop == 'eager'
+    assert torch.equal(outs[0], outs[1])
 
 
 def test_fused_network_continues_eager_state(bs):
@@ -223,10 +309,11 @@ def test_cuba_module_network_eager_and_fused(bs):
     pe, pi, V0, p = make_golden.cuba_net()
     ref = network.run_coba_lif(V0, pe, pi, p, make_golden.CUBA_NET['n_exc'], 500)
     assert ref['counts'].sum() > 100
-    with bs.environ.context(dt=0.1):
+    def make():
         net = _CUBANet(bs)
-        spikes = bs.transform.for_loop(net.update, torch.arange(200) * 0.1)
-    assert np.array_equal(spikes.cpu().numpy(), ref['raster'][:200])
+        return net.update, net
+    for spikes, _ in _for_loop_paths(bs, make, 200):
+        assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'][:200])
     with bs.environ.context(dt=0.1):
         net = _CUBANet(bs)
         r = bs.nn.fuse(net.N, net.E, net.I, n_exc=net.n_exc, inp=make_golden.CUBA_NET['I_ext'])
@@ -263,7 +350,7 @@ def test_tutorial_network_modules_soft_reset(bs):
             m.init_state()
         return N, E, I
 
-    with bs.environ.context(dt=0.1):
+    def make():
         N, E, I = build()
 
         def step(t):
@@ -271,9 +358,10 @@ def test_tutorial_network_modules_soft_reset(bs):
             E(spk[:c['n_exc']])
             I(spk[c['n_exc']:])
             return N(c['I_ext'])
-
-        spikes = bs.transform.for_loop(step, torch.arange(300) * 0.1)
-    assert np.array_equal(spikes.cpu().numpy(), ref['raster'][:300])
+        return step, N
+    for spikes, N_ in _for_loop_paths(bs, make, c['steps']):
+        assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'])
+        assert np.array_equal(N_.V.value.cpu().numpy(), ref['V'])
     with bs.environ.context(dt=0.1):
         N, E, I = build()
         r = bs.nn.fuse(N, E, I, n_exc=c['n_exc'], inp=c['I_ext'])
