@@ -352,6 +352,63 @@ def bench_conn(args):
              'speedup': (host + h2d) / min(dev), 'bit_equal_to_numpy': equal}]
 
 
+def bench_for_loop(args):
+    """brainstate.transform.for_loop(net.update, times) of a module-built E/I net (LIFRef +
+    two AlignPostProj on EventFixedProb, homogeneous 0.6 / 6.7, constant input 20) at
+    configs[0] (4000 neurons, K = 80, 1000 steps) and configs[2] (1M neurons, K = 100):
+    the loop stepped eagerly (per-step kernels; 1000 steps at 1M) against the default, which
+    hands it to the persistent runner after two recorded steps (10,000 steps at 1M, building
+    the runner from the modules included)."""
+    import torch
+    import brainstate_amd as bs
+    lines = []
+    for n, k, T_eager, T_fused, label in ((4000, 80, 1000, 1000, 'configs[0]'),
+                                          (1_000_000, 100, 1000, 10000, 'configs[2]')):
+        n_exc = n * 4 // 5
+        V0 = np.random.RandomState(3).uniform(-60., -50., n).astype(np.float32)
+
+        def build():
+            N = bs.nn.LIFRef(n, V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=5.,
+                             V_initializer=lambda s: V0)
+            E = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n_exc, n, k, 0.6, seed=1),
+                                    syn=bs.nn.Expon.desc(n, tau=5.), out=bs.nn.COBA.desc(E=0.),
+                                    post=N)
+            I = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n - n_exc, n, k, 6.7, seed=2),
+                                    syn=bs.nn.Expon.desc(n, tau=10.),
+                                    out=bs.nn.COBA.desc(E=-80.), post=N)
+            for m in (E.syn, I.syn, N):
+                m.init_state()
+
+            def update(t):
+                spk = N.get_spike() != 0.
+                E(spk[:n_exc])
+                I(spk[n_exc:])
+                return N(20.)
+            return update
+
+        res = {'workload': f'for_loop(net.update) module E/I net {label}', 'neurons': n,
+               'fan_out': k}
+        for fused, T in ((False, T_eager), (True, T_fused)):
+            bs.transform.fuse_loops = fused
+            with bs.environ.context(dt=0.1):
+                update = build()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                spikes = bs.transform.for_loop(update, torch.arange(T) * 0.1)
+                torch.cuda.synchronize()
+                el = time.perf_counter() - t0
+            key = 'fused' if fused else 'eager'
+            assert bs.transform.last_loop == key
+            res[f'{key}_steps'] = T
+            res[f'{key}_s'] = el
+            res[f'{key}_us_per_step'] = el / T * 1e6
+            res[f'{key}_spikes'] = int((spikes != 0).sum().item())
+            del spikes
+        bs.transform.fuse_loops = True
+        lines.append(res)
+    return lines
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -370,12 +427,13 @@ def main():
     ap.add_argument('--summarize', default=None,
                     help='only print a text summary of a rocprofv3 results database')
     ap.add_argument('--workload', default='coba_lif_1m',
-                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn', 'batch'],
+                    choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn', 'batch',
+                             'for_loop'],
                     help='coba_lif_1m is the reported line; the others measure the other configs')
     args = ap.parse_args()
     if args.workload != 'coba_lif_1m':
         fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh,
-              'conn': bench_conn, 'batch': bench_batch}
+              'conn': bench_conn, 'batch': bench_batch, 'for_loop': bench_for_loop}
         for line in fn[args.workload](args):
             print(json.dumps(line), flush=True)
         return
