@@ -136,6 +136,32 @@ def _timed(fn, reps, warm=2):
     return a.elapsed_time(b) / 1e3 / reps
 
 
+def _graph_timed(fn, reps, replays=4):
+    """Per-call GPU time of fn captured reps times in one HIP graph (warm-up on the capture
+    stream first), replayed `replays` times: the device's time without the host's per-call
+    launch cost."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / (replays * reps)
+
+
 def bench_sparse(args):
     """event CSR mat-vec 100k x 100k, K=1000, w ~ N(0.5, 0.1), p in {.001,.01,.1}.
     Destination-bucketed scatter (LDS atomics, no global atomics), scatter (compaction + atomic
@@ -176,10 +202,14 @@ def bench_sparse(args):
         tg = _timed(gather, 20)
         tf = _timed(fused, 20)
         tb = _timed(bucket, 50)
+        hint = int(bkt['_hint'][1][0])   # the estimate the timed calls left: their mode
+        tbg = _graph_timed(bucket, 50)
         b_s = n * 1 + E * 8 + n * 4
         b_g = (n + 1) * 4 + sell['padded'] * 4 + E * 4 + n + n * 4
         lines.append({'workload': f'event_matvec_100k_K1000_p{p}', 'events': E,
                       'bucket_us': tb * 1e6, 'bucket_GSOPs': E / tb / 1e9,
+                      'bucket_graph_us': tbg * 1e6,
+                      'bucket_mode': 'single launch' if hint == 1 else f'split, {hint} row groups',
                       'bucket_alg_GBs': b_s / tb / 1e9, 'bucket_frac': b_s / tb / PEAK_HBM,
                       'fused_matvec_us': tf * 1e6, 'fused_GSOPs': E / tf / 1e9,
                       'scatter_us': ts * 1e6, 'scatter_GSOPs': E / ts / 1e9,

@@ -86,7 +86,8 @@ SIGNATURES = {
                                        c_vp, c_vp, c_vp, c_vp, c_vp]),
     'bs_event_bucket_workspace_size': (c_size, [c_i32, c_i32, c_i32]),
     'bs_event_bucket_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
-                                           c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_size, c_vp]),
+                                           c_vp, c_vp, c_f32, c_vp, c_i32, c_vp, c_size, c_i32,
+                                           c_vp, c_vp]),
     'bs_spike_pack': (ctypes.c_int, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     'bs_event_gather_f32': (ctypes.c_int, [c_vp, c_i32, c_vp, c_vp, c_vp, c_f32, c_i32, c_vp,
                                            c_vp]),

@@ -20,12 +20,23 @@
 // and accumulates their bucket-b synapses into an LDS copy of the bucket with integer LDS
 // atomics: each weight rounded to a multiple of 2^-S and added as a 64-bit integer (event
 // counts for a homogeneous weight).  It writes the bucket as partial r; a second kernel adds
-// the R partials exactly and rounds once: out = fl32(sum) * 2^-S, whatever the order of the
+// the partials exactly and rounds once: out = fl32(sum) * 2^-S, whatever the order of the
 // atomics (deterministic), within half an fp32 ulp of the exact sum of the rounded weights.
 // Homogeneous weights: the exact event count c, then w added c times in one chain, which is
 // the sequential scatter's result bit for bit.  Non-finite weights fall back to fp32 LDS
-// atomics (unspecified order).  HBM traffic: the active rows' synapses once (E x (2 + 4 het)
-// bytes) + R partial rows of n_post x 8 bytes written and read.
+// atomics (unspecified order).
+//
+// The number of row groups follows the spike density, on the device: the grid is launched
+// for R groups, every workgroup counts the active rows of the same leading sample of the
+// spike vector and derives R_eff <= R (about kActivePer active rows per group); groups
+// r >= R_eff exit at once.  With R_eff = 1 the workgroups write `out` themselves and the
+// second kernel returns at once, so a sparse step costs one pass over the spikes and the
+// active synapses instead of R partial rows written and read.  Integer sums make the result
+// independent of R_eff and of the partition.  HBM traffic: the active rows' synapses once
+// (E x (2 + 4 het) bytes) + R_eff partial rows of n_post x 8 bytes written and read (none
+// at R_eff = 1).
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -40,10 +51,17 @@ constexpr int kMaxNb = 1024;      // buckets
 // 76 us.
 constexpr int kRowsPer = 4;       // active rows a wave works on at once
 constexpr int kPasses = 2;        // 64-synapse passes per row issued together
-constexpr int kSpan = 4096;       // rows compacted per span
+constexpr int kSpan = 4096;       // active rows held in LDS before their synapses are added
 constexpr int kTargetWgs = 256;   // step grid the row groups aim for
-constexpr int kMinRows = 64;      // rows per row group, at least
+constexpr int kMinRows = 64;      // rows per row group, at least (and the group alignment)
 constexpr int kMinNb = 8;         // buckets, at least (the grid is nb x row groups)
+constexpr int kSample = 16384;    // leading spike rows whose active count sets R_eff
+constexpr int kActivePer = 256;   // active rows per row group the step aims for
+constexpr int kDepth = 8;         // 16-byte spike loads per thread in flight together
+constexpr int kHdr = 256;         // workspace bytes ahead of the partials (word 0: R_eff)
+// single launch: workgroups per bucket.  Measured at config [2] p = 0.001 (one launch of
+// 9 x n workgroups): n = 2 13.0 us, 4 12.7 us, 8 12.55 us per step (HIP graph replay).
+constexpr int kSubSingle = 8;
 
 // ---- layout build: one wave per pre row ----
 // s_run[wave][b]: synapses of bucket b placed so far (b = nb: out-of-range targets).
@@ -151,64 +169,267 @@ __global__ void k_bucket_qexp(const uint32_t* wmax, int64_t nnz_fixed, const int
 }
 
 // ---- step ----
-// Phases per span of up to kSpan rows of the workgroup's row group:
-//   1. compaction of the span's active rows into s_beg (ballots, ascending);
-//   2. every thread loads the bucket-b bounds of some active rows (all in flight) into
-//      s_beg / s_len;
+// 16 bytes of spikes (16 u8 rows or 4 f32 rows) of block blk = rows [blk*E, blk*E + E), rows
+// outside [r0, r1) read as 0: one vector load when the whole block lies inside and the
+// vector is 16-byte aligned, else one load per row in range.
+template <typename T, bool kVec>
+__device__ __forceinline__ uint4 spike_block(const T* __restrict__ spk, uint32_t blk, uint32_t r0,
+                                             uint32_t r1) {
+  constexpr uint32_t kE = 16 / sizeof(T);
+  const uint32_t row = blk * kE;  // rows < 2^31: 32-bit index math (a 64-bit op costs two)
+  if (kVec && row >= r0 && row + kE <= r1) return *(const uint4*)(spk + row);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (uint32_t e = 0; e < kE; ++e) {
+    const uint32_t i = row + e;
+    if (i >= r0 && i < r1) {
+      if (sizeof(T) == 1) w[e >> 2] |= (uint32_t)((const uint8_t*)spk)[i] << (8 * (e & 3));
+      else w[e] = __float_as_uint(((const float*)spk)[i]);
+    }
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Active rows of a block as a bit mask (u8: byte != 0; f32: value != 0, so -0 is inactive and
+// NaN active, as `spk[i] != 0`), with word-parallel tests (a wave64 VALU op costs 4 cycles of
+// its SIMD, and every lane tests 16 bytes per block):
+//   u8:  bit 4k + q <-> byte k of word q = row 4q + k of the block (row_of below);
+//   f32: bit q <-> row q.
+template <typename T>
+__device__ __forceinline__ uint32_t spike_bits(uint4 v) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  if (sizeof(T) == 1) {
+    uint32_t u = 0u;  // byte k, bit q: byte k of word q is not zero
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // bit 8k+7 of y: byte k of the word is not zero (no carry leaves a byte)
+      const uint32_t y = (((w[q] & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | w[q]) & 0x80808080u;
+      u |= y >> (7 - q);
+    }
+    const uint32_t t = u | (u >> 4);            // byte 0: nibbles 0, 1; byte 2: nibbles 2, 3
+    return (t & 0xFFu) | ((t >> 8) & 0xFF00u);
+  }
+  uint32_t m = 0u;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) m |= (((w[q] & 0x7FFFFFFFu) + 0x7FFFFFFFu) >> 31) << q;
+  return m;
+}
+
+// fl32(q), round to nearest even: below 2^53 in magnitude q is exact in double (high word
+// * 2^32 + low word, both exact), so one double -> float rounding gives fl32(q); above, the
+// compiler's 64-bit conversion.
+__device__ __forceinline__ float i64_to_f32(int64_t q) {
+  if ((uint64_t)(q + (1ll << 53)) < (1ull << 54)) {
+    const double d = (double)(int32_t)(q >> 32) * 4294967296.0 + (double)(uint32_t)q;
+    return (float)d;
+  }
+  return (float)q;
+}
+
+// spike_bits, skipped (0) for the whole wave when none of its 64 blocks holds a non-zero
+// word: two VALU ops and a ballot instead of the byte tests (sparse spikes leave many waves'
+// blocks empty).
+template <typename T>
+__device__ __forceinline__ uint32_t spike_bits_sparse(uint4 v) {
+  const bool any = (v.x | v.y | v.z | v.w) != 0u;
+  return bs_ballot(any) != 0ull ? spike_bits<T>(v) : 0u;
+}
+
+// Row (inside its block) of bit e of spike_bits<T>.
+template <typename T>
+__device__ __forceinline__ int row_of(int e) {
+  return sizeof(T) == 1 ? 4 * (e & 3) + (e >> 2) : e;
+}
+
+// Exclusive prefix over the wave's lanes of c (0 <= c < 2^kBits) and the wave's total, from
+// the ballots of c's bits.
+template <int kBits>
+__device__ __forceinline__ void wave_prefix(uint32_t c, int& excl, int& total) {
+  excl = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < kBits; ++k) {
+    const uint64_t m = bs_ballot((c >> k) & 1u);
+    excl += bs_rank_below(m) << k;
+    total += (int)__popcll(m) << k;
+  }
+}
+
+// Workgroup (b, r):
+//   0. R_eff from the active count of the leading kSample rows (every workgroup reads the
+//      same rows, so all agree); groups r >= R_eff return;
+//   1. the group's rows in blocks of 16 bytes per thread, kDepth blocks' loads in flight;
+//      each batch's active rows are appended to s_beg (ballot prefixes, one barrier);
+//   2. when the list would pass kSpan rows, and at the end: every thread loads the bucket-b
+//      bounds of some listed rows (all in flight) into s_beg / s_len;
 //   3. waves take kRowsPer rows at a time and issue the loads of up to kPasses 64-synapse
-//      passes of all of them before their LDS atomics.
-template <typename T, bool kHet>
-__global__ __launch_bounds__(kSB) void k_bucket_scatter(const T* __restrict__ spk, int32_t n_pre,
-                                                        int32_t rows, int32_t nb, int32_t P,
-                                                        const int32_t* __restrict__ seg,
-                                                        const uint16_t* __restrict__ lidx,
-                                                        const float* __restrict__ lw,
-                                                        const int32_t* __restrict__ qexp,
-                                                        int32_t n_post, uint64_t* __restrict__ part) {
-  __shared__ uint64_t s_acc[kMaxP];        // fixed-point sums, fp32 sums or event counts
+//      passes of all of them before their LDS atomics;
+//   4. R_eff = 1: the bucket's outputs, with k_bucket_reduce's arithmetic; else partial r.
+template <typename T, bool kHet, bool kVec>
+__global__ __launch_bounds__(kSB) void k_bucket_scatter(
+    const T* __restrict__ spk, int32_t n_pre, int32_t R, int32_t Rmax, int32_t nb, int32_t P,
+    int32_t nsub,
+    const int32_t* __restrict__ seg, const uint16_t* __restrict__ lidx,
+    const float* __restrict__ lw, const int32_t* __restrict__ qexp, int32_t n_post,
+    float w_homo, int32_t accumulate, float* __restrict__ out, int32_t* __restrict__ hdr,
+    int32_t* __restrict__ est_out, uint64_t* __restrict__ part) {
+  constexpr int kE = 16 / (int)sizeof(T);  // rows per block
+  constexpr int kW = kSB / BS_WAVE;
+  __shared__ __align__(16) uint64_t s_acc[kMaxP];  // fixed-point sums, fp32 sums or counts
   uint32_t* s_acc32 = (uint32_t*)s_acc;
   __shared__ int32_t s_beg[kSpan];
   __shared__ int32_t s_len[kSpan];
-  __shared__ int32_t s_wave[kSB / BS_WAVE];
+  __shared__ int32_t s_wave[2][kW];
   const int lane = bs_lane();
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / BS_WAVE));
+  // workgroup (b, sub, r): bucket b, sub-range sub of its posts (nsub > 1 only with R = 1),
+  // row group r
   const int32_t b = blockIdx.x % nb;
-  const int32_t r = blockIdx.x / nb;
-  const int32_t p0 = b * P;
-  const int32_t pn = n_post - p0 < P ? n_post - p0 : P;  // posts in this bucket
-  for (int j = threadIdx.x; j < pn; j += kSB) s_acc[j] = 0ull;
-  // fixed point (S >= -999) unless a weight is not finite; scale = 2^S exactly
+  const int32_t sub = (blockIdx.x / nb) % nsub;
+  const int32_t r = blockIdx.x / nb / nsub;
+  // workgroup-wide exclusive prefix and total of c (< 2^kBits per thread), one barrier; s_wave
+  // alternates halves, so the next call's writes never meet this call's reads
+  int par = 0;
+  auto prefix = [&](auto bits_tag, uint32_t c, int& excl, int& total) {
+    int we, wt;
+    wave_prefix<decltype(bits_tag)::value>(c, we, wt);
+    if (lane == 0) s_wave[par][wid] = wt;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int v = 0; v < kW; ++v) {
+      const int x = s_wave[par][v];
+      base += v < wid ? x : 0;
+      tot += x;
+    }
+    par ^= 1;
+    excl = base + we;
+    total = tot;
+  };
+  using B5 = std::integral_constant<int, 5>;   // counts of up to 16 rows
+  using B8 = std::integral_constant<int, 8>;   // counts of up to 128 rows
+  // fixed point (S >= -999) unless a weight is not finite; loaded first, so that its latency
+  // hides behind the spike loads (a barrier waits for every outstanding scalar load)
   const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
+  // 0. R_eff = ceil(active rows / kActivePer), the active count estimated from the leading
+  // ns rows (blocks d < kSmpD of every thread).  The first round of the group's rows is
+  // loaded now too, before R_eff is known, on a guess that saves a memory round trip when it
+  // holds: group 0 (which always starts at row 0) loads rows [0, n_pre) and clips them to its
+  // end once R_eff is known; the other groups guess R_eff = R (the dense case) when their
+  // group then fits the kDepth - kSmpD spare loads, and reload if the guess was wrong.
+  constexpr int kSmpD = kSample / (kSB * kE);
+  static_assert(kSmpD >= 1 && kSmpD < kDepth, "sample is part of the first round");
+  const int32_t ns = n_pre < kSample ? n_pre : kSample;
+  const uint32_t N = (uint32_t)n_pre;
+  const uint32_t nblk = (N + kE - 1) / kE;
+  // rows per group, a multiple of kMinRows (32-bit division: a 64-bit one is ~80 VALU ops,
+  // and every wave of the workgroup computes it)
+  auto group_rows = [&](int32_t groups) -> uint32_t {
+    const uint32_t per = (N + (uint32_t)groups - 1u) / (uint32_t)groups;
+    return (per + kMinRows - 1) / kMinRows * kMinRows;
+  };
+  // group r's rows when there are `groups` groups: [lo, hi) (64-bit product: r * rows may
+  // pass 2^32 before the clamp)
+  auto group_lo = [&](uint32_t rows) -> uint32_t {
+    const uint64_t x = (uint64_t)r * rows;
+    return x < N ? (uint32_t)x : N;
+  };
+  const uint32_t rowsR = group_rows(R);
+  const uint32_t g0R = group_lo(rowsR);
+  const uint32_t g1R = N - g0R > rowsR ? g0R + rowsR : N;
+  const bool specR = r != 0 && rowsR <= (uint32_t)(kDepth - kSmpD) * kSB * kE;
+  // v0[d]: d < kSmpD the sample, then group 0's or the R-guess's blocks (raw: their masks are
+  // computed once R_eff says which of them the group needs)
+  uint4 v0[kDepth];
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) {
+    // slot d: uniform first block, row range and block limit; one compare per lane
+    const uint32_t first = d < kSmpD || r == 0 ? (uint32_t)d * kSB : g0R / kE + (uint32_t)(d - kSmpD) * kSB;
+    const uint32_t lo = d < kSmpD || r == 0 ? 0u : g0R;
+    const uint32_t hi = d < kSmpD ? (uint32_t)ns : (r == 0 ? N : g1R);
+    const uint32_t lim = d < kSmpD ? ((uint32_t)ns + kE - 1) / kE
+                                   : (r == 0 ? nblk : (specR ? (g1R + kE - 1) / kE : 0u));
+    const uint32_t blk = first + threadIdx.x;
+    const bool want = blk < lim;
+    v0[d] = want ? spike_block<T, kVec>(spk, blk, lo, hi) : make_uint4(0u, 0u, 0u, 0u);
+  }
+  // the bucket's LDS accumulator cleared while the loads are in flight (16-byte stores)
+  // this workgroup's posts: [p0, p0 + pn), at offsets [lo_t, lo_t + pn) of bucket b
+  const int32_t pnb = n_post - b * P < P ? n_post - b * P : P;  // posts in bucket b
+  const int32_t ps = (P + nsub - 1) / nsub;
+  const int32_t lo_t = sub * ps;
+  const int32_t pn = pnb - lo_t < ps ? (pnb - lo_t > 0 ? pnb - lo_t : 0) : ps;
+  const int32_t p0 = b * P + lo_t;
+  for (int j = threadIdx.x; 2 * j < pn; j += kSB) ((uint4*)s_acc)[j] = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t smk[kSmpD];  // masks of the sample's blocks
+  uint32_t cs = 0;
+#pragma unroll
+  for (int d = 0; d < kSmpD; ++d) {
+    smk[d] = spike_bits_sparse<T>(v0[d]);
+    cs += __popc(smk[d]);
+  }
+  int ex0, act0;
+  prefix(B5(), cs, ex0, act0);
+  // ceil(act0 * n_pre / (ns * kActivePer)) in double: the numerator (< 2^45) and the
+  // denominator (<= 2^22) are exact, and a quotient that is not an integer lies at least
+  // 2^-22 from one, far beyond the division's rounding, so the ceiling is exact
+  const double re = ceil((double)act0 * (double)n_pre / ((double)ns * kActivePer));
+  const int32_t est = re < 1.0 ? 1 : (re > (double)Rmax ? Rmax : (int32_t)re);
+  const int32_t R_eff = est < R ? est : R;  // R = 1: one launch, the step writes out
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *hdr = R_eff;
+    if (est_out) *est_out = est;  // the host's hint for its next call
+  }
+  if (r >= R_eff) return;  // whole workgroup
+  const bool haveR = specR && R_eff == R;  // the R-guess held: mk0[kSmpD...] is the group
   const bool fixed = kHet && S > -1000;
   const double scale = fixed ? ldexp(1.0, S) : 1.0;
-  const int64_t r0 = (int64_t)r * rows;
-  const int64_t r1 = r0 + rows < n_pre ? r0 + rows : n_pre;
-  const int stride = nb + 1;
-  for (int64_t c0 = r0; c0 < r1; c0 += kSpan) {
-    // 1. active rows of the span, ascending
-    int32_t count = 0;
-    for (int32_t o = 0; o < kSpan; o += kSB) {
-      const int64_t row = c0 + o + threadIdx.x;
-      const bool a = row < r1 && spk[row] != T(0);
-      const uint64_t m = bs_ballot(a);
-      if (lane == 0) s_wave[wid] = __popcll(m);
-      __syncthreads();
-      int32_t pos = count, tot = 0;
+  // the group's rows [g0, g1): R_eff groups, boundaries at multiples of kMinRows
+  const uint32_t rows_g = group_rows(R_eff);
+  const uint32_t g0 = group_lo(rows_g);
+  const uint32_t g1 = N - g0 > rows_g ? g0 + rows_g : N;
+  const uint32_t bk0 = g0 / kE, bk1 = (g1 + kE - 1) / kE;  // the group's blocks
+  // masks of the first round read in phase 0, for the slots that hold blocks of the group
+  // (a slot past the group's end is skipped whole: its mask work would be wasted)
+  uint32_t mk0[kDepth];
 #pragma unroll
-      for (int v = 0; v < kSB / BS_WAVE; ++v) {
-        pos += v < wid ? s_wave[v] : 0;
-        tot += s_wave[v];
-      }
-      if (a) s_beg[pos + bs_rank_below(m)] = (int32_t)row;
-      count += tot;
-      __syncthreads();  // s_wave is rewritten next round
+  for (int d = 0; d < kDepth; ++d) {
+    mk0[d] = 0u;
+    if (r == 0) {
+      const uint32_t blk = (uint32_t)d * kSB + threadIdx.x;
+      if ((uint32_t)d * kSB < bk1 && blk < bk1)
+        mk0[d] = d < kSmpD ? smk[d] : spike_bits_sparse<T>(v0[d]);
+    } else if (haveR && d < kDepth - kSmpD) {
+      const uint32_t blk = bk0 + (uint32_t)d * kSB + threadIdx.x;
+      if ((uint32_t)d * kSB < bk1 - bk0 && blk < bk1) mk0[d] = spike_bits_sparse<T>(v0[kSmpD + d]);
     }
-    // 2. bounds of bucket b in each active row
-    for (int32_t x = threadIdx.x; x < count; x += kSB) {
-      const int32_t* sr = seg + (int64_t)s_beg[x] * stride + b;
-      const int32_t lo = sr[0], hi = sr[1];
-      s_beg[x] = lo;
-      s_len[x] = hi - lo;
+  }
+  const int stride = nb + 1;
+  int32_t count = 0;  // rows listed in s_beg (the same in every thread)
+  auto flush = [&]() {
+    __syncthreads();  // the listed rows are in s_beg
+    // 2. bounds of bucket b in each listed row (count <= kSpan: all loads in flight)
+    {
+      constexpr int kU = kSpan / kSB;
+      int32_t lo[kU], hi[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int32_t x = u * kSB + threadIdx.x;
+        lo[u] = hi[u] = 0;
+        if (x < count) {
+          const int32_t* sr = seg + (uint64_t)(uint32_t)s_beg[x] * stride + b;
+          lo[u] = sr[0];
+          hi[u] = sr[1];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int32_t x = u * kSB + threadIdx.x;
+        if (x < count) {
+          s_beg[x] = lo[u];
+          s_len[x] = hi[u] - lo[u];
+        }
+      }
     }
     __syncthreads();
     // 3. synapses of kRowsPer rows, up to kPasses x 64 each, loads in flight together
@@ -233,8 +454,8 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(const T* __restrict__ sp
             t[u][q] = 0xFFFFu;
             v[u][q] = 0.0f;
             if (e < len[q]) {
-              t[u][q] = lidx[(int64_t)beg[q] + e];
-              if (kHet) v[u][q] = lw[(int64_t)beg[q] + e];
+              t[u][q] = lidx[(uint32_t)(beg[q] + e)];
+              if (kHet) v[u][q] = lw[(uint32_t)(beg[q] + e)];
             }
           }
         }
@@ -242,48 +463,163 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(const T* __restrict__ sp
         for (int u = 0; u < kPasses; ++u) {
 #pragma unroll
           for (int q = 0; q < kRowsPer; ++q) {
-            if (t[u][q] != 0xFFFFu) {
+            // offset inside this workgroup's posts; the 0xFFFF of an idle lane is never < pn
+            const uint32_t tl = (uint32_t)t[u][q] - (uint32_t)lo_t;
+            if (tl < (uint32_t)pn) {
               if (!kHet) {
-                atomicAdd(&s_acc32[t[u][q]], 1u);
+                atomicAdd(&s_acc32[tl], 1u);
               } else if (fixed) {
                 const int64_t qv = (int64_t)__builtin_rint((double)v[u][q] * scale);
-                atomicAdd((unsigned long long*)&s_acc[t[u][q]], (unsigned long long)qv);
+                atomicAdd((unsigned long long*)&s_acc[tl], (unsigned long long)qv);
               } else {
-                atomicAdd((float*)&s_acc32[t[u][q]], v[u][q]);
+                atomicAdd((float*)&s_acc32[tl], v[u][q]);
               }
             }
           }
         }
       }
     }
-    __syncthreads();  // s_beg / s_len are rewritten by the next span
+    __syncthreads();  // s_beg / s_len are rewritten next
+    count = 0;
+  };
+  // appends the rows of the set bits e of m at s_beg[pos...]: row0 + row_of(e), or, for
+  // nibble q of a u8 mask (bit e <-> word e, byte q of the block), row0 + 4e + q
+  auto put = [&](uint32_t m, uint32_t row0, int pos, int q) {
+    while (m) {
+      const int e = __builtin_ctz(m);
+      s_beg[pos++] = (int32_t)(row0 + (q < 0 ? row_of<T>(e) : 4 * e + q));
+      m &= m - 1u;
+    }
+  };
+  // one batch (one block per thread) through the list, flushing it when it would overflow
+  auto add_batch = [&](uint32_t m, uint32_t row0) {
+    int ex, tot;
+    prefix(B5(), (uint32_t)__popc(m), ex, tot);
+    if (count + tot <= kSpan) {
+      put(m, row0, count + ex, -1);
+      count += tot;
+      return;
+    }
+    if (count > 0) flush();
+    if (tot <= kSpan) {
+      put(m, row0, ex, -1);
+      count = tot;
+      return;
+    }
+    // more than kSpan active rows in one batch (u8 only): nibble by nibble, <= 4 per thread
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t mq = (m >> (4 * q)) & 15u;
+      int exq, totq;
+      prefix(B5(), (uint32_t)__popc(mq), exq, totq);
+      if (count + totq > kSpan) flush();
+      put(mq, row0, count + exq, q);
+      count += totq;
+    }
+  };
+  // 1. the group's blocks, kDepth x kSB at a time: all loads first, then the whole round
+  // through one prefix when its rows fit the list, else batch by batch
+  for (uint32_t bb = bk0; bb < bk1; bb += (uint32_t)kDepth * kSB) {
+    uint32_t mk[kDepth];
+    if (bb == bk0 && (r == 0 || haveR)) {  // read in phase 0
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) mk[d] = mk0[d];
+    } else {
+      uint4 v[kDepth];
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        const uint32_t blk = bb + (uint32_t)d * kSB + threadIdx.x;
+        v[d] = blk < bk1 ? spike_block<T, kVec>(spk, blk, g0, g1) : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) mk[d] = spike_bits_sparse<T>(v[d]);
+    }
+    uint32_t call = 0;
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) call += __popc(mk[d]);
+    int ex, tot;
+    prefix(B8(), call, ex, tot);
+    if (count + tot <= kSpan) {
+      int pos = count + ex;
+#pragma unroll
+      for (int d = 0; d < kDepth; ++d) {
+        put(mk[d], (bb + (uint32_t)d * kSB + threadIdx.x) * kE, pos, -1);
+        pos += __popc(mk[d]);
+      }
+      count += tot;
+      continue;
+    }
+    const int nbat = (int)((bk1 - bb + kSB - 1) / kSB < kDepth ? (bk1 - bb + kSB - 1) / kSB
+                                                                 : kDepth);
+#pragma unroll 1
+    for (int d = 0; d < nbat; ++d) {
+      const uint32_t m = mk[0];
+#pragma unroll
+      for (int e = 0; e + 1 < kDepth; ++e) mk[e] = mk[e + 1];  // static indices: registers
+      add_batch(m, (bb + (uint32_t)d * kSB + threadIdx.x) * kE);
+    }
   }
-  __syncthreads();
-  uint64_t* dst = part + (int64_t)r * n_post + p0;
-  if (kHet && fixed) {
-    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc[j];
+  if (count > 0) flush();
+  __syncthreads();  // s_acc complete (and zeroed, for a group without active rows)
+  // 4. output
+  if (R_eff == 1) {
+    float* o = out + p0;
+    for (int j = threadIdx.x; j < pn; j += kSB) {
+      float acc = accumulate ? o[j] : 0.0f;
+      if (kHet && fixed) {
+        const float v = ldexpf(i64_to_f32((int64_t)s_acc[j]), -S);
+        acc = accumulate ? acc + v : v;
+      } else if (kHet) {
+        acc += __uint_as_float(s_acc32[j]);
+      } else {
+        const uint32_t c = s_acc32[j];
+        for (uint32_t u = 0; u < c; ++u) acc += w_homo;
+      }
+      o[j] = acc;
+    }
   } else {
-    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
+    uint64_t* dst = part + (int64_t)r * n_post + p0;
+    if (kHet && fixed) {
+      for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc[j];
+    } else {
+      for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
+    }
   }
 }
 
-// out[j] = (accumulate ? out[j] : 0) + the bucket sums of j:
+// out[j] = (accumulate ? out[j] : 0) + the bucket sums of j, over the R = *hdr partials the
+// step kernel wrote (R = 1: it wrote out itself, nothing to do).  The first min(8, Rmax)
+// partials are loaded together with the header, not after it: one memory round trip, not two.
 //   fixed point: the R partials added exactly (64-bit), then fl32(sum) * 2^-S;
 //   homogeneous: the total count c of events, then c additions of w (the sequential chain);
 //   fp32 fallback: the R partials added in row-group order.
 template <bool kHet>
-__global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t R,
+__global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t Rmax,
+                                                       const int32_t* __restrict__ hdr,
                                                        const uint64_t* __restrict__ part,
                                                        const int32_t* __restrict__ qexp,
                                                        float w_homo, int32_t accumulate,
                                                        float* __restrict__ out) {
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= n_post) return;
+  constexpr int kFirst = 8;
+  uint64_t x0[kFirst];
+#pragma unroll
+  for (int u = 0; u < kFirst; ++u) x0[u] = u < Rmax ? part[(int64_t)u * n_post + j] : 0ull;
+  const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
   float acc = accumulate ? out[j] : 0.0f;
-  const int32_t S = kHet ? *qexp : 0;
+  const int32_t R = __builtin_amdgcn_readfirstlane(*hdr);
+  // (the loads above are consumed on both paths, so they stay ahead of this test)
+  uint64_t any = __float_as_uint(acc) + (uint32_t)S;
+#pragma unroll
+  for (int u = 0; u < kFirst; ++u) any |= x0[u];
+  if (R <= 1 && any != 0x5A5A5A5A5A5A5A5Aull) return;
+  const int32_t r0 = R < kFirst ? R : kFirst;
   if (kHet && S > -1000) {
     int64_t q = 0;
-    int32_t r = 0;
+#pragma unroll
+    for (int u = 0; u < kFirst; ++u) q += u < r0 ? (int64_t)x0[u] : 0;
+    int32_t r = r0;
     for (; r + 8 <= R; r += 8) {
       int64_t x[8];
 #pragma unroll
@@ -292,13 +628,20 @@ __global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t R
       for (int u = 0; u < 8; ++u) q += x[u];
     }
     for (; r < R; ++r) q += (int64_t)part[(int64_t)r * n_post + j];
-    const float v = ldexpf((float)q, -S);
+    const float v = ldexpf(i64_to_f32(q), -S);
     acc = accumulate ? acc + v : v;
   } else if (kHet) {
-    for (int32_t r = 0; r < R; ++r) acc += __uint_as_float((uint32_t)part[(int64_t)r * n_post + j]);
+    // fp32 fallback: the partials in row-group order
+#pragma unroll
+    for (int u = 0; u < kFirst; ++u)
+      if (u < r0) acc += __uint_as_float((uint32_t)x0[u]);
+    for (int32_t r = r0; r < R; ++r)
+      acc += __uint_as_float((uint32_t)part[(int64_t)r * n_post + j]);
   } else {
     uint32_t c = 0;
-    for (int32_t r = 0; r < R; ++r) c += (uint32_t)part[(int64_t)r * n_post + j];
+#pragma unroll
+    for (int u = 0; u < kFirst; ++u) c += u < r0 ? (uint32_t)x0[u] : 0u;
+    for (int32_t r = r0; r < R; ++r) c += (uint32_t)part[(int64_t)r * n_post + j];
     for (uint32_t u = 0; u < c; ++u) acc += w_homo;
   }
   out[j] = acc;
@@ -391,14 +734,15 @@ extern "C" int bs_bucket_build(int32_t n_pre, const int32_t* indptr, const int32
 extern "C" size_t bs_event_bucket_workspace_size(int32_t n_pre, int32_t n_post, int32_t nb) {
   bs_clear_error();
   if (n_pre <= 0 || n_post <= 0 || nb <= 0) return 0;
-  return (size_t)row_groups(n_pre, nb) * n_post * sizeof(uint64_t);
+  return (size_t)kHdr + (size_t)row_groups(n_pre, nb) * n_post * sizeof(uint64_t);
 }
 
 extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
                                    int32_t n_post, int32_t nb, int32_t P, const int32_t* seg,
                                    const uint16_t* lidx, const float* lw, const int32_t* qexp,
                                    float w_homo, float* out, int32_t accumulate, void* workspace,
-                                   size_t workspace_bytes, bs_stream_t stream) {
+                                   size_t workspace_bytes, int32_t single_launch,
+                                   int32_t* est_out, bs_stream_t stream) {
   bs_clear_error();
   int rc = check_layout(n_pre, n_post, nb, P, "bs_event_bucket_f32");
   if (rc) return rc;
@@ -409,25 +753,41 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
   hipStream_t s = bs_stream(stream);
   if (n_pre == 0) return accumulate ? BS_OK : bs_fill_f32(out, n_post, 0.0f, s);
   BS_CHECK_ARG(spk && seg && lidx, "bs_event_bucket_f32: NULL pointer");
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || (uintptr_t)spk % sizeof(float) == 0,
+               "bs_event_bucket_f32: f32 spikes not 4-byte aligned");
   BS_CHECK_ARG(lw == nullptr || qexp != nullptr, "bs_event_bucket_f32: qexp is NULL");
-  const int32_t R = row_groups(n_pre, nb);
-  const size_t need = (size_t)R * n_post * sizeof(uint64_t);
+  const int32_t Rmax = row_groups(n_pre, nb);
+  const int32_t R = single_launch ? 1 : Rmax;  // one group per bucket: no partials, no reduce
+  // single launch: each bucket's posts split over nsub workgroups (every one scans the spikes
+  // and the bucket's synapses, and adds and writes only its slice)
+  const int32_t nsub = single_launch ? (kSubSingle < P ? kSubSingle : P) : 1;
+  const size_t need = (size_t)kHdr + (single_launch ? 0 : (size_t)R * n_post * sizeof(uint64_t));
   BS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                "bs_event_bucket_f32: workspace of %zu bytes needed (got %zu)", need,
                workspace ? workspace_bytes : (size_t)0);
-  const int32_t rows = (int32_t)(((int64_t)n_pre + R - 1) / R);
-  uint64_t* part = (uint64_t*)workspace;
-  const int64_t g = (int64_t)nb * R;
-#define BS_BK(T, H)                                                                        \
-  k_bucket_scatter<T, H><<<(int)g, kSB, 0, s>>>((const T*)spk, n_pre, rows, nb, P, seg, lidx, \
-                                                lw, qexp, n_post, part)
-  if (spk_dtype == BS_SPK_U8) { if (lw) BS_BK(uint8_t, true); else BS_BK(uint8_t, false); }
-  else { if (lw) BS_BK(float, true); else BS_BK(float, false); }
+  BS_CHECK_ARG((uintptr_t)workspace % 8 == 0,
+               "bs_event_bucket_f32: workspace not 8-byte aligned");
+  int32_t* hdr = (int32_t*)workspace;  // R_eff, written by the step kernel
+  uint64_t* part = (uint64_t*)((char*)workspace + kHdr);
+  const int64_t g = (int64_t)nb * nsub * R;
+  const bool vec = (uintptr_t)spk % 16 == 0;  // 16-byte spike loads
+#define BS_BK(T, H, V)                                                                      \
+  k_bucket_scatter<T, H, V><<<(int)g, kSB, 0, s>>>((const T*)spk, n_pre, R, Rmax, nb, P, nsub, seg, \
+                                                   lidx, lw, qexp, n_post, w_homo, accumulate, \
+                                                   out, hdr, est_out, part)
+#define BS_BK2(T, H) \
+  do { if (vec) BS_BK(T, H, true); else BS_BK(T, H, false); } while (0)
+  if (spk_dtype == BS_SPK_U8) { if (lw) BS_BK2(uint8_t, true); else BS_BK2(uint8_t, false); }
+  else { if (lw) BS_BK2(float, true); else BS_BK2(float, false); }
+#undef BS_BK2
 #undef BS_BK
   BS_CHECK_LAUNCH();
+  if (single_launch) return BS_OK;
   const int gr = (int)(((int64_t)n_post + 255) / 256);
-  if (lw) k_bucket_reduce<true><<<gr, 256, 0, s>>>(n_post, R, part, qexp, w_homo, accumulate, out);
-  else k_bucket_reduce<false><<<gr, 256, 0, s>>>(n_post, R, part, qexp, w_homo, accumulate, out);
+  if (lw)
+    k_bucket_reduce<true><<<gr, 256, 0, s>>>(n_post, R, hdr, part, qexp, w_homo, accumulate, out);
+  else
+    k_bucket_reduce<false><<<gr, 256, 0, s>>>(n_post, R, hdr, part, qexp, w_homo, accumulate, out);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

@@ -292,25 +292,60 @@ def build_buckets(indices, n_post, w=None, w_homo=0.0, indptr=None, k=None):
                 w=lw, qexp=qexp, w_homo=float(w_homo))
 
 
-def event_bucket(spk, layout, out=None, accumulate=False):
-    """``EventArray(spk) @ conn`` on a destination-bucketed layout (``build_buckets``)."""
+def _bucket_call_args(L):
+    """The layout's fixed arguments of bs_event_bucket_f32 and its workspace size, computed
+    once per layout (the tensors they point into live in the layout dict)."""
+    opt = lambda t: N.ptr(t) if t is not None else None
+    nbytes = int(N.lib().bs_event_bucket_workspace_size(L['n_pre'], L['n_post'], L['nb']))
+    return ((L['n_pre'], L['n_post'], L['nb'], L['P'], N.ptr(L['seg']), N.ptr(L['lidx']),
+             opt(L['w']), opt(L['qexp']), L['w_homo']), nbytes,
+            (L['seg'], L['lidx'], L['w'], L['qexp']))
+
+
+def _bucket_hint(L):
+    """The layout's density hint: an int32 in pinned host memory that each step's kernel
+    overwrites with its estimate of the row groups the spikes need (0: no step yet)."""
+    h = L.get('_hint')
+    if h is None:
+        t = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        h = L['_hint'] = (t, t.numpy(), ctypes.c_void_p(t.data_ptr()))
+    return h
+
+
+def event_bucket(spk, layout, out=None, accumulate=False, mode='auto'):
+    """``EventArray(spk) @ conn`` on a destination-bucketed layout (``build_buckets``).
+
+    mode 'auto' launches one kernel (no partial sums, no reduce) when the previous step on
+    this layout estimated one row group, else the two-kernel form; 'single' / 'split' force
+    one.  The estimate is read without a synchronisation, so it may lag a step or two; both
+    forms give the same bits."""
     spk = _spk_view(spk)
     L = layout
     dev = L['seg'].device
+    cached = L.get('_call')
+    if cached is None or any(a is not b for a, b in
+                             zip(cached[2], (L['seg'], L['lidx'], L['w'], L['qexp']))):
+        cached = L['_call'] = _bucket_call_args(L)
+    fixed, nbytes = cached[0], cached[1]
+    hint = _bucket_hint(L)
+    if mode == 'auto':
+        single = 1 if hint[1][0] == 1 else 0
+    elif mode in ('single', 'split'):
+        single = 1 if mode == 'single' else 0
+    else:
+        raise ValueError(f"event_bucket: mode must be 'auto', 'single' or 'split', got {mode!r}")
     if out is None:
         out = torch.empty(L['n_post'], dtype=torch.float32, device=dev)
-    nbytes = int(N.lib().bs_event_bucket_workspace_size(L['n_pre'], L['n_post'], L['nb']))
-    key = ('bucket', dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    key = ('bucket', dev.index, sh)
     ws = _WS_CACHE.get(key)
     if nbytes > 0 and (ws is None or ws.numel() < nbytes):
         ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
         _WS_CACHE[key] = ws
     N.check(N.lib().bs_event_bucket_f32(
-        N.ptr(spk), _spk_dtype(spk), L['n_pre'], L['n_post'], L['nb'], L['P'], N.ptr(L['seg']),
-        N.ptr(L['lidx']), N.ptr(L['w']) if L['w'] is not None else None,
-        N.ptr(L['qexp']) if L['qexp'] is not None else None, L['w_homo'], N.ptr(out),
-        1 if accumulate else 0, N.ptr(ws) if nbytes > 0 else None, nbytes,
-        N.stream_handle(dev)), 'bs_event_bucket_f32')
+        N.ptr(spk), _spk_dtype(spk), *fixed, N.ptr(out), 1 if accumulate else 0,
+        N.ptr(ws) if nbytes > 0 else None, nbytes, single, hint[2], ctypes.c_void_p(sh)),
+        'bs_event_bucket_f32')
     return out
 
 

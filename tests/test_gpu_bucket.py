@@ -222,3 +222,158 @@ def test_matvec_2000_fixture_on_every_path(torch_cuda):
         assert sha(ops.event_matvec(d_spk, d_idx, c['w_homo'], c['n_post']).cpu().numpy()) \
             == case['homo_sha256']
         assert sha(ops.event_gather(d_spk, sell).cpu().numpy()) == case['het_sequential_sha256']
+
+
+def _bucket_ws_header(torch, dev_index=0):
+    """R_eff the last bucketed step on the current stream chose (workspace word 0)."""
+    from brainstate_amd import ops
+    key = ('bucket', dev_index, torch.cuda.current_stream(dev_index).cuda_stream)
+    return int(ops._WS_CACHE[key][:4].view(torch.int32).item())
+
+
+def _expected_row_groups(s, n_pre, nb):
+    """The documented rule: R_eff = ceil(active rows of the leading min(n_pre, 16384) rows,
+    scaled to n_pre, / 256), within [1, R], R = min(256 // nb, ceil(n_pre / 64))."""
+    ns = min(n_pre, 16384)
+    act = int(np.count_nonzero(np.asarray(s)[:ns]))
+    re = -(-act * n_pre // (ns * 256))
+    R = max(1, min(256 // nb, -(-n_pre // 64)))
+    return max(1, min(R, re))
+
+
+@pytest.mark.parametrize('n_pre,n_post,k,p,het,accumulate,sdt', [
+    (100_000, 100_000, 100, 0.001, True, False, 'u8'),   # R_eff = 1: the step writes out
+    (20_000, 100_000, 200, 0.1, True, True, 'u8'),       # R_eff = 8 of 28 partials
+    (20_000, 100_000, 200, 0.1, False, False, 'u8'),
+    (100_000, 50_000, 20, 0.5, True, False, 'u8'),       # R_eff = R (capped)
+    (60_000, 30_000, 20, 0.5, True, False, 'f32'),       # R_eff = R, f32 spikes
+    (60_000, 30_000, 20, 0.002, False, True, 'f32')])    # R_eff = 1, f32 spikes
+def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, accumulate,
+                                          sdt):
+    """The step picks its number of row groups from the spikes on the device; whatever it
+    picks, the sums are the fixed-point restatement's bit for bit (homogeneous: the
+    sequential scatter's), and accumulate adds onto out with the same arithmetic."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket row groups', n_pre, n_post, k, p, het, accumulate, sdt)
+    rng = np.random.RandomState(n_pre + k)
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F) if het else None
+    act = rng.rand(n_pre) < p
+    s = act.astype(np.uint8) if sdt == 'u8' else np.where(act, rng.rand(n_pre) + 0.5, 0).astype(F)
+    L = ops.build_buckets(dev(torch, idx), n_post, w=w, w_homo=0.6)
+    base = rng.rand(n_post).astype(F)
+    R_est = _expected_row_groups(s, n_pre, L['nb'])
+    gots = {}
+    for mode in ('split', 'single', 'auto'):
+        out = dev(torch, base.copy())
+        gots[mode] = ops.event_bucket(dev(torch, s), L, out=out, accumulate=accumulate,
+                                      mode=mode).cpu().numpy()
+        # R_eff the step used (single: 1) and the estimate it left in the pinned hint
+        used = 1 if mode == 'single' or (mode == 'auto' and R_est == 1) else R_est
+        assert _bucket_ws_header(torch) == used, mode
+        assert int(L['_hint'][1][0]) == R_est, mode
+    got = gots['split']
+    assert np.array_equal(gots['single'], got) and np.array_equal(gots['auto'], got)
+    indptr = np.arange(n_pre + 1, dtype=np.int64) * k
+    if het:
+        S = int(L['qexp'].item())
+        want = event.scatter_fixed_point(s, indptr, idx.reshape(-1), w, n_post, S)
+        if accumulate:
+            want = (base + want).astype(F)
+    else:
+        # homogeneous: counted events, then w added c times from out (or 0) in one chain
+        cnt = np.zeros(n_post, np.int64)
+        np.add.at(cnt, idx[act].reshape(-1), 1)
+        want = (base.copy() if accumulate else np.zeros(n_post, F))
+        for c in range(1, int(cnt.max()) + 1):
+            want = np.where(cnt >= c, (want + F(0.6)).astype(F), want).astype(F)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize('het', [True, False])
+def test_bucket_skewed_activity(torch_cuda, het):
+    """A silent leading sample (R_eff = 1) followed by 23,616 active rows: one row group lists
+    more than 4096 active rows per 16,384-row batch, so the batches split in four and the list
+    is flushed many times; the sums stay exact."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket skewed activity', het)
+    n_pre, n_post, k = 40_000, 50_000, 64
+    rng = np.random.RandomState(77)
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F) if het else None
+    s = np.zeros(n_pre, np.uint8)
+    s[16384:] = 1
+    L = ops.build_buckets(dev(torch, idx), n_post, w=w, w_homo=0.6)
+    got = ops.event_bucket(dev(torch, s), L).cpu().numpy()
+    assert _bucket_ws_header(torch) == 1
+    if het:
+        indptr = np.arange(n_pre + 1, dtype=np.int64) * k
+        want = event.scatter_fixed_point(s, indptr, idx.reshape(-1), w, n_post,
+                                         int(L['qexp'].item()))
+    else:
+        want = event.scatter_fixed(s, idx, F(0.6), n_post)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize('sdt,p', [('u8', 0.01), ('u8', 0.3), ('f32', 0.05)])
+def test_bucket_unaligned_spike_views(torch_cuda, sdt, p):
+    """Spike vectors that do not start on a 16-byte boundary (a row of a [T, n] tensor with
+    n % 16 != 0) take the per-row loads and give the same sums."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket unaligned', sdt, p)
+    n_pre, n_post, k = 30_001, 20_000, 30
+    rng = np.random.RandomState(3)
+    idx = rng.randint(0, n_post, (n_pre, k)).astype(np.int32)
+    w = rng.normal(0.5, 0.1, (n_pre, k)).astype(F)
+    s = rng.rand(n_pre) < p
+    spk = s.astype(np.uint8) if sdt == 'u8' else np.where(s, rng.rand(n_pre) + 0.5, 0).astype(F)
+    buf = dev(torch, np.concatenate([np.zeros(1, spk.dtype), spk]))
+    view = buf[1:]
+    assert view.data_ptr() % 16 != 0
+    L = ops.build_buckets(dev(torch, idx), n_post, w=w)
+    got = ops.event_bucket(view, L).cpu().numpy()
+    aligned = ops.event_bucket(dev(torch, spk), L).cpu().numpy()
+    indptr = np.arange(n_pre + 1, dtype=np.int64) * k
+    want = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, n_post,
+                                     int(L['qexp'].item()))
+    assert np.array_equal(got, want) and np.array_equal(aligned, want)
+
+
+def test_bucket_graph_replays(torch_cuda):
+    """The step captured in a HIP graph: each replay re-reads the spike buffer and picks its
+    row groups on the device (sparse and dense contents alternate), with eager calls and
+    synchronisations between replays; every replay equals the eager result."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('bucket graph replays')
+    n_pre, n_post, k = 50_000, 60_000, 100
+    rng = np.random.RandomState(21)
+    idx = dev(torch, rng.randint(0, n_post, (n_pre, k)).astype(np.int32))
+    w = dev(torch, rng.normal(0.5, 0.1, (n_pre, k)).astype(F))
+    L = ops.build_buckets(idx, n_post, w=w)
+    spks = [dev(torch, (rng.rand(n_pre) < p).astype(np.uint8)) for p in (0.001, 0.2, 0.02)]
+    eager = [ops.event_bucket(x, L).cpu().numpy() for x in spks]
+    x = torch.zeros(n_pre, dtype=torch.uint8, device='cuda')
+    out = torch.empty(n_post, device='cuda')
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        x.copy_(spks[1])
+        ops.event_bucket(x, L, out=out)  # workspace of the capture stream allocated here
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        ops.event_bucket(x, L, out=out)
+    for rep in range(6):
+        j = rep % 3
+        x.copy_(spks[j])
+        out.fill_(-1.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager[j]), rep
+        again = ops.event_bucket(spks[(j + 1) % 3], L).cpu().numpy()
+        assert np.array_equal(again, eager[(j + 1) % 3])
