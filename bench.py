@@ -101,13 +101,19 @@ def cpu_baseline(idx_e, idx_i, V0, n_exc, k, budget_s, single_s=4.0):
                               'ms_per_sim_step': el1 / steps1 * 1e3}}
 
 
-def summarize_rocpd(path):
+def summarize_rocpd(path, parts=1, anchor=None):
     """Text summary of a rocprofv3 results database: kernel stats, and PMC counters per
-    dispatch of each kernel when the database holds them."""
+    dispatch of each kernel when the database holds them.  With parts > 1 and an anchor kernel
+    (a substring of its name), the anchor's dispatches are cut in `parts` equal runs in time
+    order (a workload that runs the same calls once per setting, e.g. per spike density) and
+    every dispatch is given to the run its start falls in: median durations and mean counter
+    values per run follow."""
     import sqlite3
     db = sqlite3.connect(path)
     cur = db.cursor()
     tabs = {r[0] for r in cur.execute("select name from sqlite_master")}
+    if parts > 1 and anchor:
+        return _summarize_parts(cur, tabs, parts, anchor)
     out = ['kernel | calls | total_us | avg_us | pct']
     for name, calls, tot, avg, pct in cur.execute(
             'select name, total_calls, total_duration, average, percentage from top_kernels'):
@@ -119,6 +125,43 @@ def summarize_rocpd(path):
              'group by kernel_name, counter_name order by avg(value) desc')
         for kname, cname, ndisp, val in cur.execute(q):
             out.append(f'{kname[:110]} | {cname} | {ndisp} | {val:.1f}')
+    return '\n'.join(out)
+
+
+def _summarize_parts(cur, tabs, parts, anchor):
+    disp = list(cur.execute('select name, start, end, grid_x from kernels order by start'))
+    starts = [s0 for name, s0, _, _ in disp if anchor in name]
+    if not starts:
+        return f'no dispatch of {anchor!r}'
+    # a run ends at its last anchor dispatch: what follows belongs to the next setting
+    cuts = [starts[len(starts) * i // parts - 1] for i in range(1, parts)]
+    part_of = lambda t: sum(t > c for c in cuts)
+    rows = {}
+    for name, s0, e0, grid in disp:
+        rows.setdefault(name, [[] for _ in range(parts)])[part_of(s0)].append(
+            ((e0 - s0) / 1e3, grid))
+    out = [f'median duration (us) per run [dispatches, grid threads]; a run ends with its '
+           f'last dispatch of {anchor}']
+    for name, per in sorted(rows.items(), key=lambda kv: -sum(len(p) for p in kv[1])):
+        cells = []
+        for p in per:
+            if p:
+                grids = sorted({g for _, g in p})
+                cells.append(f'{np.median([d for d, _ in p]):.2f} [{len(p)}, '
+                             f'{"/".join(str(g) for g in grids)}]')
+            else:
+                cells.append('-')
+        out.append(f'{name[:90]} | ' + ' | '.join(cells))
+    if 'counters_collection' in tabs:
+        out.append('')
+        out.append('kernel | counter | mean value per dispatch per run [dispatches]')
+        vals = {}
+        for kname, cname, v, s0 in cur.execute(
+                'select kernel_name, counter_name, value, start from counters_collection'):
+            vals.setdefault((kname, cname), [[] for _ in range(parts)])[part_of(s0)].append(v)
+        for (kname, cname), per in sorted(vals.items()):
+            cells = [f'{np.mean(p):.1f} [{len(p)}]' if p else '-' for p in per]
+            out.append(f'{kname[:90]} | {cname} | ' + ' | '.join(cells))
     return '\n'.join(out)
 
 
@@ -203,12 +246,12 @@ def bench_sparse(args):
         tf = _timed(fused, 20)
         tb = _timed(bucket, 50)
         hint = int(bkt['_hint'][1][0])   # the estimate the timed calls left: their mode
-        tbg = _graph_timed(bucket, 50)
+        tbg = None if args.no_graph else _graph_timed(bucket, 50)
         b_s = n * 1 + E * 8 + n * 4
         b_g = (n + 1) * 4 + sell['padded'] * 4 + E * 4 + n + n * 4
         lines.append({'workload': f'event_matvec_100k_K1000_p{p}', 'events': E,
                       'bucket_us': tb * 1e6, 'bucket_GSOPs': E / tb / 1e9,
-                      'bucket_graph_us': tbg * 1e6,
+                      'bucket_graph_us': tbg * 1e6 if tbg is not None else None,
                       'bucket_mode': 'single launch' if hint == 1 else f'split, {hint} row groups',
                       'bucket_alg_GBs': b_s / tb / 1e9, 'bucket_frac': b_s / tb / PEAK_HBM,
                       'fused_matvec_us': tf * 1e6, 'fused_GSOPs': E / tf / 1e9,
@@ -452,10 +495,15 @@ def main():
                          'the reported line is D = 0, as the config')
     ap.add_argument('--cpu-budget', type=float, default=12.0)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--no-graph', action='store_true',
+                    help='sparse workload: skip the HIP-graph replay timing (counter runs)')
     ap.add_argument('--copy-calibration-mb', type=int, default=0,
                     help='only run a plain device copy of this many MiB (PMC counter scale)')
     ap.add_argument('--summarize', default=None,
                     help='only print a text summary of a rocprofv3 results database')
+    ap.add_argument('--parts', type=int, default=1,
+                    help='--summarize: cut the run in this many parts at --anchor dispatches')
+    ap.add_argument('--anchor', default=None, help='--summarize: kernel name substring')
     ap.add_argument('--workload', default='coba_lif_1m',
                     choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn', 'batch',
                              'for_loop'],
@@ -468,7 +516,7 @@ def main():
             print(json.dumps(line), flush=True)
         return
     if args.summarize:
-        print(summarize_rocpd(args.summarize))
+        print(summarize_rocpd(args.summarize, args.parts, args.anchor))
         return
     if args.copy_calibration_mb:
         import torch
@@ -549,6 +597,11 @@ def main():
                      'kernel_ms_per_launch': float(np.mean(kern_ms)),
                      'alg_bytes_per_launch': float(np.mean(alg))},
     }
+    # release the device memory before the interpreter exits (nothing of the runner is left
+    # for the HIP runtime's own teardown)
+    del runner, counts, wcounts
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     if not args.no_cpu:
         print('[bench] timing CPU baseline', file=sys.stderr, flush=True)
         res['cpu_baseline'] = cpu_baseline(idx_e, idx_i, V0, n_exc, k, args.cpu_budget)
