@@ -147,14 +147,17 @@ struct LifModel {
     return bs_lif_update<kCuba, kSoft>(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
   }
   // Whether the neuron may spike this step: a zero-input forward-Euler estimate of the next
-  // V within 15 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
-  // estimate never decides a spike.
+  // V within 7 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
+  // estimate never decides a spike.  Measured at config [3] (us per step): margin 0.02 7.45,
+  // 0.05 7.24, 0.07 7.235, 0.10 7.25, 0.15 7.33, 0.20 7.51; V alone against a 0.15 / 0.25
+  // margin 7.96 / 8.13 (too many rows); extrapolating V by the step's own change 7.76-8.03
+  // (misses the neurons the next input pushes over).
   __device__ static bool near(const Params& p, const Regs& r) {
     const float I = kCuba ? p.I_ext + r.ge * p.decay_e * p.scale_e + r.gi * p.decay_i * p.scale_i
                           : p.I_ext + r.ge * p.decay_e * (p.E_e - r.V) +
                                 r.gi * p.decay_i * (p.E_i - r.V);
     const float vp = r.V + p.dt * p.inv_tau * ((p.V_rest - r.V) + p.R * I);
-    return r.ref <= 0 && vp >= p.V_th - 0.15f * (p.V_th - p.V_reset);
+    return r.ref <= 0 && vp >= p.V_th - 0.07f * (p.V_th - p.V_reset);
   }
 };
 
@@ -274,6 +277,16 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / BS_WAVE);  // wave-uniform
   const int64_t base = (int64_t)me * kChunk;
   const int64_t n = a.n;
+  // this thread's neurons jv0 + q * kBlock (n < 2^31: 32-bit), and which of them exist and
+  // are excitatory, as bit q of two masks: the same every step, so tested once per launch
+  // (a 64-bit compare costs two VALU ops on every lane, and every step used several)
+  const uint32_t jv0 = (uint32_t)me * kChunk + threadIdx.x;
+  uint32_t valid = 0u, exc = 0u;
+#pragma unroll
+  for (int q = 0; q < NPT; ++q) {
+    valid |= (jv0 + q * kBlock < (uint32_t)a.n ? 1u : 0u) << q;
+    exc |= (jv0 + q * kBlock < (uint32_t)a.n_exc ? 1u : 0u) << q;
+  }
   WsHeader* hdr = (WsHeader*)a.ws;
   uint64_t* cnt = (uint64_t*)(a.ws + L.off_cnt);
   const uint64_t* ofs = (const uint64_t*)(a.ws + L.off_ofs);
@@ -345,9 +358,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // loads write to LDS (s_junk) rather than registers, so no register is held for them.
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
-      const int64_t j = base + q * kBlock + threadIdx.x;
-      if (j < n && Model::near(p, r[q])) {
-        int32_t jv = (int32_t)j;
+      if (((valid >> q) & 1u) && Model::near(p, r[q])) {
+        int32_t jv = (int32_t)(jv0 + q * kBlock);
         asm volatile("" : "+v"(jv));  // keeps the row addresses from being hoisted out of the loop
         const Row rw = row_of(a, jv);
         const int last = rw.k - 1;
@@ -427,10 +439,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     uint32_t h = 0;
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
-      const int64_t j = base + q * kBlock + threadIdx.x;
       const int loc = q * kBlock + threadIdx.x;
       last[q] = false;
-      if (j < n) {
+      if ((valid >> q) & 1u) {
         const uint2 acc = *(uint2*)&s_acc[2 * loc];
         *(uint2*)&s_acc[2 * loc] = make_uint2(0u, 0u);
         float in_e, in_i;
@@ -442,8 +453,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           in_i = repeated_sum(s_tab[1], a.w_i_homo, acc.y);
         }
         last[q] = Model::update(p, r[q], in_e, in_i);
-        if (last[q]) h += bs_mix32((uint32_t)j);
-        if (a.raster) a.raster[(int64_t)t * n + j] = last[q] ? 1 : 0;
+        if (last[q]) h += bs_mix32(jv0 + q * kBlock);
+        if (a.raster) a.raster[(int64_t)t * n + (jv0 + q * kBlock)] = last[q] ? 1 : 0;
       }
     }
 
@@ -456,9 +467,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       uint32_t wE = 0, wI = 0;
 #pragma unroll
       for (int q = 0; q < NPT; ++q) {
-        const int64_t j = base + q * kBlock + threadIdx.x;
-        mE[q] = bs_ballot(last[q] && j < a.n_exc);
-        mI[q] = bs_ballot(last[q] && j >= a.n_exc);
+        const bool e = (exc >> q) & 1u;
+        mE[q] = bs_ballot(last[q] && e);
+        mI[q] = bs_ballot(last[q] && !e);
         wE += (uint32_t)__popcll(mE[q]);
         wI += (uint32_t)__popcll(mI[q]);
       }
@@ -471,9 +482,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       bI = __builtin_amdgcn_readfirstlane(bI);
 #pragma unroll
       for (int q = 0; q < NPT; ++q) {
-        const int32_t j = (int32_t)(base + q * kBlock + threadIdx.x);
+        const int32_t j = (int32_t)(jv0 + q * kBlock);
         if (last[q]) {
-          if (j < a.n_exc) s_list[bE + bs_rank_below(mE[q])] = j;
+          if ((exc >> q) & 1u) s_list[bE + bs_rank_below(mE[q])] = j;
           else s_list[kChunk - 1 - (int)(bI + bs_rank_below(mI[q]))] = j;
         }
         bE += (uint32_t)__popcll(mE[q]);
