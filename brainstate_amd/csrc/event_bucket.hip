@@ -172,12 +172,13 @@ __global__ void k_bucket_qexp(const uint32_t* wmax, int64_t nnz_fixed, const int
 // 16 bytes of spikes (16 u8 rows or 4 f32 rows) of block blk = rows [blk*E, blk*E + E), rows
 // outside [r0, r1) read as 0: one vector load when the whole block lies inside and the
 // vector is 16-byte aligned, else one load per row in range.
-template <typename T, bool kVec>
-__device__ __forceinline__ uint4 spike_block(const T* __restrict__ spk, uint32_t blk, uint32_t r0,
-                                             uint32_t r1) {
+// The per-row form, out of line: it runs only for a block cut by the range or an unaligned
+// vector, and kept inline its code (in every load slot) would be fetched by the instruction
+// cache on every path (measured: 5x the misses of a compact kernel, ~2 us of a dense step).
+template <typename T>
+__device__ __noinline__ uint4 spike_block_rows(const T* __restrict__ spk, uint32_t row,
+                                               uint32_t r0, uint32_t r1) {
   constexpr uint32_t kE = 16 / sizeof(T);
-  const uint32_t row = blk * kE;  // rows < 2^31: 32-bit index math (a 64-bit op costs two)
-  if (kVec && row >= r0 && row + kE <= r1) return *(const uint4*)(spk + row);
   uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (uint32_t e = 0; e < kE; ++e) {
@@ -188,6 +189,15 @@ __device__ __forceinline__ uint4 spike_block(const T* __restrict__ spk, uint32_t
     }
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <typename T, bool kVec>
+__device__ __forceinline__ uint4 spike_block(const T* __restrict__ spk, uint32_t blk, uint32_t r0,
+                                             uint32_t r1) {
+  constexpr uint32_t kE = 16 / sizeof(T);
+  const uint32_t row = blk * kE;  // rows < 2^31: 32-bit index math (a 64-bit op costs two)
+  if (kVec && row >= r0 && row + kE <= r1) return *(const uint4*)(spk + row);
+  return spike_block_rows<T>(spk, row, r0, r1);
 }
 
 // Active rows of a block as a bit mask (u8: byte != 0; f32: value != 0, so -0 is inactive and
@@ -344,7 +354,8 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
 #pragma unroll
   for (int d = 0; d < kDepth; ++d) {
     // slot d: uniform first block, row range and block limit; one compare per lane
-    const uint32_t first = d < kSmpD || r == 0 ? (uint32_t)d * kSB : g0R / kE + (uint32_t)(d - kSmpD) * kSB;
+    const uint32_t first = d < kSmpD || r == 0 ? (uint32_t)d * kSB
+                                               : g0R / kE + (uint32_t)(d - kSmpD) * kSB;
     const uint32_t lo = d < kSmpD || r == 0 ? 0u : g0R;
     const uint32_t hi = d < kSmpD ? (uint32_t)ns : (r == 0 ? N : g1R);
     const uint32_t lim = d < kSmpD ? ((uint32_t)ns + kE - 1) / kE
@@ -587,6 +598,130 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
   }
 }
 
+// Dense spikes (mode 2: the previous call estimated the maximum R): every workgroup owns a
+// fixed row group of `rows` rows, known on the host, so nothing waits for an estimate.  Per
+// span of kSB-row compaction steps: one byte per thread, ballots and a workgroup prefix, the
+// active rows in ascending order; then the bucket bounds of those rows, then phase 3 as in the
+// adaptive kernel.  This compact form is what dense steps are fastest with (config [2] at
+// p = 0.1: 31.6 us against 33.6 us for the adaptive kernel run at R = max).  Workgroup 0
+// writes R to the header and the next call's estimate from its own group's active rows.
+template <typename T, bool kHet>
+__global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
+    const T* __restrict__ spk, int32_t n_pre, int32_t rows, int32_t R, int32_t Rmax, int32_t nb,
+    int32_t P, const int32_t* __restrict__ seg, const uint16_t* __restrict__ lidx,
+    const float* __restrict__ lw, const int32_t* __restrict__ qexp, int32_t n_post,
+    int32_t* __restrict__ hdr, int32_t* __restrict__ est_out, uint64_t* __restrict__ part) {
+  __shared__ uint64_t s_acc[kMaxP];        // fixed-point sums, fp32 sums or event counts
+  uint32_t* s_acc32 = (uint32_t*)s_acc;
+  __shared__ int32_t s_beg[kSpan];
+  __shared__ int32_t s_len[kSpan];
+  __shared__ int32_t s_wave[kSB / BS_WAVE];
+  const int lane = bs_lane();
+  const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / BS_WAVE));
+  const int32_t b = blockIdx.x % nb;
+  const int32_t r = blockIdx.x / nb;
+  const int32_t p0 = b * P;
+  const int32_t pn = n_post - p0 < P ? n_post - p0 : P;  // posts in this bucket
+  for (int j = threadIdx.x; j < pn; j += kSB) s_acc[j] = 0ull;
+  // fixed point (S >= -999) unless a weight is not finite; scale = 2^S exactly
+  const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
+  const bool fixed = kHet && S > -1000;
+  const double scale = fixed ? ldexp(1.0, S) : 1.0;
+  const int64_t r0 = (int64_t)r * rows;
+  const int64_t r1 = r0 + rows < n_pre ? r0 + rows : n_pre;
+  const int stride = nb + 1;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *hdr = R;
+  int32_t group_active = 0;  // active rows of the group (for workgroup 0's estimate)
+  for (int64_t c0 = r0; c0 < r1; c0 += kSpan) {
+    // 1. active rows of the span, ascending
+    int32_t count = 0;
+    for (int32_t o = 0; o < kSpan; o += kSB) {
+      const int64_t row = c0 + o + threadIdx.x;
+      const bool a = row < r1 && spk[row] != T(0);
+      const uint64_t m = bs_ballot(a);
+      if (lane == 0) s_wave[wid] = __popcll(m);
+      __syncthreads();
+      int32_t pos = count, tot = 0;
+#pragma unroll
+      for (int v = 0; v < kSB / BS_WAVE; ++v) {
+        pos += v < wid ? s_wave[v] : 0;
+        tot += s_wave[v];
+      }
+      if (a) s_beg[pos + bs_rank_below(m)] = (int32_t)row;
+      count += tot;
+      __syncthreads();  // s_wave is rewritten next round
+    }
+    group_active += count;
+    // 2. bounds of bucket b in each active row
+    for (int32_t x = threadIdx.x; x < count; x += kSB) {
+      const int32_t* sr = seg + (int64_t)s_beg[x] * stride + b;
+      const int32_t lo = sr[0], hi = sr[1];
+      s_beg[x] = lo;
+      s_len[x] = hi - lo;
+    }
+    __syncthreads();
+    // 3. synapses of kRowsPer rows, up to kPasses x 64 each, loads in flight together
+    for (int32_t a0 = wid * kRowsPer; a0 < count; a0 += (kSB / BS_WAVE) * kRowsPer) {
+      int32_t beg[kRowsPer], len[kRowsPer];
+      int32_t maxlen = 0;
+#pragma unroll
+      for (int q = 0; q < kRowsPer; ++q) {
+        const bool ok = a0 + q < count;
+        beg[q] = ok ? s_beg[a0 + q] : 0;
+        len[q] = ok ? s_len[a0 + q] : 0;
+        maxlen = len[q] > maxlen ? len[q] : maxlen;
+      }
+      for (int32_t e0 = 0; e0 < maxlen; e0 += kPasses * BS_WAVE) {
+        uint16_t t[kPasses][kRowsPer];
+        float v[kPasses][kRowsPer];
+#pragma unroll
+        for (int u = 0; u < kPasses; ++u) {
+#pragma unroll
+          for (int q = 0; q < kRowsPer; ++q) {
+            const int32_t e = e0 + u * BS_WAVE + lane;
+            t[u][q] = 0xFFFFu;
+            v[u][q] = 0.0f;
+            if (e < len[q]) {
+              t[u][q] = lidx[(int64_t)beg[q] + e];
+              if (kHet) v[u][q] = lw[(int64_t)beg[q] + e];
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kPasses; ++u) {
+#pragma unroll
+          for (int q = 0; q < kRowsPer; ++q) {
+            if (t[u][q] != 0xFFFFu) {
+              if (!kHet) {
+                atomicAdd(&s_acc32[t[u][q]], 1u);
+              } else if (fixed) {
+                const int64_t qv = (int64_t)__builtin_rint((double)v[u][q] * scale);
+                atomicAdd((unsigned long long*)&s_acc[t[u][q]], (unsigned long long)qv);
+              } else {
+                atomicAdd((float*)&s_acc32[t[u][q]], v[u][q]);
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // s_beg / s_len are rewritten by the next span
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0 && est_out && r1 > r0) {
+    // the next call's hint: the group's share of active rows, scaled to n_pre
+    const double re = ceil((double)group_active * (double)n_pre /
+                           ((double)(r1 - r0) * kActivePer));
+    *est_out = re < 1.0 ? 1 : (re > (double)Rmax ? Rmax : (int32_t)re);
+  }
+  __syncthreads();
+  uint64_t* dst = part + (int64_t)r * n_post + p0;
+  if (kHet && fixed) {
+    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc[j];
+  } else {
+    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
+  }
+}
+
 // out[j] = (accumulate ? out[j] : 0) + the bucket sums of j, over the R = *hdr partials the
 // step kernel wrote (R = 1: it wrote out itself, nothing to do).  The first min(8, Rmax)
 // partials are loaded together with the header, not after it: one memory round trip, not two.
@@ -594,7 +729,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
 //   homogeneous: the total count c of events, then c additions of w (the sequential chain);
 //   fp32 fallback: the R partials added in row-group order.
 template <bool kHet>
-__global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t Rmax,
+__global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t Rmax, int32_t Rfix,
                                                        const int32_t* __restrict__ hdr,
                                                        const uint64_t* __restrict__ part,
                                                        const int32_t* __restrict__ qexp,
@@ -608,7 +743,8 @@ __global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t R
   for (int u = 0; u < kFirst; ++u) x0[u] = u < Rmax ? part[(int64_t)u * n_post + j] : 0ull;
   const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
   float acc = accumulate ? out[j] : 0.0f;
-  const int32_t R = __builtin_amdgcn_readfirstlane(*hdr);
+  // Rfix > 0: the host fixed the row groups, no header to wait for
+  const int32_t R = Rfix > 0 ? Rfix : __builtin_amdgcn_readfirstlane(*hdr);
   // (the loads above are consumed on both paths, so they stay ahead of this test)
   uint64_t any = __float_as_uint(acc) + (uint32_t)S;
 #pragma unroll
@@ -741,8 +877,8 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
                                    int32_t n_post, int32_t nb, int32_t P, const int32_t* seg,
                                    const uint16_t* lidx, const float* lw, const int32_t* qexp,
                                    float w_homo, float* out, int32_t accumulate, void* workspace,
-                                   size_t workspace_bytes, int32_t single_launch,
-                                   int32_t* est_out, bs_stream_t stream) {
+                                   size_t workspace_bytes, int32_t mode, int32_t* est_out,
+                                   bs_stream_t stream) {
   bs_clear_error();
   int rc = check_layout(n_pre, n_post, nb, P, "bs_event_bucket_f32");
   if (rc) return rc;
@@ -756,7 +892,10 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
   BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || (uintptr_t)spk % sizeof(float) == 0,
                "bs_event_bucket_f32: f32 spikes not 4-byte aligned");
   BS_CHECK_ARG(lw == nullptr || qexp != nullptr, "bs_event_bucket_f32: qexp is NULL");
+  BS_CHECK_ARG(mode >= 0 && mode <= 2, "bs_event_bucket_f32: mode %d outside [0, 2]", mode);
   const int32_t Rmax = row_groups(n_pre, nb);
+  const bool single_launch = mode == 1;
+  const bool dense = mode == 2;
   const int32_t R = single_launch ? 1 : Rmax;  // one group per bucket: no partials, no reduce
   // single launch: each bucket's posts split over nsub workgroups (every one scans the spikes
   // and the bucket's synapses, and adds and writes only its slice)
@@ -777,17 +916,31 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
                                                    out, hdr, est_out, part)
 #define BS_BK2(T, H) \
   do { if (vec) BS_BK(T, H, true); else BS_BK(T, H, false); } while (0)
-  if (spk_dtype == BS_SPK_U8) { if (lw) BS_BK2(uint8_t, true); else BS_BK2(uint8_t, false); }
-  else { if (lw) BS_BK2(float, true); else BS_BK2(float, false); }
+#define BS_BD(T, H)                                                                         \
+  k_bucket_scatter_dense<T, H><<<(int)g, kSB, 0, s>>>((const T*)spk, n_pre, rows, R, Rmax, nb, P, \
+                                                      seg, lidx, lw, qexp, n_post, hdr, est_out, \
+                                                      part)
+  if (dense) {
+    const int32_t rows = (int32_t)(((int64_t)n_pre + R - 1) / R);
+    if (spk_dtype == BS_SPK_U8) { if (lw) BS_BD(uint8_t, true); else BS_BD(uint8_t, false); }
+    else { if (lw) BS_BD(float, true); else BS_BD(float, false); }
+  } else if (spk_dtype == BS_SPK_U8) {
+    if (lw) BS_BK2(uint8_t, true); else BS_BK2(uint8_t, false);
+  } else {
+    if (lw) BS_BK2(float, true); else BS_BK2(float, false);
+  }
+#undef BS_BD
 #undef BS_BK2
 #undef BS_BK
   BS_CHECK_LAUNCH();
   if (single_launch) return BS_OK;
   const int gr = (int)(((int64_t)n_post + 255) / 256);
   if (lw)
-    k_bucket_reduce<true><<<gr, 256, 0, s>>>(n_post, R, hdr, part, qexp, w_homo, accumulate, out);
+    k_bucket_reduce<true><<<gr, 256, 0, s>>>(n_post, R, dense ? R : 0, hdr, part, qexp, w_homo,
+                                             accumulate, out);
   else
-    k_bucket_reduce<false><<<gr, 256, 0, s>>>(n_post, R, hdr, part, qexp, w_homo, accumulate, out);
+    k_bucket_reduce<false><<<gr, 256, 0, s>>>(n_post, R, dense ? R : 0, hdr, part, qexp, w_homo,
+                                              accumulate, out);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

@@ -297,9 +297,10 @@ def _bucket_call_args(L):
     once per layout (the tensors they point into live in the layout dict)."""
     opt = lambda t: N.ptr(t) if t is not None else None
     nbytes = int(N.lib().bs_event_bucket_workspace_size(L['n_pre'], L['n_post'], L['nb']))
+    rmax = (nbytes - 256) // (8 * L['n_post']) if nbytes > 0 else 1   # row groups at most
     return ((L['n_pre'], L['n_post'], L['nb'], L['P'], N.ptr(L['seg']), N.ptr(L['lidx']),
              opt(L['w']), opt(L['qexp']), L['w_homo']), nbytes,
-            (L['seg'], L['lidx'], L['w'], L['qexp']))
+            (L['seg'], L['lidx'], L['w'], L['qexp']), rmax)
 
 
 def _bucket_hint(L):
@@ -312,13 +313,17 @@ def _bucket_hint(L):
     return h
 
 
+_BUCKET_MODES = {'split': 0, 'single': 1, 'dense': 2}
+
+
 def event_bucket(spk, layout, out=None, accumulate=False, mode='auto'):
     """``EventArray(spk) @ conn`` on a destination-bucketed layout (``build_buckets``).
 
-    mode 'auto' launches one kernel (no partial sums, no reduce) when the previous step on
-    this layout estimated one row group, else the two-kernel form; 'single' / 'split' force
-    one.  The estimate is read without a synchronisation, so it may lag a step or two; both
-    forms give the same bits."""
+    mode 'auto' follows the previous step's estimate of the row groups the spikes need: one
+    launch with no partial sums when it was one ('single'), the row groups fixed at their
+    maximum when it was that ('dense'), else row groups chosen on the device ('split').  The
+    estimate is read without a synchronisation, so it may lag a step or two; every mode gives
+    the same bits."""
     spk = _spk_view(spk)
     L = layout
     dev = L['seg'].device
@@ -326,14 +331,16 @@ def event_bucket(spk, layout, out=None, accumulate=False, mode='auto'):
     if cached is None or any(a is not b for a, b in
                              zip(cached[2], (L['seg'], L['lidx'], L['w'], L['qexp']))):
         cached = L['_call'] = _bucket_call_args(L)
-    fixed, nbytes = cached[0], cached[1]
+    fixed, nbytes, rmax = cached[0], cached[1], cached[3]
     hint = _bucket_hint(L)
     if mode == 'auto':
-        single = 1 if hint[1][0] == 1 else 0
-    elif mode in ('single', 'split'):
-        single = 1 if mode == 'single' else 0
+        h = int(hint[1][0])
+        m = 1 if h == 1 else (2 if h >= rmax > 1 else 0)
+    elif mode in _BUCKET_MODES:
+        m = _BUCKET_MODES[mode]
     else:
-        raise ValueError(f"event_bucket: mode must be 'auto', 'single' or 'split', got {mode!r}")
+        raise ValueError(f"event_bucket: mode must be 'auto', 'single', 'split' or 'dense', "
+                         f"got {mode!r}")
     if out is None:
         out = torch.empty(L['n_post'], dtype=torch.float32, device=dev)
     sh = torch.cuda.current_stream(dev).cuda_stream
@@ -344,7 +351,7 @@ def event_bucket(spk, layout, out=None, accumulate=False, mode='auto'):
         _WS_CACHE[key] = ws
     N.check(N.lib().bs_event_bucket_f32(
         N.ptr(spk), _spk_dtype(spk), *fixed, N.ptr(out), 1 if accumulate else 0,
-        N.ptr(ws) if nbytes > 0 else None, nbytes, single, hint[2], ctypes.c_void_p(sh)),
+        N.ptr(ws) if nbytes > 0 else None, nbytes, m, hint[2], ctypes.c_void_p(sh)),
         'bs_event_bucket_f32')
     return out
 

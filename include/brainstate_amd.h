@@ -148,15 +148,18 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
  *   - homogeneous weight (lw == NULL): w_homo added once per event onto j, in one chain
  *     starting from out[j] (or 0): bit-identical to a sequential scatter;
  *   - a non-finite per-synapse weight: fp32 sums in an unspecified order.
- * The step is one kernel over nb x R row groups plus a reduce of the partials; R follows the
- * spikes on the device (about 256 active rows per group, estimated from the leading 16,384
- * rows), and at R = 1 the reduce has nothing to do.  single_launch != 0 asks for one launch of
- * nb workgroups that write out themselves (R = 1 whatever the density: right for sparse
- * spikes, slow for dense ones); the sums are the same bits in both modes.  est_out (NULL, or
- * an int32 the device can write, e.g. in pinned host memory) receives the call's estimate of
- * R, so that a caller can pick single_launch for its next call from it without a
+ * The step is one kernel over nb x R row groups plus a reduce of the partials.  mode:
+ *   0  R follows the spikes on the device (about 256 active rows per group, estimated from
+ *      the leading 16,384 rows; at R = 1 the reduce has nothing to do);
+ *   1  one launch of nb x 8 workgroups that write out themselves (R = 1 whatever the
+ *      density: right for sparse spikes, slow for dense ones);
+ *   2  R = its maximum (row_groups), fixed on the host: no estimate on the critical path
+ *      (right for dense spikes).
+ * The sums are the same bits in every mode.  est_out (NULL, or an int32 the device can write,
+ * e.g. in pinned host memory) receives the call's estimate of R (from the leading rows; mode 2:
+ * from row group 0), so that a caller can pick the next call's mode from it without a
  * synchronisation (a stale estimate costs time, never correctness).
- * `workspace`: bs_event_bucket_workspace_size bytes (single_launch: 256 bytes are enough), 8-byte
+ * `workspace`: bs_event_bucket_workspace_size bytes (mode 1: 256 bytes are enough), 8-byte
  * aligned, no initialisation needed. */
 BS_API int bs_bucket_plan(int32_t n_post, int32_t* P_out);
 BS_API int bs_bucket_build(int32_t n_pre, const int32_t* indptr, const int32_t* indices, int32_t k,
@@ -168,7 +171,7 @@ BS_API int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n_pre
                                int32_t nb, int32_t P, const int32_t* seg, const uint16_t* lidx,
                                const float* lw, const int32_t* qexp, float w_homo, float* out,
                                int32_t accumulate, void* workspace, size_t workspace_bytes,
-                               int32_t single_launch, int32_t* est_out, bs_stream_t stream);
+                               int32_t mode, int32_t* est_out, bs_stream_t stream);
 
 /* ---------------------------------------------------------------- N2b event gather
  * Same operator as N2a, post-major and deterministic (no atomics).  Spikes come as a

@@ -264,17 +264,23 @@ def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, 
     L = ops.build_buckets(dev(torch, idx), n_post, w=w, w_homo=0.6)
     base = rng.rand(n_post).astype(F)
     R_est = _expected_row_groups(s, n_pre, L['nb'])
+    R_max = max(1, min(256 // L['nb'], -(-n_pre // 64)))
     gots = {}
-    for mode in ('split', 'single', 'auto'):
+    # 'single' last before 'auto': its estimate (from the leading rows) steers 'auto'
+    for mode in ('split', 'dense', 'single', 'auto'):
         out = dev(torch, base.copy())
         gots[mode] = ops.event_bucket(dev(torch, s), L, out=out, accumulate=accumulate,
                                       mode=mode).cpu().numpy()
-        # R_eff the step used (single: 1) and the estimate it left in the pinned hint
-        used = 1 if mode == 'single' or (mode == 'auto' and R_est == 1) else R_est
+        # row groups the step used (single: 1, dense: the maximum) and its estimate
+        used = {'single': 1, 'dense': R_max}.get(mode, R_est)
         assert _bucket_ws_header(torch) == used, mode
-        assert int(L['_hint'][1][0]) == R_est, mode
+        if mode == 'dense':   # estimated from row group 0's rows
+            assert 1 <= int(L['_hint'][1][0]) <= R_max
+        else:
+            assert int(L['_hint'][1][0]) == R_est, mode
     got = gots['split']
-    assert np.array_equal(gots['single'], got) and np.array_equal(gots['auto'], got)
+    for mode in ('single', 'dense', 'auto'):
+        assert np.array_equal(gots[mode], got), mode
     indptr = np.arange(n_pre + 1, dtype=np.int64) * k
     if het:
         S = int(L['qexp'].item())
