@@ -9,7 +9,7 @@ Restates brainstate/nn/_event_fixedprob.py:142-196:
     ``indptr = [0, cumsum(K * selected)]`` (:185-190).
 
 Pinned by: NumPy's legacy MT19937 stream is frozen, so these arrays are the
-reference's arrays bit for bit; tests/test_oracle_conn.py checks the construction
+reference's arrays bit for bit; tests/test_oracle_event.py checks the construction
 branches against SHA-256 digests recorded in tests/golden/ and against the
 closed-form indptr.
 
