@@ -142,6 +142,10 @@ struct LifModel {
     s.ref[j] = r.ref;
   }
   static constexpr bool kPrepare = false;  // every operation of the step needs the input
+  // parameters and row pointers held in VGPRs (see k_run)
+  static constexpr bool kParamVgprs = true;
+  // count words published by the loop over write-out slots (see k_run)
+  static constexpr bool kPubByLane = false;
   __device__ static void prepare(const Params&, Regs&) {}
   __device__ static bool update(const Params& p, Regs& r, float in_e, float in_i) {
     return bs_lif_update<kCuba, kSoft>(p, r.V, r.ge, r.gi, r.ref, in_e, in_i);
@@ -189,6 +193,13 @@ struct HhModel {
   // The gate updates and channel conductances need only the previous state, so they run
   // before the step's inputs are awaited; the rest of the step follows once they are in.
   static constexpr bool kPrepare = true;
+  // HH keeps 11 values per neuron in registers: its 14 parameters and the row pointers stay
+  // scalar (in VGPRs they pushed the 4-neuron kernel to 128 VGPRs and 76 bytes of spills;
+  // config [5] 9.86 -> 9.49 us per step without them)
+  static constexpr bool kParamVgprs = false;
+  // count words published one destination per lane (config [5] 9.48 -> 9.17 us per step;
+  // the LIF runner measured 7.21 -> 7.25 with it)
+  static constexpr bool kPubByLane = true;
   __device__ static void prepare(const Params& p, Regs& r) {
     r.pre = bs_hh_prepare(p, r.V, r.m, r.h, r.n);
   }
@@ -244,10 +255,11 @@ __device__ __forceinline__ int32_t quantize(float w, float scale) {
 template <class Model, int NPT, bool kHet>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
                                                 typename Model::Params p_arg) {
-  // The parameters live in VGPRs (uniform values, one register each): the update reads them
-  // as vector operands, so they take no scalar registers in a loop that is short of them.
+  // The parameters live in VGPRs (uniform values, one register each) where the model allows:
+  // the update reads them as vector operands, so they take no scalar registers in a loop that
+  // is short of them.
   typename Model::Params p = p_arg;
-  {
+  if constexpr (Model::kParamVgprs) {
     static_assert(sizeof(p) % 4 == 0, "parameters are 32-bit words");
     uint32_t* pw = reinterpret_cast<uint32_t*>(&p);
 #pragma unroll
@@ -335,8 +347,10 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   while ((BS_WAVE << lgE) < a.k_e) ++lgE;
   while ((BS_WAVE << lgI) < a.k_i) ++lgI;
   // values used only in vector arithmetic and addresses: VGPRs, like the parameters
-  asm volatile("" : "+v"(a.idx_e), "+v"(a.w_e), "+v"(a.idx_i), "+v"(a.w_i));
-  asm volatile("" : "+v"(a.n_exc), "+v"(a.k_e), "+v"(a.k_i), "+v"(a.w_e_homo), "+v"(a.w_i_homo));
+  if constexpr (Model::kParamVgprs) {
+    asm volatile("" : "+v"(a.idx_e), "+v"(a.w_e), "+v"(a.idx_i), "+v"(a.w_i));
+    asm volatile("" : "+v"(a.n_exc), "+v"(a.k_e), "+v"(a.k_i), "+v"(a.w_e_homo), "+v"(a.w_i_homo));
+  }
   if (threadIdx.x == 0) {
     s_nsp[0][0] = s_nsp[0][1] = s_nsp[1][0] = s_nsp[1][1] = 0;
     s_ovf = 0u;
@@ -575,34 +589,54 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       for (int x = threadIdx.x; x < nb * kSlots; x += kBlock) {
         const int d = x / kSlots;
         const uint32_t slot = (uint32_t)(x - d * kSlots);
+        // one LDS round trip: the round count, the cursor and the slot (read even when
+        // empty), the cursor reused for its advance (7.24 -> 7.19 us per step at config [3])
         const uint32_t rc = s_rcnt[d];
+        const uint32_t p0 = s_pos[d];
+        uint64_t ent = s_stage[x];
+        asm volatile("" : "+v"(ent));  // keeps the read beside the other two
         if (slot < rc) {
-          const uint32_t pos = s_pos[d] + slot;
-          if (kHet) st_dev64((uint64_t*)ob + pos, s_stage[x]);
-          else st_dev32((uint32_t*)ob + pos, (uint32_t)s_stage[x]);
+          if (kHet) st_dev64((uint64_t*)ob + p0 + slot, ent);
+          else st_dev32((uint32_t*)ob + p0 + slot, (uint32_t)ent);
         }
         if (slot == 0 && rc) {
-          s_pos[d] += rc;
+          s_pos[d] = p0 + rc;
           s_rcnt[d] = 0;
         }
       }
       if (rnd + 1 < rounds) __syncthreads();  // slots and round counts are reused
     }
+    // read before the wait, so that no LDS access follows it before the first publication
+    const bool ovf = rounds > 0 && s_ovf != 0u;   // uniform: set before the round barrier
     __builtin_amdgcn_s_waitcnt(0);  // this wave's entries are complete at device scope
     // Destination d's staged entries were all written by the wave of write-out slots
     // [d*kSlots, (d+1)*kSlots), so that wave alone publishes d once its own stores are
     // complete -- unless an entry went past the slots (stored by another wave): then every
     // wave's stores are awaited first.
-    const bool ovf = rounds > 0 && s_ovf != 0u;   // uniform: set before the round barrier
     if (ovf) __syncthreads();
     {
       uint64_t* cout = cnt + (int64_t)slot_wr * nb * nb;
       const uint64_t tag = (uint64_t)(uint32_t)(ta + 1) << 32;
-      for (int x = threadIdx.x; x < nb * kSlots; x += kBlock) {
-        if (x % kSlots) continue;
-        const int d = x / kSlots;
-        st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - s_ofs_out[d]));
-        s_pos[d] = s_ofs_out[d];
+      if constexpr (Model::kPubByLane) {
+        // the wave's destinations (kSpw per write-out iteration), one lane each: one LDS
+        // round trip instead of one per iteration
+        constexpr int kSpw = BS_WAVE / kSlots;   // destinations per wave and iteration
+        constexpr int kDpi = kBlock / kSlots;    // destinations per iteration
+        constexpr int kPubLanes = kSpw * ((kMaxBlocks + kDpi - 1) / kDpi);
+        static_assert(kPubLanes <= BS_WAVE, "one lane per destination of the wave");
+        const int d = (lane / kSpw) * kDpi + wid * kSpw + lane % kSpw;
+        if (lane < kPubLanes && d < nb) {
+          const uint32_t o0 = s_ofs_out[d];
+          st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - o0));
+          s_pos[d] = o0;
+        }
+      } else {
+        for (int x = threadIdx.x; x < nb * kSlots; x += kBlock) {
+          if (x % kSlots) continue;
+          const int d = x / kSlots;
+          st_dev64(cout + (int64_t)d * nb + me, tag | (s_pos[d] - s_ofs_out[d]));
+          s_pos[d] = s_ofs_out[d];
+        }
       }
       if (ovf) {
         __syncthreads();

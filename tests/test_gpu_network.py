@@ -414,6 +414,51 @@ def test_coba_lif_long_run_across_launches(torch_cuda):
     assert int(ras1.sum().item()) == int(c_ref.sum())
 
 
+@pytest.mark.parametrize('het,D', [(True, 0), (False, 4)])
+def test_runner_rerun_and_reseed_on_one_workspace(torch_cuda, het, D):
+    """Count words carry the step they belong to, so what an earlier run left on the
+    workspace is never taken for a later run's.  On one runner: a rerun from step 0 repeats
+    the first run bit for bit; for delay 0, a run seeded mid-way from another runner's state
+    repeats that runner's remaining steps."""
+    torch = torch_cuda
+    say('rerun / reseed', het, D)
+    T = 300
+    r = _lif_runner(torch, het, delay_steps=D)
+    init = {k: v.clone() for k, v in r.state.items()}
+
+    def go(runner, steps):
+        c = torch.zeros(steps, dtype=torch.int32, device='cuda')
+        h = torch.zeros(steps, dtype=torch.int32, device='cuda')
+        runner.run(steps, counts=c, hashes=h)
+        runner.check()
+        return c.cpu().numpy(), h.cpu().numpy()
+
+    c1, h1 = go(r, T)
+    V1 = r.state['V'].cpu().numpy()
+    assert c1.sum() > 1000
+    for k, v in init.items():
+        r.state[k].copy_(v)
+    r.spk.zero_()
+    r.t = 0
+    c2, h2 = go(r, T)
+    assert np.array_equal(c1, c2) and np.array_equal(h1, h2)
+    assert np.array_equal(r.state['V'].cpu().numpy(), V1)
+    if D:
+        return
+    r2 = _lif_runner(torch, het)
+    go(r2, 150)
+    mid = {k: v.clone() for k, v in r2.state.items()}
+    spk_mid = r2.spk.clone()
+    c_ref, h_ref = go(r2, T - 150)
+    for k, v in mid.items():  # r's workspace still holds the end of its own run
+        r.state[k].copy_(v)
+    r.seed(spk_mid, t0=150)
+    c3, h3 = go(r, T - 150)
+    assert np.array_equal(c3, c_ref) and np.array_equal(h3, h_ref)
+    assert np.array_equal(c_ref, c1[150:])
+    assert np.array_equal(r.state['V'].cpu().numpy(), r2.state['V'].cpu().numpy())
+
+
 def test_coba_hh_2000_raster_bit_exact(torch_cuda):
     torch = torch_cuda
     from brainstate_amd import ops
