@@ -156,8 +156,8 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
  *   2  R = its maximum (row_groups), fixed on the host: no estimate on the critical path
  *      (right for dense spikes).
  * The sums are the same bits in every mode.  est_out (NULL, or an int32 the device can write,
- * e.g. in pinned host memory) receives the call's estimate of R (from the leading rows; mode 2:
- * from row group 0), so that a caller can pick the next call's mode from it without a
+ * e.g. in pinned host memory) receives the call's estimate of R (mode 0: from the leading
+ * rows; mode 1: ceil(active rows / 256) from the exact count; mode 2: from row group 0), so that a caller can pick the next call's mode from it without a
  * synchronisation (a stale estimate costs time, never correctness).
  * `workspace`: bs_event_bucket_workspace_size bytes (mode 1: 256 bytes are enough), 8-byte
  * aligned, no initialisation needed. */

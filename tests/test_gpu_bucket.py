@@ -266,7 +266,7 @@ def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, 
     R_est = _expected_row_groups(s, n_pre, L['nb'])
     R_max = max(1, min(256 // L['nb'], -(-n_pre // 64)))
     gots = {}
-    # 'single' last before 'auto': its estimate (from the leading rows) steers 'auto'
+    # 'single' last before 'auto': its estimate (from the exact count) steers 'auto'
     for mode in ('split', 'dense', 'single', 'auto'):
         out = dev(torch, base.copy())
         gots[mode] = ops.event_bucket(dev(torch, s), L, out=out, accumulate=accumulate,
@@ -276,6 +276,9 @@ def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, 
         assert _bucket_ws_header(torch) == used, mode
         if mode == 'dense':   # estimated from row group 0's rows
             assert 1 <= int(L['_hint'][1][0]) <= R_max
+        elif mode == 'single':   # from the exact active count
+            want_hint = max(1, min(R_max, -(-int(np.count_nonzero(s)) // 256)))
+            assert int(L['_hint'][1][0]) == want_hint, mode
         else:
             assert int(L['_hint'][1][0]) == R_est, mode
     got = gots['split']
