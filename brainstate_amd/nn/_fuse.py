@@ -29,12 +29,16 @@ def _proj_arrays(proj, n_pre, n):
         raise NotImplementedError('fuse() needs fixed-num (EventFixedProb) projections')
     if conn.shape != (n_pre, n):
         raise ValueError(f'projection shape {conn.shape} does not match ({n_pre}, {n})')
-    idx = conn.indices.cpu().numpy()
+    # device tensors stay on the device (no round trip through the host for one replica)
+    idx = conn.indices
     w = proj.comm.weight.value
     if torch.is_tensor(w):
-        w = w.detach().cpu().numpy()
+        w = w.detach()
+        return idx, (float(w.reshape(())) if w.numel() == 1 else
+                     w.to(torch.float32).expand(idx.shape))
     w = np.asarray(w, np.float32)
-    return idx, (float(w.reshape(())) if w.size == 1 else np.broadcast_to(w, idx.shape))
+    return idx, (float(w.reshape(())) if w.size == 1 else
+                 torch.as_tensor(np.broadcast_to(w, idx.shape).copy(), device=idx.device))
 
 
 def _union_perm(B, n, n_exc):
@@ -66,15 +70,17 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     B = int(Vs.shape[0]) if Vs.dim() == 2 else 1   # init_all_states(batch_size=B)
     idx_e, w_e = _proj_arrays(proj_e, n_exc, n)
     idx_i, w_i = _proj_arrays(proj_i, n - n_exc, n)
-    if np.ndim(w_e) != np.ndim(w_i):   # one heterogeneous -> both per synapse
-        w_e = np.broadcast_to(np.float32(w_e), idx_e.shape)
-        w_i = np.broadcast_to(np.float32(w_i), idx_i.shape)
+    dev = idx_e.device
+    if isinstance(w_e, float) != isinstance(w_i, float):   # one heterogeneous -> both per synapse
+        w_e = torch.full(idx_e.shape, w_e, device=dev) if isinstance(w_e, float) else w_e
+        w_i = torch.full(idx_i.shape, w_i, device=dev) if isinstance(w_i, float) else w_i
     perm = _union_perm(B, n, n_exc)
     if B > 1:   # block-diagonal union of the replicas, one runner
-        idx_e = np.concatenate([perm[b][idx_e] for b in range(B)]).astype(np.int32)
-        idx_i = np.concatenate([perm[b][idx_i] for b in range(B)]).astype(np.int32)
-        if np.ndim(w_e):
-            w_e, w_i = np.tile(w_e, (B, 1)), np.tile(w_i, (B, 1))
+        pm = torch.as_tensor(perm, device=dev)
+        idx_e = torch.cat([pm[b][idx_e.long()] for b in range(B)]).to(torch.int32)
+        idx_i = torch.cat([pm[b][idx_i.long()] for b in range(B)]).to(torch.int32)
+        if not isinstance(w_e, float):
+            w_e, w_i = w_e.repeat(B, 1), w_i.repeat(B, 1)
     pt = torch.as_tensor(perm.reshape(-1), device=Vs.device)
 
     def to_runner(x):
@@ -85,7 +91,7 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     def from_runner(x):
         return x[pt].reshape(Vs.shape).clone()
 
-    V0 = to_runner(Vs).cpu().numpy()
+    V0 = to_runner(Vs)
     if isinstance(neuron, HH):
         model = 'hh'
     elif isinstance(neuron, LIFRef):

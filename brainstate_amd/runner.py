@@ -14,6 +14,22 @@ from . import _native as N
 from . import ops
 
 
+def _ndim(x):
+    return x.dim() if torch.is_tensor(x) else np.ndim(x)
+
+
+def _dev_array(x, dtype, shape, dev, like=None):
+    """``x`` as a contiguous ``dtype`` tensor on ``dev`` of ``shape`` (or broadcast to the
+    shape of ``like``); a tensor already in that form is returned as it is."""
+    if torch.is_tensor(x):
+        t = x.to(device=dev, dtype=dtype)
+    else:
+        np_dtype = np.int32 if dtype == torch.int32 else np.float32
+        t = torch.from_numpy(np.ascontiguousarray(np.asarray(x, np_dtype))).to(dev)
+    t = t.expand(like.shape) if like is not None else t.reshape(shape)
+    return t.contiguous()
+
+
 class EINetRunner:
     """E/I network: neurons [0, n_exc) project with (idx_e, w_e), [n_exc, n) with (idx_i, w_i).
 
@@ -35,34 +51,30 @@ class EINetRunner:
         self.n, self.n_exc = int(n), int(n_exc)
         self.device = torch.device(device)
         dev = self.device
-        idx_e = np.asarray(idx_e, np.int32).reshape(self.n_exc, -1)
-        idx_i = np.asarray(idx_i, np.int32).reshape(self.n - self.n_exc, -1)
-        for name, idx in (('idx_e', idx_e), ('idx_i', idx_i)):
-            if idx.size and (idx.min() < 0 or idx.max() >= self.n):
+        # connectivity: numpy arrays are uploaded; tensors already on the device are used as
+        # they are (a net built on the device is not copied through the host)
+        self.idx_e = _dev_array(idx_e, torch.int32, (self.n_exc, -1), dev)
+        self.idx_i = _dev_array(idx_i, torch.int32, (self.n - self.n_exc, -1), dev)
+        for name, idx in (('idx_e', self.idx_e), ('idx_i', self.idx_i)):
+            if idx.numel() and (int(idx.min()) < 0 or int(idx.max()) >= self.n):
                 raise ValueError(f'{name}: target index out of range [0, {self.n})')
-        self.k_e, self.k_i = idx_e.shape[1], idx_i.shape[1]
-        self.idx_e = torch.from_numpy(idx_e).to(dev)
-        self.idx_i = torch.from_numpy(idx_i).to(dev)
-        het = np.ndim(w_e) > 0 or np.ndim(w_i) > 0
+        self.k_e, self.k_i = self.idx_e.shape[1], self.idx_i.shape[1]
+        het = _ndim(w_e) > 0 or _ndim(w_i) > 0
         if het:
-            we, wi = (np.asarray(w, np.float32) for w in (w_e, w_i))
-            if we.shape != idx_e.shape or not we.flags.writeable:
-                we = np.array(np.broadcast_to(we, idx_e.shape))
-            if wi.shape != idx_i.shape or not wi.flags.writeable:
-                wi = np.array(np.broadcast_to(wi, idx_i.shape))
-            if not (np.isfinite(we).all() and np.isfinite(wi).all()):
+            self.w_e = _dev_array(w_e, torch.float32, None, dev, like=self.idx_e)
+            self.w_i = _dev_array(w_i, torch.float32, None, dev, like=self.idx_i)
+            if not bool(torch.isfinite(self.w_e).all() & torch.isfinite(self.w_i).all()):
                 raise ValueError('per-synapse weights must be finite')
-            self.w_e = torch.from_numpy(np.ascontiguousarray(we)).to(dev)
-            self.w_i = torch.from_numpy(np.ascontiguousarray(wi)).to(dev)
             self.w_e_homo = self.w_i_homo = 0.0
         else:
             self.w_e = self.w_i = None
-            self.w_e_homo, self.w_i_homo = float(np.float32(w_e)), float(np.float32(w_i))
+            self.w_e_homo, self.w_i_homo = (float(np.float32(float(w))) for w in (w_e, w_i))
         self.params = params
         f32 = dict(dtype=torch.float32, device=dev)
         self.spk = torch.zeros(self.n, dtype=torch.uint8, device=dev)
         self.t = 0   # absolute index of the next step
-        V0 = torch.as_tensor(np.asarray(V0, np.float32)).to(dev)
+        V0 = (V0.to(device=dev, dtype=torch.float32).reshape(-1) if torch.is_tensor(V0) else
+              torch.as_tensor(np.asarray(V0, np.float32)).to(dev))
         if model == 'lif':
             self.state = dict(V=V0.clone(), ge=torch.zeros(self.n, **f32),
                               gi=torch.zeros(self.n, **f32),

@@ -102,15 +102,25 @@ def _fused_loop(f, xs, length):
     r = fuse(neuron, proj_e, proj_i, n_exc, inp)
     T = length - 2
     want = outs[0] is not None
-    raster = torch.zeros(T, r.n, dtype=torch.uint8, device=r.device) if want else None
+    # the runner writes every neuron of every step into the raster
+    raster = torch.empty(T, r.n, dtype=torch.uint8, device=r.device) if want else None
     r.run(T, raster=raster)
     r.check()
     r.write_back()
     if not want:
         return outs, [None] * length
-    perm = torch.as_tensor(np.asarray(r.replica_index).reshape(-1), device=raster.device)
-    rest = raster[:, perm].reshape((T,) + tuple(outs[0].shape)).to(outs[0].dtype)
-    return outs, torch.cat([torch.stack(outs), rest])
+    # the stacked result assembled in place: the eager steps' outputs, then the raster in
+    # their order and dtype (one conversion, no intermediate copy of the [length, ...] result)
+    res = torch.empty((length,) + tuple(outs[0].shape), dtype=outs[0].dtype,
+                      device=outs[0].device)
+    res[0].copy_(outs[0])
+    res[1].copy_(outs[1])
+    perm = np.asarray(r.replica_index).reshape(-1)
+    if np.array_equal(perm, np.arange(perm.size)):
+        res[2:].view(T, -1).copy_(raster)
+    else:
+        res[2:].view(T, -1).copy_(raster[:, torch.as_tensor(perm, device=raster.device)])
+    return outs, res
 
 
 def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
