@@ -914,7 +914,14 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
   const int32_t R = single_launch ? 1 : Rmax;  // one group per bucket: no partials, no reduce
   // single launch: each bucket's posts split over nsub workgroups (every one scans the spikes
   // and the bucket's synapses, and adds and writes only its slice)
-  const int32_t nsub = single_launch ? (kSubSingle < P ? kSubSingle : P) : 1;
+  // every workgroup of the single launch scans the whole spike vector: at most kSubSingle
+  // per bucket, and about kTargetWgs in all when there are many buckets
+  int32_t nsub = 1;
+  if (single_launch) {
+    nsub = kTargetWgs / nb < kSubSingle ? kTargetWgs / nb : kSubSingle;
+    if (nsub > P) nsub = P;
+    if (nsub < 1) nsub = 1;
+  }
   const size_t need = (size_t)kHdr + (single_launch ? 0 : (size_t)R * n_post * sizeof(uint64_t));
   BS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                "bs_event_bucket_f32: workspace of %zu bytes needed (got %zu)", need,

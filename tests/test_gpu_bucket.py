@@ -247,7 +247,8 @@ def _expected_row_groups(s, n_pre, nb):
     (20_000, 100_000, 200, 0.1, False, False, 'u8'),
     (100_000, 50_000, 20, 0.5, True, False, 'u8'),       # R_eff = R (capped)
     (60_000, 30_000, 20, 0.5, True, False, 'f32'),       # R_eff = R, f32 spikes
-    (60_000, 30_000, 20, 0.002, False, True, 'f32')])    # R_eff = 1, f32 spikes
+    (60_000, 30_000, 20, 0.002, False, True, 'f32'),     # R_eff = 1, f32 spikes
+    (3_000, 500_000, 50, 0.01, True, False, 'u8')])      # 41 buckets: 6 sub-ranges each
 def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, accumulate,
                                           sdt):
     """The step picks its number of row groups from the spikes on the device; whatever it
