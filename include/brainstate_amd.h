@@ -151,8 +151,8 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
  * The step is one kernel over nb x R row groups plus a reduce of the partials.  mode:
  *   0  R follows the spikes on the device (about 256 active rows per group, estimated from
  *      the leading 16,384 rows; at R = 1 the reduce has nothing to do);
- *   1  one launch of nb x 8 workgroups that write out themselves (R = 1 whatever the
- *      density: right for sparse spikes, slow for dense ones);
+ *   1  one launch of nb x min(8, 256 / nb) workgroups that write out themselves, no estimate
+ *      (R = 1 whatever the density: right for sparse spikes, slow for dense ones);
  *   2  R = its maximum (row_groups), fixed on the host: no estimate on the critical path
  *      (right for dense spikes).
  * The sums are the same bits in every mode.  est_out (NULL, or an int32 the device can write,
