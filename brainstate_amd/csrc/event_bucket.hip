@@ -53,6 +53,9 @@ constexpr int kMaxNb = 1024;      // buckets
 // pass 53 us; a 512-workgroup target 40 us.  fp32 LDS atomics instead of 64-bit integers:
 // 76 us.
 constexpr int kRowsPer = 4;       // active rows a wave works on at once
+// the same in the single launch: measured at config [2] p = 0.001 (~100 active rows) with
+// 1 .. 8 rows per wave: 10.9, 10.2, 9.96, 10.9, 10.4, 10.6, 10.8, 11.0 us per step
+constexpr int kRowsSingle = 3;
 constexpr int kPasses = 2;        // 64-synapse passes per row issued together
 constexpr int kSpan = 4096;       // active rows held in LDS before their synapses are added
 constexpr int kTargetWgs = 256;   // step grid the row groups aim for
@@ -454,24 +457,25 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
       }
       __syncthreads();
     }
-    // 3. synapses of kRowsPer rows, up to kPasses x 64 each, loads in flight together
-    for (int32_t a0 = wid * kRowsPer; a0 < count; a0 += (kSB / BS_WAVE) * kRowsPer) {
-      int32_t beg[kRowsPer], len[kRowsPer];
+    // 3. synapses of kRP rows, up to kPasses x 64 each, loads in flight together
+    constexpr int kRP = kSingle ? kRowsSingle : kRowsPer;
+    for (int32_t a0 = wid * kRP; a0 < count; a0 += (kSB / BS_WAVE) * kRP) {
+      int32_t beg[kRP], len[kRP];
       int32_t maxlen = 0;
 #pragma unroll
-      for (int q = 0; q < kRowsPer; ++q) {
+      for (int q = 0; q < kRP; ++q) {
         const bool ok = a0 + q < count;
         beg[q] = ok ? s_beg[a0 + q] : 0;
         len[q] = ok ? s_len[a0 + q] : 0;
         maxlen = len[q] > maxlen ? len[q] : maxlen;
       }
       for (int32_t e0 = 0; e0 < maxlen; e0 += kPasses * BS_WAVE) {
-        uint16_t t[kPasses][kRowsPer];
-        float v[kPasses][kRowsPer];
+        uint16_t t[kPasses][kRP];
+        float v[kPasses][kRP];
 #pragma unroll
         for (int u = 0; u < kPasses; ++u) {
 #pragma unroll
-          for (int q = 0; q < kRowsPer; ++q) {
+          for (int q = 0; q < kRP; ++q) {
             const int32_t e = e0 + u * BS_WAVE + lane;
             t[u][q] = 0xFFFFu;
             v[u][q] = 0.0f;
@@ -484,7 +488,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
 #pragma unroll
         for (int u = 0; u < kPasses; ++u) {
 #pragma unroll
-          for (int q = 0; q < kRowsPer; ++q) {
+          for (int q = 0; q < kRP; ++q) {
             // offset inside this workgroup's posts; the 0xFFFF of an idle lane is never < pn
             const uint32_t tl = (uint32_t)t[u][q] - (uint32_t)lo_t;
             if (tl < (uint32_t)pn) {
