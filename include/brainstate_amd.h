@@ -138,8 +138,9 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
  *        [indptr[i], indptr[i+1]) (fixed-num: [i*k, i*k+k)), sorted by bucket with the
  *        original order kept inside a bucket; bucket b's synapses of row i are
  *        [seg[i][b], seg[i][b+1]) with lidx = target - b*P; valid synapses end at seg[i][nb]
- *        (out-of-range targets follow and are never read).  S = *qexp = 60 - e_w - e_n with
- *        max|w| < 2^e_w and nnz <= 2^e_n (-1000 if a weight is not finite).
+ *        (out-of-range targets follow and are never read).  S = *qexp = 30 - e_w with
+ *        max|w| < 2^e_w, so every rounded weight is an integer below 2^30 in magnitude (-1000
+ *        if a weight is not finite).
  * bs_event_bucket_f32: out[j] = (accumulate ? out[j] : 0) + v_j, where v_j is
  *   - per-synapse weights, finite: each weight of an event onto j rounded to a multiple of
  *     2^-S (round to nearest even), the rounded weights summed exactly (64-bit integers),

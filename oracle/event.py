@@ -147,8 +147,9 @@ def event_linear(spk, W, float_as_event=True, n_out=None, chunk_rows=None):
 # ---- destination-bucketed operator: exact fixed-point sums ----
 
 def bucket_qexp(w, nnz):
-    """Fixed-point exponent S of the bucketed layout: 60 - e_w - e_n with max|w| < 2^e_w and
-    nnz <= 2^e_n; -1000 if a weight is not finite, 0 if every weight is 0."""
+    """Fixed-point exponent S of the bucketed layout: 30 - e_w with max|w| < 2^e_w (every
+    rounded weight an integer below 2^30 in magnitude; ``nnz`` does not enter); -1000 if a
+    weight is not finite, 0 if every weight is 0 (csrc/event_bucket.hip, k_bucket_qexp)."""
     w = np.abs(np.asarray(w, dtype=F).reshape(-1))
     if w.size and not np.all(np.isfinite(w)):
         return -1000
@@ -156,10 +157,7 @@ def bucket_qexp(w, nnz):
     if wmax == 0.0:
         return 0
     e_w = int(np.frexp(np.float64(wmax))[1])          # wmax = m * 2^e_w, 0.5 <= m < 1
-    e_n = 0
-    while (1 << e_n) < nnz:
-        e_n += 1
-    return 60 - e_w - e_n
+    return 30 - e_w
 
 
 def scatter_fixed_point(spk, indptr, indices, w, n_post, S):

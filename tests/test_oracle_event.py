@@ -187,19 +187,28 @@ def test_event_linear_chunked_order(L):
 # ---- bucketed operator: fixed-point exponent and exact sums ----
 
 def test_bucket_qexp_bounds_every_sum():
-    """S keeps nnz * max|w| below 2^60 units and is as large as that allows (one more bit
-    would break the bound for some nnz / max|w|)."""
+    """S keeps every rounded weight below 2^30 in magnitude and is as large as that allows
+    (one more bit would break it for the largest weight), so the weight rounds exactly in fp32
+    and 2^33 events onto one output cannot overflow an int64 sum; rint(w * 2^S) computed in
+    float64 equals its fp32 form (ldexp, rint, convert) for every weight, tiny ones included."""
     rng = np.random.RandomState(3)
     for _ in range(200):
         nnz = int(rng.randint(1, 10**8))
         wmax = F(rng.lognormal(0, 8))
         S = event.bucket_qexp(np.array([wmax, -wmax / 2], F), nnz)
-        assert nnz * float(wmax) * 2.0 ** S < 2.0 ** 60
-        assert nnz * float(wmax) * 2.0 ** (S + 2) >= 2.0 ** 60 or nnz == 1
+        assert float(wmax) * 2.0 ** S < 2.0 ** 30
+        assert float(wmax) * 2.0 ** (S + 1) >= 2.0 ** 30
+        assert 2.0 ** 33 * 2.0 ** 30 <= 2.0 ** 63
+        w = np.concatenate([np.array([wmax, -wmax], F),
+                            (rng.uniform(-1, 1, 1000) * wmax).astype(F),
+                            (rng.uniform(-1, 1, 100) * wmax * F(1e-30)).astype(F)])
+        exact = np.rint(w.astype(np.float64) * 2.0 ** S)
+        f32 = np.rint(np.ldexp(w, S).astype(F)).astype(np.float64)
+        assert np.array_equal(exact, f32) and np.abs(exact).max() <= 2.0 ** 30
     assert event.bucket_qexp(np.zeros(5, F), 5) == 0
     assert event.bucket_qexp(np.array([1.0, np.inf], F), 2) == -1000
     assert event.bucket_qexp(np.array([np.nan], F), 1) == -1000
-    assert event.bucket_qexp(np.array([0.75], F), 1) == 60       # 0.75 < 2^0, nnz = 2^0
+    assert event.bucket_qexp(np.array([0.75], F), 1) == 30       # 0.75 < 2^0
 
 
 def test_fixed_point_scatter_is_the_rounded_exact_sum():
