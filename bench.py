@@ -252,7 +252,10 @@ def bench_sparse(args):
         lines.append({'workload': f'event_matvec_100k_K1000_p{p}', 'events': E,
                       'bucket_us': tb * 1e6, 'bucket_GSOPs': E / tb / 1e9,
                       'bucket_graph_us': tbg * 1e6 if tbg is not None else None,
-                      'bucket_mode': 'single launch' if hint == 1 else f'split, {hint} row groups',
+                      'bucket_mode': {'single': 'single launch',
+                                      'dense': f'fixed grid, {bkt["_call"][3]} row groups',
+                                      'split': f'split, about {hint} row groups'}[
+                                          ops.bucket_auto_mode(bkt)],
                       'bucket_alg_GBs': b_s / tb / 1e9, 'bucket_frac': b_s / tb / PEAK_HBM,
                       'fused_matvec_us': tf * 1e6, 'fused_GSOPs': E / tf / 1e9,
                       'scatter_us': ts * 1e6, 'scatter_GSOPs': E / ts / 1e9,

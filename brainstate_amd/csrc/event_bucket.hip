@@ -55,6 +55,10 @@ constexpr int kMaxNb = 1024;      // buckets
 // pass 53 us; a 512-workgroup target 40 us.  fp32 LDS atomics instead of 64-bit integers:
 // 76 us.
 constexpr int kRowsPer = 4;       // active rows a wave works on at once
+// the same in the fixed-grid dense kernel: measured at config [2] p = 0.1 / 0.3 with 2, 4, 6, 8
+// rows per wave: 28.4-28.6 / 55.5-56.2, 28.6-28.8 / 53.2-53.5, 29.2-29.4 / 54.3-54.5,
+// 29.6-29.8 / 54.9-55.1 us per step
+constexpr int kRowsDense = 4;
 // the same in the single launch: measured at config [2] p = 0.001 (~100 active rows) with
 // 1 .. 8 rows per wave: 10.9, 10.2, 9.96, 10.9, 10.4, 10.6, 10.8, 11.0 us per step
 constexpr int kRowsSingle = 3;
@@ -64,7 +68,10 @@ constexpr int kTargetWgs = 256;   // step grid the row groups aim for
 constexpr int kMinRows = 64;      // rows per row group, at least (and the group alignment)
 constexpr int kMinNb = 8;         // buckets, at least (the grid is nb x row groups)
 constexpr int kSample = 16384;    // leading spike rows whose active count sets R_eff
-constexpr int kActivePer = 256;   // active rows per row group the step aims for
+// active rows per row group the step aims for: measured at config [2] (mode 0, HIP graph)
+// p = 0.003 / 0.01 with 256: 16.5 / 19.05 us, 128: 15.4 / 19.07 us (one box); on another,
+// 256: 16.7 / 18.8 us, 64: 14.9 / 20.5 us
+constexpr int kActivePer = 128;
 constexpr int kDepth = 8;         // 16-byte spike loads per thread in flight together
 constexpr int kHdr = 256;         // workspace bytes ahead of the partials (word 0: R_eff)
 // single launch: workgroups per bucket.  Measured at config [2] p = 0.001 (one launch of
@@ -690,9 +697,9 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
 
 // Dense spikes (mode 2: the previous call estimated the maximum R): every workgroup owns a
 // fixed row group of `rows` rows, known on the host, so nothing waits for an estimate.  Per
-// span of kSB-row compaction steps: one byte per thread, ballots and a workgroup prefix, the
-// active rows in ascending order; then the bucket bounds of those rows, then phase 3 as in the
-// adaptive kernel.  This compact form is what dense steps are fastest with (config [2] at
+// span of kSpan rows: kU spike bytes per thread and the bucket bounds of the active ones,
+// loaded together, then ballots and one workgroup prefix that lists the active rows' bounds
+// in ascending row order; then phase 3 as in the adaptive kernel.  This compact form is what dense steps are fastest with (config [2] at
 // p = 0.1: 31.6 us against 33.6 us for the adaptive kernel run at R = max).  Workgroup 0
 // writes R to the header and the next call's estimate from its own group's active rows.
 template <typename T, bool kHet>
@@ -703,9 +710,10 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
     int32_t* __restrict__ hdr, int32_t* __restrict__ est_out, uint64_t* __restrict__ part) {
   __shared__ uint64_t s_acc[kMaxP];        // fixed-point sums, fp32 sums or event counts
   uint32_t* s_acc32 = (uint32_t*)s_acc;
+  constexpr int kU = kSpan / kSB;          // span rows per thread
   __shared__ int32_t s_beg[kSpan];
   __shared__ int32_t s_len[kSpan];
-  __shared__ int32_t s_wave[kSB / BS_WAVE];
+  __shared__ int32_t s_wave[kU][kSB / BS_WAVE];
   const int lane = bs_lane();
   const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / BS_WAVE));
   const int32_t b = blockIdx.x % nb;
@@ -722,51 +730,68 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
   if (blockIdx.x == 0 && threadIdx.x == 0) *hdr = R;
   int32_t group_active = 0;  // active rows of the group (for workgroup 0's estimate)
   for (int64_t c0 = r0; c0 < r1; c0 += kSpan) {
-    // 1. active rows of the span, ascending
+    // 1+2. active rows of the span, ascending, with the bounds of bucket b in each: every
+    // thread loads its kU spike bytes together and, for the active ones, the bounds, before
+    // the one prefix that places them (one memory round trip and one barrier ahead of the
+    // synapses, where a round per kSB rows took kU of each)
+    int32_t lo[kU], hi[kU];
+    uint64_t m[kU];
+    {
+      T sv[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t row = c0 + u * kSB + threadIdx.x;
+        sv[u] = row < r1 ? spk[row] : T(0);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        lo[u] = hi[u] = 0;
+        if (sv[u] != T(0)) {
+          const int32_t* sr = seg + (c0 + u * kSB + threadIdx.x) * stride + b;
+          lo[u] = sr[0];
+          hi[u] = sr[1];
+        }
+        m[u] = bs_ballot(sv[u] != T(0));
+        if (lane == 0) s_wave[u][wid] = __popcll(m[u]);
+      }
+    }
+    __syncthreads();
     int32_t count = 0;
-    for (int32_t o = 0; o < kSpan; o += kSB) {
-      const int64_t row = c0 + o + threadIdx.x;
-      const bool a = row < r1 && spk[row] != T(0);
-      const uint64_t m = bs_ballot(a);
-      if (lane == 0) s_wave[wid] = __popcll(m);
-      __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
       int32_t pos = count, tot = 0;
 #pragma unroll
       for (int v = 0; v < kSB / BS_WAVE; ++v) {
-        pos += v < wid ? s_wave[v] : 0;
-        tot += s_wave[v];
+        pos += v < wid ? s_wave[u][v] : 0;
+        tot += s_wave[u][v];
       }
-      if (a) s_beg[pos + bs_rank_below(m)] = (int32_t)row;
+      if ((m[u] >> lane) & 1ull) {
+        pos += bs_rank_below(m[u]);
+        s_beg[pos] = lo[u];
+        s_len[pos] = hi[u] - lo[u];
+      }
       count += tot;
-      __syncthreads();  // s_wave is rewritten next round
     }
     group_active += count;
-    // 2. bounds of bucket b in each active row
-    for (int32_t x = threadIdx.x; x < count; x += kSB) {
-      const int32_t* sr = seg + (int64_t)s_beg[x] * stride + b;
-      const int32_t lo = sr[0], hi = sr[1];
-      s_beg[x] = lo;
-      s_len[x] = hi - lo;
-    }
     __syncthreads();
-    // 3. synapses of kRowsPer rows, up to kPasses x 64 each, loads in flight together
-    for (int32_t a0 = wid * kRowsPer; a0 < count; a0 += (kSB / BS_WAVE) * kRowsPer) {
-      int32_t beg[kRowsPer], len[kRowsPer];
+    // 3. synapses of kRowsDense rows, up to kPasses x 64 each, loads in flight together
+    for (int32_t a0 = wid * kRowsDense; a0 < count; a0 += (kSB / BS_WAVE) * kRowsDense) {
+      int32_t beg[kRowsDense], len[kRowsDense];
       int32_t maxlen = 0;
 #pragma unroll
-      for (int q = 0; q < kRowsPer; ++q) {
+      for (int q = 0; q < kRowsDense; ++q) {
         const bool ok = a0 + q < count;
         beg[q] = ok ? s_beg[a0 + q] : 0;
         len[q] = ok ? s_len[a0 + q] : 0;
         maxlen = len[q] > maxlen ? len[q] : maxlen;
       }
       for (int32_t e0 = 0; e0 < maxlen; e0 += kPasses * BS_WAVE) {
-        uint16_t t[kPasses][kRowsPer];
-        float v[kPasses][kRowsPer];
+        uint16_t t[kPasses][kRowsDense];
+        float v[kPasses][kRowsDense];
 #pragma unroll
         for (int u = 0; u < kPasses; ++u) {
 #pragma unroll
-          for (int q = 0; q < kRowsPer; ++q) {
+          for (int q = 0; q < kRowsDense; ++q) {
             const int32_t e = e0 + u * BS_WAVE + lane;
             t[u][q] = 0xFFFFu;
             v[u][q] = 0.0f;
@@ -779,7 +804,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
 #pragma unroll
         for (int u = 0; u < kPasses; ++u) {
 #pragma unroll
-          for (int q = 0; q < kRowsPer; ++q) {
+          for (int q = 0; q < kRowsDense; ++q) {
             if (t[u][q] != 0xFFFFu) {
               if (!kHet) {
                 atomicAdd(&s_acc32[t[u][q]], 1u);

@@ -150,7 +150,7 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
  *     starting from out[j] (or 0): bit-identical to a sequential scatter;
  *   - a non-finite per-synapse weight: fp32 sums in an unspecified order.
  * The step is one kernel over nb x R row groups plus a reduce of the partials.  mode:
- *   0  R follows the spikes on the device (about 256 active rows per group, estimated from
+ *   0  R follows the spikes on the device (about 128 active rows per group, estimated from
  *      the leading 16,384 rows; at R = 1 the reduce has nothing to do);
  *   1  one launch of nb x min(8, 256 / nb) workgroups that write out themselves, no estimate
  *      (R = 1 whatever the density: right for sparse spikes, slow for dense ones);
@@ -158,7 +158,7 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
  *      (right for dense spikes).
  * The sums are the same bits in every mode.  est_out (NULL, or an int32 the device can write,
  * e.g. in pinned host memory) receives the call's estimate of R (mode 0: from the leading
- * rows; mode 1: ceil(active rows / 256) from the exact count; mode 2: from row group 0), so that a caller can pick the next call's mode from it without a
+ * rows; mode 1: ceil(active rows / 128) from the exact count; mode 2: from row group 0), so that a caller can pick the next call's mode from it without a
  * synchronisation (a stale estimate costs time, never correctness).
  * `workspace`: bs_event_bucket_workspace_size bytes (mode 1: 256 bytes are enough), 8-byte
  * aligned, no initialisation needed. */

@@ -233,17 +233,17 @@ def _bucket_ws_header(torch, dev_index=0):
 
 def _expected_row_groups(s, n_pre, nb):
     """The documented rule: R_eff = ceil(active rows of the leading min(n_pre, 16384) rows,
-    scaled to n_pre, / 256), within [1, R], R = min(256 // nb, ceil(n_pre / 64))."""
+    scaled to n_pre, / 128), within [1, R], R = min(256 // nb, ceil(n_pre / 64))."""
     ns = min(n_pre, 16384)
     act = int(np.count_nonzero(np.asarray(s)[:ns]))
-    re = -(-act * n_pre // (ns * 256))
+    re = -(-act * n_pre // (ns * 128))
     R = max(1, min(256 // nb, -(-n_pre // 64)))
     return max(1, min(R, re))
 
 
 @pytest.mark.parametrize('n_pre,n_post,k,p,het,accumulate,sdt', [
     (100_000, 100_000, 100, 0.001, True, False, 'u8'),   # R_eff = 1: the step writes out
-    (20_000, 100_000, 200, 0.1, True, True, 'u8'),       # R_eff = 8 of 28 partials
+    (20_000, 100_000, 200, 0.1, True, True, 'u8'),       # R_eff = 16 of 28 partials
     (20_000, 100_000, 200, 0.1, False, False, 'u8'),
     (100_000, 50_000, 20, 0.5, True, False, 'u8'),       # R_eff = R (capped)
     (60_000, 30_000, 20, 0.5, True, False, 'f32'),       # R_eff = R, f32 spikes
@@ -267,18 +267,21 @@ def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, 
     R_est = _expected_row_groups(s, n_pre, L['nb'])
     R_max = max(1, min(256 // L['nb'], -(-n_pre // 64)))
     gots = {}
-    # 'single' last before 'auto': its estimate (from the exact count) steers 'auto'
+    want_hint = max(1, min(R_max, -(-int(np.count_nonzero(s)) // 128)))
+    # 'single' last before 'auto': its estimate (from the exact count) steers 'auto': one
+    # launch at 1, the fixed grid above half the maximum, else groups chosen on the device
+    auto = 'single' if want_hint == 1 else ('dense' if 2 * want_hint > R_max > 1 else 'split')
     for mode in ('split', 'dense', 'single', 'auto'):
         out = dev(torch, base.copy())
         gots[mode] = ops.event_bucket(dev(torch, s), L, out=out, accumulate=accumulate,
                                       mode=mode).cpu().numpy()
+        ran = auto if mode == 'auto' else mode
         # row groups the step used (single: 1, dense: the maximum) and its estimate
-        used = {'single': 1, 'dense': R_max}.get(mode, R_est)
+        used = {'single': 1, 'dense': R_max}.get(ran, R_est)
         assert _bucket_ws_header(torch) == used, mode
-        if mode == 'dense':   # estimated from row group 0's rows
+        if ran == 'dense':   # estimated from row group 0's rows
             assert 1 <= int(L['_hint'][1][0]) <= R_max
-        elif mode == 'single':   # from the exact active count
-            want_hint = max(1, min(R_max, -(-int(np.count_nonzero(s)) // 256)))
+        elif ran == 'single':   # from the exact active count
             assert int(L['_hint'][1][0]) == want_hint, mode
         else:
             assert int(L['_hint'][1][0]) == R_est, mode
