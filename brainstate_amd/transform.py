@@ -28,6 +28,103 @@ fuse_loops = True   # False: for_loop always steps eagerly
 last_loop = None    # how the last for_loop ran: 'fused' (persistent runner) or 'eager'
 
 
+class ProgressBar:
+    """Progress of a ``for_loop`` (brainstate/transform/_progress_bar.py:265-453): the same
+    arguments and checks.  ``freq`` steps per update (default: every 5 % of the steps, or
+    every step up to 20), or ``count`` updates in all; ``desc`` a string or a
+    ``(format_string, fn)`` pair, ``fn`` mapping ``{'i': step}`` to the format's fields.
+    Drawn with tqdm when it is importable, else as a line on stderr per update.  A loop
+    that runs in the persistent runner advances the bar once for the steps of its launch."""
+
+    def __init__(self, freq=None, count=None, desc=None, **kwargs):
+        if isinstance(freq, int) and freq <= 0:
+            raise ValueError(f'Print rate (freq) should be > 0, but got {freq}.')
+        if freq is not None and count is not None:
+            raise ValueError('Cannot specify both count and freq.')
+        if desc is not None and not isinstance(desc, str):
+            if not isinstance(desc, (tuple, list)):
+                raise TypeError(f'desc must be a string or a (format_string, callable) '
+                                f'tuple/list, but got {type(desc).__name__}.')
+            if len(desc) != 2:
+                raise ValueError(f'desc tuple/list must have exactly two elements '
+                                 f'(format_string, callable), but got {len(desc)}.')
+            if not isinstance(desc[0], str):
+                raise TypeError(f'The first element of a desc tuple must be a format '
+                                f'string, but got {type(desc[0]).__name__}.')
+            if not callable(desc[1]):
+                raise TypeError(f'The second element of a desc tuple must be callable, '
+                                f'but got {type(desc[1]).__name__}.')
+        self.print_freq = freq
+        self.print_count = count
+        self.desc = desc
+        self.kwargs = {k: v for k, v in kwargs.items()
+                       if k not in ('total', 'mininterval', 'maxinterval', 'miniters')}
+
+    def init(self, n):
+        """The bar of an n-step loop: steps per update as the reference resolves them."""
+        freq, count = self.print_freq, self.print_count
+        if count is not None:
+            freq = n // count
+            if freq == 0:
+                raise ValueError(f'Count {count} is too large for n {n}.')
+        elif freq is None:
+            freq = int(n / 20) if n > 20 else 1
+        elif freq > n:
+            raise ValueError(f'Print rate should be less than the number of steps {n}, '
+                             f'got {freq}')
+        return _Bar(n, freq, self.desc, self.kwargs)
+
+
+class _Bar:
+    """One loop's bar: ``step(i)`` after step i, ``advance(k, i)`` after k steps ending at i,
+    ``close()`` at the end (which also draws the steps past the last whole ``freq``)."""
+
+    def __init__(self, n, freq, desc, kwargs):
+        self.n, self.freq, self.desc, self.done, self.shown = n, freq, desc, 0, 0
+        try:
+            from tqdm.auto import tqdm
+            self.bar = tqdm(total=n, **kwargs)
+        except ImportError:
+            self.bar = None
+        self._describe(0)
+
+    def _describe(self, i):
+        if self.desc is None:
+            msg = f'Running for {self.n:,} iterations'
+        elif isinstance(self.desc, str):
+            msg = self.desc
+        else:
+            msg = self.desc[0].format(**self.desc[1]({'i': i}))
+        if self.bar is not None:
+            self.bar.set_description(msg, refresh=False)
+        self.msg = msg
+
+    def _show(self, i):
+        k = self.done - self.shown
+        if k <= 0:
+            return
+        self._describe(i)
+        if self.bar is not None:
+            self.bar.update(k)
+        else:
+            import sys
+            print(f'{self.msg}: {self.done}/{self.n}', file=sys.stderr)
+        self.shown = self.done
+
+    def step(self, i):
+        self.advance(1, i)
+
+    def advance(self, k, i):
+        self.done += k
+        if self.done - self.shown >= self.freq:
+            self._show(i)
+
+    def close(self):
+        self._show(self.n - 1)
+        if self.bar is not None:
+            self.bar.close()
+
+
 def _ei_step(log, spk_before=None):
     """The E/I step the persistent runner runs, read off the module calls one step made:
     ``(neuron, proj_e, proj_i, n_exc, inp)`` when they were exactly the two projections onto
@@ -139,19 +236,36 @@ def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
         if not xs:
             raise ValueError('for_loop needs xs or length')
         length = len(xs[0])
+    if isinstance(pbar, int) and not isinstance(pbar, bool):
+        pbar = ProgressBar(freq=pbar)   # an int is the update frequency, as in the reference
+    bar = pbar.init(length) if pbar is not None else None
     last_loop = 'eager'
-    if fuse_loops and not reverse and length >= 3:
-        done, stacked = _fused_loop(f, xs, length)
-        if stacked is not None:
-            last_loop = 'fused'
-            return stacked if torch.is_tensor(stacked) else _stack(stacked)
-        outs = done + [f(*[x[i] for x in xs]) for i in range(len(done), length)]
+    try:
+        if fuse_loops and not reverse and length >= 3:
+            done, stacked = _fused_loop(f, xs, length)
+            if bar is not None:
+                bar.advance(len(done) if stacked is None else length, length - 1)
+            if stacked is not None:
+                last_loop = 'fused'
+                return stacked if torch.is_tensor(stacked) else _stack(stacked)
+            outs = done
+            for i in range(len(done), length):
+                outs.append(f(*[x[i] for x in xs]))
+                if bar is not None:
+                    bar.step(i)
+            return _stack(outs)
+        order = range(length - 1, -1, -1) if reverse else range(length)
+        outs = []
+        for i in order:
+            outs.append(f(*[x[i] for x in xs]))
+            if bar is not None:
+                bar.step(i)
+        if reverse:
+            outs = outs[::-1]
         return _stack(outs)
-    order = range(length - 1, -1, -1) if reverse else range(length)
-    outs = [f(*[x[i] for x in xs]) for i in order]
-    if reverse:
-        outs = outs[::-1]
-    return _stack(outs)
+    finally:
+        if bar is not None:
+            bar.close()
 
 
 def jit(fn=None, **kwargs):

@@ -89,6 +89,50 @@ def test_for_loop_stacks_like_scan():            # brainstate/transform/_loop_co
     assert bs.transform.jit(f) is f
 
 
+def test_progress_bar_arguments():               # brainstate/transform/_progress_bar_test.py:83-131
+    PB = bs.transform.ProgressBar
+    with pytest.raises(ValueError):
+        PB(freq=0)
+    with pytest.raises(ValueError):
+        PB(freq=2, count=5)
+    assert PB(desc='Running').desc == 'Running'
+    assert PB(desc=('step {i}', lambda d: {'i': d['i']})).desc[0] == 'step {i}'
+    with pytest.raises(TypeError):
+        PB(desc=('step {i}', 'not-callable'))
+    with pytest.raises(TypeError):
+        PB(desc=(123, lambda d: d))
+    with pytest.raises(TypeError):
+        PB(desc=123)
+    with pytest.raises(ValueError):
+        PB(desc=('only-one',))
+
+
+def test_progress_bar_in_for_loop(capsys):       # _progress_bar_test.py:134-200
+    PB, loop = bs.transform.ProgressBar, bs.transform.for_loop
+    # steps per update as the reference resolves them: count -> n // count, default 5 %
+    # (every step up to 20), explicit freq; updates stop at n, the close draws the rest
+    assert PB(count=2).init(4).freq == 2
+    assert PB().init(10).freq == 1 and PB().init(40).freq == 2
+    assert PB(freq=3).init(10).freq == 3
+    for n, pbar in ((4, PB(count=2)), (10, PB()), (40, PB()), (10, PB(freq=3)),
+                    (5, PB(freq=2, desc='run')),
+                    (5, PB(freq=2, desc=('iter {i}', lambda d: {'i': d['i']})))):
+        ys = loop(lambda x: x * 2, torch.arange(float(n)), pbar=pbar)
+        assert ys.tolist() == [2.0 * i for i in range(n)]
+    with pytest.raises(ValueError):
+        loop(lambda x: x * 2, torch.arange(4.0), pbar=PB(count=100))
+    with pytest.raises(ValueError):
+        loop(lambda x: x * 2, torch.arange(4.0), pbar=PB(freq=100))
+    # an int is ProgressBar(freq=int)
+    assert loop(lambda x: x + 1, torch.arange(6.0), pbar=2).tolist() == [1, 2, 3, 4, 5, 6]
+    bar = PB(freq=3).init(10)
+    for i in range(10):
+        bar.step(i)
+    assert bar.shown == 9
+    bar.close()
+    assert bar.shown == 10
+
+
 def test_checkpointed_scan_known_answer_sequence():
     # brainstate/transform/_loop_collect_return_test.py:66-79: ys = [0, 0, 2, 6, 12]
     c = bs.State(torch.zeros(()))

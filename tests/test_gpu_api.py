@@ -162,7 +162,9 @@ def _for_loop_paths(bs, make_step, T, dt=0.1):
         try:
             with bs.environ.context(dt=dt):
                 step, net = make_step()
-                res.append((bs.transform.for_loop(step, torch.arange(T) * dt), net))
+                # the fused pass with a progress bar, as examples/105_COBA_HH_2007_braincell.py:91
+                pbar = bs.transform.ProgressBar(10) if fused and T >= 10 else None
+                res.append((bs.transform.for_loop(step, torch.arange(T) * dt, pbar=pbar), net))
         finally:
             bs.transform.fuse_loops = True
         assert bs.transform.last_loop == ('fused' if fused else 'eager')
