@@ -35,7 +35,8 @@ class Net(ctypes.Structure):
     _fields_ = [('n', c_i32), ('n_exc', c_i32), ('k_e', c_i32), ('k_i', c_i32),
                 ('idx_e', c_vp), ('w_e', c_vp), ('w_e_homo', c_f32),
                 ('idx_i', c_vp), ('w_i', c_vp), ('w_i_homo', c_f32),
-                ('spk', c_vp), ('blocks_per_cu', c_i32), ('delay_steps', c_i32)]
+                ('spk', c_vp), ('blocks_per_cu', c_i32), ('delay_steps', c_i32),
+                ('I_ext', c_vp)]
 
 
 class LifState(ctypes.Structure):
@@ -107,7 +108,11 @@ SIGNATURES = {
                                                       c_vp]),
     'bs_coba_lif_step': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                         ctypes.POINTER(LifParams), c_vp, c_vp]),
+    'bs_coba_lif_step_in': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                           ctypes.POINTER(LifParams), c_vp, c_vp]),
     'bs_hh_init': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    'bs_coba_hh_step_in': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                          c_vp, ctypes.POINTER(HhParams), c_vp, c_vp]),
     'bs_coba_hh_step': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                        ctypes.POINTER(HhParams), c_vp, c_vp]),
     'bs_net_workspace_size': (c_size, [ctypes.POINTER(Net)]),

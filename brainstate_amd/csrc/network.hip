@@ -118,9 +118,17 @@ struct NetArgs {
   uint32_t* counts;  // per-workgroup spike counts [steps][nb] (workspace), or NULL
   uint32_t* hash;    // per-workgroup spike hashes [steps][nb] (workspace), or NULL
   uint8_t* raster;
+  const float* iext;  // per-neuron external input [n], or NULL (the parameters' I_ext)
   char* ws;
   NetLayout L;
 };
+
+// The parameters with a neuron's own external input.
+template <class P>
+__device__ __forceinline__ P with_input(P p, float x) {
+  p.I_ext = x;
+  return p;
+}
 
 // ---- neuron models: register-resident state, one fused update per neuron-step ----
 
@@ -252,7 +260,7 @@ __device__ __forceinline__ int32_t quantize(float w, float scale) {
   return (int32_t)bs_rint(w * scale);
 }
 
-template <class Model, int NPT, bool kHet>
+template <class Model, int NPT, bool kHet, bool kIn>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
                                                 typename Model::Params p_arg) {
   // The parameters live in VGPRs (uniform values, one register each) where the model allows:
@@ -334,10 +342,15 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   }
 
   typename Model::Regs r[NPT];
+  float iext[NPT];  // kIn: each neuron's external input, read once per launch
 #pragma unroll
   for (int q = 0; q < NPT; ++q) {
     const int64_t j = base + q * kBlock + threadIdx.x;
-    if (j < n) r[q] = Model::load(st, j);
+    iext[q] = 0.0f;
+    if (j < n) {
+      r[q] = Model::load(st, j);
+      if constexpr (kIn) iext[q] = a.iext[j];
+    }
   }
   bool last[NPT];
 #pragma unroll
@@ -372,7 +385,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // loads write to LDS (s_junk) rather than registers, so no register is held for them.
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
-      if (((valid >> q) & 1u) && Model::near(p, r[q])) {
+      if (((valid >> q) & 1u) && Model::near(kIn ? with_input(p, iext[q]) : p, r[q])) {
         int32_t jv = (int32_t)(jv0 + q * kBlock);
         asm volatile("" : "+v"(jv));  // keeps the row addresses from being hoisted out of the loop
         const Row rw = row_of(a, jv);
@@ -466,7 +479,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           in_e = repeated_sum(s_tab[0], a.w_e_homo, acc.x);
           in_i = repeated_sum(s_tab[1], a.w_i_homo, acc.y);
         }
-        last[q] = Model::update(p, r[q], in_e, in_i);
+        last[q] = Model::update(kIn ? with_input(p, iext[q]) : p, r[q], in_e, in_i);
         if (last[q]) h += bs_mix32(jv0 + q * kBlock);
         if (a.raster) a.raster[(int64_t)t * n + (jv0 + q * kBlock)] = last[q] ? 1 : 0;
       }
@@ -954,16 +967,17 @@ NetArgs make_args(const bs_net* net, const NetLayout& L, void* ws) {
   a.counts = nullptr;
   a.hash = nullptr;
   a.raster = nullptr;
+  a.iext = net->I_ext;
   a.ws = (char*)ws;
   a.L = L;
   return a;
 }
 
-template <class Model, int NPT, bool kHet>
+template <class Model, int NPT, bool kHet, bool kIn>
 int launch_one(const NetArgs& a, const typename Model::State& st, const typename Model::Params& p,
                hipStream_t s) {
   int occ = 0;
-  BS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_run<Model, NPT, kHet>,
+  BS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_run<Model, NPT, kHet, kIn>,
                                                             kBlock, 0));
   if ((int64_t)occ * bs_num_cus() < a.L.nb) {
     bs_set_error("runner: %d workgroups cannot be co-resident (occupancy %d x %d CUs)", a.L.nb,
@@ -974,19 +988,19 @@ int launch_one(const NetArgs& a, const typename Model::State& st, const typename
   typename Model::State ss = st;
   typename Model::Params pp = p;
   void* args[] = {(void*)&aa, (void*)&ss, (void*)&pp};
-  BS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)k_run<Model, NPT, kHet>, dim3(a.L.nb),
+  BS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)k_run<Model, NPT, kHet, kIn>, dim3(a.L.nb),
                                           dim3(kBlock), args, 0, s));
   return BS_OK;
 }
 
-template <class Model, bool kHet>
+template <class Model, bool kHet, bool kIn>
 int dispatch_npt(const NetArgs& a, const typename Model::State& st,
                  const typename Model::Params& p, hipStream_t s) {
   switch (a.L.npt) {
-    case 1: return launch_one<Model, 1, kHet>(a, st, p, s);
-    case 2: return launch_one<Model, 2, kHet>(a, st, p, s);
-    case 4: return launch_one<Model, 4, kHet>(a, st, p, s);
-    case 8: return launch_one<Model, 8, kHet>(a, st, p, s);
+    case 1: return launch_one<Model, 1, kHet, kIn>(a, st, p, s);
+    case 2: return launch_one<Model, 2, kHet, kIn>(a, st, p, s);
+    case 4: return launch_one<Model, 4, kHet, kIn>(a, st, p, s);
+    case 8: return launch_one<Model, 8, kHet, kIn>(a, st, p, s);
   }
   bs_set_error("runner: unsupported neurons-per-thread %d", a.L.npt);
   return BS_ERR_UNSUPPORTED;
@@ -1024,8 +1038,12 @@ int run(const bs_net* net, const typename Model::State* st, const typename Model
     a.counts = counts_out ? part : nullptr;
     a.hash = hash_out ? part + (size_t)kRunSteps * L.nb : nullptr;
     a.raster = raster_out ? raster_out + (int64_t)done * net->n : nullptr;
-    rc = net->w_e != nullptr ? dispatch_npt<Model, true>(a, *st, *p, s)
-                             : dispatch_npt<Model, false>(a, *st, *p, s);
+    if (net->I_ext)
+      rc = net->w_e != nullptr ? dispatch_npt<Model, true, true>(a, *st, *p, s)
+                               : dispatch_npt<Model, false, true>(a, *st, *p, s);
+    else
+      rc = net->w_e != nullptr ? dispatch_npt<Model, true, false>(a, *st, *p, s)
+                               : dispatch_npt<Model, false, false>(a, *st, *p, s);
     if (rc) return rc;
     if (counts_out || hash_out) {
       k_sum_parts<<<(len + 3) / 4, 256, 0, s>>>(L.nb, len, a.counts, a.hash,

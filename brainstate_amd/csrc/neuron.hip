@@ -16,14 +16,17 @@ __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restric
                                                      int32_t* __restrict__ ref,
                                                      const float* __restrict__ in_e,
                                                      const float* __restrict__ in_i,
+                                                     const float* __restrict__ iext,
                                                      bs_lif_params p,
                                                      uint8_t* __restrict__ spk) {
   for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
        j += (int64_t)gridDim.x * kBlock) {
     float v = V[j], e = ge[j], i = gi[j];
     int32_t r = ref[j];
+    bs_lif_params q = p;
+    if (iext) q.I_ext = iext[j];  // per-neuron external input
     const bool s =
-        bs_lif_update<kCuba, kSoft>(p, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
+        bs_lif_update<kCuba, kSoft>(q, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
     V[j] = v;
     ge[j] = e;
     gi[j] = i;
@@ -51,11 +54,14 @@ __global__ __launch_bounds__(kBlock) void k_hh_step(int32_t n, float* __restrict
                                                     float* __restrict__ gi,
                                                     const float* __restrict__ in_e,
                                                     const float* __restrict__ in_i,
+                                                    const float* __restrict__ iext,
                                                     bs_hh_params p, uint8_t* __restrict__ spk) {
   for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
        j += (int64_t)gridDim.x * kBlock) {
     float v = V[j], mm = m[j], hh = h[j], nn = ng[j], e = ge[j], i = gi[j];
-    const bool s = bs_hh_update(p, v, mm, hh, nn, e, i, in_e ? in_e[j] : 0.0f,
+    bs_hh_params q = p;
+    if (iext) q.I_ext = iext[j];  // per-neuron external input
+    const bool s = bs_hh_update(q, v, mm, hh, nn, e, i, in_e ? in_e[j] : 0.0f,
                                 in_i ? in_i[j] : 0.0f);
     V[j] = v;
     m[j] = mm;
@@ -107,9 +113,10 @@ int grid(int32_t n) {
 
 }  // namespace
 
-extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
-                                const float* in_e, const float* in_i, const bs_lif_params* p,
-                                uint8_t* spk_out, bs_stream_t stream) {
+extern "C" int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                                   const float* in_e, const float* in_i, const float* I_ext,
+                                   const bs_lif_params* p, uint8_t* spk_out,
+                                   bs_stream_t stream) {
   bs_clear_error();
   BS_CHECK_ARG(n >= 0, "bs_coba_lif_step: n=%d < 0", n);
   BS_CHECK_ARG(p != nullptr, "bs_coba_lif_step: params are NULL");
@@ -118,12 +125,18 @@ extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32
   BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
   hipStream_t s = bs_stream(stream);
 #define BS_LIF(C, S) \
-  k_lif_step<C, S><<<grid(n), kBlock, 0, s>>>(n, V, ge, gi, ref, in_e, in_i, *p, spk_out)
+  k_lif_step<C, S><<<grid(n), kBlock, 0, s>>>(n, V, ge, gi, ref, in_e, in_i, I_ext, *p, spk_out)
   if (p->cuba) { if (p->soft_reset) BS_LIF(true, true); else BS_LIF(true, false); }
   else { if (p->soft_reset) BS_LIF(false, true); else BS_LIF(false, false); }
 #undef BS_LIF
   BS_CHECK_LAUNCH();
   return BS_OK;
+}
+
+extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                                const float* in_e, const float* in_i, const bs_lif_params* p,
+                                uint8_t* spk_out, bs_stream_t stream) {
+  return bs_coba_lif_step_in(n, V, ge, gi, ref, in_e, in_i, nullptr, p, spk_out, stream);
 }
 
 extern "C" int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng,
@@ -137,19 +150,26 @@ extern "C" int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* 
   return BS_OK;
 }
 
-extern "C" int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
-                               float* gi, const float* in_e, const float* in_i,
-                               const bs_hh_params* p, uint8_t* spk_out, bs_stream_t stream) {
+extern "C" int bs_coba_hh_step_in(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
+                                  float* gi, const float* in_e, const float* in_i,
+                                  const float* I_ext, const bs_hh_params* p, uint8_t* spk_out,
+                                  bs_stream_t stream) {
   bs_clear_error();
   BS_CHECK_ARG(n >= 0, "bs_coba_hh_step: n=%d < 0", n);
   BS_CHECK_ARG(p != nullptr, "bs_coba_hh_step: params are NULL");
   BS_CHECK_ARG(p->inv_C == p->inv_C, "bs_coba_hh_step: inv_C is NaN");
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && m && h && ng && ge && gi, "bs_coba_hh_step: NULL state pointer");
-  k_hh_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng, ge, gi, in_e, in_i, *p,
-                                                        spk_out);
+  k_hh_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng, ge, gi, in_e, in_i,
+                                                        I_ext, *p, spk_out);
   BS_CHECK_LAUNCH();
   return BS_OK;
+}
+
+extern "C" int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
+                               float* gi, const float* in_e, const float* in_i,
+                               const bs_hh_params* p, uint8_t* spk_out, bs_stream_t stream) {
+  return bs_coba_hh_step_in(n, V, m, h, ng, ge, gi, in_e, in_i, nullptr, p, spk_out, stream);
 }
 
 extern "C" int bs_exp_euler_f32(int64_t n, const float* x, const float* drift, const float* jac,

@@ -3,7 +3,8 @@
 ``fuse(neuron, proj_e, proj_i, n_exc, inp)`` takes the pieces of the reference's E/I net
 (examples/105_COBA_HH_2007_braincell.py:54-82: ``N``, ``E`` fed by ``spk[:n_exc]``, ``I`` fed
 by ``spk[n_exc:]``) and returns an ``EINetRunner`` that advances the same network many steps
-per launch, with the constant external input ``inp`` the script passes as ``N(inp)``.
+per launch, with the constant external input ``inp`` the script passes as ``N(inp)`` (a
+scalar, or an array broadcast to the population's state shape: one input per neuron).
 Spikes of the last step that the neurons hold (a loop stepped eagerly so far) become the
 runner's first inputs (synaptic delay 0).  ``delay`` (ms) is the synaptic delay of a net whose
 projections read
@@ -99,8 +100,14 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     else:
         raise NotImplementedError(type(neuron).__name__)
     delay_steps = _get_delay(delay, environ.get_dt())[1]
-    r = EINetRunner(model, B * n, B * n_exc, idx_e, idx_i, w_e, w_i, neuron.params(float(inp)),
-                    V0, delay_steps=delay_steps)
+    if (torch.is_tensor(inp) or isinstance(inp, np.ndarray)) and np.prod(tuple(inp.shape)) != 1:
+        I0, I_arr = 0.0, to_runner(torch.broadcast_to(
+            torch.as_tensor(inp, dtype=torch.float32, device=Vs.device), Vs.shape))
+    else:
+        I0 = float(inp.reshape(()).item() if torch.is_tensor(inp) else np.reshape(inp, ()))
+        I_arr = None
+    r = EINetRunner(model, B * n, B * n_exc, idx_e, idx_i, w_e, w_i, neuron.params(I0),
+                    V0, delay_steps=delay_steps, I_ext=I_arr)
     # carry the current state over (the runner initialised HH gates at steady state)
     r.state['ge'].copy_(to_runner(proj_e.syn.g.value))
     r.state['gi'].copy_(to_runner(proj_i.syn.g.value))

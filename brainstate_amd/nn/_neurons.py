@@ -171,13 +171,20 @@ def _initial_V(V_initializer, n, batch_size, shape):
     return torch.as_tensor(np.ascontiguousarray(V, np.float32).reshape(shape), device=_dev())
 
 
-def _ext_input(x):
+def _ext_input(x, V):
+    """(scalar input, per-neuron input or None): a one-element input is a scalar; an array
+    must broadcast to the population's state shape (V's) and becomes each neuron's input."""
     if torch.is_tensor(x) or isinstance(x, np.ndarray):
-        if np.prod(tuple(x.shape)) != 1:
-            raise NotImplementedError('per-neuron external input arrays are not supported by '
-                                      'the fused kernel; pass a scalar')
-        return float(x.reshape(()).item() if torch.is_tensor(x) else x.reshape(()))
-    return float(x)
+        if np.prod(tuple(x.shape)) == 1:
+            return float(x.reshape(()).item() if torch.is_tensor(x) else x.reshape(())), None
+        t = torch.as_tensor(x, dtype=torch.float32, device=V.device)
+        try:
+            t = torch.broadcast_to(t, V.shape)
+        except RuntimeError:
+            raise ValueError(f'external input of shape {tuple(t.shape)} does not broadcast to '
+                             f'the population\'s shape {tuple(V.shape)}') from None
+        return 0.0, t.contiguous()
+    return float(x), None
 
 
 class LIFRef(_COBANeuron, _Describable):
@@ -222,8 +229,10 @@ class LIFRef(_COBANeuron, _Describable):
 
     def update(self, x=0.):
         g, ins, E, tau = self._channel_args()
-        p = self.params(_ext_input(x))
-        spk = ops.coba_lif_step(self.V.value, g[0], g[1], self.ref.value, ins[0], ins[1], p)
+        I, arr = _ext_input(x, self.V.value)
+        p = self.params(I)
+        spk = ops.coba_lif_step(self.V.value, g[0], g[1], self.ref.value, ins[0], ins[1], p,
+                                I_ext=arr)
         self._finish_channels(g)
         self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value
@@ -270,9 +279,10 @@ class HH(_COBANeuron, _Describable):
 
     def update(self, x=0.):
         g, ins, E, tau = self._channel_args()
-        p = self.params(_ext_input(x))
+        I, arr = _ext_input(x, self.V.value)
+        p = self.params(I)
         spk = ops.coba_hh_step(self.V.value, self.m.value, self.h.value, self.n.value, g[0],
-                               g[1], ins[0], ins[1], p)
+                               g[1], ins[0], ins[1], p, I_ext=arr)
         self._finish_channels(g)
         self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value

@@ -565,13 +565,25 @@ def hh_params(ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03, C=1.0, V_
                       float(np.float32(np.exp(-dt / tau_i))))
 
 
-def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None):
+def _input_array(I_ext, V):
+    """A per-neuron external input as a contiguous fp32 tensor of V's size on V's device."""
+    if I_ext is None:
+        return None
+    t = torch.as_tensor(I_ext, dtype=torch.float32, device=V.device)
+    return t.expand(V.shape).contiguous() if t.shape != V.shape else t.contiguous()
+
+
+def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None, I_ext=None):
+    """One COBA/CUBA-LIF step of every neuron; ``I_ext`` (optional, broadcast to V) is each
+    neuron's external input in place of ``params.I_ext`` (bs_coba_lif_step_in)."""
     n = V.numel()
     if spk_out is None:
         spk_out = torch.empty(n, dtype=torch.uint8, device=V.device)
-    N.check(N.lib().bs_coba_lif_step(n, N.ptr(V), N.ptr(ge), N.ptr(gi), N.ptr(ref), N.ptr(in_e),
-                                     N.ptr(in_i), ctypes_ref(params), N.ptr(spk_out),
-                                     N.stream_handle(V.device)), 'bs_coba_lif_step')
+    arr = _input_array(I_ext, V)
+    N.check(N.lib().bs_coba_lif_step_in(n, N.ptr(V), N.ptr(ge), N.ptr(gi), N.ptr(ref),
+                                        N.ptr(in_e), N.ptr(in_i), N.ptr(arr), ctypes_ref(params),
+                                        N.ptr(spk_out), N.stream_handle(V.device)),
+            'bs_coba_lif_step')
     return spk_out
 
 
@@ -580,12 +592,15 @@ def hh_init(V, m, h, n):
                                N.stream_handle(V.device)), 'bs_hh_init')
 
 
-def coba_hh_step(V, m, h, n, ge, gi, in_e, in_i, params, spk_out=None):
+def coba_hh_step(V, m, h, n, ge, gi, in_e, in_i, params, spk_out=None, I_ext=None):
+    """One COBA-HH step of every neuron; ``I_ext`` as in ``coba_lif_step``."""
     if spk_out is None:
         spk_out = torch.empty(V.numel(), dtype=torch.uint8, device=V.device)
-    N.check(N.lib().bs_coba_hh_step(V.numel(), N.ptr(V), N.ptr(m), N.ptr(h), N.ptr(n), N.ptr(ge),
-                                    N.ptr(gi), N.ptr(in_e), N.ptr(in_i), ctypes_ref(params),
-                                    N.ptr(spk_out), N.stream_handle(V.device)), 'bs_coba_hh_step')
+    arr = _input_array(I_ext, V)
+    N.check(N.lib().bs_coba_hh_step_in(V.numel(), N.ptr(V), N.ptr(m), N.ptr(h), N.ptr(n),
+                                       N.ptr(ge), N.ptr(gi), N.ptr(in_e), N.ptr(in_i), N.ptr(arr),
+                                       ctypes_ref(params), N.ptr(spk_out),
+                                       N.stream_handle(V.device)), 'bs_coba_hh_step')
     return spk_out
 
 

@@ -41,10 +41,12 @@ class EINetRunner:
     sum inside int32), summed exactly, then rounded once to fp32.
     ``delay_steps`` D: step t's synaptic inputs come from the spikes of step t-1-D (the
     reference's ``N.prefetch_delay('spike', D*dt)``; no spikes before the first step).
+    ``I_ext`` (optional, [n]): each neuron's constant external input, in place of
+    ``params.I_ext``.
     """
 
     def __init__(self, model, n, n_exc, idx_e, idx_i, w_e, w_i, params, V0, device='cuda',
-                 blocks_per_cu=0, delay_steps=0):
+                 blocks_per_cu=0, delay_steps=0, I_ext=None):
         N.require_gpu()
         self.delay_steps = int(delay_steps)
         self.model = model
@@ -70,6 +72,7 @@ class EINetRunner:
             self.w_e = self.w_i = None
             self.w_e_homo, self.w_i_homo = (float(np.float32(float(w))) for w in (w_e, w_i))
         self.params = params
+        self.I_ext = None if I_ext is None else _dev_array(I_ext, torch.float32, (self.n,), dev)
         f32 = dict(dtype=torch.float32, device=dev)
         self.spk = torch.zeros(self.n, dtype=torch.uint8, device=dev)
         self.t = 0   # absolute index of the next step
@@ -91,7 +94,8 @@ class EINetRunner:
                           self.w_e_homo,
                           self.idx_i.data_ptr(), None if self.w_i is None else self.w_i.data_ptr(),
                           self.w_i_homo, self.spk.data_ptr(), int(blocks_per_cu),
-                          self.delay_steps)
+                          self.delay_steps,
+                          None if self.I_ext is None else self.I_ext.data_ptr())
         nbytes = int(N.lib().bs_net_workspace_size(ctypes.byref(self._net)))
         if nbytes == 0:
             N.check(N.BS_ERR_INVALID, 'bs_net_workspace_size')

@@ -130,7 +130,8 @@ def _ei_step(log, spk_before=None):
     ``(neuron, proj_e, proj_i, n_exc, inp)`` when they were exactly the two projections onto
     one LIFRef / HH population, each given spikes of the population's shape (E: its first
     n_exc neurons, I: the rest) -- equal to ``spk_before``, its spikes before the step, when
-    given -- then that population with one constant input; else None."""
+    given -- then that population with one constant input (a scalar, or an array of the
+    population's state shape, one input per neuron); else None."""
     from .nn._event import FixedPostNumConn
     from .nn._neurons import HH, AlignPostProj, LIFRef
     if len(log) != 3:
@@ -160,13 +161,30 @@ def _ei_step(log, spk_before=None):
         if spk_before is not None and not torch.equal(args[0] != 0, spk_before[..., lo:hi] != 0):
             return None
     inp = an[0] if an else 0.0
+    if isinstance(inp, np.ndarray):
+        inp = torch.as_tensor(inp)
     if torch.is_tensor(inp):
         if inp.numel() != 1:
-            return None
+            if not torch.is_floating_point(inp) and inp.dtype not in (torch.int32, torch.int64):
+                return None
+            shape = tuple(neuron.V.value.shape)
+            try:   # one input per neuron: must broadcast to the population's state shape
+                if tuple(torch.broadcast_shapes(tuple(inp.shape), shape)) != shape:
+                    return None
+            except RuntimeError:
+                return None
+            return neuron, proj_e, proj_i, n_exc, inp.detach().to(torch.float32).clone()
         inp = inp.item()
     if not isinstance(inp, (int, float, np.floating, np.integer)):
         return None
     return neuron, proj_e, proj_i, n_exc, float(inp)
+
+
+def _same_input(a, b):
+    if torch.is_tensor(a) or torch.is_tensor(b):
+        return (torch.is_tensor(a) and torch.is_tensor(b) and a.shape == b.shape and
+                a.device == b.device and torch.equal(a, b))
+    return a == b
 
 
 def _fused_loop(f, xs, length):
@@ -193,7 +211,8 @@ def _fused_loop(f, xs, length):
                                     torch.equal(out != 0, spk != 0)):
             return outs, None
         steps.append(step)
-    if any(a is not b for a, b in zip(steps[0][:3], steps[1][:3])) or steps[0][3:] != steps[1][3:]:
+    if any(a is not b for a, b in zip(steps[0][:3], steps[1][:3])) or \
+            steps[0][3] != steps[1][3] or not _same_input(steps[0][4], steps[1][4]):
         return outs, None
     neuron, proj_e, proj_i, n_exc, inp = steps[1]
     r = fuse(neuron, proj_e, proj_i, n_exc, inp)

@@ -279,6 +279,12 @@ typedef struct {
 BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
                      const float* in_e, const float* in_i, const bs_lif_params* p,
                      uint8_t* spk_out, bs_stream_t stream);
+/* The same step with a per-neuron external input: I_ext [n] (NULL: p->I_ext for every
+ * neuron) in place of p->I_ext, as when the reference's neuron is called with an input array
+ * (brainpy.state LIFRef.update(x), x of the population's shape). */
+BS_API int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                               const float* in_e, const float* in_i, const float* I_ext,
+                               const bs_lif_params* p, uint8_t* spk_out, bs_stream_t stream);
 
 /* One recurrent step of a packed EventLinear driving COBA-LIF neurons, in one launch:
  * cur = the bs_event_dense_packed_f32 product of spk [batch, n_in] with `packed`, then the
@@ -317,6 +323,12 @@ BS_API int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng, 
 BS_API int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge, float* gi,
                     const float* in_e, const float* in_i, const bs_hh_params* p,
                     uint8_t* spk_out, bs_stream_t stream);
+/* The same step with a per-neuron external input I_ext [n] (NULL: p->I_ext), as for an input
+ * array passed to the HH neuron (examples/100_hh_neuron_model.py:72-93 with x of shape [n]). */
+BS_API int bs_coba_hh_step_in(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
+                              float* gi, const float* in_e, const float* in_i,
+                              const float* I_ext, const bs_hh_params* p, uint8_t* spk_out,
+                              bs_stream_t stream);
 
 /* ---------------------------------------------------------------- whole-loop runners
  * Replace `brainstate.transform.for_loop(net.update, times)` over an E/I network
@@ -343,6 +355,9 @@ typedef struct {
                             of step t-1-D, as `N.prefetch_delay('spike', D*dt)` gives
                             (brainstate/nn/_dynamics.py:222-262, _delay.py:762-790); no spikes
                             before the first step; workspace grows as 2(D+1) inbox slots */
+  const float* I_ext;    /* [n] per-neuron constant external input, in place of the neuron
+                            parameters' I_ext (NULL: the parameters' I_ext for every neuron),
+                            as a script calling N(x) with an input array x of shape [n] */
 } bs_net;
 
 typedef struct { float* V; float* ge; float* gi; int32_t* ref; } bs_lif_state;

@@ -312,7 +312,7 @@ static inline uint8_t o_hh(const bso_hh_params* p, float* Vp, float* mp, float* 
 static long long o_run(int model, const o_net* g, const void* params, void* const* st,
                        uint8_t* spk, void* in_e_ring, void* in_i_ring, int steps,
                        int32_t* counts, uint32_t* hashes, int nthreads, int delay,
-                       long long t0) {
+                       long long t0, const float* iext) {
   const int n = g->n;
   int32_t* active = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n > 0 ? n : 1));
   long long total = 0;
@@ -332,7 +332,9 @@ static long long o_run(int model, const o_net* g, const void* params, void* cons
 #pragma omp parallel for schedule(static) reduction(+ : h)
       for (int j = 0; j < n; ++j) {
         const float ie = o_take(g, in_e, 0, j), ii = o_take(g, in_i, 1, j);
-        const uint8_t s = o_lif(p, &V[j], &ge[j], &gi[j], &ref[j], ie, ii);
+        bso_lif_params q = *p;
+        if (iext) q.I_ext = iext[j];  /* per-neuron external input */
+        const uint8_t s = o_lif(&q, &V[j], &ge[j], &gi[j], &ref[j], ie, ii);
         spk[j] = s;
         if (s) h += o_mix32((uint32_t)j);
       }
@@ -347,7 +349,9 @@ static long long o_run(int model, const o_net* g, const void* params, void* cons
 #pragma omp parallel for schedule(static) reduction(+ : h)
       for (int j = 0; j < n; ++j) {
         const float ie = o_take(g, in_e, 0, j), ii = o_take(g, in_i, 1, j);
-        const uint8_t s = o_hh(p, &V[j], &m[j], &hg[j], &ng[j], &ge[j], &gi[j], ie, ii);
+        bso_hh_params q = *p;
+        if (iext) q.I_ext = iext[j];
+        const uint8_t s = o_hh(&q, &V[j], &m[j], &hg[j], &ng[j], &ge[j], &gi[j], ie, ii);
         spk[j] = s;
         if (s) h += o_mix32((uint32_t)j);
       }
@@ -373,12 +377,12 @@ long long bso_coba_lif_run(int n, int n_exc, int k_e, int k_i, const int32_t* id
                            float* V, float* ge, float* gi, int32_t* ref, uint8_t* spk,
                            void* in_e_ring, void* in_i_ring, int steps, int32_t* counts,
                            uint32_t* hashes, int nthreads, int delay, long long t0,
-                           const int32_t* qexp) {
+                           const int32_t* qexp, const float* iext) {
   o_net g;
   o_net_init(&g, n, n_exc, k_e, k_i, idx_e, w_e, w_e_homo, idx_i, w_i, w_i_homo, qexp);
   void* st[4] = {V, ge, gi, ref};
   return o_run(0, &g, pp, st, spk, in_e_ring, in_i_ring, steps, counts, hashes, nthreads, delay,
-               t0);
+               t0, iext);
 }
 
 __attribute__((target_clones("fma", "default")))
@@ -388,12 +392,12 @@ long long bso_coba_hh_run(int n, int n_exc, int k_e, int k_i, const int32_t* idx
                           float* m, float* h, float* ng, float* ge, float* gi, uint8_t* spk,
                           void* in_e_ring, void* in_i_ring, int steps, int32_t* counts,
                           uint32_t* hashes, int nthreads, int delay, long long t0,
-                          const int32_t* qexp) {
+                          const int32_t* qexp, const float* iext) {
   o_net g;
   o_net_init(&g, n, n_exc, k_e, k_i, idx_e, w_e, w_e_homo, idx_i, w_i, w_i_homo, qexp);
   void* st[6] = {V, m, h, ng, ge, gi};
   return o_run(1, &g, pp, st, spk, in_e_ring, in_i_ring, steps, counts, hashes, nthreads, delay,
-               t0);
+               t0, iext);
 }
 
 /* Steady-state gates x_inf = a / (a + b) at V (examples/100_hh_neuron_model.py:66-70). */

@@ -116,7 +116,8 @@ def coba_lif_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, cou
     With ``delay`` D > 0, in_e / in_i are rings of D+1 input slots ([(D+1) * n]) and
     ``state['t']`` (absolute index of the next step, default 0) is advanced.  With
     per-synapse weights the rings hold int32 fixed-point sums (start them at zero) and
-    ``state['qexp']`` caches the exponents."""
+    ``state['qexp']`` caches the exponents.  ``state['I_ext']`` (optional, float32 [n]) is each
+    neuron's external input in place of ``p.I_ext``."""
     args, qexp, t0 = _common(state, idx_e, idx_i, w_e, w_i, delay)
     args[1] = ctypes.c_int(n_exc)
     state['t'] = t0 + int(steps)
@@ -125,7 +126,13 @@ def coba_lif_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, cou
         _ptr(state['V']), _ptr(state['ge']), _ptr(state['gi']), _ptr(state['ref']),
         _ptr(state['spk']), _ptr(state['in_e']), _ptr(state['in_i']), ctypes.c_int(steps),
         _ptr(counts), _ptr(hashes), ctypes.c_int(nthreads), ctypes.c_int(delay),
-        ctypes.c_longlong(t0), _ptr(qexp))
+        ctypes.c_longlong(t0), _ptr(qexp), _ptr(_input(state)))
+
+
+def _input(state):
+    import numpy as np
+    x = state.get('I_ext')
+    return None if x is None else np.ascontiguousarray(x, np.float32)
 
 
 def coba_hh_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, counts=None,
@@ -139,7 +146,8 @@ def coba_hh_run(state, idx_e, idx_i, w_e, w_i, p, n_exc, steps, nthreads=0, coun
         _ptr(state['V']), _ptr(state['m']), _ptr(state['h']), _ptr(state['n']),
         _ptr(state['ge']), _ptr(state['gi']), _ptr(state['spk']), _ptr(state['in_e']),
         _ptr(state['in_i']), ctypes.c_int(steps), _ptr(counts), _ptr(hashes),
-        ctypes.c_int(nthreads), ctypes.c_int(delay), ctypes.c_longlong(t0), _ptr(qexp))
+        ctypes.c_int(nthreads), ctypes.c_int(delay), ctypes.c_longlong(t0), _ptr(qexp),
+        _ptr(_input(state)))
 
 
 def hh_init(V):

@@ -192,6 +192,33 @@ def test_module_ei_network_matches_oracle(bs):
         assert np.array_equal(net.N.spike.value.cpu().numpy(), ref['spk'])
 
 
+def test_module_ei_network_per_neuron_input(bs):
+    """The same script with one external input per neuron (N(x), x of shape [n]): eager
+    steps and the persistent runner (for_loop hands the loop over with the array) both equal
+    the oracle given that array."""
+    import torch
+    print('[case] module E/I net, per-neuron input', flush=True)
+    T = 300
+    pe, pi, V0, p = make_golden.config1_net()
+    I = (20. + np.random.RandomState(5).uniform(-3., 3., V0.size)).astype(F)
+    ref = network.run_coba_lif(V0, pe, pi, neuron.LIFParams(I_ext=I), 3200, T)
+    dI = torch.as_tensor(I, device='cuda')
+
+    def make():
+        net = _EINet(bs)
+
+        def step(t):
+            spk = net.N.get_spike() != 0.
+            net.E(spk[:net.n_exc])
+            net.I(spk[net.n_exc:])
+            return net.N(dI)
+        return step, net
+    for spikes, net in _for_loop_paths(bs, make, T):
+        assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'])
+        assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+        assert np.array_equal(net.N.ref.value.cpu().numpy(), ref['ref'])
+
+
 def test_hh_module_network_for_loop(bs):
     """A COBA-HH E/I net (the shape of examples/105_COBA_HH_2007_braincell.py) built from the
     modules: for_loop eagerly and through the runner, both equal to the oracle's golden run."""

@@ -194,6 +194,57 @@ def test_coba_lif_large_matches_c(torch_cuda, n, steps, weights, D):
     assert np.array_equal(r.spk.cpu().numpy(), st['spk'])
 
 
+@pytest.mark.parametrize('model', ['lif', 'hh'])
+def test_runner_per_neuron_input_matches_c(torch_cuda, model):
+    """One external input per neuron (bs_net.I_ext) at the bench's instantiation (1M neurons,
+    4 per thread, per-synapse weights): counts, hashes and final state equal the C
+    restatement given the same array."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    torch = torch_cuda
+    n, T = 1_000_000, 300
+    say('runner per-neuron input', model, n, T)
+    rs = np.random.RandomState(11)
+    if model == 'lif':
+        n_exc, idx_e, idx_i, w_e, w_i, V0 = _big_net(n, 100, 100, 'normal')
+        I = rs.uniform(15., 25., n).astype(F)
+        r = EINetRunner('lif', n, n_exc, idx_e, idx_i, w_e, w_i, ops.lif_params(I_ext=0.), V0,
+                        I_ext=I)
+    else:
+        n_exc, idx_e, idx_i, w_e, w_i, V0 = _big_net(n, 80, 101, 'homo')
+        w_e, w_i = 0.05, 0.3
+        V0 = rs.uniform(-70., -50., n).astype(F)
+        I = rs.uniform(0., 13., n).astype(F)
+        r = EINetRunner('hh', n, n_exc, idx_e, idx_i, w_e, w_i, ops.hh_params(I_ext=0.), V0,
+                        I_ext=I)
+    counts, hashes = _run_chunks(torch, r, T, [T // 3, T - T // 3])
+    say('  gpu done, running the C restatement on', _host_threads(), 'threads')
+    if model == 'lif':
+        from oracle import cbuild
+        st = cbuild.lif_state(V0)
+        st['I_ext'] = I
+        c_ref = np.zeros(T, np.int32)
+        h_ref = np.zeros(T, np.uint32)
+        cbuild.coba_lif_run(st, idx_e, idx_i, w_e, w_i, neuron.LIFParams(I_ext=0.), n_exc, T,
+                            nthreads=_host_threads(), counts=c_ref, hashes=h_ref)
+        keys = ('V', 'ge', 'gi', 'ref')
+    else:
+        from oracle import cbuild
+        st = cbuild.hh_state(V0)
+        st['I_ext'] = I
+        c_ref = np.zeros(T, np.int32)
+        h_ref = np.zeros(T, np.uint32)
+        cbuild.coba_hh_run(st, idx_e, idx_i, w_e, w_i, neuron.HHParams(I_ext=0.), n_exc, T,
+                           nthreads=_host_threads(), counts=c_ref, hashes=h_ref)
+        keys = ('V', 'm', 'h', 'n', 'ge', 'gi')
+    assert c_ref.sum() > T * n // 5000
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    for key in keys:
+        assert np.array_equal(r.state[key].cpu().numpy(), st[key]), key
+
+
 @pytest.mark.parametrize('weights', ['const', 'normal'])
 def test_coba_hh_1m_matches_c(torch_cuda, weights):
     """Config [5]: 1M COBA-HH neurons, K = 80 (4 neurons per thread), bench.py's drive (I_ext

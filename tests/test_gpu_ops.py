@@ -247,6 +247,43 @@ def test_hh_init_and_step_bit_exact(torch_cuda):
     assert np.array_equal(spk.cpu().numpy().astype(bool), exp[6])
 
 
+def test_step_kernels_take_per_neuron_input(torch_cuda):
+    """bs_coba_lif_step_in / bs_coba_hh_step_in: one external input per neuron in place of
+    the parameters' I_ext, bit-exact against the oracle given the same array (the neuron
+    called with an input array of its shape)."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    say('step kernels, per-neuron input')
+    n = 50_001
+    rng = np.random.RandomState(3)
+    I = rng.uniform(10., 30., n).astype(F)
+    V = rng.uniform(-62, -48, n).astype(F)
+    ge, gi = rng.exponential(0.5, n).astype(F), rng.exponential(2.0, n).astype(F)
+    ref_c = rng.choice([0, 0, 0, 1, 7], n).astype(np.int32)
+    in_e = (rng.rand(n) < 0.1).astype(F) * F(0.6)
+    in_i = (rng.rand(n) < 0.05).astype(F) * F(6.7)
+    eV, ege, egi, eref, espk = neuron.coba_lif_step(V, ge, gi, ref_c, in_e, in_i,
+                                                    neuron.LIFParams(I_ext=I))
+    tV, tge, tgi, tref = (dev(torch, a) for a in (V, ge, gi, ref_c))
+    spk = ops.coba_lif_step(tV, tge, tgi, tref, dev(torch, in_e), dev(torch, in_i),
+                            ops.lif_params(I_ext=0.), I_ext=dev(torch, I))
+    assert np.array_equal(tV.cpu().numpy(), eV) and np.array_equal(tref.cpu().numpy(), eref)
+    assert np.array_equal(spk.cpu().numpy().astype(bool), espk) and espk.sum() > 100
+    # HH
+    V = rng.uniform(-75, -50, n).astype(F)
+    m, h, ng = neuron.hh_init(V)
+    I = rng.uniform(0., 12., n).astype(F)
+    ge, gi = rng.exponential(0.1, n).astype(F), rng.exponential(0.3, n).astype(F)
+    exp = neuron.hh_step(V, m, h, ng, ge, gi, in_e * F(0.1), in_i * F(0.05),
+                         neuron.HHParams(I_ext=I))
+    t = [dev(torch, a) for a in (V, m, h, ng, ge, gi)]
+    spk = ops.coba_hh_step(*t, dev(torch, in_e * F(0.1)), dev(torch, in_i * F(0.05)),
+                           ops.hh_params(I_ext=0.), I_ext=dev(torch, I))
+    for g, e in zip(t, exp[:6]):
+        assert np.array_equal(g.cpu().numpy(), e)
+    assert np.array_equal(spk.cpu().numpy().astype(bool), exp[6])
+
+
 # ---------------------------------------------------------------- fused spike-vector mat-vec
 
 @pytest.mark.parametrize('n_pre,n_post,k,p,het,csr', [

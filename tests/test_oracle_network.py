@@ -224,6 +224,26 @@ def test_c_restatement_equals_numpy_oracle(nthreads):
     assert make_golden.sha(st['V']) == gold['final_V_sha256']
 
 
+def test_per_neuron_input_c_equals_numpy():
+    """An input array (one external input per neuron, as N(x) with x of the population's
+    shape): the C restatement equals the numpy oracle given the same array; the array changes
+    the run (it is not the scalar I_ext), and a constant array equals that scalar."""
+    pe, pi, V0, p = make_golden.config1_net()
+    n, T = V0.size, 300
+    I = (20. + np.random.RandomState(5).uniform(-3., 3., n)).astype(F)
+    ref = network.run_coba_lif(V0, pe, pi, neuron.LIFParams(I_ext=I), 3200, T)
+    base = network.run_coba_lif(V0, pe, pi, p, 3200, T)
+    assert not np.array_equal(ref['counts'], base['counts'])
+    for arr, want in ((I, ref), (np.full(n, p.I_ext, F), base)):
+        st = cbuild.lif_state(V0)
+        st['I_ext'] = arr
+        counts = np.zeros(T, np.int32)
+        cbuild.coba_lif_run(st, pe.idx, pi.idx, pe.w_scalar, pi.w_scalar, p, 3200, T,
+                            nthreads=4, counts=counts)
+        assert counts.tolist() == want['counts'].tolist()
+        assert np.array_equal(st['V'], want['V'])
+
+
 def test_spike_hash_matches_mix32_definition():
     spk = np.zeros(100, bool)
     spk[[3, 50]] = True
