@@ -163,3 +163,46 @@ def test_batched_net_fused_union_runner(bs):
         assert np.array_equal(ras[:, b], ref['raster']), b
         assert np.array_equal(net.N.V.value[b].cpu().numpy(), ref['V']), b
         assert np.array_equal(net.E.syn.g.value[b].cpu().numpy(), ref['ge']), b
+
+
+def test_batched_net_per_replica_input(bs):
+    """A sweep over the drive: replica b gets its own external input (N(x) with x of shape
+    [B, 1], broadcast over its neurons) -- eager for_loop, the loop handed to the union runner,
+    and fuse() with the array; every replica equals its own oracle run with that input."""
+    import torch
+    from oracle import neuron
+    B, T = 4, 200
+    say('batched net, per-replica input', B, T)
+    V0s = _replica_V0(B)
+    pe, pi, _, _ = make_golden.config1_net()
+    I = np.array([16., 19., 22., 25.], F)[:, None]
+    dI = torch.as_tensor(I, device='cuda')
+    refs = [network.run_coba_lif(V0s[b], pe, pi, neuron.LIFParams(I_ext=I[b, 0]), 3200, T)
+            for b in range(B)]
+    assert len({int(r['counts'].sum()) for r in refs}) == B   # the inputs matter
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                net = _BatchedEINet(bs, V0s)
+
+                def step(t):
+                    spk = net.N.get_spike() != 0.
+                    net.E(spk[..., :net.n_exc])
+                    net.I(spk[..., net.n_exc:])
+                    return net.N(dI)
+                spikes = bs.transform.for_loop(step, torch.arange(T) * 0.1).cpu().numpy()
+        finally:
+            bs.transform.fuse_loops = True
+        assert bs.transform.last_loop == ('fused' if fused else 'eager')
+        for b in range(B):
+            assert np.array_equal(spikes[:, b] != 0, refs[b]['raster']), (fused, b)
+            assert np.array_equal(net.N.V.value[b].cpu().numpy(), refs[b]['V']), (fused, b)
+    with bs.environ.context(dt=0.1):
+        net = _BatchedEINet(bs, V0s)
+        r = bs.nn.fuse(net.N, net.E, net.I, n_exc=3200, inp=dI)
+        r.run(T)
+        r.check()
+        r.write_back()
+    for b in range(B):
+        assert np.array_equal(net.N.V.value[b].cpu().numpy(), refs[b]['V']), b
