@@ -742,11 +742,27 @@ __global__ __launch_bounds__(kBlock) void k_caps(NetArgs a, uint32_t* cap) {
   const int64_t chunk = (int64_t)1 << a.L.shift;
   const int64_t lo = (int64_t)me * chunk;
   const int64_t hi = lo + chunk < a.n ? lo + chunk : a.n;
-  for (int64_t i = lo; i < hi; ++i) {
-    const Row rw = row_of(a, (int32_t)i);
-    for (int tt = threadIdx.x; tt < rw.k; tt += kBlock) {
-      const int32_t tgt = rw.idx[tt];
-      if ((uint32_t)tgt < (uint32_t)a.n) atomicAdd(&hist[tgt >> a.L.shift], 1u);
+  // kRows rows per wave at a time, lane l reading synapse l (+ 64 j) of each, their loads in
+  // flight together (one row per workgroup and iteration waited ~1 us per row: ~4 ms for the
+  // 4,096-row slices of a 1M-neuron net)
+  constexpr int kRows = 4;
+  const int lane = bs_lane();
+  const int wid = threadIdx.x / BS_WAVE;
+  for (int64_t i0 = lo + (int64_t)wid * kRows; i0 < hi; i0 += (int64_t)kWaves * kRows) {
+    Row rw[kRows];
+    int32_t kmax = 0;
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+      rw[u] = i0 + u < hi ? row_of(a, (int32_t)(i0 + u)) : Row{nullptr, nullptr, 0, false};
+      kmax = rw[u].k > kmax ? rw[u].k : kmax;
+    }
+    for (int32_t t0 = 0; t0 < kmax; t0 += BS_WAVE) {
+      int32_t tgt[kRows];
+#pragma unroll
+      for (int u = 0; u < kRows; ++u) tgt[u] = t0 + lane < rw[u].k ? rw[u].idx[t0 + lane] : -1;
+#pragma unroll
+      for (int u = 0; u < kRows; ++u)
+        if ((uint32_t)tgt[u] < (uint32_t)a.n) atomicAdd(&hist[tgt[u] >> a.L.shift], 1u);
     }
   }
   __syncthreads();
