@@ -118,6 +118,10 @@ def _no_autodiff(*ts):
 
 
 _BUCKET_AUTO_POSTS = 16384   # 'auto': bucketed above this many outputs (one LDS accumulator)
+# True while a loop records steps it may hand to the persistent runner: a homogeneous weight's
+# mat-vec then takes the one-launch kernel instead of building a bucketed layout the runner
+# does not use (same bits: w added once per event, every addend equal)
+defer_layouts = False
 
 
 def _wants_grad(*ts):
@@ -290,7 +294,8 @@ class FixedNumConn(Module):
         x = x if torch.is_tensor(x) else _to_dev(x, torch.float32)
         if x.device.type != 'cuda':
             x = x.to(_device())
-        if not value and x.dim() == 1 and self._bucketed() and _no_autodiff(x, w):
+        if not value and x.dim() == 1 and self._bucketed() and _no_autodiff(x, w) and \
+                not (defer_layouts and self._bucket is None and w.numel() == 1):
             return ops.event_bucket(x, self._bucket_layout(w))
         conn = self.conn.with_data(w)
         return conn.matvec_events(x, value)   # [..., n_pre] -> [..., n_post], one launch

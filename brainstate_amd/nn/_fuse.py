@@ -75,22 +75,25 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     if isinstance(w_e, float) != isinstance(w_i, float):   # one heterogeneous -> both per synapse
         w_e = torch.full(idx_e.shape, w_e, device=dev) if isinstance(w_e, float) else w_e
         w_i = torch.full(idx_i.shape, w_i, device=dev) if isinstance(w_i, float) else w_i
-    perm = _union_perm(B, n, n_exc)
+    # one replica: the runner's order is the net's (no permutation to build or apply)
+    perm = _union_perm(B, n, n_exc) if B > 1 else np.arange(n, dtype=np.int64)[None, :]
     if B > 1:   # block-diagonal union of the replicas, one runner
         pm = torch.as_tensor(perm, device=dev)
         idx_e = torch.cat([pm[b][idx_e.long()] for b in range(B)]).to(torch.int32)
         idx_i = torch.cat([pm[b][idx_i.long()] for b in range(B)]).to(torch.int32)
         if not isinstance(w_e, float):
             w_e, w_i = w_e.repeat(B, 1), w_i.repeat(B, 1)
-    pt = torch.as_tensor(perm.reshape(-1), device=Vs.device)
+    pt = torch.as_tensor(perm.reshape(-1), device=Vs.device) if B > 1 else None
 
     def to_runner(x):
+        if pt is None:
+            return x.reshape(-1).clone()
         out = torch.empty(B * n, dtype=x.dtype, device=x.device)
         out[pt] = x.reshape(-1)
         return out
 
     def from_runner(x):
-        return x[pt].reshape(Vs.shape).clone()
+        return (x if pt is None else x[pt]).reshape(Vs.shape).clone()
 
     V0 = to_runner(Vs)
     if isinstance(neuron, HH):
@@ -135,5 +138,6 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
 
     r.write_back = write_back
     r.replica_index = perm   # runner neuron of (replica b, neuron j), for rasters
+    r.replica_identity = B == 1   # replica_index is the identity
     r.dt = environ.get_dt()
     return r

@@ -195,13 +195,17 @@ def _fused_loop(f, xs, length):
     steps in one launch from the state the eager steps left -- pending spikes included -- and
     writes the final state back.  Returns (outputs of the eager steps, the stacked output of
     all steps or None when the loop must go on eagerly)."""
-    from .nn import _module
+    from .nn import _event, _module
     from .nn._fuse import fuse
     outs, steps = [], []
     for i in range(2):
         before = steps[0][0].spike.value.clone() if steps else None
-        with _module.record_calls() as log:
-            out = f(*[x[i] for x in xs])
+        _event.defer_layouts = True
+        try:
+            with _module.record_calls() as log:
+                out = f(*[x[i] for x in xs])
+        finally:
+            _event.defer_layouts = False
         outs.append(out)
         step = _ei_step(log, before)
         if step is None:
@@ -218,24 +222,33 @@ def _fused_loop(f, xs, length):
     r = fuse(neuron, proj_e, proj_i, n_exc, inp)
     T = length - 2
     want = outs[0] is not None
-    # the runner writes every neuron of every step into the raster
-    raster = torch.empty(T, r.n, dtype=torch.uint8, device=r.device) if want else None
+    res = raster = None
+    direct = False
+    if want:
+        # the stacked result: the eager steps' outputs, then the runner's raster (every neuron
+        # of every step as 0/1) in their order and dtype.  A bool or uint8 result in the
+        # runner's neuron order is the raster itself: the runner writes rows 2.. in place
+        # (a separate raster and its conversion took 18 ms for 10,000 steps of 1M neurons)
+        res = torch.empty((length,) + tuple(outs[0].shape), dtype=outs[0].dtype,
+                          device=outs[0].device)
+        perm = np.asarray(r.replica_index).reshape(-1)
+        ident = getattr(r, 'replica_identity', False) or np.array_equal(perm,
+                                                                         np.arange(perm.size))
+        direct = ident and res.dtype in (torch.bool, torch.uint8) and res.device == r.device
+        raster = (res[2:].view(torch.uint8).view(T, -1) if direct else
+                  torch.empty(T, r.n, dtype=torch.uint8, device=r.device))
     r.run(T, raster=raster)
     r.check()
     r.write_back()
     if not want:
         return outs, [None] * length
-    # the stacked result assembled in place: the eager steps' outputs, then the raster in
-    # their order and dtype (one conversion, no intermediate copy of the [length, ...] result)
-    res = torch.empty((length,) + tuple(outs[0].shape), dtype=outs[0].dtype,
-                      device=outs[0].device)
     res[0].copy_(outs[0])
     res[1].copy_(outs[1])
-    perm = np.asarray(r.replica_index).reshape(-1)
-    if np.array_equal(perm, np.arange(perm.size)):
-        res[2:].view(T, -1).copy_(raster)
-    else:
-        res[2:].view(T, -1).copy_(raster[:, torch.as_tensor(perm, device=raster.device)])
+    if not direct:
+        if ident:
+            res[2:].view(T, -1).copy_(raster)
+        else:
+            res[2:].view(T, -1).copy_(raster[:, torch.as_tensor(perm, device=raster.device)])
     return outs, res
 
 

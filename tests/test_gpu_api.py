@@ -219,6 +219,41 @@ def test_module_ei_network_per_neuron_input(bs):
         assert np.array_equal(net.N.ref.value.cpu().numpy(), ref['ref'])
 
 
+def test_for_loop_1m_fused_equals_eager(bs):
+    """A 1M-neuron module net (K = 100, homogeneous weights): for_loop handed to the runner
+    equals the loop stepped eagerly, whose mat-vecs take the bucketed layout while the fused
+    loop's two recorded steps take the one-launch kernel (no layout built)."""
+    import torch
+    print('[case] 1M module net, for_loop fused = eager', flush=True)
+    n, k, T = 1_000_000, 100, 40
+    n_exc = n * 4 // 5
+    V0 = np.random.RandomState(3).uniform(-60., -50., n).astype(F)
+
+    def make():
+        N = bs.nn.LIFRef(n, V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=5.,
+                         V_initializer=lambda s: V0)
+        E = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n_exc, n, k, 0.6, seed=1),
+                                syn=bs.nn.Expon.desc(n, tau=5.), out=bs.nn.COBA.desc(E=0.),
+                                post=N)
+        I = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n - n_exc, n, k, 6.7, seed=2),
+                                syn=bs.nn.Expon.desc(n, tau=10.), out=bs.nn.COBA.desc(E=-80.),
+                                post=N)
+        for m in (E.syn, I.syn, N):
+            m.init_state()
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            E(spk[:n_exc])
+            I(spk[n_exc:])
+            return N(20.)
+        return step, (N, E)
+    (eager, (Ne, Ee)), (fused, (Nf, Ef)) = _for_loop_paths(bs, make, T)
+    assert Ee.comm._bucket is not None and Ef.comm._bucket is None
+    assert int(eager.sum()) > T * 500
+    assert torch.equal(eager, fused)
+    assert torch.equal(Ne.V.value, Nf.V.value)
+
+
 def test_hh_module_network_for_loop(bs):
     """A COBA-HH E/I net (the shape of examples/105_COBA_HH_2007_braincell.py) built from the
     modules: for_loop eagerly and through the runner, both equal to the oracle's golden run."""
