@@ -110,6 +110,9 @@ SIGNATURES = {
                                         ctypes.POINTER(LifParams), c_vp, c_vp]),
     'bs_coba_lif_step_in': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                            ctypes.POINTER(LifParams), c_vp, c_vp]),
+    'bs_event_matvec_vjp_batch_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                                     c_i32, c_vp, c_f32, c_i32, c_vp, c_vp,
+                                                     c_vp, c_vp]),
     'bs_hh_init': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'bs_coba_hh_step_in': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                           c_vp, ctypes.POINTER(HhParams), c_vp, c_vp]),

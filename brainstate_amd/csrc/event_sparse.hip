@@ -299,6 +299,68 @@ __global__ __launch_bounds__(kBlock) void k_matvec_vjp(const T* __restrict__ spk
   }
 }
 
+// The same gradients for B batch rows in one launch (spk [B, n_pre], g [B, n_post]): one wave
+// per pre row i, the row's synapses read once per batch row (from cache after the first):
+//   grad_x[b, i] as k_matvec_vjp forms it for row b (lane partials, then a wave sum);
+//   grad_w[i, k] = sum_b x[b, i] * g[b, idx[i, k]], the products added in b order, as adding
+//   the per-row gradients one after another does (fp32, no contraction);
+//   homogeneous: grad_w[0] += x[b, i] * sum_k g[b, idx[i, k]] per (row, b), one atomic each.
+template <typename T, bool kCsr, bool kHet>
+__global__ __launch_bounds__(kBlock) void k_matvec_vjp_batch(
+    const T* __restrict__ spk, int32_t batch, int32_t n_pre, const int32_t* __restrict__ indptr,
+    const int32_t* __restrict__ indices, int32_t k, const float* __restrict__ w, float w_homo,
+    int32_t n_post, const float* __restrict__ g, float* __restrict__ gx,
+    float* __restrict__ gw) {
+  const int lane = bs_lane();
+  const int64_t nw = (int64_t)gridDim.x * (kBlock / BS_WAVE);
+  const int32_t nnz = kCsr ? indptr[n_pre] : 0;
+  for (int64_t row = ((int64_t)blockIdx.x * kBlock + threadIdx.x) / BS_WAVE; row < n_pre;
+       row += nw) {
+    int64_t beg, end;
+    if (kCsr) {
+      beg = indptr[row];
+      end = indptr[row + 1];
+      beg = beg < 0 ? 0 : beg;
+      end = end > nnz ? nnz : end;
+    } else {
+      beg = row * k;
+      end = beg + k;
+    }
+    for (int32_t b = 0; b < batch; ++b) {
+      const float xv = (float)spk[(int64_t)b * n_pre + row];
+      const float* gb = g + (int64_t)b * n_post;
+      float sx = 0.0f, sg = 0.0f;
+      for (int64_t s = beg + lane; s < end; s += BS_WAVE) {
+        const int32_t j = indices[s];
+        const float gj = (uint32_t)j < (uint32_t)n_post ? gb[j] : 0.0f;
+        if (gx) sx += (kHet ? w[s] : w_homo) * gj;
+        sg += gj;
+      }
+#pragma unroll
+      for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+        sx += __shfl_xor(sx, o);
+        sg += __shfl_xor(sg, o);
+      }
+      if (lane == 0) {
+        if (gx) gx[(int64_t)b * n_pre + row] = sx;
+        if (!kHet && gw && xv != 0.0f) bs_atomic_add_f32(gw, xv * sg);
+      }
+    }
+    if (kHet && gw) {
+      for (int64_t s = beg + lane; s < end; s += BS_WAVE) {
+        const int32_t j = indices[s];
+        float acc = 0.0f;
+        for (int32_t b = 0; b < batch; ++b) {
+          const float gj = (uint32_t)j < (uint32_t)n_post ? g[(int64_t)b * n_post + j] : 0.0f;
+          const float prod = (float)spk[(int64_t)b * n_pre + row] * gj;
+          acc = acc + prod;
+        }
+        gw[s] = acc;
+      }
+    }
+  }
+}
+
 int grid_for(int64_t work_items_waves) {
   const int64_t cap = (int64_t)bs_num_cus() * 16;
   int64_t b = (work_items_waves + (kBlock / BS_WAVE) - 1) / (kBlock / BS_WAVE);
@@ -489,6 +551,48 @@ extern "C" int bs_value_matvec_batch_f32(const float* x, int32_t batch, int32_t 
   bs_clear_error();
   return matvec_launch<true>(x, BS_SPK_F32, batch, n_pre, indptr, indices, k, w, w_homo, n_post,
                              out, accumulate, bs_stream(stream), "bs_value_matvec_batch_f32");
+}
+
+extern "C" int bs_event_matvec_vjp_batch_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                             int32_t n_pre, const int32_t* indptr,
+                                             const int32_t* indices, int32_t k, const float* w,
+                                             float w_homo, int32_t n_post, const float* grad_out,
+                                             float* grad_spk, float* grad_w,
+                                             bs_stream_t stream) {
+  bs_clear_error();
+  BS_CHECK_ARG(batch >= 0 && n_pre >= 0 && n_post >= 0,
+               "bs_event_matvec_vjp_batch_f32: negative size");
+  BS_CHECK_ARG(indptr != nullptr || k >= 0, "bs_event_matvec_vjp_batch_f32: k=%d < 0", k);
+  BS_CHECK_ARG(spk_dtype == BS_SPK_U8 || spk_dtype == BS_SPK_F32,
+               "bs_event_matvec_vjp_batch_f32: unknown spike dtype %d", spk_dtype);
+  hipStream_t s = bs_stream(stream);
+  const bool het = w != nullptr, csr = indptr != nullptr;
+  if (grad_w && !het) {  // homogeneous: one scalar, accumulated with atomics below
+    int rc = bs_fill_f32(grad_w, 1, 0.0f, s);
+    if (rc) return rc;
+  }
+  if (n_pre == 0 || (!grad_spk && !grad_w)) return BS_OK;
+  BS_CHECK_ARG(spk && indices && (grad_out || n_post == 0 || batch == 0),
+               "bs_event_matvec_vjp_batch_f32: NULL pointer");
+  if (!csr && k == 0) {  // no synapse: grad_spk is zero, grad_w empty
+    return grad_spk ? bs_fill_f32(grad_spk, (int64_t)batch * n_pre, 0.0f, s) : BS_OK;
+  }
+  // batch == 0 or n_post == 0 go through the kernel: it writes grad_w = 0 (g never read)
+  const int g = grid_for(n_pre);
+#define BS_VJPB(T, C, H)                                                                    \
+  k_matvec_vjp_batch<T, C, H><<<g, kBlock, 0, s>>>((const T*)spk, batch, n_pre, indptr,       \
+                                                   indices, k, w, w_homo, n_post, grad_out,   \
+                                                   grad_spk, grad_w)
+  if (spk_dtype == BS_SPK_U8) {
+    if (csr) { if (het) BS_VJPB(uint8_t, true, true); else BS_VJPB(uint8_t, true, false); }
+    else { if (het) BS_VJPB(uint8_t, false, true); else BS_VJPB(uint8_t, false, false); }
+  } else {
+    if (csr) { if (het) BS_VJPB(float, true, true); else BS_VJPB(float, true, false); }
+    else { if (het) BS_VJPB(float, false, true); else BS_VJPB(float, false, false); }
+  }
+#undef BS_VJPB
+  BS_CHECK_LAUNCH();
+  return BS_OK;
 }
 
 extern "C" int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,

@@ -75,15 +75,14 @@ class _EventMatvecFn(torch.autograd.Function):
         n_pre = spk.shape[-1] if spk.dim() else 1
         rows = spk.reshape(-1, n_pre)
         grows = g.reshape(-1, ctx.n_post)
-        gs_rows, gw = [], None
-        for b in range(rows.shape[0]):   # per batch row; weight gradients add up
-            gs_b, gw_b = ops.event_matvec_vjp(rows[b], indices, _kw(w), ctx.n_post,
-                                              grows[b].contiguous(), indptr=indptr,
-                                              need_spk=need_s, need_w=need_w)
-            gs_rows.append(gs_b)
-            if gw_b is not None:
-                gw = gw_b if gw is None else gw + gw_b
-        gs = torch.stack(gs_rows).reshape(spk.shape).to(spk.dtype) if need_s else None
+        if rows.shape[0] == 1:
+            gs, gw = ops.event_matvec_vjp(rows[0], indices, _kw(w), ctx.n_post,
+                                          grows[0].contiguous(), indptr=indptr,
+                                          need_spk=need_s, need_w=need_w)
+        else:   # every batch row in one launch; weight gradients summed in row order
+            gs, gw = ops.event_matvec_vjp_batch(rows, indices, _kw(w), ctx.n_post, grows,
+                                                indptr=indptr, need_spk=need_s, need_w=need_w)
+        gs = gs.reshape(spk.shape).to(spk.dtype) if need_s else None
         if gw is not None:
             gw = gw.reshape(w.shape)
         return gs, gw, None, None, None, None

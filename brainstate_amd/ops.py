@@ -166,6 +166,29 @@ def event_matvec_vjp(spk, indices, w, n_post, grad_out, k=None, indptr=None, nee
     return gs, gw
 
 
+def event_matvec_vjp_batch(spk, indices, w, n_post, grad_out, k=None, indptr=None,
+                           need_spk=True, need_w=True):
+    """event_matvec_vjp for spk [B, n_pre] and grad_out [B, n_post] in one launch: grad_spk
+    [B, n_pre] (row b as event_matvec_vjp gives it) and grad_w summed over the rows in row
+    order (bs_event_matvec_vjp_batch_f32)."""
+    spk = _spk_view(spk)
+    dev = indices.device
+    B, n_pre = int(spk.shape[0]), int(spk.shape[1])
+    k = _rows(n_pre, indices, k, indptr)
+    homo = not torch.is_tensor(w) or w.numel() == 1
+    g = grad_out.to(torch.float32).reshape(B, n_post).contiguous()
+    gs = torch.empty(B, n_pre, dtype=torch.float32, device=dev) if need_spk else None
+    gw = None
+    if need_w:
+        gw = torch.empty((), dtype=torch.float32, device=dev) if homo else \
+            torch.empty(w.shape, dtype=torch.float32, device=dev)
+    N.check(N.lib().bs_event_matvec_vjp_batch_f32(
+        N.ptr(spk), _spk_dtype(spk), B, n_pre, N.ptr(indptr), N.ptr(indices.contiguous()), k,
+        None if homo else N.ptr(w.contiguous()), float(w) if homo else 0.0, int(n_post),
+        N.ptr(g), N.ptr(gs), N.ptr(gw), N.stream_handle(dev)), 'bs_event_matvec_vjp_batch_f32')
+    return gs, gw
+
+
 def event_dense_vjp(spk, W, grad_out, need_spk=True, need_w=True):
     """Reverse mode of event_dense: (grad_spk [B, n_in] or None, grad_W [n_in, n_out] or None),
     the gradients of spk_values @ W."""

@@ -125,6 +125,17 @@ BS_API int bs_event_matvec_vjp_f32(const void* spk, int32_t spk_dtype, int32_t n
                                    const float* w, float w_homo, int32_t n_post,
                                    const float* grad_out, float* grad_spk, float* grad_w,
                                    bs_stream_t stream);
+/* The same for `batch` rows (spk [batch, n_pre], grad_out [batch, n_post], grad_spk [batch,
+ * n_pre]) in one launch, the reverse mode of bs_event_matvec_batch_f32 (the batched module's
+ * gradient, brainstate/nn/_event_fixedprob.py:202-209 under init_all_states(batch_size)):
+ * grad_spk row b as bs_event_matvec_vjp_f32 gives it for row b; per-synapse grad_w[s] =
+ * sum_b x[b, i] * g[b, idx[s]] with the products added in row order (the per-row gradients
+ * added one after another); a homogeneous grad_w[0] sums over rows and synapses. */
+BS_API int bs_event_matvec_vjp_batch_f32(const void* spk, int32_t spk_dtype, int32_t batch,
+                                         int32_t n_pre, const int32_t* indptr,
+                                         const int32_t* indices, int32_t k, const float* w,
+                                         float w_homo, int32_t n_post, const float* grad_out,
+                                         float* grad_spk, float* grad_w, bs_stream_t stream);
 
 /* ---------------------------------------------------------------- N2a, destination-bucketed
  * Same operator as bs_event_scatter_f32 / bs_event_matvec_f32 (replaces `EventArray(spk) @

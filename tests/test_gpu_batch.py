@@ -91,6 +91,45 @@ def test_batched_module_and_gradients(bs):
     assert np.allclose(jv.cpu().numpy(), want, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize('het,csr,sdt', [(True, False, 'u8'), (True, True, 'f32'),
+                                         (False, False, 'u8'), (True, False, 'f32')])
+def test_batched_vjp_kernel_equals_rows(bs, het, csr, sdt):
+    """bs_event_matvec_vjp_batch_f32: grad_spk row b equals bs_event_matvec_vjp_f32 on row b
+    bit for bit, and per-synapse grad_w equals the per-row gradients added in row order (bit
+    for bit); a homogeneous grad_w equals their sum within fp32 rounding."""
+    import torch
+    from brainstate_amd import ops
+    say('batched vjp kernel', het, csr, sdt)
+    rs = np.random.RandomState(9)
+    B, n_pre, n_post, k = 7, 3000, 2500, 40
+    idx = rs.randint(-3, n_post, (n_pre, k)).astype(np.int32)   # a few out-of-range targets
+    indptr = None
+    if csr:
+        lens = rs.randint(0, 2 * k, n_pre)
+        indptr = torch.as_tensor(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32),
+                                 device='cuda')
+        idx = rs.randint(0, n_post, int(lens.sum())).astype(np.int32)
+    d_idx = torch.as_tensor(idx, device='cuda')
+    w = torch.as_tensor(rs.randn(*idx.shape).astype(F), device='cuda') if het else \
+        torch.tensor(0.7, device='cuda')
+    act = rs.rand(B, n_pre) < 0.3
+    spk = torch.as_tensor(act.astype(np.uint8) if sdt == 'u8' else
+                          np.where(act, rs.rand(B, n_pre), 0).astype(F), device='cuda')
+    g = torch.as_tensor(rs.randn(B, n_post).astype(F), device='cuda')
+    gs, gw = ops.event_matvec_vjp_batch(spk, d_idx, w, n_post, g, indptr=indptr)
+    gw_sum = None
+    for b in range(B):
+        gs_b, gw_b = ops.event_matvec_vjp(spk[b], d_idx, w, n_post, g[b].contiguous(),
+                                          indptr=indptr)
+        assert torch.equal(gs[b], gs_b), b
+        gw_sum = gw_b if gw_sum is None else gw_sum + gw_b
+    if het:
+        assert torch.equal(gw, gw_sum)
+    else:
+        assert torch.allclose(gw, gw_sum, rtol=1e-5)
+    assert float(gs.abs().sum()) > 0
+
+
 class _BatchedEINet:
     """Config [1]'s E/I net (examples/105_COBA_HH_2007_braincell.py:54-82) with states
     [B, n]: replica b starts from its own V0."""
