@@ -176,3 +176,18 @@ def test_exp_euler_operand_check_rejects_host_tensors():
     x = torch.zeros(4)
     with pytest.raises(ValueError, match='on a GPU'):
         _exp_euler._check_operands((x, x, x, x), 4)
+
+
+def test_external_input_forms():                 # N(x): scalar, one element, or one per neuron
+    from brainstate_amd.nn._neurons import _ext_input
+    V = torch.zeros(2, 5)
+    assert _ext_input(20., V) == (20.0, None)
+    assert _ext_input(np.array([3.5]), V) == (3.5, None)
+    assert _ext_input(torch.tensor([[1.5]]), V) == (1.5, None)
+    I, arr = _ext_input(torch.arange(5.), V)          # broadcast over the batch rows
+    assert I == 0.0 and arr.shape == (2, 5) and arr.is_contiguous()
+    assert arr[1].tolist() == [0., 1., 2., 3., 4.]
+    I, arr = _ext_input(np.array([[1.], [2.]], np.float32), V)   # one input per replica
+    assert arr[:, 3].tolist() == [1., 2.]
+    with pytest.raises(ValueError, match='does not broadcast'):
+        _ext_input(torch.ones(3), V)
