@@ -39,6 +39,10 @@ class Net(ctypes.Structure):
                 ('I_ext', c_vp)]
 
 
+class LifArrays(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'ref_steps')]
+
+
 class LifState(ctypes.Structure):
     _fields_ = [('V', c_vp), ('ge', c_vp), ('gi', c_vp), ('ref', c_vp)]
 
@@ -113,6 +117,9 @@ SIGNATURES = {
     'bs_event_matvec_vjp_batch_f32': (ctypes.c_int, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp,
                                                      c_i32, c_vp, c_f32, c_i32, c_vp, c_vp,
                                                      c_vp, c_vp]),
+    'bs_coba_lif_step_arr': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                            ctypes.POINTER(LifArrays),
+                                            ctypes.POINTER(LifParams), c_vp, c_vp]),
     'bs_hh_init': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'bs_coba_hh_step_in': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                           c_vp, ctypes.POINTER(HhParams), c_vp, c_vp]),

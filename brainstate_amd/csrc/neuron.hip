@@ -17,7 +17,7 @@ __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restric
                                                      const float* __restrict__ in_e,
                                                      const float* __restrict__ in_i,
                                                      const float* __restrict__ iext,
-                                                     bs_lif_params p,
+                                                     bs_lif_arrays pa, bs_lif_params p,
                                                      uint8_t* __restrict__ spk) {
   for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
        j += (int64_t)gridDim.x * kBlock) {
@@ -25,6 +25,13 @@ __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restric
     int32_t r = ref[j];
     bs_lif_params q = p;
     if (iext) q.I_ext = iext[j];  // per-neuron external input
+    // per-neuron parameters (uniform branches: each array is given or not)
+    if (pa.V_rest) q.V_rest = pa.V_rest[j];
+    if (pa.V_th) q.V_th = pa.V_th[j];
+    if (pa.V_reset) q.V_reset = pa.V_reset[j];
+    if (pa.inv_tau) q.inv_tau = pa.inv_tau[j];
+    if (pa.R) q.R = pa.R[j];
+    if (pa.ref_steps) q.ref_steps = pa.ref_steps[j];
     const bool s =
         bs_lif_update<kCuba, kSoft>(q, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
     V[j] = v;
@@ -113,10 +120,11 @@ int grid(int32_t n) {
 
 }  // namespace
 
-extern "C" int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
-                                   const float* in_e, const float* in_i, const float* I_ext,
-                                   const bs_lif_params* p, uint8_t* spk_out,
-                                   bs_stream_t stream) {
+extern "C" int bs_coba_lif_step_arr(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                                    const float* in_e, const float* in_i, const float* I_ext,
+                                    const bs_lif_arrays* arr, const bs_lif_params* p,
+                                    uint8_t* spk_out, bs_stream_t stream) {
+  const bs_lif_arrays pa = arr ? *arr : bs_lif_arrays{};
   bs_clear_error();
   BS_CHECK_ARG(n >= 0, "bs_coba_lif_step: n=%d < 0", n);
   BS_CHECK_ARG(p != nullptr, "bs_coba_lif_step: params are NULL");
@@ -125,7 +133,8 @@ extern "C" int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, in
   BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
   hipStream_t s = bs_stream(stream);
 #define BS_LIF(C, S) \
-  k_lif_step<C, S><<<grid(n), kBlock, 0, s>>>(n, V, ge, gi, ref, in_e, in_i, I_ext, *p, spk_out)
+  k_lif_step<C, S><<<grid(n), kBlock, 0, s>>>(n, V, ge, gi, ref, in_e, in_i, I_ext, pa, *p, \
+                                              spk_out)
   if (p->cuba) { if (p->soft_reset) BS_LIF(true, true); else BS_LIF(true, false); }
   else { if (p->soft_reset) BS_LIF(false, true); else BS_LIF(false, false); }
 #undef BS_LIF
@@ -133,10 +142,18 @@ extern "C" int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, in
   return BS_OK;
 }
 
+extern "C" int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                                   const float* in_e, const float* in_i, const float* I_ext,
+                                   const bs_lif_params* p, uint8_t* spk_out,
+                                   bs_stream_t stream) {
+  return bs_coba_lif_step_arr(n, V, ge, gi, ref, in_e, in_i, I_ext, nullptr, p, spk_out, stream);
+}
+
 extern "C" int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
                                 const float* in_e, const float* in_i, const bs_lif_params* p,
                                 uint8_t* spk_out, bs_stream_t stream) {
-  return bs_coba_lif_step_in(n, V, ge, gi, ref, in_e, in_i, nullptr, p, spk_out, stream);
+  return bs_coba_lif_step_arr(n, V, ge, gi, ref, in_e, in_i, nullptr, nullptr, p, spk_out,
+                              stream);
 }
 
 extern "C" int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng,

@@ -66,6 +66,9 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
         if hist is not None and any(bool(h.any()) for h in _leaves(hist.value)):
             raise NotImplementedError('fuse() starts from a state without pending spikes '
                                       '(a delay history holds spikes)')
+    if getattr(neuron, 'has_param_arrays', lambda: False)():
+        raise NotImplementedError('fuse(): the runner takes scalar neuron parameters; a '
+                                  'population with per-neuron parameters steps eagerly')
     n = neuron.num
     Vs = neuron.V.value
     B = int(Vs.shape[0]) if Vs.dim() == 2 else 1   # init_all_states(batch_size=B)

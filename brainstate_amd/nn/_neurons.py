@@ -187,6 +187,14 @@ def _ext_input(x, V):
     return float(x), None
 
 
+def _scalar_or_array(v):
+    """A neuron parameter: a float, or (more than one element) an fp32 numpy array."""
+    if torch.is_tensor(v):
+        v = v.detach().cpu().numpy()
+    a = np.asarray(v, np.float64)
+    return float(a.reshape(())) if a.size == 1 else a.astype(np.float32)
+
+
 class LIFRef(_COBANeuron, _Describable):
     """Leaky integrate-and-fire with refractory period; ``spk_reset='hard'`` sets V_reset after
     a spike, ``'soft'`` subtracts V_th - V_reset.  ``ref_rule`` fixes how many steps tau_ref
@@ -203,9 +211,32 @@ class LIFRef(_COBANeuron, _Describable):
             raise ValueError(f"ref_rule must be 'open' or 'closed', got {ref_rule!r}")
         self.spk_reset = spk_reset
         self.ref_rule = ref_rule
-        self.R, self.tau, self.tau_ref = float(R), float(tau), float(tau_ref)
-        self.V_th, self.V_reset, self.V_rest = float(V_th), float(V_reset), float(V_rest)
+        # scalars, or arrays of the population's shape (one value per neuron; eager steps only)
+        self.R, self.tau, self.tau_ref = (_scalar_or_array(v) for v in (R, tau, tau_ref))
+        self.V_th, self.V_reset, self.V_rest = (_scalar_or_array(v)
+                                                for v in (V_th, V_reset, V_rest))
         self.V_initializer = V_initializer
+
+    def has_param_arrays(self):
+        return any(isinstance(v, np.ndarray) for v in
+                   (self.R, self.tau, self.tau_ref, self.V_th, self.V_reset, self.V_rest))
+
+    def _param_arrays(self, V):
+        """Per-neuron parameters for the step kernel (None when every one is a scalar)."""
+        if not self.has_param_arrays():
+            return None
+        arr = lambda v: v if isinstance(v, np.ndarray) else None   # noqa: E731
+        inv_tau = None
+        if isinstance(self.tau, np.ndarray):
+            inv_tau = (np.float32(1.0) / self.tau).astype(np.float32)   # fp32 reciprocal
+        ref_steps = None
+        if isinstance(self.tau_ref, np.ndarray):
+            q = self.tau_ref.astype(np.float64) / float(environ.get_dt())
+            n = np.ceil(q - 1e-9) - 1 if self.ref_rule == 'open' else np.floor(q + 1e-9)
+            ref_steps = np.maximum(n, 0).astype(np.int32)
+        return ops.lif_arrays(V, V_rest=arr(self.V_rest), V_th=arr(self.V_th),
+                              V_reset=arr(self.V_reset), inv_tau=inv_tau, R=arr(self.R),
+                              ref_steps=ref_steps)
 
     def init_state(self, batch_size=None, **kwargs):
         shape = _state_shape(self.num, batch_size)
@@ -214,15 +245,20 @@ class LIFRef(_COBANeuron, _Describable):
         self.spike = ShortTermState(torch.zeros(shape, dtype=torch.bool, device=_dev()))
 
     def params(self, I_ext=0.0):
+        """The scalar parameters (an array-valued one takes a placeholder here; the step
+        reads it per neuron)."""
         _, _, E, tau = self._channel_args()   # E holds the CUBA scales for CUBA channels
+        sc = lambda v, d: d if isinstance(v, np.ndarray) else v   # noqa: E731
+        V_rest, V_th, V_reset = sc(self.V_rest, 0.0), sc(self.V_th, 0.0), sc(self.V_reset, 0.0)
+        tau_m, R, tau_ref = sc(self.tau, 1.0), sc(self.R, 1.0), sc(self.tau_ref, 0.0)
         if self._cuba():
-            return ops.lif_params(V_rest=self.V_rest, V_th=self.V_th, V_reset=self.V_reset,
-                                  tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
+            return ops.lif_params(V_rest=V_rest, V_th=V_th, V_reset=V_reset,
+                                  tau=tau_m, R=R, tau_ref=tau_ref, I_ext=I_ext,
                                   tau_e=tau[0], tau_i=tau[1], dt=environ.get_dt(),
                                   out='cuba', scale_e=E[0], scale_i=E[1],
                                   spk_reset=self.spk_reset, ref_rule=self.ref_rule)
-        return ops.lif_params(V_rest=self.V_rest, V_th=self.V_th, V_reset=self.V_reset,
-                              tau=self.tau, R=self.R, tau_ref=self.tau_ref, I_ext=I_ext,
+        return ops.lif_params(V_rest=V_rest, V_th=V_th, V_reset=V_reset,
+                              tau=tau_m, R=R, tau_ref=tau_ref, I_ext=I_ext,
                               E_e=E[0], E_i=E[1], tau_e=tau[0], tau_i=tau[1],
                               dt=environ.get_dt(), spk_reset=self.spk_reset,
                               ref_rule=self.ref_rule)
@@ -232,7 +268,7 @@ class LIFRef(_COBANeuron, _Describable):
         I, arr = _ext_input(x, self.V.value)
         p = self.params(I)
         spk = ops.coba_lif_step(self.V.value, g[0], g[1], self.ref.value, ins[0], ins[1], p,
-                                I_ext=arr)
+                                I_ext=arr, arrays=self._param_arrays(self.V.value))
         self._finish_channels(g)
         self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value

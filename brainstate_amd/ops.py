@@ -596,17 +596,41 @@ def _input_array(I_ext, V):
     return t.expand(V.shape).contiguous() if t.shape != V.shape else t.contiguous()
 
 
-def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None, I_ext=None):
+_LIF_ARRAYS = ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'ref_steps')
+
+
+def lif_arrays(V, **arrays):
+    """Per-neuron LIF parameters for ``coba_lif_step(..., arrays=)``: each given value (any
+    of V_rest, V_th, V_reset, inv_tau, R, ref_steps) broadcast to V's shape on V's device
+    (ref_steps int32, the others fp32); the tensors stay referenced by the returned dict."""
+    out = {}
+    for k, v in arrays.items():
+        if k not in _LIF_ARRAYS:
+            raise ValueError(f'unknown per-neuron LIF parameter {k!r}')
+        if v is None:
+            continue
+        dt = torch.int32 if k == 'ref_steps' else torch.float32
+        t = torch.as_tensor(v, dtype=dt, device=V.device)
+        out[k] = torch.broadcast_to(t, V.shape).contiguous()
+    return out
+
+
+def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None, I_ext=None, arrays=None):
     """One COBA/CUBA-LIF step of every neuron; ``I_ext`` (optional, broadcast to V) is each
-    neuron's external input in place of ``params.I_ext`` (bs_coba_lif_step_in)."""
+    neuron's external input in place of ``params.I_ext``; ``arrays`` (``lif_arrays``) per-neuron
+    parameters in place of the scalars (bs_coba_lif_step_arr)."""
     n = V.numel()
     if spk_out is None:
         spk_out = torch.empty(n, dtype=torch.uint8, device=V.device)
     arr = _input_array(I_ext, V)
-    N.check(N.lib().bs_coba_lif_step_in(n, N.ptr(V), N.ptr(ge), N.ptr(gi), N.ptr(ref),
-                                        N.ptr(in_e), N.ptr(in_i), N.ptr(arr), ctypes_ref(params),
-                                        N.ptr(spk_out), N.stream_handle(V.device)),
-            'bs_coba_lif_step')
+    pa = None
+    if arrays:
+        pa = N.LifArrays(*[N.ptr(arrays.get(k)) for k in _LIF_ARRAYS])
+    N.check(N.lib().bs_coba_lif_step_arr(n, N.ptr(V), N.ptr(ge), N.ptr(gi), N.ptr(ref),
+                                         N.ptr(in_e), N.ptr(in_i), N.ptr(arr),
+                                         ctypes.byref(pa) if pa is not None else None,
+                                         ctypes_ref(params), N.ptr(spk_out),
+                                         N.stream_handle(V.device)), 'bs_coba_lif_step')
     return spk_out
 
 

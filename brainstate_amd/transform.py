@@ -139,6 +139,8 @@ def _ei_step(log, spk_before=None):
     (pa, aa, ka), (pb, ab, kb), (neuron, an, kn) = log
     if not isinstance(neuron, (LIFRef, HH)) or ka or kb or kn or len(an) > 1:
         return None
+    if getattr(neuron, 'has_param_arrays', lambda: False)():   # the runner's are scalars
+        return None
     chans = getattr(neuron, '_channels', [])
     if len(chans) != 2 or {id(pa), id(pb)} != {id(c) for c in chans}:
         return None

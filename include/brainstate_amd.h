@@ -290,12 +290,25 @@ typedef struct {
 BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
                      const float* in_e, const float* in_i, const bs_lif_params* p,
                      uint8_t* spk_out, bs_stream_t stream);
+/* Per-neuron LIF parameters: each non-NULL array [n] replaces the scalar of bs_lif_params
+ * for its neuron (a population built with array-valued V_rest, V_th, V_reset, tau, R or
+ * tau_ref; inv_tau = fp32(1 / tau), ref_steps = the refractory steps of that neuron's tau_ref). */
+typedef struct {
+  const float* V_rest; const float* V_th; const float* V_reset; const float* inv_tau;
+  const float* R; const int32_t* ref_steps;
+} bs_lif_arrays;
+
 /* The same step with a per-neuron external input: I_ext [n] (NULL: p->I_ext for every
  * neuron) in place of p->I_ext, as when the reference's neuron is called with an input array
  * (brainpy.state LIFRef.update(x), x of the population's shape). */
 BS_API int bs_coba_lif_step_in(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
                                const float* in_e, const float* in_i, const float* I_ext,
                                const bs_lif_params* p, uint8_t* spk_out, bs_stream_t stream);
+/* ... and with per-neuron parameters (arr NULL, or any of its arrays NULL: the scalars). */
+BS_API int bs_coba_lif_step_arr(int32_t n, float* V, float* ge, float* gi, int32_t* ref,
+                                const float* in_e, const float* in_i, const float* I_ext,
+                                const bs_lif_arrays* arr, const bs_lif_params* p,
+                                uint8_t* spk_out, bs_stream_t stream);
 
 /* One recurrent step of a packed EventLinear driving COBA-LIF neurons, in one launch:
  * cur = the bs_event_dense_packed_f32 product of spk [batch, n_in] with `packed`, then the

@@ -124,13 +124,14 @@ def test_event_linear_batched_bit_exact(bs):
 class _EINet:
     """examples/105_COBA_HH_2007_braincell.py:54-82 with config-[1] LIF parameters."""
 
-    def __init__(self, bs):
+    def __init__(self, bs, **lif):
         c = make_golden.CONFIG1
         self.bs = bs
         self.n_exc, self.num = c['n_exc'], c['n']
         V0 = np.random.RandomState(c['seed_v']).uniform(-60., -50., c['n']).astype(F)
-        self.N = bs.nn.LIFRef(self.num, V_rest=-60., V_th=-50., V_reset=-60., tau=20.,
-                              tau_ref=5., V_initializer=lambda s: V0)
+        kw = dict(V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=5.)
+        kw.update(lif)   # e.g. per-neuron parameter arrays
+        self.N = bs.nn.LIFRef(self.num, V_initializer=lambda s: V0, **kw)
         self.E = bs.nn.AlignPostProj(
             comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=0.02, conn_weight=0.6,
                                       seed=c['seed_e']),
@@ -252,6 +253,43 @@ def test_for_loop_1m_fused_equals_eager(bs):
     assert int(eager.sum()) > T * 500
     assert torch.equal(eager, fused)
     assert torch.equal(Ne.V.value, Nf.V.value)
+
+
+def test_module_ei_network_per_neuron_parameters(bs):
+    """LIFRef with array-valued V_th, tau and tau_ref (one value per neuron): the eager step
+    (bs_coba_lif_step_arr) equals the oracle given the same arrays (tau as its fp32
+    reciprocal, tau_ref as each neuron's refractory steps); for_loop keeps such a net eager
+    (the runner's parameters are scalars) and fuse() says so."""
+    import torch
+    print('[case] module E/I net, per-neuron parameters', flush=True)
+    T = 200
+    c = make_golden.CONFIG1
+    pe, pi, V0, p = make_golden.config1_net()
+    rs = np.random.RandomState(12)
+    V_th = rs.uniform(-52., -48., c['n']).astype(F)
+    tau = rs.uniform(15., 25., c['n']).astype(F)
+    tau_ref = rs.choice([2., 5., 8.], c['n']).astype(F)
+    p.V_th, p.tau = V_th, tau
+    p.inv_tau = (F(1.0) / tau).astype(F)
+    p.ref_steps = np.array([neuron.ref_steps(x, 0.1) for x in tau_ref], np.int32)
+    ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
+    with bs.environ.context(dt=0.1):
+        net = _EINet(bs, V_th=V_th, tau=tau, tau_ref=tau_ref)
+        N = net.N
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            net.E(spk[:net.n_exc])
+            net.I(spk[net.n_exc:])
+            return N(20.)
+        spikes = bs.transform.for_loop(step, torch.arange(T) * 0.1)
+        assert bs.transform.last_loop == 'eager'
+        with pytest.raises(NotImplementedError, match='per-neuron parameters'):
+            bs.nn.fuse(N, net.E, net.I, n_exc=3200, inp=20.)
+    assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'])
+    assert np.array_equal(N.V.value.cpu().numpy(), ref['V'])
+    assert np.array_equal(N.ref.value.cpu().numpy(), ref['ref'])
+    assert ref['counts'].sum() > 100
 
 
 def test_hh_module_network_for_loop(bs):
