@@ -43,6 +43,10 @@ class LifArrays(ctypes.Structure):
     _fields_ = [(n, c_vp) for n in ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'ref_steps')]
 
 
+class HhArrays(ctypes.Structure):
+    _fields_ = [(n, c_vp) for n in ('ENa', 'gNa', 'EK', 'gK', 'EL', 'gL', 'inv_C', 'V_th')]
+
+
 class LifState(ctypes.Structure):
     _fields_ = [('V', c_vp), ('ge', c_vp), ('gi', c_vp), ('ref', c_vp)]
 
@@ -120,6 +124,9 @@ SIGNATURES = {
     'bs_coba_lif_step_arr': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                             ctypes.POINTER(LifArrays),
                                             ctypes.POINTER(LifParams), c_vp, c_vp]),
+    'bs_coba_hh_step_arr': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                           c_vp, c_vp, ctypes.POINTER(HhArrays),
+                                           ctypes.POINTER(HhParams), c_vp, c_vp]),
     'bs_hh_init': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'bs_coba_hh_step_in': (ctypes.c_int, [c_i32, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                                           c_vp, ctypes.POINTER(HhParams), c_vp, c_vp]),

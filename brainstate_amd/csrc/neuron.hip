@@ -62,12 +62,21 @@ __global__ __launch_bounds__(kBlock) void k_hh_step(int32_t n, float* __restrict
                                                     const float* __restrict__ in_e,
                                                     const float* __restrict__ in_i,
                                                     const float* __restrict__ iext,
-                                                    bs_hh_params p, uint8_t* __restrict__ spk) {
+                                                    bs_hh_arrays pa, bs_hh_params p,
+                                                    uint8_t* __restrict__ spk) {
   for (int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x; j < n;
        j += (int64_t)gridDim.x * kBlock) {
     float v = V[j], mm = m[j], hh = h[j], nn = ng[j], e = ge[j], i = gi[j];
     bs_hh_params q = p;
-    if (iext) q.I_ext = iext[j];  // per-neuron external input
+    if (iext) q.I_ext = iext[j];
+    if (pa.ENa) q.ENa = pa.ENa[j];  // per-neuron parameters (uniform branches)
+    if (pa.gNa) q.gNa = pa.gNa[j];
+    if (pa.EK) q.EK = pa.EK[j];
+    if (pa.gK) q.gK = pa.gK[j];
+    if (pa.EL) q.EL = pa.EL[j];
+    if (pa.gL) q.gL = pa.gL[j];
+    if (pa.inv_C) q.inv_C = pa.inv_C[j];
+    if (pa.V_th) q.V_th = pa.V_th[j];  // per-neuron external input
     const bool s = bs_hh_update(q, v, mm, hh, nn, e, i, in_e ? in_e[j] : 0.0f,
                                 in_i ? in_i[j] : 0.0f);
     V[j] = v;
@@ -167,10 +176,11 @@ extern "C" int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* 
   return BS_OK;
 }
 
-extern "C" int bs_coba_hh_step_in(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
-                                  float* gi, const float* in_e, const float* in_i,
-                                  const float* I_ext, const bs_hh_params* p, uint8_t* spk_out,
-                                  bs_stream_t stream) {
+extern "C" int bs_coba_hh_step_arr(int32_t n, float* V, float* m, float* h, float* ng,
+                                   float* ge, float* gi, const float* in_e, const float* in_i,
+                                   const float* I_ext, const bs_hh_arrays* arr,
+                                   const bs_hh_params* p, uint8_t* spk_out, bs_stream_t stream) {
+  const bs_hh_arrays pa = arr ? *arr : bs_hh_arrays{};
   bs_clear_error();
   BS_CHECK_ARG(n >= 0, "bs_coba_hh_step: n=%d < 0", n);
   BS_CHECK_ARG(p != nullptr, "bs_coba_hh_step: params are NULL");
@@ -178,15 +188,24 @@ extern "C" int bs_coba_hh_step_in(int32_t n, float* V, float* m, float* h, float
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && m && h && ng && ge && gi, "bs_coba_hh_step: NULL state pointer");
   k_hh_step<<<grid(n), kBlock, 0, bs_stream(stream)>>>(n, V, m, h, ng, ge, gi, in_e, in_i,
-                                                        I_ext, *p, spk_out);
+                                                        I_ext, pa, *p, spk_out);
   BS_CHECK_LAUNCH();
   return BS_OK;
+}
+
+extern "C" int bs_coba_hh_step_in(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
+                                  float* gi, const float* in_e, const float* in_i,
+                                  const float* I_ext, const bs_hh_params* p, uint8_t* spk_out,
+                                  bs_stream_t stream) {
+  return bs_coba_hh_step_arr(n, V, m, h, ng, ge, gi, in_e, in_i, I_ext, nullptr, p, spk_out,
+                             stream);
 }
 
 extern "C" int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
                                float* gi, const float* in_e, const float* in_i,
                                const bs_hh_params* p, uint8_t* spk_out, bs_stream_t stream) {
-  return bs_coba_hh_step_in(n, V, m, h, ng, ge, gi, in_e, in_i, nullptr, p, spk_out, stream);
+  return bs_coba_hh_step_arr(n, V, m, h, ng, ge, gi, in_e, in_i, nullptr, nullptr, p, spk_out,
+                             stream);
 }
 
 extern "C" int bs_exp_euler_f32(int64_t n, const float* x, const float* drift, const float* jac,

@@ -292,8 +292,9 @@ class HH(_COBANeuron, _Describable):
     def __init__(self, in_size, ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03,
                  V_th=20., C=1.0, V_initializer=-65., name=None):
         super().__init__(in_size, name=name)
-        self.ENa, self.gNa, self.EK, self.gK = float(ENa), float(gNa), float(EK), float(gK)
-        self.EL, self.gL, self.V_th, self.C = float(EL), float(gL), float(V_th), float(C)
+        # scalars, or arrays of the population's shape (one value per neuron; eager steps only)
+        self.ENa, self.gNa, self.EK, self.gK = (_scalar_or_array(v) for v in (ENa, gNa, EK, gK))
+        self.EL, self.gL, self.V_th, self.C = (_scalar_or_array(v) for v in (EL, gL, V_th, C))
         self.V_initializer = V_initializer
 
     def init_state(self, batch_size=None, **kwargs):
@@ -305,12 +306,30 @@ class HH(_COBANeuron, _Describable):
         self.m, self.h, self.n = HiddenState(m), HiddenState(h), HiddenState(nn_)
         self.spike = ShortTermState(torch.zeros(shape, dtype=torch.bool, device=dev))
 
+    def has_param_arrays(self):
+        return any(isinstance(v, np.ndarray) for v in
+                   (self.ENa, self.gNa, self.EK, self.gK, self.EL, self.gL, self.V_th, self.C))
+
+    def _param_arrays(self, V):
+        """Per-neuron parameters for the step kernel (None when every one is a scalar)."""
+        if not self.has_param_arrays():
+            return None
+        arr = lambda v: v if isinstance(v, np.ndarray) else None   # noqa: E731
+        inv_C = (np.float32(1.0) / self.C).astype(np.float32) if isinstance(self.C, np.ndarray) \
+            else None
+        return ops.hh_arrays(V, ENa=arr(self.ENa), gNa=arr(self.gNa), EK=arr(self.EK),
+                             gK=arr(self.gK), EL=arr(self.EL), gL=arr(self.gL), inv_C=inv_C,
+                             V_th=arr(self.V_th))
+
     def params(self, I_ext=0.0):
+        """The scalar parameters (an array-valued one takes a placeholder here)."""
         if self._cuba():
             raise NotImplementedError('the HH kernels implement COBA channels only')
         _, _, E, tau = self._channel_args()
-        return ops.hh_params(ENa=self.ENa, gNa=self.gNa, EK=self.EK, gK=self.gK, EL=self.EL,
-                             gL=self.gL, C=self.C, V_th=self.V_th, I_ext=I_ext, E_e=E[0],
+        sc = lambda v, d: d if isinstance(v, np.ndarray) else v   # noqa: E731
+        return ops.hh_params(ENa=sc(self.ENa, 0.), gNa=sc(self.gNa, 0.), EK=sc(self.EK, 0.),
+                             gK=sc(self.gK, 0.), EL=sc(self.EL, 0.), gL=sc(self.gL, 0.),
+                             C=sc(self.C, 1.), V_th=sc(self.V_th, 0.), I_ext=I_ext, E_e=E[0],
                              E_i=E[1], tau_e=tau[0], tau_i=tau[1], dt=environ.get_dt())
 
     def update(self, x=0.):
@@ -318,7 +337,8 @@ class HH(_COBANeuron, _Describable):
         I, arr = _ext_input(x, self.V.value)
         p = self.params(I)
         spk = ops.coba_hh_step(self.V.value, self.m.value, self.h.value, self.n.value, g[0],
-                               g[1], ins[0], ins[1], p, I_ext=arr)
+                               g[1], ins[0], ins[1], p, I_ext=arr,
+                               arrays=self._param_arrays(self.V.value))
         self._finish_channels(g)
         self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value

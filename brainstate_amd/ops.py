@@ -599,6 +599,22 @@ def _input_array(I_ext, V):
 _LIF_ARRAYS = ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'ref_steps')
 
 
+_HH_ARRAYS = ('ENa', 'gNa', 'EK', 'gK', 'EL', 'gL', 'inv_C', 'V_th')
+
+
+def hh_arrays(V, **arrays):
+    """Per-neuron HH parameters for ``coba_hh_step(..., arrays=)`` (any of ENa, gNa, EK, gK,
+    EL, gL, inv_C, V_th), fp32 and broadcast to V's shape on V's device."""
+    out = {}
+    for k, v in arrays.items():
+        if k not in _HH_ARRAYS:
+            raise ValueError(f'unknown per-neuron HH parameter {k!r}')
+        if v is not None:
+            t = torch.as_tensor(v, dtype=torch.float32, device=V.device)
+            out[k] = torch.broadcast_to(t, V.shape).contiguous()
+    return out
+
+
 def lif_arrays(V, **arrays):
     """Per-neuron LIF parameters for ``coba_lif_step(..., arrays=)``: each given value (any
     of V_rest, V_th, V_reset, inv_tau, R, ref_steps) broadcast to V's shape on V's device
@@ -639,15 +655,19 @@ def hh_init(V, m, h, n):
                                N.stream_handle(V.device)), 'bs_hh_init')
 
 
-def coba_hh_step(V, m, h, n, ge, gi, in_e, in_i, params, spk_out=None, I_ext=None):
-    """One COBA-HH step of every neuron; ``I_ext`` as in ``coba_lif_step``."""
+def coba_hh_step(V, m, h, n, ge, gi, in_e, in_i, params, spk_out=None, I_ext=None,
+                 arrays=None):
+    """One COBA-HH step of every neuron; ``I_ext`` and ``arrays`` (``hh_arrays``) as in
+    ``coba_lif_step`` (bs_coba_hh_step_arr)."""
     if spk_out is None:
         spk_out = torch.empty(V.numel(), dtype=torch.uint8, device=V.device)
     arr = _input_array(I_ext, V)
-    N.check(N.lib().bs_coba_hh_step_in(V.numel(), N.ptr(V), N.ptr(m), N.ptr(h), N.ptr(n),
-                                       N.ptr(ge), N.ptr(gi), N.ptr(in_e), N.ptr(in_i), N.ptr(arr),
-                                       ctypes_ref(params), N.ptr(spk_out),
-                                       N.stream_handle(V.device)), 'bs_coba_hh_step')
+    pa = N.HhArrays(*[N.ptr(arrays.get(k)) for k in _HH_ARRAYS]) if arrays else None
+    N.check(N.lib().bs_coba_hh_step_arr(V.numel(), N.ptr(V), N.ptr(m), N.ptr(h), N.ptr(n),
+                                        N.ptr(ge), N.ptr(gi), N.ptr(in_e), N.ptr(in_i),
+                                        N.ptr(arr), ctypes.byref(pa) if pa is not None else None,
+                                        ctypes_ref(params), N.ptr(spk_out),
+                                        N.stream_handle(V.device)), 'bs_coba_hh_step')
     return spk_out
 
 

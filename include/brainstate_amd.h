@@ -347,12 +347,24 @@ BS_API int bs_hh_init(int32_t n, const float* V, float* m, float* h, float* ng, 
 BS_API int bs_coba_hh_step(int32_t n, float* V, float* m, float* h, float* ng, float* ge, float* gi,
                     const float* in_e, const float* in_i, const bs_hh_params* p,
                     uint8_t* spk_out, bs_stream_t stream);
+/* Per-neuron HH parameters: each non-NULL array [n] replaces the scalar of bs_hh_params for
+ * its neuron (inv_C = fp32(1 / C)). */
+typedef struct {
+  const float* ENa; const float* gNa; const float* EK; const float* gK; const float* EL;
+  const float* gL; const float* inv_C; const float* V_th;
+} bs_hh_arrays;
+
 /* The same step with a per-neuron external input I_ext [n] (NULL: p->I_ext), as for an input
  * array passed to the HH neuron (examples/100_hh_neuron_model.py:72-93 with x of shape [n]). */
 BS_API int bs_coba_hh_step_in(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
                               float* gi, const float* in_e, const float* in_i,
                               const float* I_ext, const bs_hh_params* p, uint8_t* spk_out,
                               bs_stream_t stream);
+/* ... and with per-neuron parameters (arr NULL, or any of its arrays NULL: the scalars). */
+BS_API int bs_coba_hh_step_arr(int32_t n, float* V, float* m, float* h, float* ng, float* ge,
+                               float* gi, const float* in_e, const float* in_i,
+                               const float* I_ext, const bs_hh_arrays* arr,
+                               const bs_hh_params* p, uint8_t* spk_out, bs_stream_t stream);
 
 /* ---------------------------------------------------------------- whole-loop runners
  * Replace `brainstate.transform.for_loop(net.update, times)` over an E/I network

@@ -327,6 +327,45 @@ def test_hh_module_network_for_loop(bs):
         assert make_golden.sha(N.V.value.cpu().numpy()) == gold['final_V_sha256']
 
 
+def test_hh_module_network_per_neuron_parameters(bs):
+    """HH with array-valued gL, gK and V_th (one value per neuron): the eager steps
+    (bs_coba_hh_step_arr) equal the oracle given the same arrays; for_loop stays eager."""
+    import torch
+    print('[case] HH module net, per-neuron parameters', flush=True)
+    c = make_golden.HH_NET
+    T = 300
+    pe, pi, V0, p = make_golden.hh_net()
+    rs = np.random.RandomState(14)
+    gL = rs.uniform(0.02, 0.04, c['n']).astype(F)
+    gK = rs.uniform(30., 40., c['n']).astype(F)
+    V_th = rs.uniform(15., 25., c['n']).astype(F)
+    p.gL, p.gK, p.V_th = gL, gK, V_th
+    ref = network.run_coba_hh(V0, pe, pi, p, c['n_exc'], T)
+    with bs.environ.context(dt=0.05):
+        N = bs.nn.HH(c['n'], gL=gL, gK=gK, V_th=V_th, V_initializer=lambda s: V0)
+        E = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n_exc'], c['n'], c['k'], c['w_e'], seed=c['seed_e']),
+            syn=bs.nn.Expon.desc(c['n'], tau=5.), out=bs.nn.COBA.desc(E=0.), post=N)
+        I = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n'] - c['n_exc'], c['n'], c['k'], c['w_i'],
+                                      seed=c['seed_i']),
+            syn=bs.nn.Expon.desc(c['n'], tau=10.), out=bs.nn.COBA.desc(E=-80.), post=N)
+        bs.nn.init_all_states(N)
+        for m in (E.syn, I.syn):
+            m.init_state()
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            E(spk[:c['n_exc']])
+            I(spk[c['n_exc']:])
+            return N(c['I_ext'])
+        spikes = bs.transform.for_loop(step, torch.arange(T) * 0.05)
+        assert bs.transform.last_loop == 'eager'
+    assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'])
+    assert np.array_equal(N.V.value.cpu().numpy(), ref['V'])
+    assert ref['counts'].sum() > 50
+
+
 def test_for_loop_stays_eager_for_other_steps(bs):
     """A step whose input changes with time is not the runner's step: after its two recorded
     steps the loop goes on eagerly, and equals the loop stepped eagerly from the start."""
