@@ -23,7 +23,7 @@ class LifParams(ctypes.Structure):
     _fields_ = [(n, c_f32) for n in ('V_rest', 'V_th', 'V_reset', 'inv_tau', 'R', 'I_ext', 'E_e',
                                        'E_i', 'dt', 'decay_e', 'decay_i')] + [
         ('ref_steps', c_i32), ('cuba', c_i32), ('scale_e', c_f32), ('scale_i', c_f32),
-        ('soft_reset', c_i32)]
+        ('soft_reset', c_i32), ('deferred_reset', c_i32)]
 
 
 class HhParams(ctypes.Structure):

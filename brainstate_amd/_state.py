@@ -7,6 +7,8 @@ State here is a named, mutable handle on device memory.
 """
 import torch
 
+from . import _trace
+
 
 class State:
     __module__ = 'brainstate_amd'
@@ -17,10 +19,16 @@ class State:
 
     @property
     def value(self):
+        tr = _trace._active.trace
+        if tr is not None:   # a for_loop recording pass (brainstate_amd/_trace.py)
+            return tr.read(self, self._value)
         return self._value
 
     @value.setter
     def value(self, v):
+        tr = _trace._active.trace
+        if tr is not None:
+            tr.write(self)
         if isinstance(v, State):
             raise ValueError('Cannot assign a State object to State.value; assign its value.')
         old = self._value
@@ -33,6 +41,9 @@ class State:
         return self._name
 
     def restore_value(self, v):
+        tr = _trace._active.trace
+        if tr is not None:
+            tr.write(self)
         self._value = v
 
     def __repr__(self):

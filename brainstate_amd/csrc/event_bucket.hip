@@ -12,10 +12,11 @@
 // contiguous but sorted by bucket (stable: original order inside a bucket), with the target
 // stored as a 16-bit offset inside its bucket; seg[i][b] is where row i's bucket-b synapses
 // start and seg[i][nb] where its valid synapses end (out-of-range targets follow and are
-// never read).  The build also fixes a fixed-point exponent S = 30 - e_w from max|w| < 2^e_w:
-// every weight rounded to a multiple of 2^-S is an integer of at most 2^30 in magnitude, formed
-// exactly in fp32 (ldexp, round to nearest even, convert), and 64-bit sums of them cannot
-// overflow below 2^33 events per output.
+// never read).  The build also fixes a fixed-point exponent S = min(30 - e_w - e_d, 100) from
+// max|w| < 2^e_w and the largest in-degree D <= 2^e_d -- the persistent runner's rule, so an
+// E/I step run through this operator adds the same integers as the runner -- : every weight
+// rounded to a multiple of 2^-S is an integer below 2^(30 - e_d) in magnitude, formed exactly
+// in fp32 (ldexp, round to nearest even, convert), and every output's sum is below 2^30.
 //
 // Step (bs_event_bucket_f32): workgroup (b, r) owns bucket b and the pre rows of row group r.
 // It compacts the active rows of its group into LDS (ballots), loads their bucket-b bounds,
@@ -167,23 +168,54 @@ __global__ __launch_bounds__(kBB) void k_bucket_place(int32_t n_pre, const int32
   }
 }
 
-__global__ void k_u32_zero(uint32_t* p) { *p = 0u; }
+// Valid synapses onto each post (per-synapse weights: the D of the exponent rule below).
+__global__ __launch_bounds__(kBB) void k_bucket_indeg(int32_t n_pre, const int32_t* indptr,
+                                                      const int32_t* indices, int32_t k,
+                                                      int32_t n_post, uint32_t* deg) {
+  const int64_t s0 = indptr ? (int64_t)indptr[0] : 0;
+  const int64_t s1 = indptr ? (int64_t)indptr[n_pre] : (int64_t)n_pre * k;
+  for (int64_t s = s0 + (int64_t)blockIdx.x * kBB + threadIdx.x; s < s1;
+       s += (int64_t)gridDim.x * kBB) {
+    const int32_t t = indices[s];
+    if ((uint32_t)t < (uint32_t)n_post) atomicAdd(&deg[t], 1u);
+  }
+}
 
-// S = 30 - e_w with max|w| < 2^e_w: every rounded weight fits int32 (|w| * 2^S < 2^30), so the
-// step rounds it exactly with three fp32 operations (measured against the former 64-bit rule,
-// S = 60 - e_w - e_n rounded through double precision: config [2] 9.93 -> 9.74 / 19.57 ->
-// 19.25 / 30.16 -> 29.88 us at p = 0.001 / 0.01 / 0.1).  -1000 flags a non-finite weight; 0
-// when every weight is 0.
-__global__ void k_bucket_qexp(const uint32_t* wmax, int64_t nnz_fixed, const int32_t* indptr,
-                              int32_t n_pre, int32_t* qexp) {
+__global__ void k_u32_fill0(uint32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// The persistent runner's exponent rule, so that a projection stepped through this operator
+// and the same projection inside the runner add the same integers: with W = max|w| over the
+// valid synapses, W < 2^e_w (e_w from W's exponent field, -126 for a zero or subnormal W),
+// and D = the largest number of valid synapses onto one post, D <= 2^e_d,
+// S = min(30 - e_w - e_d, 100).  Every rounded weight is then an integer below 2^(30 - e_d)
+// in magnitude, formed exactly in fp32 (ldexp, round to nearest even, convert), and every
+// output's sum stays below 2^30 + D/2 (the runner sums in 32 bits, this operator in 64).
+// -1000 flags a non-finite weight (or S < -100: weights too large for fixed point).
+// One workgroup.
+__global__ __launch_bounds__(kBB) void k_bucket_qexp(const uint32_t* wmax, const uint32_t* deg,
+                                                     int32_t n_post, int32_t* qexp) {
+  __shared__ uint32_t s_max[kBB / BS_WAVE];
+  uint32_t m = 0u;
+  for (int64_t j = threadIdx.x; j < n_post; j += kBB) m = deg[j] > m ? deg[j] : m;
+  for (int o = BS_WAVE / 2; o > 0; o >>= 1) {
+    const uint32_t v = (uint32_t)__shfl_xor((int)m, o);
+    m = v > m ? v : m;
+  }
+  if (bs_lane() == 0) s_max[threadIdx.x / BS_WAVE] = m;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  uint32_t D = 0u;
+  for (int w = 0; w < kBB / BS_WAVE; ++w) D = s_max[w] > D ? s_max[w] : D;
   const uint32_t bits = *wmax;
-  if (bits >= 0x7F800000u) { *qexp = -1000; return; }
-  if (bits == 0u) { *qexp = 0; return; }
-  (void)nnz_fixed;
-  (void)indptr;
-  (void)n_pre;
-  const int e_w = ilogbf(__uint_as_float(bits)) + 1;
-  *qexp = 30 - e_w;
+  const int e_w = (bits >> 23) ? (int)(bits >> 23) - 126 : -126;
+  const int e_d = D <= 1u ? 0 : 32 - __clz(D - 1u);
+  int S = 30 - e_w - e_d;
+  if (S > 100) S = 100;
+  *qexp = (bits >= 0x7F800000u || S < -100) ? -1000 : S;
 }
 
 // ---- step ----
@@ -946,7 +978,8 @@ extern "C" int bs_bucket_build(int32_t n_pre, const int32_t* indptr, const int32
   BS_CHECK_ARG((w == nullptr) == (lw == nullptr),
                "bs_bucket_build: w and lw must both be given or both be NULL");
   BS_CHECK_ARG(w == nullptr || (qexp != nullptr && workspace != nullptr),
-               "bs_bucket_build: per-synapse weights need qexp and a 4-byte workspace");
+               "bs_bucket_build: per-synapse weights need qexp and a workspace of "
+               "4 * (n_post + 1) bytes");
   if (n_pre == 0) return BS_OK;
   BS_CHECK_ARG(seg != nullptr, "bs_bucket_build: seg is NULL");
   const bool any = indptr != nullptr || k > 0;
@@ -958,24 +991,27 @@ extern "C" int bs_bucket_build(int32_t n_pre, const int32_t* indptr, const int32
                                           P, seg);
   BS_CHECK_LAUNCH();
   if (!any) {
-    if (w) {
-      k_u32_zero<<<1, 1, 0, s>>>((uint32_t*)workspace);
+    if (w) {  // no synapse: W = 0, D = 0
+      k_u32_fill0<<<1, 256, 0, s>>>((uint32_t*)workspace, 1);
       BS_CHECK_LAUNCH();
-      k_bucket_qexp<<<1, 1, 0, s>>>((uint32_t*)workspace, 0, nullptr, n_pre, qexp);
+      k_bucket_qexp<<<1, kBB, 0, s>>>((uint32_t*)workspace, nullptr, 0, qexp);
       BS_CHECK_LAUNCH();
     }
     return BS_OK;
   }
   uint32_t* wmax = (uint32_t*)workspace;
+  uint32_t* deg = wmax + 1;  // [n_post] valid synapses onto each post
   if (w) {
-    k_u32_zero<<<1, 1, 0, s>>>(wmax);
+    k_u32_fill0<<<256, 256, 0, s>>>(wmax, (int64_t)n_post + 1);
+    BS_CHECK_LAUNCH();
+    k_bucket_indeg<<<2048, kBB, 0, s>>>(n_pre, indptr, indices, k, n_post, deg);
     BS_CHECK_LAUNCH();
   }
   k_bucket_place<<<(int)g, kBB, shm, s>>>(n_pre, indptr, indices, w, k, n_post, nb, P, seg, lidx,
                                           lw, w ? wmax : nullptr);
   BS_CHECK_LAUNCH();
   if (w) {
-    k_bucket_qexp<<<1, 1, 0, s>>>(wmax, (int64_t)n_pre * k, indptr, n_pre, qexp);
+    k_bucket_qexp<<<1, kBB, 0, s>>>(wmax, deg, n_post, qexp);
     BS_CHECK_LAUNCH();
   }
   return BS_OK;
@@ -1009,7 +1045,9 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
   BS_CHECK_ARG(mode >= 0 && mode <= 2, "bs_event_bucket_f32: mode %d outside [0, 2]", mode);
   const int32_t Rmax = row_groups(n_pre, nb);
   const bool single_launch = mode == 1;
-  const bool dense = mode == 2;
+  // the fixed-grid kernel only writes partials: with a single row group (Rmax = 1) there is
+  // nothing for the reduce to add, so that case runs as mode 0, whose one group writes out
+  const bool dense = mode == 2 && Rmax > 1;
   const int32_t R = single_launch ? 1 : Rmax;  // one group per bucket: no partials, no reduce
   // single launch: each bucket's posts split over nsub workgroups (every one scans the spikes
   // and the bucket's synapses, and adds and writes only its slice)

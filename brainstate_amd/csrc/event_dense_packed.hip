@@ -516,6 +516,8 @@ extern "C" int bs_event_dense_packed_lif_step(const void* spk, int32_t spk_dtype
   bs_clear_error();
   const char* fn = "bs_event_dense_packed_lif_step";
   BS_CHECK_ARG(p != nullptr, "%s: params are NULL", fn);
+  BS_CHECK_ARG(!p->deferred_reset, "%s: deferred_reset is not supported by the fused step "
+               "(use bs_event_dense_packed_f32 and bs_coba_lif_step)", fn);
   BS_CHECK_ARG((int64_t)batch * n_out <= 0 || (V && ge && gi && ref), "%s: NULL state pointer",
                fn);
   // Workgroups of other column tiles read the spikes of a batch row while one writes that

@@ -75,6 +75,7 @@ struct NetLayout {
   uint64_t off_ofs;    // uint64 [nb dst][nb src] + 1  inbox entry offsets (dst-major)
   uint64_t off_part;   // uint32 [2][kRunSteps][nb]  per-workgroup spike counts / hashes
   uint64_t off_deg;    // uint32 [2][n]  in-degree per kind (prepare, per-synapse weights)
+  uint64_t off_vprev;  // fp32 [n]  V before a run's last step (deferred reset)
   uint64_t off_inbox;  // entries [R][total]
   uint64_t bytes;
 };
@@ -942,6 +943,8 @@ int plan(const bs_net* net, NetLayout* L) {
   o = align256(o + (size_t)2 * kRunSteps * nb * sizeof(uint32_t));
   L->off_deg = o;
   if (net->w_e) o = align256(o + (size_t)2 * net->n * sizeof(uint32_t));
+  L->off_vprev = o;
+  o = align256(o + (size_t)net->n * sizeof(float));
   L->off_inbox = o;
   o = align256(o + (size_t)L->ring * L->total * L->entry);
   L->bytes = o;
@@ -1156,6 +1159,79 @@ extern "C" int bs_net_seed_spikes(const bs_net* net, const uint8_t* spk, int64_t
   return BS_OK;
 }
 
+namespace {
+
+// Deferred reset around a run (bs_lif_params.deferred_reset): the state handed over keeps
+// V' >= V_th for the neurons that spiked in the step before the run (their spikes in
+// net->spk), so those are reset first, with the update's own reset arithmetic.
+template <bool kSoft>
+__global__ __launch_bounds__(256) void k_lif_defer_in(int32_t n, float* V, const uint8_t* spk,
+                                                      bs_lif_params p) {
+  for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * 256)
+    if (spk[j]) V[j] = bs_lif_reset<kSoft>(p, V[j]);
+}
+
+// ... and after it, each neuron that spiked in the last step gets back its V' of that step:
+// the update's membrane step from its V before the step (vprev) and its conductances after
+// it, the same operations (bs_lif_vnext) the runner applied before resetting.
+template <bool kCuba>
+__global__ __launch_bounds__(256) void k_lif_defer_out(int32_t n, float* V, const float* vprev,
+                                                       const float* ge, const float* gi,
+                                                       const uint8_t* spk, const float* iext,
+                                                       bs_lif_params p) {
+  for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < n;
+       j += (int64_t)gridDim.x * 256) {
+    if (!spk[j]) continue;
+    bs_lif_params q = p;
+    if (iext) q.I_ext = iext[j];
+    V[j] = bs_lif_vnext<kCuba>(q, vprev[j], ge[j], gi[j]);
+  }
+}
+
+template <bool kCuba, bool kSoft>
+int lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p, int64_t t0,
+            int32_t steps, int32_t* counts_out, uint32_t* hash_out, uint8_t* raster_out,
+            void* workspace, bs_stream_t stream) {
+  const char* who = "bs_coba_lif_run";
+  if (!p || !p->deferred_reset || steps <= 0)
+    return run<LifModel<kCuba, kSoft>>(net, st, p, t0, steps, counts_out, hash_out, raster_out,
+                                       workspace, stream, who);
+  int rc = check_net(net, who);
+  if (rc) return rc;
+  BS_CHECK_ARG(st && workspace, "%s: NULL state/workspace", who);
+  NetLayout L;
+  if (plan(net, &L)) {
+    bs_set_error("%s: n=%d needs more than %d neurons per thread", who, net->n, kMaxNpt);
+    return BS_ERR_UNSUPPORTED;
+  }
+  hipStream_t s = bs_stream(stream);
+  const int g = (int)((net->n + 255) / 256 < 2048 ? (net->n + 255) / 256 : 2048);
+  k_lif_defer_in<kSoft><<<g, 256, 0, s>>>(net->n, st->V, net->spk, *p);
+  BS_CHECK_LAUNCH();
+  // all but the last step, then V before it, then the last step
+  if (steps > 1) {
+    rc = run<LifModel<kCuba, kSoft>>(net, st, p, t0, steps - 1, counts_out, hash_out,
+                                     raster_out, workspace, stream, who);
+    if (rc) return rc;
+  }
+  float* vprev = (float*)((char*)workspace + L.off_vprev);
+  BS_CHECK_HIP(hipMemcpyAsync(vprev, st->V, (size_t)net->n * sizeof(float),
+                              hipMemcpyDeviceToDevice, s));
+  const int64_t k = steps - 1;
+  rc = run<LifModel<kCuba, kSoft>>(net, st, p, t0 + k, 1, counts_out ? counts_out + k : nullptr,
+                                   hash_out ? hash_out + k : nullptr,
+                                   raster_out ? raster_out + k * net->n : nullptr, workspace,
+                                   stream, who);
+  if (rc) return rc;
+  k_lif_defer_out<kCuba><<<g, 256, 0, s>>>(net->n, st->V, vprev, st->ge, st->gi, net->spk,
+                                           net->I_ext, *p);
+  BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+}  // namespace
+
 extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p,
                                int64_t t0, int32_t steps, int32_t* counts_out,
                                uint32_t* hash_out, uint8_t* raster_out, void* workspace,
@@ -1166,8 +1242,8 @@ extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const 
   }
   if (p) BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_run: inv_tau is NaN");
 #define BS_RUN(C, S)                                                                    \
-  return run<LifModel<C, S>>(net, st, p, t0, steps, counts_out, hash_out, raster_out,      \
-                             workspace, stream, "bs_coba_lif_run")
+  return lif_run<C, S>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,  \
+                       stream)
   const bool cuba = p && p->cuba, soft = p && p->soft_reset;
   if (cuba) { if (soft) BS_RUN(true, true); else BS_RUN(true, false); }
   if (soft) BS_RUN(false, true);

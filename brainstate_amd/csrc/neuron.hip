@@ -32,8 +32,14 @@ __global__ __launch_bounds__(kBlock) void k_lif_step(int32_t n, float* __restric
     if (pa.inv_tau) q.inv_tau = pa.inv_tau[j];
     if (pa.R) q.R = pa.R[j];
     if (pa.ref_steps) q.ref_steps = pa.ref_steps[j];
-    const bool s =
-        bs_lif_update<kCuba, kSoft>(q, v, e, i, r, in_e ? in_e[j] : 0.0f, in_i ? in_i[j] : 0.0f);
+    const float xe = in_e ? in_e[j] : 0.0f, xi = in_i ? in_i[j] : 0.0f;
+    bool s;
+    if (p.deferred_reset) {  // spk holds the previous step's spikes: their reset comes first
+      if (spk[j]) v = bs_lif_reset<kSoft>(q, v);
+      s = bs_lif_update<kCuba, kSoft, true>(q, v, e, i, r, xe, xi);
+    } else {
+      s = bs_lif_update<kCuba, kSoft, false>(q, v, e, i, r, xe, xi);
+    }
     V[j] = v;
     ge[j] = e;
     gi[j] = i;
@@ -140,6 +146,9 @@ extern "C" int bs_coba_lif_step_arr(int32_t n, float* V, float* ge, float* gi, i
   BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_step: inv_tau is NaN");
   if (n == 0) return BS_OK;
   BS_CHECK_ARG(V && ge && gi && ref, "bs_coba_lif_step: NULL state pointer");
+  BS_CHECK_ARG(!p->deferred_reset || spk_out != nullptr,
+               "bs_coba_lif_step: deferred_reset reads the previous spikes from spk_out, "
+               "which is NULL");
   hipStream_t s = bs_stream(stream);
 #define BS_LIF(C, S) \
   k_lif_step<C, S><<<grid(n), kBlock, 0, s>>>(n, V, ge, gi, ref, in_e, in_i, I_ext, pa, *p, \

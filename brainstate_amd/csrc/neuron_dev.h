@@ -11,16 +11,18 @@
 #include "bs_math.h"
 #include "common.h"
 
-// brainpy.state Expon + COBA (kCuba: CUBA) + LIFRef for one neuron; see bs_lif_params in the
-// header.  Returns the spike; updates V, ge, gi, ref in place.  The CUBA current does not
-// depend on V, so the exp-Euler Jacobian is -1 * inv_tau.  kSoft: a spike subtracts
-// V_th - V_reset from V' (p.soft_reset) instead of setting V_reset.  Both are compile-time
-// choices so that the persistent runner's update carries no per-neuron selects.
-template <bool kCuba = false, bool kSoft = false>
-__device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, float& ge,
-                                              float& gi, int32_t& ref, float in_e, float in_i) {
-  ge = bs_fma(ge, p.decay_e, in_e);
-  gi = bs_fma(gi, p.decay_i, in_i);
+// V after a spike: V_reset (hard reset) or V' - (V_th - V_reset) (kSoft: subtractive).
+template <bool kSoft>
+__device__ __forceinline__ float bs_lif_reset(const bs_lif_params& p, float v) {
+  return kSoft ? v - (p.V_th - p.V_reset) : p.V_reset;
+}
+
+// The exp-Euler membrane step V -> V' given the conductances after this step's update
+// (everything of bs_lif_update that V' depends on: V, ge', gi' and the parameters).  The CUBA
+// current does not depend on V, so the exp-Euler Jacobian is -1 * inv_tau.
+template <bool kCuba>
+__device__ __forceinline__ float bs_lif_vnext(const bs_lif_params& p, float V, float ge,
+                                              float gi) {
   float I, J;
   if constexpr (kCuba) {
     I = bs_fma(ge, p.scale_e, p.I_ext);
@@ -33,7 +35,20 @@ __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, 
   }
   const float f = bs_fma(p.R, I, p.V_rest - V) * p.inv_tau;
   const float phi = bs_exprel(p.dt * J);
-  float Vn = bs_fma(p.dt * phi, f, V);
+  return bs_fma(p.dt * phi, f, V);
+}
+
+// brainpy.state Expon + COBA (kCuba: CUBA) + LIFRef for one neuron; see bs_lif_params in the
+// header.  Returns the spike; updates V, ge, gi, ref in place.  kSoft: a spike subtracts
+// V_th - V_reset from V' (p.soft_reset) instead of setting V_reset.  kKeep: a spiking neuron
+// keeps V' (the reset is left to the start of its next step, p.deferred_reset).  All are
+// compile-time choices so that the persistent runner's update carries no per-neuron selects.
+template <bool kCuba = false, bool kSoft = false, bool kKeep = false>
+__device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, float& ge,
+                                              float& gi, int32_t& ref, float in_e, float in_i) {
+  ge = bs_fma(ge, p.decay_e, in_e);
+  gi = bs_fma(gi, p.decay_i, in_i);
+  float Vn = bs_lif_vnext<kCuba>(p, V, ge, gi);
   bool spk = false;
   if (ref > 0) {
     Vn = V;
@@ -41,7 +56,7 @@ __device__ __forceinline__ bool bs_lif_update(const bs_lif_params& p, float& V, 
   } else {
     spk = Vn >= p.V_th;
     if (spk) {
-      Vn = kSoft ? Vn - (p.V_th - p.V_reset) : p.V_reset;
+      if (!kKeep) Vn = bs_lif_reset<kSoft>(p, Vn);
       ref = p.ref_steps;
     } else {
       ref = 0;

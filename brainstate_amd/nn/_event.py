@@ -6,10 +6,11 @@
   fused HIP spike-vector event mat-vec (C ABI ``bs_event_matvec_f32``: per-workgroup
   compaction of the spike vector, then the pre-major scatter of the active rows) instead of
   brainevent's kernel.
-  With ``event_kernel='bucket'`` (or ``'auto'`` for outputs wider than 16,384 neurons), the
-  event path of inference runs the destination-bucketed operator instead
-  (``bs_event_bucket_f32``: no global or fp32 atomics, exact fixed-point sums, deterministic)
-  on a layout built on first use and rebuilt when the weight value changes.
+  With ``event_kernel='bucket'`` (or ``'auto'`` with per-synapse weights, or with a
+  homogeneous weight onto more than 16,384 neurons), the event path of inference runs the
+  destination-bucketed operator instead (``bs_event_bucket_f32``: no global or fp32 atomics,
+  exact fixed-point sums with the persistent runner's exponent, deterministic) on a layout
+  built on first use and rebuilt when the weight value changes.
 * ``EventLinear`` -- brainstate/nn/_event_linear.py:32-102, on ``bs_event_dense_f32``.
 
 Both are differentiable (torch autograd, reverse and forward mode) with the gradients the
@@ -116,11 +117,7 @@ def _no_autodiff(*ts):
     return True
 
 
-_BUCKET_AUTO_POSTS = 16384   # 'auto': bucketed above this many outputs (one LDS accumulator)
-# True while a loop records steps it may hand to the persistent runner: a homogeneous weight's
-# mat-vec then takes the one-launch kernel instead of building a bucketed layout the runner
-# does not use (same bits: w added once per event, every addend equal)
-defer_layouts = False
+_BUCKET_AUTO_POSTS = 16384   # 'auto', homogeneous weight: bucketed above this many outputs
 
 
 def _wants_grad(*ts):
@@ -293,16 +290,32 @@ class FixedNumConn(Module):
         x = x if torch.is_tensor(x) else _to_dev(x, torch.float32)
         if x.device.type != 'cuda':
             x = x.to(_device())
-        if not value and x.dim() == 1 and self._bucketed() and _no_autodiff(x, w) and \
-                not (defer_layouts and self._bucket is None and w.numel() == 1):
-            return ops.event_bucket(x, self._bucket_layout(w))
+        if not value and self._bucketed(w) and _no_autodiff(x, w):
+            L = self._bucket_layout(w)
+            if x.dim() == 1:
+                return ops.event_bucket(x, L)
+            # [..., n_pre] spikes: each row through the bucketed operator (the same sums as a
+            # replica inside the union runner)
+            rows = x.reshape(-1, x.shape[-1])
+            out = torch.empty(rows.shape[0], self.out_size[-1], dtype=torch.float32,
+                              device=x.device)
+            for b in range(rows.shape[0]):
+                ops.event_bucket(rows[b], L, out=out[b])
+            return out.reshape(tuple(x.shape[:-1]) + (self.out_size[-1],))
         conn = self.conn.with_data(w)
         return conn.matvec_events(x, value)   # [..., n_pre] -> [..., n_post], one launch
 
-    def _bucketed(self):
+    def _bucketed(self, w):
+        """'auto': per-synapse weights always take the bucketed operator -- its exact
+        fixed-point sums are those the persistent runner adds (same exponent rule), so an
+        eager step equals the fused one bit for bit and does not depend on the order of the
+        device's atomics -- and a homogeneous weight above 16,384 outputs (below, the atomic
+        kernel adds equal addends, whose sums do not depend on their order)."""
         if self.event_kernel == 'bucket':
             return True
-        return self.event_kernel == 'auto' and self.out_size[-1] > _BUCKET_AUTO_POSTS
+        if self.event_kernel != 'auto':
+            return False
+        return w.numel() > 1 or self.out_size[-1] > _BUCKET_AUTO_POSTS
 
     def _bucket_layout(self, w):
         """Destination-bucketed layout of the current connectivity and weight; rebuilt when the

@@ -12,7 +12,8 @@ projections read
 ceil(delay / dt) steps as brainstate's Delay computes them.  A net initialised with
 ``init_all_states(..., batch_size=B)`` ([B, n] states, the replicas sharing connectivity)
 becomes one runner over the block-diagonal union of the B replicas.  ``runner.write_back()``
-copies the state back into the modules.
+copies the state back into the modules; ``runner.set_input(x)`` changes the external input
+of the next run (``for_loop`` with an input that changes between runs of steps).
 """
 import numpy as np
 import torch
@@ -136,10 +137,24 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
             neuron.h.value = from_runner(r.state['h'])
             neuron.n.value = from_runner(r.state['n'])
 
+    def set_input(v):
+        """The external input of the next run: a number, or (a runner built with one input
+        per neuron) an array broadcast to the population's state shape."""
+        if I_arr is None:
+            if (torch.is_tensor(v) or isinstance(v, np.ndarray)) and np.prod(tuple(v.shape)) != 1:
+                raise ValueError('set_input: this runner takes one number per run (it was '
+                                 'built with a scalar input)')
+            r.params.I_ext = float(v.reshape(()).item() if torch.is_tensor(v) else
+                                   np.reshape(v, ()))
+        else:
+            r.I_ext.copy_(to_runner(torch.broadcast_to(
+                torch.as_tensor(v, dtype=torch.float32, device=Vs.device), Vs.shape)))
+
     if pending:   # the spikes of the last step drive the runner's first step
         r.seed(to_runner(neuron.spike.value.to(torch.uint8)), 1)
 
     r.write_back = write_back
+    r.set_input = set_input
     r.replica_index = perm   # runner neuron of (replica b, neuron j), for rasters
     r.replica_identity = B == 1   # replica_index is the identity
     r.dt = environ.get_dt()

@@ -12,6 +12,8 @@ from collections import OrderedDict
 
 import numpy as np
 
+from .. import _trace
+
 _calls = threading.local()
 
 
@@ -41,6 +43,9 @@ class Module:
         self.name = name
 
     def __call__(self, *args, **kwargs):
+        tr = _trace._active.trace
+        if tr is not None:   # a for_loop recording pass: logged, not run
+            return tr.call(self, args, kwargs)
         log = getattr(_calls, 'log', None)
         if log is None:
             return self._run(*args, **kwargs)

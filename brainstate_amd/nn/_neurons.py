@@ -187,51 +187,98 @@ def _ext_input(x, V):
     return float(x), None
 
 
-def _scalar_or_array(v):
-    """A neuron parameter: a float, or (more than one element) an fp32 numpy array."""
+def _scalar_or_array(v, dtype=np.float32):
+    """A neuron parameter: a float, or (more than one element) a numpy array of ``dtype``
+    (fp32, as the step computes; float64 for a refractory period, whose step count is taken
+    from the value given, as for a scalar)."""
     if torch.is_tensor(v):
         v = v.detach().cpu().numpy()
     a = np.asarray(v, np.float64)
-    return float(a.reshape(())) if a.size == 1 else a.astype(np.float32)
+    return float(a.reshape(())) if a.size == 1 else a.astype(dtype)
+
+
+class _ParamCache:
+    """The device arrays of a population's per-neuron parameters, built on first use and
+    kept until a parameter is assigned another value (object), dt changes or the state's
+    shape or device does (an array changed in place is not seen)."""
+
+    def __init__(self):
+        self.key = None
+        self.value = None
+
+    @staticmethod
+    def _same(a, b):
+        if isinstance(a, np.ndarray) or isinstance(b, np.ndarray):
+            return a is b   # the cache holds the arrays, so an id is not reused meanwhile
+        return type(a) is type(b) and a == b
+
+    def get(self, key, build):
+        if self.key is None or len(self.key) != len(key) or \
+                not all(self._same(a, b) for a, b in zip(self.key, key)):
+            self.value = build()
+            self.key = key
+        return self.value
 
 
 class LIFRef(_COBANeuron, _Describable):
     """Leaky integrate-and-fire with refractory period; ``spk_reset='hard'`` sets V_reset after
     a spike, ``'soft'`` subtracts V_th - V_reset.  ``ref_rule`` fixes how many steps tau_ref
     holds a neuron after its spike step: ``'open'`` those with k*dt < tau_ref, ``'closed'``
-    those with k*dt <= tau_ref (one more when tau_ref is a multiple of dt)."""
+    those with k*dt <= tau_ref (one more when tau_ref is a multiple of dt).
+
+    ``reset_timing``: ``'next'`` (default) applies the reset at the start of the neuron's next
+    update, as brainpy.state's neurons do (``last_V = V - (V_th - V_reset) * last_spk`` before
+    the update; the reference-held neuron of examples/203_braintrace_for_snns.py:173-176 does
+    the same): after a spike step ``V`` keeps the value that crossed ``V_th``, so ``V >=
+    V_th`` exactly where ``get_spike()`` is set.  ``'same'`` resets within the spike step
+    (BrainPy 2.x's LifRef): ``V`` reads ``V_reset`` right after it.  Spike trains and every
+    other state are identical either way."""
     __module__ = 'brainstate_amd.nn'
 
     def __init__(self, in_size, R=1., tau=5., tau_ref=5., V_th=1., V_reset=0., V_rest=0.,
-                 V_initializer=0., spk_reset='hard', ref_rule='open', name=None):
+                 V_initializer=0., spk_reset='hard', ref_rule='open', reset_timing='next',
+                 name=None):
         super().__init__(in_size, name=name)
         if spk_reset not in ('hard', 'soft'):
             raise ValueError(f"spk_reset must be 'hard' or 'soft', got {spk_reset!r}")
         if ref_rule not in ('open', 'closed'):
             raise ValueError(f"ref_rule must be 'open' or 'closed', got {ref_rule!r}")
+        if reset_timing not in ('next', 'same'):
+            raise ValueError(f"reset_timing must be 'next' or 'same', got {reset_timing!r}")
         self.spk_reset = spk_reset
         self.ref_rule = ref_rule
+        self.reset_timing = reset_timing
         # scalars, or arrays of the population's shape (one value per neuron; eager steps only)
-        self.R, self.tau, self.tau_ref = (_scalar_or_array(v) for v in (R, tau, tau_ref))
+        self.R, self.tau = (_scalar_or_array(v) for v in (R, tau))
+        self.tau_ref = _scalar_or_array(tau_ref, np.float64)
         self.V_th, self.V_reset, self.V_rest = (_scalar_or_array(v)
                                                 for v in (V_th, V_reset, V_rest))
         self.V_initializer = V_initializer
+        self._arrays = _ParamCache()
 
     def has_param_arrays(self):
         return any(isinstance(v, np.ndarray) for v in
                    (self.R, self.tau, self.tau_ref, self.V_th, self.V_reset, self.V_rest))
 
     def _param_arrays(self, V):
-        """Per-neuron parameters for the step kernel (None when every one is a scalar)."""
+        """Per-neuron parameters for the step kernel (None when every one is a scalar),
+        uploaded once and kept until a parameter is reassigned."""
         if not self.has_param_arrays():
             return None
+        dt = float(environ.get_dt())
+        key = (self.R, self.tau, self.tau_ref, self.V_th, self.V_reset, self.V_rest,
+               self.ref_rule, dt, tuple(V.shape), V.device)
+        return self._arrays.get(key, lambda: self._build_arrays(V, dt))
+
+    def _build_arrays(self, V, dt):
         arr = lambda v: v if isinstance(v, np.ndarray) else None   # noqa: E731
         inv_tau = None
         if isinstance(self.tau, np.ndarray):
             inv_tau = (np.float32(1.0) / self.tau).astype(np.float32)   # fp32 reciprocal
         ref_steps = None
         if isinstance(self.tau_ref, np.ndarray):
-            q = self.tau_ref.astype(np.float64) / float(environ.get_dt())
+            # ops.refractory_steps element-wise: the float64 value given over dt
+            q = self.tau_ref.astype(np.float64) / dt
             n = np.ceil(q - 1e-9) - 1 if self.ref_rule == 'open' else np.floor(q + 1e-9)
             ref_steps = np.maximum(n, 0).astype(np.int32)
         return ops.lif_arrays(V, V_rest=arr(self.V_rest), V_th=arr(self.V_th),
@@ -251,24 +298,27 @@ class LIFRef(_COBANeuron, _Describable):
         sc = lambda v, d: d if isinstance(v, np.ndarray) else v   # noqa: E731
         V_rest, V_th, V_reset = sc(self.V_rest, 0.0), sc(self.V_th, 0.0), sc(self.V_reset, 0.0)
         tau_m, R, tau_ref = sc(self.tau, 1.0), sc(self.R, 1.0), sc(self.tau_ref, 0.0)
+        deferred = self.reset_timing == 'next'
         if self._cuba():
             return ops.lif_params(V_rest=V_rest, V_th=V_th, V_reset=V_reset,
                                   tau=tau_m, R=R, tau_ref=tau_ref, I_ext=I_ext,
                                   tau_e=tau[0], tau_i=tau[1], dt=environ.get_dt(),
                                   out='cuba', scale_e=E[0], scale_i=E[1],
-                                  spk_reset=self.spk_reset, ref_rule=self.ref_rule)
+                                  spk_reset=self.spk_reset, ref_rule=self.ref_rule,
+                                  deferred_reset=deferred)
         return ops.lif_params(V_rest=V_rest, V_th=V_th, V_reset=V_reset,
                               tau=tau_m, R=R, tau_ref=tau_ref, I_ext=I_ext,
                               E_e=E[0], E_i=E[1], tau_e=tau[0], tau_i=tau[1],
                               dt=environ.get_dt(), spk_reset=self.spk_reset,
-                              ref_rule=self.ref_rule)
+                              ref_rule=self.ref_rule, deferred_reset=deferred)
 
     def update(self, x=0.):
         g, ins, E, tau = self._channel_args()
         I, arr = _ext_input(x, self.V.value)
         p = self.params(I)
         spk = ops.coba_lif_step(self.V.value, g[0], g[1], self.ref.value, ins[0], ins[1], p,
-                                I_ext=arr, arrays=self._param_arrays(self.V.value))
+                                I_ext=arr, arrays=self._param_arrays(self.V.value),
+                                spk_prev=self.spike.value if p.deferred_reset else None)
         self._finish_channels(g)
         self.spike.value = spk.view(torch.bool).reshape(self.V.value.shape)
         return self.spike.value
@@ -279,10 +329,10 @@ class LIF(LIFRef):
     __module__ = 'brainstate_amd.nn'
 
     def __init__(self, in_size, R=1., tau=5., V_th=1., V_reset=0., V_rest=0., V_initializer=0.,
-                 spk_reset='hard', name=None):
+                 spk_reset='hard', reset_timing='next', name=None):
         super().__init__(in_size, R=R, tau=tau, tau_ref=0., V_th=V_th, V_reset=V_reset,
                          V_rest=V_rest, V_initializer=V_initializer, spk_reset=spk_reset,
-                         name=name)
+                         reset_timing=reset_timing, name=name)
 
 
 class HH(_COBANeuron, _Describable):
@@ -296,6 +346,7 @@ class HH(_COBANeuron, _Describable):
         self.ENa, self.gNa, self.EK, self.gK = (_scalar_or_array(v) for v in (ENa, gNa, EK, gK))
         self.EL, self.gL, self.V_th, self.C = (_scalar_or_array(v) for v in (EL, gL, V_th, C))
         self.V_initializer = V_initializer
+        self._arrays = _ParamCache()
 
     def init_state(self, batch_size=None, **kwargs):
         shape = _state_shape(self.num, batch_size)
@@ -311,9 +362,15 @@ class HH(_COBANeuron, _Describable):
                    (self.ENa, self.gNa, self.EK, self.gK, self.EL, self.gL, self.V_th, self.C))
 
     def _param_arrays(self, V):
-        """Per-neuron parameters for the step kernel (None when every one is a scalar)."""
+        """Per-neuron parameters for the step kernel (None when every one is a scalar),
+        uploaded once and kept until a parameter is reassigned."""
         if not self.has_param_arrays():
             return None
+        key = (self.ENa, self.gNa, self.EK, self.gK, self.EL, self.gL, self.V_th, self.C,
+               tuple(V.shape), V.device)
+        return self._arrays.get(key, lambda: self._build_arrays(V))
+
+    def _build_arrays(self, V):
         arr = lambda v: v if isinstance(v, np.ndarray) else None   # noqa: E731
         inv_C = (np.float32(1.0) / self.C).astype(np.float32) if isinstance(self.C, np.ndarray) \
             else None

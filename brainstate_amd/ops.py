@@ -305,7 +305,7 @@ def build_buckets(indices, n_post, w=None, w_homo=0.0, indptr=None, k=None):
         wt = torch.as_tensor(w, dtype=torch.float32, device=dev).contiguous().reshape(-1)
         lw = torch.empty(max(nnz, 1), dtype=torch.float32, device=dev)
         qexp = torch.zeros(1, dtype=torch.int32, device=dev)
-        scratch = torch.zeros(1, dtype=torch.int32, device=dev)
+        scratch = torch.empty(int(n_post) + 1, dtype=torch.int32, device=dev)  # W, in-degrees
     opt = lambda t: N.ptr(t) if t is not None else None
     N.check(N.lib().bs_bucket_build(int(n_pre), opt(ip), N.ptr(idx), int(k),
                                     N.ptr(wt) if w is not None else None, int(n_post), nb,
@@ -563,10 +563,12 @@ def refractory_steps(tau_ref, dt, rule='open'):
 
 def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., I_ext=20.,
                E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba', scale_e=1.,
-               scale_i=1., spk_reset='hard', ref_rule='open'):
+               scale_i=1., spk_reset='hard', ref_rule='open', deferred_reset=False):
     """bs_lif_params.  ``out='coba'``: synaptic current g * (E - V); ``out='cuba'``: g * scale
     (brainpy.state CUBA; E_e / E_i unused).  ``spk_reset='soft'``: a spike subtracts
-    V_th - V_reset from V instead of setting V_reset.  ``ref_rule``: refractory_steps."""
+    V_th - V_reset from V instead of setting V_reset.  ``ref_rule``: refractory_steps.
+    ``deferred_reset``: the reset is applied at the start of the neuron's next step (a
+    spiking neuron keeps V' >= V_th until then; the step reads the previous spikes)."""
     if out not in ('coba', 'cuba'):
         raise ValueError(f"out must be 'coba' or 'cuba', got {out!r}")
     if spk_reset not in ('hard', 'soft'):
@@ -577,7 +579,7 @@ def lif_params(V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5., 
                        float(np.float32(np.exp(-dt / tau_e))),
                        float(np.float32(np.exp(-dt / tau_i))), ref_steps,
                        1 if out == 'cuba' else 0, scale_e, scale_i,
-                       1 if spk_reset == 'soft' else 0)
+                       1 if spk_reset == 'soft' else 0, 1 if deferred_reset else 0)
 
 
 def hh_params(ENa=50., gNa=120., EK=-77., gK=36., EL=-54.387, gL=0.03, C=1.0, V_th=20.,
@@ -631,12 +633,22 @@ def lif_arrays(V, **arrays):
     return out
 
 
-def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None, I_ext=None, arrays=None):
+def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None, I_ext=None, arrays=None,
+                  spk_prev=None):
     """One COBA/CUBA-LIF step of every neuron; ``I_ext`` (optional, broadcast to V) is each
     neuron's external input in place of ``params.I_ext``; ``arrays`` (``lif_arrays``) per-neuron
-    parameters in place of the scalars (bs_coba_lif_step_arr)."""
+    parameters in place of the scalars (bs_coba_lif_step_arr).  With
+    ``params.deferred_reset`` the previous step's spikes (``spk_prev``, or those ``spk_out``
+    holds; none when neither is given) are reset first, and the new spikes are returned in a
+    new tensor unless ``spk_out`` is given."""
     n = V.numel()
-    if spk_out is None:
+    if params.deferred_reset:
+        if spk_out is None:
+            spk_out = (torch.zeros(n, dtype=torch.uint8, device=V.device) if spk_prev is None
+                       else spk_prev.reshape(-1).to(torch.uint8).clone())
+        elif spk_prev is not None:
+            spk_out.copy_(spk_prev.reshape(-1))
+    elif spk_out is None:
         spk_out = torch.empty(n, dtype=torch.uint8, device=V.device)
     arr = _input_array(I_ext, V)
     pa = None

@@ -2,11 +2,14 @@
 
 The reference traces the step function once and runs it as an XLA While loop
 (brainstate/transform/_loop_collect_return.py:487-572).  Here each step launches the HIP
-kernels directly; ``for_loop`` recognises the E/I network step from the module calls of its
-first two steps and runs the rest of the loop in the persistent runner (one launch).
+kernels directly; ``for_loop`` records the step function without running it
+(brainstate_amd/_trace.py) and, when every step is the E/I network step, runs the loop in the
+persistent runner.
 """
 import numpy as np
 import torch
+
+from . import _trace
 
 
 def _stack(outs):
@@ -125,21 +128,27 @@ class _Bar:
             self.bar.close()
 
 
-def _ei_step(log, spk_before=None):
-    """The E/I step the persistent runner runs, read off the module calls one step made:
-    ``(neuron, proj_e, proj_i, n_exc, inp)`` when they were exactly the two projections onto
-    one LIFRef / HH population, each given spikes of the population's shape (E: its first
-    n_exc neurons, I: the rest) -- equal to ``spk_before``, its spikes before the step, when
-    given -- then that population with one constant input (a scalar, or an array of the
-    population's state shape, one input per neuron); else None."""
+def _ei_structure(tr, calls, out):
+    """The E/I step the persistent runner runs, read off one recorded step (``_trace``):
+    ``(neuron, proj_e, proj_i, n_exc, inp, raster_dtype)`` when the step made exactly the two
+    projection calls onto one LIFRef / HH population, each given a spike vector of that
+    population (E: its first n_exc neurons, I: the rest; the population's spike State read
+    outside the modules, sliced, compared with 0 or converted), then called the population
+    with one input, and returned the population's spikes (the call's result or its spike
+    State, as a spike vector) or nothing; else None.  ``inp`` is a number, a tensor or array
+    of the population's state shape (one input per neuron), or a ``StepArg`` (the loop's
+    per-step argument itself); ``raster_dtype`` the dtype of the stacked output (None: no
+    output)."""
     from .nn._event import FixedPostNumConn
     from .nn._neurons import HH, AlignPostProj, LIFRef
-    if len(log) != 3:
+    if len(calls) != 3:
         return None
-    (pa, aa, ka), (pb, ab, kb), (neuron, an, kn) = log
+    (pa, aa, ka), (pb, ab, kb), (neuron, an, kn) = calls
     if not isinstance(neuron, (LIFRef, HH)) or ka or kb or kn or len(an) > 1:
         return None
     if getattr(neuron, 'has_param_arrays', lambda: False)():   # the runner's are scalars
+        return None
+    if neuron.before_updates or neuron.after_updates:   # e.g. a delay recording the neuron
         return None
     chans = getattr(neuron, '_channels', [])
     if len(chans) != 2 or {id(pa), id(pb)} != {id(c) for c in chans}:
@@ -153,118 +162,237 @@ def _ei_step(log, spk_before=None):
     n, n_exc = neuron.num, conns[0].shape[0]
     if conns[0].shape != (n_exc, n) or conns[1].shape != (n - n_exc, n):
         return None
-    shape = tuple(neuron.spike.value.shape)
+    spike = neuron.spike
+    shape = tuple(spike._value.shape)
     given = {id(pa): aa, id(pb): ab}
     for proj, lo, hi in ((proj_e, 0, n_exc), (proj_i, n_exc, n)):
         args = given[id(proj)]
-        if len(args) != 1 or not torch.is_tensor(args[0]) or \
+        if len(args) != 1 or not torch.is_tensor(args[0]):
+            return None
+        m = tr.marks.get(id(args[0]))
+        if m is None or m.state is not spike or (m.lo, m.hi) != (lo, hi) or \
                 tuple(args[0].shape) != shape[:-1] + (hi - lo,):
             return None
-        if spk_before is not None and not torch.equal(args[0] != 0, spk_before[..., lo:hi] != 0):
+    # the step's output: the population's call or its full spike vector, or nothing
+    if out is None:
+        raster_dtype = None
+    elif isinstance(out, _trace.DryOut):
+        if out.index != 2:
             return None
+        raster_dtype = spike._value.dtype   # the neuron returns its spike State's value
+    elif torch.is_tensor(out) and id(out) in tr.marks:
+        m = tr.marks[id(out)]
+        if m.state is not spike or (m.lo, m.hi) != (0, n) or tuple(out.shape) != shape:
+            return None
+        raster_dtype = out.dtype
+    else:
+        return None
     inp = an[0] if an else 0.0
+    if isinstance(inp, _trace.StepArg):
+        return neuron, proj_e, proj_i, n_exc, inp, raster_dtype
+    inp = _input_value(inp, neuron)
+    if inp is None:
+        return None
+    return neuron, proj_e, proj_i, n_exc, inp, raster_dtype
+
+
+def _input_value(inp, neuron):
+    """A neuron input as the runner takes it: a float, or an fp32 device tensor of the
+    population's state shape; None when it is neither (or depends on marked state)."""
     if isinstance(inp, np.ndarray):
         inp = torch.as_tensor(inp)
     if torch.is_tensor(inp):
-        if inp.numel() != 1:
-            if not torch.is_floating_point(inp) and inp.dtype not in (torch.int32, torch.int64):
+        tr = _trace.active()
+        if tr is not None and id(inp) in tr.marks:
+            return None
+        if inp.numel() == 1:
+            return float(inp.reshape(()).item())
+        if not torch.is_floating_point(inp) and inp.dtype not in (torch.int32, torch.int64):
+            return None
+        shape = tuple(neuron.V._value.shape)
+        try:   # one input per neuron: must broadcast to the population's state shape
+            if tuple(torch.broadcast_shapes(tuple(inp.shape), shape)) != shape:
                 return None
-            shape = tuple(neuron.V.value.shape)
-            try:   # one input per neuron: must broadcast to the population's state shape
-                if tuple(torch.broadcast_shapes(tuple(inp.shape), shape)) != shape:
-                    return None
-            except RuntimeError:
-                return None
-            return neuron, proj_e, proj_i, n_exc, inp.detach().to(torch.float32).clone()
-        inp = inp.item()
-    if not isinstance(inp, (int, float, np.floating, np.integer)):
+        except RuntimeError:
+            return None
+        return inp
+    if isinstance(inp, (bool, np.bool_)) or not isinstance(inp, (int, float, np.floating,
+                                                                  np.integer)):
         return None
-    return neuron, proj_e, proj_i, n_exc, float(inp)
+    return float(inp)
 
 
 def _same_input(a, b):
     if torch.is_tensor(a) or torch.is_tensor(b):
-        return (torch.is_tensor(a) and torch.is_tensor(b) and a.shape == b.shape and
-                a.device == b.device and torch.equal(a, b))
+        if not (torch.is_tensor(a) and torch.is_tensor(b)):
+            return False
+        if a is b:
+            return True
+        return a.shape == b.shape and a.device == b.device and bool(torch.equal(a, b))
     return a == b
 
 
-def _fused_loop(f, xs, length):
-    """for_loop through the persistent runner.  Steps 0 and 1 run eagerly while their module
-    calls are recorded; when both are the same E/I step (``_ei_step``; step 1 checked against
-    the population's spikes before it), with the same constant input and with the
-    population's spikes (or nothing) as the step's output, the runner advances the other
-    steps in one launch from the state the eager steps left -- pending spikes included -- and
-    writes the final state back.  Returns (outputs of the eager steps, the stacked output of
-    all steps or None when the loop must go on eagerly)."""
-    from .nn import _event, _module
-    from .nn._fuse import fuse
-    outs, steps = [], []
-    for i in range(2):
-        before = steps[0][0].spike.value.clone() if steps else None
-        _event.defer_layouts = True
+_MAX_INPUT_BYTES = 1 << 30   # per-step input arrays a recorded loop may hold
+
+
+def _schedule(xs, j, length, neuron):
+    """Per-step inputs when the step passes its j-th argument straight to the population:
+    [(first step, steps, input)] with equal consecutive inputs merged; None when an input is
+    not one the runner takes."""
+    x = xs[j]
+    if torch.is_tensor(x) or isinstance(x, np.ndarray):
+        t = torch.as_tensor(x)
+        if t.shape[0] < length:
+            return None
+        t = t[:length]
+        if t.dim() == 1 or int(np.prod(tuple(t.shape[1:]))) == 1:   # one number per step
+            if not (torch.is_floating_point(t) or t.dtype in (torch.int32, torch.int64)):
+                return None
+            v = t.reshape(length).detach().cpu().to(torch.float64).numpy()
+            cut = np.flatnonzero(v[1:] != v[:-1]) + 1
+            starts = np.concatenate([[0], cut]).astype(np.int64)
+            ends = np.concatenate([cut, [length]]).astype(np.int64)
+            return [(int(a), int(b - a), float(v[a])) for a, b in zip(starts, ends)]
+        vals = [_input_value(t[i], neuron) for i in range(length)]
+    else:
+        vals = [_input_value(x[i], neuron) for i in range(length)]
+    return _merge(vals)
+
+
+def _merge(vals):
+    segs = []
+    for i, v in enumerate(vals):
+        if v is None:
+            return None
+        if segs and _same_input(segs[-1][2], v):
+            segs[-1][1] += 1
+        else:
+            segs.append([i, 1, v])
+    return [tuple(s) for s in segs]
+
+
+def _record(f, xs, length):
+    """The recording passes of ``for_loop(f, *xs)`` (brainstate_amd/_trace.py): returns
+    ``(neuron, proj_e, proj_i, n_exc, segments, raster_dtype)`` when every step is the E/I
+    step the runner implements -- segments [(first step, steps, input)] of equal inputs --
+    else None.  No network kernel runs; random states are restored unless the per-step
+    recording drew numbers that the runner then uses (those of the eager steps)."""
+    tr = _trace.Trace()
+    with _trace.rng_guard() as rng:
         try:
-            with _module.record_calls() as log:
-                out = f(*[x[i] for x in xs])
-        finally:
-            _event.defer_layouts = False
-        outs.append(out)
-        step = _ei_step(log, before)
-        if step is None:
-            return outs, None
-        spk = step[0].spike.value
-        if out is not None and not (torch.is_tensor(out) and out.shape == spk.shape and
-                                    torch.equal(out != 0, spk != 0)):
-            return outs, None
-        steps.append(step)
-    if any(a is not b for a, b in zip(steps[0][:3], steps[1][:3])) or \
-            steps[0][3] != steps[1][3] or not _same_input(steps[0][4], steps[1][4]):
-        return outs, None
-    neuron, proj_e, proj_i, n_exc, inp = steps[1]
-    r = fuse(neuron, proj_e, proj_i, n_exc, inp)
-    T = length - 2
-    want = outs[0] is not None
+            calls, out = tr.run(f, _trace.step_args(len(xs)))
+            st = _ei_structure(tr, calls, out)
+            if st is None:
+                return None
+            if rng.changed():   # draws inside the step: record each step's own
+                rng.restore()
+                raise _trace.Dependent()
+            neuron, pe, pi, n_exc, inp, rd = st
+            if isinstance(inp, _trace.StepArg):
+                segs = _schedule(xs, inp.index, length, neuron)
+            else:
+                segs = [(0, length, inp)]
+            return None if segs is None else (neuron, pe, pi, n_exc, segs, rd)
+        except _trace.NotFusable:
+            return None
+        except _trace.Dependent:
+            pass
+        except Exception:   # the step cannot be recorded; eager stepping shows why
+            return None
+        # the step uses its arguments: record every step with its own
+        first, vals, held = None, [], 0
+        try:
+            for i in range(length):
+                calls, out = tr.run(f, [x[i] for x in xs])
+                st = _ei_structure(tr, calls, out)
+                if st is None or isinstance(st[4], _trace.StepArg):
+                    rng.restore()
+                    return None
+                if first is None:
+                    first = st
+                elif any(a is not b for a, b in zip(first[:4], st[:4])) or first[5] != st[5]:
+                    rng.restore()
+                    return None
+                v = st[4]
+                if torch.is_tensor(v) and not (vals and vals[-1] is v):
+                    held += v.numel() * v.element_size()
+                    if held > _MAX_INPUT_BYTES:
+                        rng.restore()
+                        return None
+                vals.append(v)
+        except (_trace.NotFusable, _trace.Dependent):
+            rng.restore()
+            return None
+        except Exception:
+            rng.restore()
+            return None
+        segs = _merge(vals)
+        if segs is None:
+            rng.restore()
+            return None
+        neuron, pe, pi, n_exc, _, rd = first
+        return neuron, pe, pi, n_exc, segs, rd
+
+
+def _fused_loop(f, xs, length):
+    """for_loop through the persistent runner: the steps are recorded first (``_record``);
+    when every one is the E/I step the runner implements, the runner advances all of them
+    from the modules' state -- one launch per run of equal inputs -- and writes the final
+    state back.  Returns the stacked output (a tensor, or a list of None), or None when the
+    loop must run eagerly."""
+    from .nn._fuse import fuse
+    plan = _record(f, xs, length)
+    if plan is None:
+        return None
+    neuron, proj_e, proj_i, n_exc, segs, rdtype = plan
+    first = next((v for _, _, v in segs if torch.is_tensor(v)), segs[0][2])
+    try:
+        r = fuse(neuron, proj_e, proj_i, n_exc, first)
+    except NotImplementedError:   # a state the runner cannot start from
+        return None
+    T = length
     res = raster = None
     direct = False
-    if want:
-        # the stacked result: the eager steps' outputs, then the runner's raster (every neuron
-        # of every step as 0/1) in their order and dtype.  A bool or uint8 result in the
-        # runner's neuron order is the raster itself: the runner writes rows 2.. in place
-        # (a separate raster and its conversion took 18 ms for 10,000 steps of 1M neurons)
-        res = torch.empty((length,) + tuple(outs[0].shape), dtype=outs[0].dtype,
-                          device=outs[0].device)
+    if rdtype is not None:
+        # the stacked result [T, *spike shape] in the output's dtype; a bool or uint8 result
+        # in the runner's neuron order is the raster itself (the runner writes it in place)
+        shape = tuple(neuron.spike.value.shape)
+        res = torch.empty((T,) + shape, dtype=rdtype, device=r.device)
         perm = np.asarray(r.replica_index).reshape(-1)
         ident = getattr(r, 'replica_identity', False) or np.array_equal(perm,
                                                                          np.arange(perm.size))
-        direct = ident and res.dtype in (torch.bool, torch.uint8) and res.device == r.device
-        raster = (res[2:].view(torch.uint8).view(T, -1) if direct else
+        direct = ident and rdtype in (torch.bool, torch.uint8)
+        raster = (res.view(torch.uint8).view(T, -1) if direct else
                   torch.empty(T, r.n, dtype=torch.uint8, device=r.device))
-    r.run(T, raster=raster)
+    for t0, steps, v in segs:
+        r.set_input(v)
+        r.run(steps, raster=None if raster is None else raster[t0:t0 + steps])
     r.check()
     r.write_back()
-    if not want:
-        return outs, [None] * length
-    res[0].copy_(outs[0])
-    res[1].copy_(outs[1])
+    if rdtype is None:
+        return [None] * length
     if not direct:
-        if ident:
-            res[2:].view(T, -1).copy_(raster)
-        else:
-            res[2:].view(T, -1).copy_(raster[:, torch.as_tensor(perm, device=raster.device)])
-    return outs, res
+        src = raster if ident else raster[:, torch.as_tensor(perm, device=raster.device)]
+        res.view(T, -1).copy_(src)
+    return res
 
 
 def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
     """Call ``f(*x_t)`` for t along the leading axis of ``xs`` and stack the outputs
     (brainstate/transform/_loop_collect_return.py:487-572).
 
-    The reference traces ``f`` once and runs the whole loop as one compiled scan.  Here a
-    step function that is the E/I network step (the two event projections of one LIFRef or
-    HH population fed its spikes, then the population with a constant input -- the update
-    of examples/105_COBA_HH_2007_braincell.py and of the SNN tutorial) is recognised from the
-    module calls of its first two steps, which run eagerly, and every later step runs in
-    the persistent runner, one launch; the state is written back at the end.  Any other step
-    function runs eagerly step by step."""
+    The reference traces ``f`` once and runs the whole loop as one compiled scan
+    (:254,268).  Here ``f`` is first recorded without running its modules
+    (brainstate_amd/_trace.py): once with placeholders for the per-step arguments, and, when
+    the step uses them, once per step with the concrete values.  When every step is the E/I
+    network step the persistent runner implements (the two event projections of one LIFRef
+    or HH population fed its spikes, then the population called with one input -- the
+    update of examples/105_COBA_HH_2007_braincell.py and of the SNN tutorial), the runner
+    advances all steps, one launch per run of equal inputs, and the state is written back at
+    the end.  Anything else -- other modules, State assignments outside modules, state used
+    for anything but the projections' spike vectors, inputs the runner does not take --
+    runs eagerly step by step.  Python side effects of ``f`` happen in the recording pass
+    (once, or once per step) and again per step when the loop then runs eagerly."""
     global last_loop
     if length is None:
         if not xs:
@@ -276,18 +404,12 @@ def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
     last_loop = 'eager'
     try:
         if fuse_loops and not reverse and length >= 3:
-            done, stacked = _fused_loop(f, xs, length)
-            if bar is not None:
-                bar.advance(len(done) if stacked is None else length, length - 1)
+            stacked = _fused_loop(f, xs, length)
             if stacked is not None:
+                if bar is not None:
+                    bar.advance(length, length - 1)
                 last_loop = 'fused'
                 return stacked if torch.is_tensor(stacked) else _stack(stacked)
-            outs = done
-            for i in range(len(done), length):
-                outs.append(f(*[x[i] for x in xs]))
-                if bar is not None:
-                    bar.step(i)
-            return _stack(outs)
         order = range(length - 1, -1, -1) if reverse else range(length)
         outs = []
         for i in order:

@@ -145,13 +145,16 @@ BS_API int bs_event_matvec_vjp_batch_f32(const void* spk, int32_t spk_dtype, int
  *        (bucket b holds [b*P, min((b+1)*P, n_post)), P <= 12288, nb <= 1024);
  *   bs_bucket_build: seg[n_pre][nb+1] (int32), lidx[nnz] (uint16), lw[nnz] (fp32 or NULL)
  *        and, with per-synapse weights, the fixed-point exponent *qexp (device int32;
- *        `workspace` = 4 device bytes of scratch).  Row i's synapses stay inside
- *        [indptr[i], indptr[i+1]) (fixed-num: [i*k, i*k+k)), sorted by bucket with the
+ *        `workspace` = 4 * (n_post + 1) device bytes of scratch).  Row i's synapses stay
+ *        inside [indptr[i], indptr[i+1]) (fixed-num: [i*k, i*k+k)), sorted by bucket with the
  *        original order kept inside a bucket; bucket b's synapses of row i are
  *        [seg[i][b], seg[i][b+1]) with lidx = target - b*P; valid synapses end at seg[i][nb]
- *        (out-of-range targets follow and are never read).  S = *qexp = 30 - e_w with
- *        max|w| < 2^e_w, so every rounded weight is an integer below 2^30 in magnitude (-1000
- *        if a weight is not finite).
+ *        (out-of-range targets follow and are never read).  S = *qexp = min(30 - e_w - e_d,
+ *        100) with max|w| < 2^e_w over the valid synapses (e_w from the exponent field, -126
+ *        for 0 or a subnormal) and the largest number of valid synapses onto one post
+ *        D <= 2^e_d: the persistent runner's rule (bs_net_prepare), so a projection gives the
+ *        same sums here and inside the runner; every output's sum of rounded weights stays
+ *        below 2^30 in magnitude (-1000 if a weight is not finite or S < -100).
  * bs_event_bucket_f32: out[j] = (accumulate ? out[j] : 0) + v_j, where v_j is
  *   - per-synapse weights, finite: each weight of an event onto j rounded to a multiple of
  *     2^-S (round to nearest even), the rounded weights summed exactly (64-bit integers),
@@ -166,7 +169,8 @@ BS_API int bs_event_matvec_vjp_batch_f32(const void* spk, int32_t spk_dtype, int
  *   1  one launch of nb x min(8, 256 / nb) workgroups that write out themselves, no estimate
  *      (R = 1 whatever the density: right for sparse spikes, slow for dense ones);
  *   2  R = its maximum (row_groups), fixed on the host: no estimate on the critical path
- *      (right for dense spikes).
+ *      (right for dense spikes); a layout whose maximum is 1 (n_pre <= 64, or more than
+ *      128 buckets) runs as mode 0.
  * The sums are the same bits in every mode.  est_out (NULL, or an int32 the device can write,
  * e.g. in pinned host memory) receives the call's estimate of R (mode 0: from the leading
  * rows; mode 1: ceil(active rows / 128) from the exact count; mode 2: from row group 0), so that a caller can pick the next call's mode from it without a
@@ -285,6 +289,13 @@ typedef struct {
    * docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cells 5, 11): a spike subtracts
    * (V_th - V_reset) from V' instead of setting V' = V_reset. */
   int32_t soft_reset;
+  /* deferred_reset != 0: the reset of a spike is applied at the start of the neuron's next
+   * step, as brainpy.state's neurons do (`last_V = V - (V_th - V_reset) * last_spk` before the
+   * update; the reference-held neuron of examples/203_braintrace_for_snns.py:173-176): a
+   * spiking neuron keeps V' >= V_th in V until then.  Spike rasters and every other state
+   * are those of deferred_reset == 0.  bs_coba_lif_step then reads the previous step's
+   * spikes from spk_out before it overwrites them; the runners take them from net->spk. */
+  int32_t deferred_reset;
 } bs_lif_params;
 
 BS_API int bs_coba_lif_step(int32_t n, float* V, float* ge, float* gi, int32_t* ref,

@@ -71,6 +71,7 @@ typedef struct {
   int32_t cuba;
   float scale_e, scale_i;
   int32_t soft_reset;
+  int32_t deferred_reset;
 } bso_lif_params;
 
 typedef struct {
@@ -218,12 +219,18 @@ static void o_net_init(o_net* g, int n, int n_exc, int k_e, int k_i, const int32
   }
 }
 
-/* LIFRef + Expon + COBA/CUBA, the operation order of csrc/neuron_dev.h bs_lif_update. */
+/* LIFRef + Expon + COBA/CUBA, the operation order of csrc/neuron_dev.h bs_lif_update.
+ * deferred_reset: a neuron that spiked in the previous step (prev) is reset first, and a
+ * spiking neuron keeps V' (brainpy.state's order). */
+static inline float o_lif_reset(const bso_lif_params* p, float v) {
+  return p->soft_reset ? v - (p->V_th - p->V_reset) : p->V_reset;
+}
+
 static inline uint8_t o_lif(const bso_lif_params* p, float* Vp, float* gep, float* gip,
-                            int32_t* refp, float in_e, float in_i) {
+                            int32_t* refp, float in_e, float in_i, uint8_t prev) {
   const float g_e = fmaf(*gep, p->decay_e, in_e);
   const float g_i = fmaf(*gip, p->decay_i, in_i);
-  const float v = *Vp;
+  const float v = (p->deferred_reset && prev) ? o_lif_reset(p, *Vp) : *Vp;
   float I, J;
   if (p->cuba) {
     I = fmaf(g_e, p->scale_e, p->I_ext);
@@ -244,7 +251,7 @@ static inline uint8_t o_lif(const bso_lif_params* p, float* Vp, float* gep, floa
     r = r - 1;
   } else if (vn >= p->V_th) {
     s = 1;
-    vn = p->soft_reset ? vn - (p->V_th - p->V_reset) : p->V_reset;
+    if (!p->deferred_reset) vn = o_lif_reset(p, vn);
     r = p->ref_steps;
   } else {
     r = 0;
@@ -334,7 +341,7 @@ static long long o_run(int model, const o_net* g, const void* params, void* cons
         const float ie = o_take(g, in_e, 0, j), ii = o_take(g, in_i, 1, j);
         bso_lif_params q = *p;
         if (iext) q.I_ext = iext[j];  /* per-neuron external input */
-        const uint8_t s = o_lif(&q, &V[j], &ge[j], &gi[j], &ref[j], ie, ii);
+        const uint8_t s = o_lif(&q, &V[j], &ge[j], &gi[j], &ref[j], ie, ii, spk[j]);
         spk[j] = s;
         if (s) h += o_mix32((uint32_t)j);
       }

@@ -29,7 +29,7 @@ class _LifParams(ctypes.Structure):
                                                 'E_e', 'E_i', 'dt', 'decay_e', 'decay_i')] + \
                [('ref_steps', ctypes.c_int32), ('cuba', ctypes.c_int32),
                 ('scale_e', ctypes.c_float), ('scale_i', ctypes.c_float),
-                ('soft_reset', ctypes.c_int32)]
+                ('soft_reset', ctypes.c_int32), ('deferred_reset', ctypes.c_int32)]
 
 
 class _HhParams(ctypes.Structure):
@@ -60,7 +60,8 @@ def lif_params(p):
     return _LifParams(p.V_rest, p.V_th, p.V_reset, p.inv_tau, p.R, p.I_ext, p.E_e, p.E_i, p.dt,
                       p.de, p.di, int(p.ref_steps), int(bool(getattr(p, 'cuba', False))),
                       float(getattr(p, 'scale_e', 1.0)), float(getattr(p, 'scale_i', 1.0)),
-                      int(bool(getattr(p, 'soft_reset', False))))
+                      int(bool(getattr(p, 'soft_reset', False))),
+                      int(bool(getattr(p, 'deferred_reset', False))))
 
 
 def hh_params(p):

@@ -146,18 +146,35 @@ def event_linear(spk, W, float_as_event=True, n_out=None, chunk_rows=None):
 
 # ---- destination-bucketed operator: exact fixed-point sums ----
 
-def bucket_qexp(w, nnz):
-    """Fixed-point exponent S of the bucketed layout: 30 - e_w with max|w| < 2^e_w (every
-    rounded weight an integer below 2^30 in magnitude; ``nnz`` does not enter); -1000 if a
-    weight is not finite, 0 if every weight is 0 (csrc/event_bucket.hip, k_bucket_qexp)."""
-    w = np.abs(np.asarray(w, dtype=F).reshape(-1))
-    if w.size and not np.all(np.isfinite(w)):
+def fixed_point_qexp(wmax, D):
+    """The fixed-point exponent rule of the persistent runner and the bucketed operator (csrc
+    network.hip k_qexp, event_bucket.hip k_bucket_qexp): with W = ``wmax`` (fp32 max |w|),
+    W < 2^e_w (e_w from W's exponent field; -126 for a zero or subnormal W) and the largest
+    in-degree D <= 2^e_d, S = min(30 - e_w - e_d, 100).  Every output's sum of
+    rint(w * 2^S) then has magnitude < 2^30 + D/2.  -1000 when W is not finite or S < -100."""
+    wb = int(np.asarray(wmax, F).reshape(()).view(np.uint32)) & 0x7FFFFFFF
+    if wb >= 0x7F800000:
         return -1000
-    wmax = float(w.max()) if w.size else 0.0
-    if wmax == 0.0:
-        return 0
-    e_w = int(np.frexp(np.float64(wmax))[1])          # wmax = m * 2^e_w, 0.5 <= m < 1
-    return 30 - e_w
+    e_w = (wb >> 23) - 126 if (wb >> 23) else -126
+    D = int(D)
+    e_d = (D - 1).bit_length() if D > 1 else 0
+    S = min(30 - e_w - e_d, 100)
+    return -1000 if S < -100 else S
+
+
+def bucket_qexp(w, targets, n_post):
+    """Fixed-point exponent S of the bucketed layout: ``fixed_point_qexp`` over the valid
+    synapses (0 <= target < n_post) -- W their largest |w|, D the most of them onto one post.
+    ``w`` and ``targets`` are per synapse (same length)."""
+    w = np.asarray(w, dtype=F).reshape(-1)
+    t = np.asarray(targets).reshape(-1).astype(np.int64)
+    ok = (t >= 0) & (t < n_post)
+    wv, tv = np.abs(w[ok]), t[ok]
+    if wv.size and not np.all(np.isfinite(wv)):
+        return -1000
+    wmax = wv.max() if wv.size else F(0)
+    D = int(np.bincount(tv, minlength=n_post).max()) if tv.size else 0
+    return fixed_point_qexp(wmax, D)
 
 
 def scatter_fixed_point(spk, indptr, indices, w, n_post, S):

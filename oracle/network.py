@@ -48,10 +48,8 @@ def runner_qexp(idx, w, n_post):
     wb = int((w.view(np.uint32) & np.uint32(0x7FFFFFFF)).max()) if w.size else 0
     if wb >= 0x7F800000:
         raise ValueError('a per-synapse weight is not finite')
-    e_w = (wb >> 23) - 126 if (wb >> 23) else -126
-    e_d = (D - 1).bit_length() if D > 1 else 0
-    S = min(30 - e_w - e_d, 100)
-    if S < -100:
+    S = _event.fixed_point_qexp(np.uint32(wb).view(F), D)
+    if S == -1000:
         raise ValueError('per-synapse weights too large for the fixed-point input sums')
     return S
 
@@ -142,7 +140,7 @@ def run_coba_lif(V0, proj_e, proj_i, p, n_exc, steps, record_raster=True, init=N
         src = spk if hist is None else hist.retrieve_at_step(delay_steps)
         in_e = proj_e(src[:n_exc])
         in_i = proj_i(src[n_exc:])
-        V, ge, gi, ref, spk = _neuron.coba_lif_step(V, ge, gi, ref, in_e, in_i, p)
+        V, ge, gi, ref, spk = _neuron.coba_lif_step(V, ge, gi, ref, in_e, in_i, p, spk)
         if hist is not None:
             hist.update(spk)
         if record_raster:

@@ -27,7 +27,8 @@ from the equations and are **parity unpinned** beyond the checks above:
     ``ref_rule='closed'``); V is held there.  Which one brainpy.state uses is not pinned
     (its ``t - t_last <= tau_ref`` in float32 gives 49, 50 or 51 steps at 5 ms / 0.1 ms
     depending on how the absolute times round).
-    Spike when V' >= V_th; hard reset V' = V_reset.
+    Spike when V' >= V_th; hard reset V' = V_reset, in the spike step or (deferred_reset,
+    brainpy.state's order) at the start of the next.
 HH (examples/100_hh_neuron_model.py:49-93, reference-held): rates from the old V, V
 and the gates each by exp-Euler from the old state, spike = (V < V_th) & (V' >= V_th).
 """
@@ -68,13 +69,18 @@ class LIFParams:
     """``out='cuba'``: current-based synaptic output I += g * scale (brainpy.state CUBA, used
     by examples/400_CUBA_2005_bpu.py:42-58) instead of g * (E - V).  ``spk_reset='soft'``
     (docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cells 5, 11): a spike subtracts
-    V_th - V_reset from V' instead of setting V_reset."""
+    V_th - V_reset from V' instead of setting V_reset.  ``deferred_reset``: that reset is
+    applied at the start of the neuron's next step instead of in its spike step (brainpy.state's
+    ``last_V = V - (V_th - V_reset) * last_spk``; examples/203_braintrace_for_snns.py:173-176),
+    so a spiking neuron keeps V' >= V_th in between."""
 
     def __init__(self, V_rest=-60., V_th=-50., V_reset=-60., tau=20., R=1., tau_ref=5.,
                  I_ext=20., E_e=0., E_i=-80., tau_e=5., tau_i=10., dt=0.1, out='coba',
-                 scale_e=1., scale_i=1., spk_reset='hard', ref_rule='open'):
+                 scale_e=1., scale_i=1., spk_reset='hard', ref_rule='open',
+                 deferred_reset=False):
         self.cuba = out == 'cuba'
         self.soft_reset = spk_reset == 'soft'
+        self.deferred_reset = bool(deferred_reset)
         self.scale_e, self.scale_i = F(scale_e), F(scale_i)
         self.V_rest, self.V_th, self.V_reset = F(V_rest), F(V_th), F(V_reset)
         self.tau, self.R, self.I_ext = F(tau), F(R), F(I_ext)
@@ -103,18 +109,29 @@ def lif_membrane(V, ge, gi, p):
     return fma32((p.dt * phi).astype(F), f, V)
 
 
-def coba_lif_step(V, ge, gi, ref, in_e, in_i, p):
-    """Fused Expon + COBA + LIFRef step.  Returns (V, ge, gi, ref, spike)."""
+def lif_reset(V, p):
+    """V after a spike: V_reset, or V - (V_th - V_reset) with a soft reset."""
+    V = np.asarray(V, F)
+    if getattr(p, 'soft_reset', False):
+        return (V - (p.V_th - p.V_reset).astype(F)).astype(F)
+    return np.broadcast_to(np.asarray(p.V_reset, F), V.shape).astype(F)
+
+
+def coba_lif_step(V, ge, gi, ref, in_e, in_i, p, spk_prev=None):
+    """Fused Expon + COBA + LIFRef step.  Returns (V, ge, gi, ref, spike).  With
+    ``p.deferred_reset`` the neurons of ``spk_prev`` (the previous step's spikes) are reset
+    first and this step's spiking neurons keep V'."""
+    deferred = getattr(p, 'deferred_reset', False)
+    if deferred and spk_prev is not None:
+        V = np.where(np.asarray(spk_prev) != 0, lif_reset(V, p), V).astype(F)
     ge = fma32(ge, p.de, in_e)
     gi = fma32(gi, p.di, in_i)
     Vn = lif_membrane(V, ge, gi, p)
     refr = ref > 0
     Vn = np.where(refr, V, Vn).astype(F)
     spk = (~refr) & (Vn >= p.V_th)
-    if getattr(p, 'soft_reset', False):   # subtractive reset: V' - (V_th - V_reset)
-        Vn = np.where(spk, (Vn - (p.V_th - p.V_reset).astype(F)).astype(F), Vn).astype(F)
-    else:
-        Vn = np.where(spk, p.V_reset, Vn).astype(F)
+    if not deferred:   # hard reset V_reset, or subtractive: V' - (V_th - V_reset)
+        Vn = np.where(spk, lif_reset(Vn, p), Vn).astype(F)
     ref = np.where(spk, p.ref_steps, np.where(refr, ref - 1, 0)).astype(I32)
     return Vn, ge, gi, ref, spk
 

@@ -200,7 +200,7 @@ def main():
         spk, idx, w = matvec_case(p_spk)
         homo = event.scatter_fixed(spk, idx, np.float32(MATVEC['w_homo']), MATVEC['n_post'])
         het = event.scatter_fixed(spk, idx, w, MATVEC['n_post'])
-        S = event.bucket_qexp(w, idx.size)
+        S = event.bucket_qexp(w, idx, MATVEC['n_post'])
         indptr = np.arange(MATVEC['n_pre'] + 1, dtype=np.int64) * MATVEC['k']
         fixed = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, MATVEC['n_post'], S)
         cases.append(dict(p=p_spk, active=int(spk.sum()), homo_sha256=sha(homo),

@@ -110,9 +110,10 @@ def test_event_dense_packed_sizes_host_only():
 
 def test_struct_layouts_match_header():
     # field counts/order of the ctypes mirrors (sizes of plain C structs on x86-64)
-    assert ctypes.sizeof(N.LifParams) == 16 * 4
+    assert ctypes.sizeof(N.LifParams) == 17 * 4
     assert [f[0] for f in N.LifParams._fields_][11:] == ['ref_steps', 'cuba', 'scale_e',
-                                                         'scale_i', 'soft_reset']
+                                                         'scale_i', 'soft_reset',
+                                                         'deferred_reset']
     assert ctypes.sizeof(N.HhParams) == 14 * 4
     assert ctypes.sizeof(N.LifState) == 4 * 8
     assert ctypes.sizeof(N.HhState) == 6 * 8
@@ -129,10 +130,11 @@ def test_lif_params_offsets_match_the_compiled_header(tmp_path):
         pytest.skip('no host C compiler')
     src = tmp_path / 'off.c'
     src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "brainstate_amd.h"\n'
-                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu\\n", '
+                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu %zu\\n", '
                    'sizeof(bs_lif_params), offsetof(bs_lif_params, ref_steps), '
                    'offsetof(bs_lif_params, cuba), offsetof(bs_lif_params, scale_e), '
-                   'offsetof(bs_lif_params, scale_i), offsetof(bs_lif_params, soft_reset)); '
+                   'offsetof(bs_lif_params, scale_i), offsetof(bs_lif_params, soft_reset), '
+                   'offsetof(bs_lif_params, deferred_reset)); '
                    'return 0; }\n')
     exe = tmp_path / 'off'
     subprocess.run([cc, '-I', os.path.join(ROOT, 'include'), str(src), '-o', str(exe)],
@@ -141,4 +143,4 @@ def test_lif_params_offsets_match_the_compiled_header(tmp_path):
                                           check=True).stdout.split()]
     L = N.LifParams
     assert got == [ctypes.sizeof(L), L.ref_steps.offset, L.cuba.offset, L.scale_e.offset,
-                   L.scale_i.offset, L.soft_reset.offset]
+                   L.scale_i.offset, L.soft_reset.offset, L.deferred_reset.offset]

@@ -124,7 +124,7 @@ def test_event_linear_batched_bit_exact(bs):
 class _EINet:
     """examples/105_COBA_HH_2007_braincell.py:54-82 with config-[1] LIF parameters."""
 
-    def __init__(self, bs, **lif):
+    def __init__(self, bs, w_e=0.6, w_i=6.7, **lif):
         c = make_golden.CONFIG1
         self.bs = bs
         self.n_exc, self.num = c['n_exc'], c['n']
@@ -133,12 +133,12 @@ class _EINet:
         kw.update(lif)   # e.g. per-neuron parameter arrays
         self.N = bs.nn.LIFRef(self.num, V_initializer=lambda s: V0, **kw)
         self.E = bs.nn.AlignPostProj(
-            comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=0.02, conn_weight=0.6,
+            comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=0.02, conn_weight=w_e,
                                       seed=c['seed_e']),
             syn=bs.nn.Expon.desc(self.num, tau=5.), out=bs.nn.COBA.desc(E=0.), post=self.N)
         self.I = bs.nn.AlignPostProj(
             comm=bs.nn.EventFixedProb(self.num - self.n_exc, self.num, conn_num=0.02,
-                                      conn_weight=6.7, seed=c['seed_i']),
+                                      conn_weight=w_i, seed=c['seed_i']),
             syn=bs.nn.Expon.desc(self.num, tau=10.), out=bs.nn.COBA.desc(E=-80.), post=self.N)
         for m in (self.E.syn, self.I.syn, self.N):
             m.init_state()
@@ -179,6 +179,7 @@ def test_module_ei_network_matches_oracle(bs):
     print('[case] module E/I net for_loop eager + fused', flush=True)
     T = 300
     pe, pi, V0, p = make_golden.config1_net()
+    p.deferred_reset = True   # LIFRef's default reset_timing='next'
     ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
 
     def make():
@@ -202,7 +203,8 @@ def test_module_ei_network_per_neuron_input(bs):
     T = 300
     pe, pi, V0, p = make_golden.config1_net()
     I = (20. + np.random.RandomState(5).uniform(-3., 3., V0.size)).astype(F)
-    ref = network.run_coba_lif(V0, pe, pi, neuron.LIFParams(I_ext=I), 3200, T)
+    ref = network.run_coba_lif(V0, pe, pi, neuron.LIFParams(I_ext=I, deferred_reset=True),
+                               3200, T)
     dI = torch.as_tensor(I, device='cuda')
 
     def make():
@@ -272,6 +274,7 @@ def test_module_ei_network_per_neuron_parameters(bs):
     p.V_th, p.tau = V_th, tau
     p.inv_tau = (F(1.0) / tau).astype(F)
     p.ref_steps = np.array([neuron.ref_steps(x, 0.1) for x in tau_ref], np.int32)
+    p.deferred_reset = True
     ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
     with bs.environ.context(dt=0.1):
         net = _EINet(bs, V_th=V_th, tau=tau, tau_ref=tau_ref)
@@ -366,12 +369,12 @@ def test_hh_module_network_per_neuron_parameters(bs):
     assert ref['counts'].sum() > 50
 
 
-def test_for_loop_stays_eager_for_other_steps(bs):
-    """A step whose input changes with time is not the runner's step: after its two recorded
-    steps the loop goes on eagerly, and equals the loop stepped eagerly from the start."""
+def test_for_loop_input_changing_every_step(bs):
+    """A step whose input changes every step (20 + t) is recorded step by step and run in the
+    runner with one launch per step; it equals the loop stepped eagerly."""
     import torch
     print('[case] for_loop time-varying input', flush=True)
-    outs = []
+    outs, nets = [], []
     for fused in (False, True):
         bs.transform.fuse_loops = fused
         try:
@@ -385,10 +388,273 @@ def test_for_loop_stays_eager_for_other_steps(bs):
                     return net.N(20. + float(t))
 
                 outs.append(bs.transform.for_loop(step, torch.arange(50) * 0.1))
+                nets.append(net)
         finally:
             bs.transform.fuse_loops = True
-        assert bs.transform.last_loop == 'eager'
+        assert bs.transform.last_loop == ('fused' if fused else 'eager')
+    assert int(outs[0].sum()) > 0
     assert torch.equal(outs[0], outs[1])
+    assert torch.equal(nets[0].N.V.value, nets[1].N.V.value)
+    assert torch.equal(nets[0].E.syn.g.value, nets[1].E.syn.g.value)
+
+
+def _switch_oracle(T, t_switch, I_on, I_off):
+    """The oracle's run of the config-[1] net with input I_on for steps [0, t_switch) and
+    I_off after, continuing one run's state in the next."""
+    pe, pi, V0, _ = make_golden.config1_net()
+    a = network.run_coba_lif(V0, pe, pi, neuron.LIFParams(I_ext=I_on, deferred_reset=True),
+                             3200, t_switch)
+    init = (a['V'], a['ge'], a['gi'], a['ref'], a['spk'])
+    b = network.run_coba_lif(V0, pe, pi, neuron.LIFParams(I_ext=I_off, deferred_reset=True),
+                             3200, T - t_switch, init=init)
+    b['raster'] = np.concatenate([a['raster'], b['raster']])
+    return b
+
+
+def test_for_loop_drive_switch(bs):
+    """for_loop(lambda t: net.update(20 if t < 5 ms else 0), times): the step uses its
+    argument, so every step is recorded with its value; the inputs form two runs of equal
+    input, run as two launches, and the loop equals the loop stepped eagerly and the oracle
+    (input 20 for 50 steps, then 0) -- raster, final V, conductances, refractory counts."""
+    import torch
+    print('[case] for_loop drive switching at 5 ms', flush=True)
+    T = 300
+    ref = _switch_oracle(T, 50, 20., 0.)
+    assert ref['raster'][:50].sum() > 0 and ref['raster'].sum() > ref['raster'][:50].sum()
+
+    class Net(_EINet):
+        def update(self, t):
+            with self.bs.environ.context(t=t):
+                spk = self.N.get_spike() != 0.
+                self.E(spk[:self.n_exc])
+                self.I(spk[self.n_exc:])
+                return self.N(20. if t < 5. else 0.)
+
+    def make():
+        net = Net(bs)
+        return net.update, net
+    for spikes, net in _for_loop_paths(bs, make, T):
+        assert spikes.dtype == torch.bool and spikes.shape == (T, 4000)
+        assert np.array_equal(spikes.cpu().numpy(), ref['raster'])
+        assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+        assert np.array_equal(net.E.syn.g.value.cpu().numpy(), ref['ge'])
+        assert np.array_equal(net.I.syn.g.value.cpu().numpy(), ref['gi'])
+        assert np.array_equal(net.N.ref.value.cpu().numpy(), ref['ref'])
+        assert np.array_equal(net.N.spike.value.cpu().numpy(), ref['spk'])
+
+
+def test_for_loop_input_from_xs(bs):
+    """The input passed straight from the loop's own argument (for_loop(step, times,
+    inputs) with N(inp)): taken from xs without calling the step per step, one launch per
+    run of equal values; equals eager stepping and the oracle."""
+    import torch
+    print('[case] for_loop input from xs', flush=True)
+    T = 200
+    ref = _switch_oracle(T, 120, 20., 14.)
+    inputs = torch.cat([torch.full((120,), 20.), torch.full((80,), 14.)])
+
+    def make():
+        net = _EINet(bs)
+
+        def step(t, inp):
+            spk = net.N.get_spike() != 0.
+            net.E(spk[:net.n_exc])
+            net.I(spk[net.n_exc:])
+            return net.N(inp)
+        return step, net
+    res = []
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                step, net = make()
+                res.append((bs.transform.for_loop(step, torch.arange(T) * 0.1, inputs), net))
+        finally:
+            bs.transform.fuse_loops = True
+        assert bs.transform.last_loop == ('fused' if fused else 'eager')
+    for spikes, net in res:
+        assert np.array_equal(spikes.cpu().numpy(), ref['raster'])
+        assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+
+
+@pytest.mark.parametrize('kind', ['assign_state', 'state_as_input', 'reduce_spikes',
+                                  'extra_module', 'late_change'])
+def test_for_loop_steps_the_runner_cannot_take_stay_eager(bs, kind):
+    """Steps with an effect the runner would not reproduce run eagerly and equal the loop
+    stepped eagerly: a State assigned outside the modules (V clamped), the neuron's state fed
+    back as its input, the spikes used for anything but the projections, another module
+    called, and a step whose structure changes after some steps (an extra call from step 7)."""
+    import torch
+    print('[case] for_loop stays eager:', kind, flush=True)
+    T = 40
+    res = []
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                net = _EINet(bs)
+                other = bs.nn.LIFRef(10, V_initializer=0.)
+                other.init_state()
+                log = []
+
+                def step(t):
+                    spk = net.N.get_spike() != 0.
+                    net.E(spk[:net.n_exc])
+                    net.I(spk[net.n_exc:])
+                    if kind == 'assign_state':
+                        net.N.V.value = torch.clamp(net.N.V.value, max=-50.5)
+                        out = net.N(20.)
+                    elif kind == 'state_as_input':
+                        out = net.N(net.N.V.value * 0. + 20.)
+                    elif kind == 'reduce_spikes':
+                        log.append(spk.sum())
+                        out = net.N(20.)
+                    elif kind == 'extra_module':
+                        other(1.)
+                        out = net.N(20.)
+                    else:
+                        if float(t) > 0.65:
+                            other(1.)
+                        out = net.N(20.)
+                    return out
+
+                res.append((bs.transform.for_loop(step, torch.arange(T) * 0.1), net))
+        finally:
+            bs.transform.fuse_loops = True
+        assert bs.transform.last_loop == 'eager', kind
+    (a, na), (b, nb) = res
+    assert torch.equal(a, b)
+    assert torch.equal(na.N.V.value, nb.N.V.value)
+
+
+def _het_module_oracle(T):
+    pe, pi, V0, p = make_golden.config1_het_net()
+    p.deferred_reset = True
+    return pe, pi, network.run_coba_lif(V0, pe, pi, p, 3200, T)
+
+
+def test_for_loop_per_synapse_weights_4000(bs):
+    """A module net with per-synapse weights N(0.6, 0.06) / N(6.7, 0.67) (the weights of the
+    coba_lif_4000_het fixture): eager steps take the bucketed operator, whose fixed-point
+    exponent is the runner's, so stepping eagerly, for_loop through the runner and the
+    oracle's fixed-point sums agree bit for bit; eager stepping twice gives the same bits."""
+    import torch
+    print('[case] module net, per-synapse weights, 4000', flush=True)
+    T = 300
+    pe, pi, ref = _het_module_oracle(T)
+    assert ref['counts'].sum() > 500
+
+    def make():
+        net = _EINet(bs, w_e=pe.w, w_i=pi.w)
+        return net.update, net
+    runs = _for_loop_paths(bs, make, T) + _for_loop_paths(bs, make, T)[:1]
+    for spikes, net in runs:
+        assert np.array_equal(spikes.cpu().numpy() != 0, ref['raster'])
+        assert np.array_equal(net.N.V.value.cpu().numpy(), ref['V'])
+        assert np.array_equal(net.E.syn.g.value.cpu().numpy(), ref['ge'])
+        assert np.array_equal(net.I.syn.g.value.cpu().numpy(), ref['gi'])
+    assert torch.equal(runs[0][0], runs[2][0])
+
+
+def test_for_loop_per_synapse_weights_1m(bs):
+    """The same at 1M neurons (K = 100, weights N(0.6, 0.06) / N(6.7, 0.67)): eager module
+    steps, for_loop through the runner and the C restatement's fixed-point sums agree bit
+    for bit over 60 steps."""
+    import torch
+    from oracle import cbuild
+    print('[case] module net, per-synapse weights, 1M', flush=True)
+    n, k, T = 1_000_000, 100, 60
+    n_exc = n * 4 // 5
+    V0 = np.random.RandomState(3).uniform(-60., -50., n).astype(F)
+    rs = np.random.RandomState(8)
+    w_e = rs.normal(0.6, 0.06, (n_exc, k)).astype(F)
+    w_i = rs.normal(6.7, 0.67, (n - n_exc, k)).astype(F)
+
+    def make():
+        N = bs.nn.LIFRef(n, V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=5.,
+                         V_initializer=lambda s: V0)
+        E = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n_exc, n, k, w_e, seed=1),
+                                syn=bs.nn.Expon.desc(n, tau=5.), out=bs.nn.COBA.desc(E=0.),
+                                post=N)
+        I = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n - n_exc, n, k, w_i, seed=2),
+                                syn=bs.nn.Expon.desc(n, tau=10.), out=bs.nn.COBA.desc(E=-80.),
+                                post=N)
+        for m in (E.syn, I.syn, N):
+            m.init_state()
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            E(spk[:n_exc])
+            I(spk[n_exc:])
+            return N(20.)
+        return step, (N, E)
+    (eager, (Ne, Ee)), (fused, (Nf, Ef)) = _for_loop_paths(bs, make, T)
+    idx_e = Ee.comm.conn.indices.cpu().numpy()
+    idx_i = Ne._channels[1].comm.conn.indices.cpu().numpy()
+    st = cbuild.lif_state(V0)
+    c = np.zeros(T, np.int32)
+    p = neuron.LIFParams(deferred_reset=True)
+    cbuild.coba_lif_run(st, idx_e, idx_i, w_e, w_i, p, n_exc, T, counts=c)
+    assert int(c.sum()) > T * 300
+    assert eager.sum(1).cpu().numpy().tolist() == c.tolist()
+    assert torch.equal(eager, fused)
+    assert np.array_equal(Ne.V.value.cpu().numpy(), st['V'])
+    assert np.array_equal(Nf.V.value.cpu().numpy(), st['V'])
+    assert np.array_equal(Nf.spike.value.cpu().numpy().astype(np.uint8), st['spk'])
+
+
+def test_deferred_reset_state_after_a_spike_step(bs):
+    """LIFRef's default reset_timing='next' (brainpy.state's order): after a spike step V
+    keeps the value that crossed V_th and get_spike() is set exactly where V >= V_th; the next
+    step starts from V_reset (hard) or V - (V_th - V_reset) (soft).  reset_timing='same'
+    gives V_reset right away, and both give the same spikes, conductances and refractory
+    counts step by step; the oracle's deferred step gives the same V."""
+    import torch
+    print('[case] deferred reset', flush=True)
+    n = 64
+    V0 = np.linspace(-50.6, -49.9, n).astype(F)   # some cross V_th = -50 at once
+    for soft in (False, True):
+        kw = dict(V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=0.3,
+                  V_initializer=lambda s: V0, spk_reset='soft' if soft else 'hard')
+        with bs.environ.context(dt=0.1):
+            Nn = bs.nn.LIFRef(n, reset_timing='next', **kw)
+            Ns = bs.nn.LIFRef(n, reset_timing='same', **kw)
+            Nn.init_state()
+            Ns.init_state()
+            p = neuron.LIFParams(V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=0.3,
+                                 I_ext=15., spk_reset='soft' if soft else 'hard',
+                                 deferred_reset=True)
+            V, ge, gi, ref = V0.copy(), np.zeros(n, F), np.zeros(n, F), np.zeros(n, np.int32)
+            spk = np.zeros(n, bool)
+            seen = 0
+            for t in range(12):
+                sn, ss = Nn(15.), Ns(15.)
+                V, ge, gi, ref, spk = neuron.coba_lif_step(V, ge, gi, ref, np.zeros(n, F),
+                                                           np.zeros(n, F), p, spk)
+                assert torch.equal(sn, ss) and torch.equal(Nn.ref.value, Ns.ref.value)
+                s = sn.cpu().numpy()
+                vn, vs = Nn.V.value.cpu().numpy(), Ns.V.value.cpu().numpy()
+                assert np.array_equal(s, spk) and np.array_equal(vn, V)
+                assert np.array_equal(Nn.get_spike().cpu().numpy(), s)
+                assert np.all(vn[s] >= -50.) and np.all(vn[~s] == vs[~s])
+                want = (vn[s] - F(10.)).astype(F) if soft else np.full(s.sum(), F(-60.))
+                assert np.array_equal(vs[s], want)
+                seen += int(s.sum())
+            assert seen > n // 4
+
+
+def test_array_tau_ref_counts_like_the_scalar(bs):
+    """Per-neuron tau_ref arrays give the refractory steps of the scalar value (kept in
+    float64 before dividing by dt): 0.3 ms and 4.9 ms at dt = 0.1 ms, 'open' and 'closed'."""
+    from brainstate_amd import ops
+    print('[case] tau_ref arrays', flush=True)
+    with bs.environ.context(dt=0.1):
+        for rule in ('open', 'closed'):
+            for tr in (0.3, 0.6, 0.7, 1.1, 2.3, 4.9, 5.0):
+                N = bs.nn.LIFRef(4, tau_ref=np.full(4, tr), ref_rule=rule)
+                N.init_state()
+                got = N._param_arrays(N.V.value)['ref_steps'].cpu().numpy()
+                assert np.all(got == ops.refractory_steps(tr, 0.1, rule)), (rule, tr)
 
 
 def test_fused_network_continues_eager_state(bs):
@@ -396,6 +662,7 @@ def test_fused_network_continues_eager_state(bs):
     print('[case] module E/I net fused', flush=True)
     T = 300
     pe, pi, V0, p = make_golden.config1_net()
+    p.deferred_reset = True
     ref = network.run_coba_lif(V0, pe, pi, p, 3200, T)
     with bs.environ.context(dt=0.1):
         net = _EINet(bs)
@@ -448,6 +715,7 @@ def test_cuba_module_network_eager_and_fused(bs):
     import torch
     print('[case] module CUBA net eager + fused', flush=True)
     pe, pi, V0, p = make_golden.cuba_net()
+    p.deferred_reset = True
     ref = network.run_coba_lif(V0, pe, pi, p, make_golden.CUBA_NET['n_exc'], 500)
     assert ref['counts'].sum() > 100
     def make():
@@ -475,6 +743,7 @@ def test_tutorial_network_modules_soft_reset(bs):
     print('[case] tutorial net modules', flush=True)
     c = make_golden.TUT_NET
     pe, pi, V0, p = make_golden.tut_net()
+    p.deferred_reset = True
     ref = network.run_coba_lif(V0, pe, pi, p, c['n_exc'], c['steps'])
 
     def build():

@@ -171,6 +171,7 @@ def test_batched_module_net_eager(bs):
     say('batched module net eager', B, T)
     V0s = _replica_V0(B)
     pe, pi, _, p = make_golden.config1_net()
+    p.deferred_reset = True   # LIFRef's default reset_timing='next'
     with bs.environ.context(dt=0.1):
         net = _BatchedEINet(bs, V0s)
         assert tuple(net.N.V.value.shape) == (B, 4000)
@@ -188,6 +189,7 @@ def test_batched_net_fused_union_runner(bs):
     say('batched fused union', B, T)
     V0s = _replica_V0(B)
     pe, pi, _, p = make_golden.config1_net()
+    p.deferred_reset = True
     with bs.environ.context(dt=0.1):
         net = _BatchedEINet(bs, V0s)
         r = bs.nn.fuse(net.N, net.E, net.I, n_exc=3200, inp=20.)
@@ -216,7 +218,8 @@ def test_batched_net_per_replica_input(bs):
     pe, pi, _, _ = make_golden.config1_net()
     I = np.array([16., 19., 22., 25.], F)[:, None]
     dI = torch.as_tensor(I, device='cuda')
-    refs = [network.run_coba_lif(V0s[b], pe, pi, neuron.LIFParams(I_ext=I[b, 0]), 3200, T)
+    refs = [network.run_coba_lif(V0s[b], pe, pi,
+                                 neuron.LIFParams(I_ext=I[b, 0], deferred_reset=True), 3200, T)
             for b in range(B)]
     assert len({int(r['counts'].sum()) for r in refs}) == B   # the inputs matter
     for fused in (False, True):

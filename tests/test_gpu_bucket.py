@@ -103,7 +103,7 @@ def test_bucket_matvec_matches_oracle(torch_cuda, n_pre, n_post, k, p, het, sdt)
     ref = event.scatter_fixed(spk, idx, w, n_post)
     if het:
         S = int(L['qexp'].item())
-        assert S == event.bucket_qexp(w, idx.size)
+        assert S == event.bucket_qexp(w, idx, n_post)
         indptr = np.arange(n_pre + 1, dtype=np.int64) * k
         exact = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, n_post, S)
         assert np.array_equal(got, exact)                      # the documented arithmetic
@@ -138,7 +138,7 @@ def test_bucket_csr_ragged_and_out_of_range(torch_cuda):
     ref = event.scatter_csr(spk, indptr, np.where(keep, indices, 0), np.where(keep, w, 0), n_post)
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)
     S = int(L['qexp'].item())
-    assert S == event.bucket_qexp(w[keep], indices.size)  # max over the valid synapses
+    assert S == event.bucket_qexp(w, indices, n_post)  # W and D over the valid synapses
     assert np.array_equal(got, event.scatter_fixed_point(spk, indptr, indices, w, n_post, S))
 
 
@@ -248,12 +248,16 @@ def _expected_row_groups(s, n_pre, nb):
     (100_000, 50_000, 20, 0.5, True, False, 'u8'),       # R_eff = R (capped)
     (60_000, 30_000, 20, 0.5, True, False, 'f32'),       # R_eff = R, f32 spikes
     (60_000, 30_000, 20, 0.002, False, True, 'f32'),     # R_eff = 1, f32 spikes
-    (3_000, 500_000, 50, 0.01, True, False, 'u8')])      # 41 buckets: 6 sub-ranges each
+    (3_000, 500_000, 50, 0.01, True, False, 'u8'),       # 41 buckets: 6 sub-ranges each
+    (50, 20_000, 30, 0.5, True, True, 'u8'),             # n_pre <= 64: one row group at most
+    (2_000, 1_600_000, 40, 0.3, True, True, 'u8')])      # 131 buckets: one row group at most
 def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, accumulate,
                                           sdt):
     """The step picks its number of row groups from the spikes on the device; whatever it
     picks, the sums are the fixed-point restatement's bit for bit (homogeneous: the
-    sequential scatter's), and accumulate adds onto out with the same arithmetic."""
+    sequential scatter's), and accumulate adds onto out with the same arithmetic.  Mode
+    'dense' on a layout with one row group at most runs as mode 'split' (its one group writes
+    out; the fixed-grid kernel only writes partials)."""
     torch = torch_cuda
     from brainstate_amd import ops
     say('bucket row groups', n_pre, n_post, k, p, het, accumulate, sdt)

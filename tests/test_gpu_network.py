@@ -539,3 +539,51 @@ def test_runner_rejects_bad_connectivity(torch_cuda):
     with pytest.raises(ValueError):
         EINetRunner('lif', 10, 8, idx, np.zeros((2, 4), np.int32), 0.5, 1.0, ops.lif_params(),
                     np.zeros(10, F))
+
+
+@pytest.mark.parametrize('soft,cuba,het,chunks', [
+    (False, False, True, [1, 7, 192]),   # split runs: each starts from the deferred state
+    (True, False, False, [200]),
+    (False, True, True, [50, 150]),
+    (True, True, False, [2, 198])])
+def test_runner_deferred_reset_matches_c(torch_cuda, soft, cuba, het, chunks):
+    """deferred_reset in the persistent runner: the state handed between runs keeps the
+    crossed V of the last step's spiking neurons (reset at the start of the next run with the
+    update's arithmetic; restored after a run from V before its last step).  Counts, hashes
+    and final V, g and ref equal the C restatement's deferred steps at 4,000 neurons, hard
+    and soft reset, COBA and CUBA, per-synapse and homogeneous weights, over split runs; the
+    rasters equal those without deferral."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    say('runner deferred reset', soft, cuba, het, chunks)
+    T = sum(chunks)
+    pe, pi, V0, _ = make_golden.config1_net()
+    c = make_golden.CONFIG1
+    if het:
+        w_e, w_i = make_golden.config1_het_weights(pe.idx.shape, pi.idx.shape)
+    else:
+        w_e, w_i = c['w_e'], c['w_i']
+    kw = dict(spk_reset='soft' if soft else 'hard')
+    if cuba:
+        kw.update(out='cuba', I_ext=14.)
+    p_on = neuron.LIFParams(deferred_reset=True, **kw)
+    c_on, h_on, st = _c_lif(pe.idx, pi.idx, F(w_e) if not het else w_e,
+                            F(w_i) if not het else w_i, p_on, c['n_exc'], V0, T, 0)
+    c_off, h_off, st_off = _c_lif(pe.idx, pi.idx, F(w_e) if not het else w_e,
+                                  F(w_i) if not het else w_i, neuron.LIFParams(**kw),
+                                  c['n_exc'], V0, T, 0)
+    assert np.array_equal(c_on, c_off) and np.array_equal(h_on, h_off)
+    assert int(c_on[-1]) > 0 and not np.array_equal(st['V'], st_off['V'])
+    ok = dict(spk_reset=kw['spk_reset'], deferred_reset=True)
+    if cuba:
+        ok.update(out='cuba', I_ext=14.)
+    r = EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx, w_e, w_i,
+                    ops.lif_params(**ok), V0)
+    counts, hashes = _run_chunks(torch, r, T, chunks)
+    assert np.array_equal(counts, c_on) and np.array_equal(hashes, h_on)
+    assert np.array_equal(r.state['V'].cpu().numpy(), st['V'])
+    assert np.array_equal(r.state['ge'].cpu().numpy(), st['ge'])
+    assert np.array_equal(r.state['ref'].cpu().numpy(), st['ref'])
+    assert np.array_equal(r.spk.cpu().numpy(), st['spk'])

@@ -187,28 +187,44 @@ def test_event_linear_chunked_order(L):
 # ---- bucketed operator: fixed-point exponent and exact sums ----
 
 def test_bucket_qexp_bounds_every_sum():
-    """S keeps every rounded weight below 2^30 in magnitude and is as large as that allows
-    (one more bit would break it for the largest weight), so the weight rounds exactly in fp32
-    and 2^33 events onto one output cannot overflow an int64 sum; rint(w * 2^S) computed in
-    float64 equals its fp32 form (ldexp, rint, convert) for every weight, tiny ones included."""
+    """S = min(30 - e_w - e_d, 100) keeps every output's sum of rounded weights below 2^30 in
+    magnitude (D synapses of |w| <= W onto one output: D * W * 2^S < 2^30) and lies within a
+    factor 4 of the largest S that does (D * W * 2^S > 2^28 unless capped at 100), so a wrong
+    offset or a dropped term fails; rint(w * 2^S) computed in float64 equals its fp32 form
+    (ldexp, rint, convert) for every weight, tiny ones included.  The rule is the runner's:
+    equal to oracle.network.runner_qexp on the same projection."""
+    from oracle import network
     rng = np.random.RandomState(3)
     for _ in range(200):
-        nnz = int(rng.randint(1, 10**8))
+        n_post = int(rng.randint(1, 50))
+        D = int(rng.randint(1, 3000))
         wmax = F(rng.lognormal(0, 8))
-        S = event.bucket_qexp(np.array([wmax, -wmax / 2], F), nnz)
-        assert float(wmax) * 2.0 ** S < 2.0 ** 30
-        assert float(wmax) * 2.0 ** (S + 1) >= 2.0 ** 30
-        assert 2.0 ** 33 * 2.0 ** 30 <= 2.0 ** 63
-        w = np.concatenate([np.array([wmax, -wmax], F),
-                            (rng.uniform(-1, 1, 1000) * wmax).astype(F),
-                            (rng.uniform(-1, 1, 100) * wmax * F(1e-30)).astype(F)])
-        exact = np.rint(w.astype(np.float64) * 2.0 ** S)
-        f32 = np.rint(np.ldexp(w, S).astype(F)).astype(np.float64)
+        # output 0 receives D synapses, the others fewer
+        t = np.concatenate([np.zeros(D, np.int64), rng.randint(0, n_post, D // 2)])
+        t[D:][t[D:] == 0] = n_post - 1 if n_post > 1 else -1
+        w = (rng.uniform(-1, 1, t.size) * wmax).astype(F)
+        w[0] = -wmax
+        S = event.bucket_qexp(w, t, n_post)
+        Dm = int(np.bincount(t[t >= 0], minlength=n_post).max())
+        assert Dm == D
+        assert float(wmax) * Dm * 2.0 ** S < 2.0 ** 30
+        assert S == 100 or float(wmax) * Dm * 2.0 ** S > 2.0 ** 28
+        assert S == network.runner_qexp(t[t >= 0].reshape(1, -1), w[t >= 0].reshape(1, -1),
+                                        n_post)
+        ws = np.concatenate([w, (rng.uniform(-1, 1, 100) * wmax * F(1e-30)).astype(F)])
+        exact = np.rint(ws.astype(np.float64) * 2.0 ** S)
+        f32 = np.rint(np.ldexp(ws, S).astype(F)).astype(np.float64)
         assert np.array_equal(exact, f32) and np.abs(exact).max() <= 2.0 ** 30
-    assert event.bucket_qexp(np.zeros(5, F), 5) == 0
-    assert event.bucket_qexp(np.array([1.0, np.inf], F), 2) == -1000
-    assert event.bucket_qexp(np.array([np.nan], F), 1) == -1000
-    assert event.bucket_qexp(np.array([0.75], F), 1) == 30       # 0.75 < 2^0
+    t1 = np.zeros(1, np.int64)
+    assert event.bucket_qexp(np.zeros(5, F), np.arange(5), 5) == 100     # W = 0: capped
+    assert event.bucket_qexp(np.array([1.0, np.inf], F), np.arange(2), 2) == -1000
+    assert event.bucket_qexp(np.array([np.nan], F), t1, 1) == -1000
+    assert event.bucket_qexp(np.array([0.75], F), t1, 1) == 30          # 0.75 < 2^0, D = 1
+    assert event.bucket_qexp(np.array([1.0, 1.0], F), np.zeros(2), 1) == 28   # 1 < 2^1, D = 2
+    assert event.bucket_qexp(np.array([1.0, 1.0, 1.0], F), np.zeros(3), 1) == 27  # D = 3 <= 4
+    # synapses onto invalid targets enter neither W nor D
+    assert event.bucket_qexp(np.array([0.75, 8.0], F), np.array([0, 5]), 1) == 30
+    assert event.fixed_point_qexp(F(3e38), 2 ** 31) == -1000           # S < -100
 
 
 def test_fixed_point_scatter_is_the_rounded_exact_sum():
@@ -220,7 +236,7 @@ def test_fixed_point_scatter_is_the_rounded_exact_sum():
     idx = rng.randint(0, n_post, (n_pre, k))
     indptr = np.arange(n_pre + 1) * k
     spk = rng.rand(n_pre) < 0.3
-    S = event.bucket_qexp(np.ones(1, F), n_pre * k)
+    S = event.bucket_qexp(np.ones(1, F), np.zeros(1), 1)
     wq = (rng.randint(-2**20, 2**20, n_pre * k) * 2.0 ** -18).astype(F)  # multiples of 2^-18
     got = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), wq, n_post, S)
     exact = np.zeros(n_post)
@@ -232,11 +248,13 @@ def test_fixed_point_scatter_is_the_rounded_exact_sum():
                                      wq.reshape(n_pre, k)[:, perm].reshape(-1), n_post, S)
     assert np.array_equal(got, got2)
     w = rng.normal(0.5, 0.1, n_pre * k).astype(F)
-    Sw = event.bucket_qexp(w, n_pre * k)
+    Sw = event.bucket_qexp(w, idx.reshape(-1), n_post)
     gw = event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, n_post, Sw)
     ref64 = np.zeros(n_post)
     np.add.at(ref64, idx.reshape(-1)[act], w[act].astype(np.float64))
-    assert np.allclose(gw, ref64, rtol=2e-7, atol=1e-12)
+    cnt = np.bincount(idx.reshape(-1)[act], minlength=n_post)
+    # each event's weight rounded to a multiple of 2^-S, then one fp32 rounding of the sum
+    assert np.all(np.abs(gw - ref64) <= cnt * 2.0 ** -(Sw + 1) + 2.0 ** -24 * np.abs(ref64))
     seq = event.scatter_csr(spk, indptr, idx.reshape(-1), w, n_post)
     assert np.allclose(gw, seq, rtol=1e-5, atol=1e-6)
     # a scale off by one bit would be caught
@@ -376,7 +394,7 @@ def test_matvec_2000_matches_golden():
         assert sha(event.scatter_fixed(spk, idx, F(c['w_homo']), c['n_post'])) == \
             case['homo_sha256']
         assert sha(event.scatter_fixed(spk, idx, w, c['n_post'])) == case['het_sequential_sha256']
-        S = event.bucket_qexp(w, idx.size)
+        S = event.bucket_qexp(w, idx, c['n_post'])
         indptr = np.arange(c['n_pre'] + 1, dtype=np.int64) * c['k']
         assert S == case['fixed_point_S']
         assert sha(event.scatter_fixed_point(spk, indptr, idx.reshape(-1), w, c['n_post'], S)) \
