@@ -256,6 +256,7 @@ def bench_sparse(args):
                                       'dense': f'fixed grid, {bkt["_call"][3]} row groups',
                                       'split': f'split, about {hint} row groups'}[
                                           ops.bucket_auto_mode(bkt)],
+                      'bucket_alg_bytes': b_s, 'gather_alg_bytes': b_g,
                       'bucket_alg_GBs': b_s / tb / 1e9, 'bucket_frac': b_s / tb / PEAK_HBM,
                       'fused_matvec_us': tf * 1e6, 'fused_GSOPs': E / tf / 1e9,
                       'scatter_us': ts * 1e6, 'scatter_GSOPs': E / ts / 1e9,
@@ -326,7 +327,7 @@ def bench_event_linear(args):
              'dense_kernel_us': tp * 1e6, 'stream_kernel_us': ts * 1e6, 'pack_us': tk * 1e6,
              'packed_bytes': dig, 'packed_read_GBs': dig / tp / 1e9,
              'step_us': tall * 1e6, 'step_unfused_us': tu * 1e6,
-             'GSOPs': pairs * n / tall / 1e9,
+             'GSOPs': pairs * n / tall / 1e9, 'alg_bytes': b_alg,
              'alg_GBs': b_alg / tall / 1e9, 'frac': b_alg / tall / PEAK_HBM}]
 
 
@@ -350,7 +351,7 @@ def bench_hh(args):
     E = spikes * k
     b = T * n * 49 + spikes * 4 + E * 8
     return [{'workload': 'coba_hh_1m_K80', 'steps': T, 'us_per_step': t / T * 1e6,
-             'spikes': spikes, 'GSOPs': E / t / 1e9, 'alg_GBs': b / t / 1e9,
+             'spikes': spikes, 'GSOPs': E / t / 1e9, 'alg_bytes': b, 'alg_GBs': b / t / 1e9,
              'frac': b / t / PEAK_HBM, 'firing_frac_per_step': spikes / (T * n)}]
 
 
@@ -498,6 +499,8 @@ def main():
                          'the reported line is D = 0, as the config')
     ap.add_argument('--cpu-budget', type=float, default=12.0)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--no-others', action='store_true',
+                    help='leave out the compact records of the other configs')
     ap.add_argument('--no-graph', action='store_true',
                     help='sparse workload: skip the HIP-graph replay timing (counter runs)')
     ap.add_argument('--copy-calibration-mb', type=int, default=0,
@@ -608,7 +611,41 @@ def main():
     if not args.no_cpu:
         print('[bench] timing CPU baseline', file=sys.stderr, flush=True)
         res['cpu_baseline'] = cpu_baseline(idx_e, idx_i, V0, n_exc, k, args.cpu_budget)
+    if not args.no_others and not args.delay_steps:
+        print('[bench] timing the other configs', file=sys.stderr, flush=True)
+        res['other_configs'] = other_configs(args)
     print(json.dumps(res), flush=True)
+
+
+def other_configs(args):
+    """Compact records of BASELINE configs[1], [3] and [4] for the headline line: per
+    kernel, its algorithmic bytes per call, the measured time per call (HIP events) and the
+    fraction of the 8 TB/s roofline those bytes give."""
+    out = []
+    for line in bench_sparse(args):
+        p = line['workload'].rsplit('_p', 1)[1]
+        for kern, t, b in (('bucket', line['bucket_us'], line['bucket_alg_bytes']),
+                           ('gather', line['gather_us'], line['gather_alg_bytes'])):
+            out.append({'config': f'configs[1] event mat-vec 100k x 100k, K=1000, p={p}',
+                        'kernel': {'bucket': 'k_bucket_scatter (+ reduce), destination-'
+                                             'bucketed, ' + line['bucket_mode'],
+                                   'gather': 'k_gather, SELL-64x4'}[kern],
+                        'us_per_call': t, 'alg_bytes': b, 'events': line['events'],
+                        'GSOPs': line['events'] / t / 1e3, 'frac': b / (t * 1e-6) / PEAK_HBM})
+    el = bench_event_linear(args)[0]
+    out.append({'config': 'configs[3] EventLinear [64, 4096] @ 5 % x W [4096, 4096] + LIF, '
+                          '100 steps',
+                'kernel': 'k_event_dense_packed (LIF update fused), W packed once per run',
+                'us_per_call': el['step_us'], 'alg_bytes': el['alg_bytes'],
+                'events': el['events_per_step'], 'GSOPs': el['GSOPs'], 'frac': el['frac'],
+                'product_us': el['dense_kernel_us']})
+    hh = bench_hh(args)[0]
+    out.append({'config': 'configs[4] COBA-HH 1M, K=80, 4000 steps',
+                'kernel': 'k_run<HhModel,4,true> (persistent runner)',
+                'us_per_call': hh['us_per_step'] * hh['steps'], 'us_per_step': hh['us_per_step'],
+                'alg_bytes': hh['alg_bytes'], 'events': hh['spikes'] * 80,
+                'GSOPs': hh['GSOPs'], 'frac': hh['frac']})
+    return out
 
 
 if __name__ == '__main__':

@@ -587,3 +587,56 @@ def test_runner_deferred_reset_matches_c(torch_cuda, soft, cuba, het, chunks):
     assert np.array_equal(r.state['ge'].cpu().numpy(), st['ge'])
     assert np.array_equal(r.state['ref'].cpu().numpy(), st['ref'])
     assert np.array_equal(r.spk.cpu().numpy(), st['spk'])
+
+
+def test_config3_full_length_matches_c(torch_cuda):
+    """Config [3] for its whole run: 1M LIF neurons, K = 100, per-synapse weights
+    N(0.6, 0.06) / N(6.7, 0.67), 10,000 steps in the bench's instantiation (4 neurons per
+    thread), split over two runs: every step's spike count and hash and the final V, g_e, g_i,
+    refractory counters and spikes equal the C restatement's."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    torch = torch_cuda
+    n, T = 1_000_000, 10_000
+    say('config [3] full length', n, T)
+    n_exc, idx_e, idx_i, w_e, w_i, V0 = _big_net(n, 100, 300, 'normal')
+    r = EINetRunner('lif', n, n_exc, idx_e, idx_i, w_e, w_i, ops.lif_params(), V0)
+    counts, hashes = _run_chunks(torch, r, T, [3000, 7000])
+    say('  gpu done, running the C restatement on', _host_threads(), 'threads')
+    c_ref, h_ref, st = _c_lif(idx_e, idx_i, w_e, w_i, neuron.LIFParams(), n_exc, V0, T, 0,
+                              nthreads=_host_threads())
+    assert c_ref.sum() > T * 1000   # ~0.1-0.2 % of the neurons fire per step
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    for key in ('V', 'ge', 'gi', 'ref'):
+        assert np.array_equal(r.state[key].cpu().numpy(), st[key]), key
+    assert np.array_equal(r.spk.cpu().numpy(), st['spk'])
+
+
+def test_config5_full_length_matches_c(torch_cuda):
+    """Config [5] for its whole run: 1M COBA-HH neurons, K = 80, per-synapse weights
+    N(0.05, 0.005) / N(0.3, 0.03), dt 0.05 ms, 4,000 steps: every step's spike count and hash
+    and the final V, m, h, n, g_e, g_i equal the C restatement's."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    from oracle import neuron
+    torch = torch_cuda
+    n, k, T = 1_000_000, 80, 4000
+    say('config [5] full length', n, T)
+    n_exc = n * 4 // 5
+    idx_e = np.random.RandomState(211).randint(0, n, size=(n_exc, k)).astype(np.int32)
+    idx_i = np.random.RandomState(212).randint(0, n, size=(n - n_exc, k)).astype(np.int32)
+    V0 = np.random.RandomState(213).uniform(-70., -50., n).astype(F)
+    w_e = np.random.RandomState(214).normal(0.05, 0.005, idx_e.shape).astype(F)
+    w_i = np.random.RandomState(215).normal(0.3, 0.03, idx_i.shape).astype(F)
+    r = EINetRunner('hh', n, n_exc, idx_e, idx_i, w_e, w_i, ops.hh_params(I_ext=6.5), V0)
+    counts, hashes = _run_chunks(torch, r, T, [T])
+    say('  gpu done, running the C restatement on', _host_threads(), 'threads')
+    c_ref, h_ref, st = _c_hh(idx_e, idx_i, w_e, w_i, neuron.HHParams(I_ext=6.5), n_exc, V0, T,
+                             nthreads=_host_threads())
+    assert c_ref.sum() > T * 100
+    assert counts.tolist() == c_ref.tolist()
+    assert hashes.tolist() == h_ref.tolist()
+    for key in ('V', 'm', 'h', 'n', 'ge', 'gi'):
+        assert np.array_equal(r.state[key].cpu().numpy(), st[key]), key

@@ -314,8 +314,8 @@ def test_event_matvec_fused(torch_cuda, n_pre, n_post, k, p, het, csr):
         out = ops.event_matvec(dev(torch, spk.astype(np.uint8)), dev(torch, idx),
                                dev(torch, w) if het else float(w), n_post)
     got = out.cpu().numpy()
-    if het:
-        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    if het:   # the north_star tolerance of the atomic path
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
     else:
         assert np.array_equal(got, ref)
 
