@@ -275,6 +275,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     for (int i = 0; i < (int)(sizeof(p) / 4); ++i) asm volatile("" : "+v"(pw[i]));
   }
   constexpr int kChunk = NPT * kBlock;
+  static_assert(kChunk < 65536, "a workgroup's E and I spike counts share one 32-bit word");
   constexpr int kBatch = 4;                   // phase A: entry loads in flight per thread
   constexpr int kChunks = 4;                  // phase D: 64-synapse chunks per wave and round
   constexpr int kSlots = NPT >= 8 ? 8 : 16;   // phase D: LDS slots per destination and round
@@ -284,7 +285,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   __shared__ uint64_t s_ofs_in[kMaxBlocks];   // inbox offset (me <- s)
   __shared__ uint32_t s_ofs_out[kMaxBlocks];  // first inbox entry of (d <- me)
   __shared__ int32_t s_list[kChunk];          // this step's spikes: E from the front, I from the back
-  __shared__ uint32_t s_nsp[2][2];            // (E, I) spike counts, by step parity
+  __shared__ uint32_t s_nsp[2];               // E | I << 16 spike counts, by step parity
   __shared__ uint32_t s_hash;
   __shared__ uint32_t s_ovf;                  // an entry of this step was stored past the slots
   __shared__ uint32_t s_junk[BS_WAVE];        // destination of the row prefetches (never read)
@@ -366,7 +367,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     asm volatile("" : "+v"(a.n_exc), "+v"(a.k_e), "+v"(a.k_i), "+v"(a.w_e_homo), "+v"(a.w_i_homo));
   }
   if (threadIdx.x == 0) {
-    s_nsp[0][0] = s_nsp[0][1] = s_nsp[1][0] = s_nsp[1][1] = 0;
+    s_nsp[0] = s_nsp[1] = 0;
     s_ovf = 0u;
     s_hash = 0;
   }
@@ -488,8 +489,10 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
 
     // ---- C: block list of this step's spikes ----
     // E spikes fill s_list from the front and I spikes from the back; each wave reserves its
-    // ranges with one LDS atomic per kind (no scan, one barrier).
-    uint32_t* nsp2 = s_nsp[ta & 1];  // [0]: E spikes, [1]: I spikes of this step
+    // two ranges with one LDS atomic on a word holding both counts (at most 8192 each: no
+    // carry between the halves), no scan, one barrier.  One atomic per wave instead of one
+    // per kind: config [3] 7.20 -> 7.16 us per step.
+    uint32_t* nsp2 = &s_nsp[ta & 1];  // this step's E spikes (bits 0-15), I spikes (16-31)
     {
       uint64_t mE[NPT], mI[NPT];
       uint32_t wE = 0, wI = 0;
@@ -501,13 +504,10 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         wE += (uint32_t)__popcll(mE[q]);
         wI += (uint32_t)__popcll(mI[q]);
       }
-      uint32_t bE = 0, bI = 0;
-      if (lane == 0) {
-        if (wE) bE = atomicAdd(&nsp2[0], wE);
-        if (wI) bI = atomicAdd(&nsp2[1], wI);
-      }
-      bE = __builtin_amdgcn_readfirstlane(bE);
-      bI = __builtin_amdgcn_readfirstlane(bI);
+      uint32_t b = 0;
+      if (lane == 0 && (wE | wI)) b = atomicAdd(nsp2, wE | (wI << 16));
+      b = __builtin_amdgcn_readfirstlane(b);
+      uint32_t bE = b & 0xFFFFu, bI = b >> 16;
 #pragma unroll
       for (int q = 0; q < NPT; ++q) {
         const int32_t j = (int32_t)(jv0 + q * kBlock);
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     if (h) atomicAdd(&s_hash, h);
     __syncthreads();
     if (threadIdx.x == 0) {  // per-workgroup partials, summed over workgroups after the launch
-      if (a.counts) a.counts[(int64_t)t * nb + me] = nsp2[0] + nsp2[1];
+      if (a.counts) a.counts[(int64_t)t * nb + me] = (*nsp2 & 0xFFFFu) + (*nsp2 >> 16);
       if (a.hash) a.hash[(int64_t)t * nb + me] = s_hash;
       // s_hash's last reader; the next adds come after this step's final barrier
       s_hash = 0;
@@ -537,8 +537,8 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // After one barrier the slots are written out destination by destination, so consecutive
     // lanes store to consecutive inbox addresses, and each destination's cursor advances.
     char* ob = inbox + (size_t)slot_wr * buf_bytes;
-    const uint32_t nE = __builtin_amdgcn_readfirstlane(nsp2[0]);
-    const uint32_t nI = __builtin_amdgcn_readfirstlane(nsp2[1]);
+    const uint32_t nEI = __builtin_amdgcn_readfirstlane(*nsp2);
+    const uint32_t nE = nEI & 0xFFFFu, nI = nEI >> 16;
     const uint32_t gE = nE << lgE;
     const uint32_t G = gE + (nI << lgI);
     constexpr uint32_t kPer = kWaves * kChunks;
@@ -660,10 +660,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
       // above, and their next user is step ta+2, whose adds follow step ta+1's final
       // barrier.  (Clearing the other parity here would race with step ta+1's adds when
       // phase A has no barrier, i.e. while ta+1 <= D.)
-      if (threadIdx.x == 0) {
-        s_nsp[ta & 1][0] = 0;
-        s_nsp[ta & 1][1] = 0;
-      }
+      if (threadIdx.x == 0) s_nsp[ta & 1] = 0;
     }
     slot_rd = slot_rd + 1 == ring ? 0 : slot_rd + 1;
     slot_wr = slot_wr + 1 == ring ? 0 : slot_wr + 1;
