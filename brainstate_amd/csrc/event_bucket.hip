@@ -21,8 +21,10 @@
 // Step (bs_event_bucket_f32): workgroup (b, r) owns bucket b and the pre rows of row group r.
 // It compacts the active rows of its group into LDS (ballots), loads their bucket-b bounds,
 // and accumulates their bucket-b synapses into an LDS copy of the bucket with integer LDS
-// atomics: each weight rounded to a multiple of 2^-S and added as a 64-bit integer (event
-// counts for a homogeneous weight).  It writes the bucket as partial r; a second kernel adds
+// atomics: each weight rounded to a multiple of 2^-S and added as a 32-bit integer (event
+// counts for a homogeneous weight); every sum of rounded weights stays below 2^31 in
+// magnitude, so 32-bit two's complement adds are exact (64-bit accumulators and partials
+// before the runner's exponent rule made that bound hold: config [2] p = 0.1 ... us).  It writes the bucket as partial r; a second kernel adds
 // the partials exactly and rounds once: out = fl32(sum) * 2^-S, whatever the order of the
 // atomics (deterministic), within half an fp32 ulp of the exact sum of the rounded weights.
 // Homogeneous weights: the exact event count c, then w added c times in one chain, which is
@@ -39,7 +41,7 @@
 // and workgroup 0 leaves the next call's hint from the exact active count instead (config
 // [2] p = 0.001: 12.4 -> 11.6 us per step).  Integer sums make the result
 // independent of R_eff and of the partition.  HBM traffic: the active rows' synapses once
-// (E x (2 + 4 het) bytes) + R_eff partial rows of n_post x 8 bytes written and read (none
+// (E x (2 + 4 het) bytes) + R_eff partial rows of n_post x 4 bytes written and read (none
 // at R_eff = 1).
 #include <type_traits>
 
@@ -49,7 +51,7 @@ namespace {
 
 constexpr int kBB = 256;          // build: threads per workgroup (one wave per row)
 constexpr int kSB = 1024;         // step: threads per workgroup
-constexpr int kMaxP = 12288;      // posts per bucket (96 KiB of 64-bit LDS accumulators)
+constexpr int kMaxP = 12288;      // posts per bucket (48 KiB of 32-bit LDS accumulators)
 constexpr int kMaxNb = 1024;      // buckets
 // Measured on MI355X at config [2] (100k x 100k, K = 1000, p = 0.1): 9 buckets of 11,112
 // posts with 28 row groups 30 us; 16 buckets 34 us; 32 buckets 48 us; 8 rows per wave with one
@@ -275,17 +277,6 @@ __device__ __forceinline__ uint32_t spike_bits(uint4 v) {
   return m;
 }
 
-// fl32(q), round to nearest even: below 2^53 in magnitude q is exact in double (high word
-// * 2^32 + low word, both exact), so one double -> float rounding gives fl32(q); above, the
-// compiler's 64-bit conversion.
-__device__ __forceinline__ float i64_to_f32(int64_t q) {
-  if ((uint64_t)(q + (1ll << 53)) < (1ull << 54)) {
-    const double d = (double)(int32_t)(q >> 32) * 4294967296.0 + (double)(uint32_t)q;
-    return (float)d;
-  }
-  return (float)q;
-}
-
 // spike_bits, skipped (0) for the whole wave when none of its 64 blocks holds a non-zero
 // word: two VALU ops and a ballot instead of the byte tests (sparse spikes leave many waves'
 // blocks empty).
@@ -332,11 +323,12 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
     const int32_t* __restrict__ seg, const uint16_t* __restrict__ lidx,
     const float* __restrict__ lw, const int32_t* __restrict__ qexp, int32_t n_post,
     float w_homo, int32_t accumulate, float* __restrict__ out, int32_t* __restrict__ hdr,
-    int32_t* __restrict__ est_out, uint64_t* __restrict__ part) {
+    int32_t* __restrict__ est_out, uint32_t* __restrict__ part) {
   constexpr int kE = 16 / (int)sizeof(T);  // rows per block
   constexpr int kW = kSB / BS_WAVE;
-  __shared__ __align__(16) uint64_t s_acc[kMaxP];  // fixed-point sums, fp32 sums or counts
-  uint32_t* s_acc32 = (uint32_t*)s_acc;
+  // fixed-point sums (two's complement; every sum is below 2^31 in magnitude by the choice of
+  // S), fp32 sums or event counts
+  __shared__ __align__(16) uint32_t s_acc32[kMaxP];
   __shared__ int32_t s_beg[kSpan];
   __shared__ int32_t s_len[kSpan];
   __shared__ int32_t s_wave[2][kW];
@@ -421,7 +413,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
   const int32_t lo_t = sub * ps;
   const int32_t pn = pnb - lo_t < ps ? (pnb - lo_t > 0 ? pnb - lo_t : 0) : ps;
   const int32_t p0 = b * P + lo_t;
-  for (int j = threadIdx.x; 2 * j < pn; j += kSB) ((uint4*)s_acc)[j] = make_uint4(0u, 0u, 0u, 0u);
+  for (int j = threadIdx.x; 4 * j < pn; j += kSB) ((uint4*)s_acc32)[j] = make_uint4(0u, 0u, 0u, 0u);
   uint32_t smk[kSmpD];  // masks of the sample's blocks
   uint32_t cs = 0;
 #pragma unroll
@@ -538,8 +530,8 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
               if (!kHet) {
                 atomicAdd(&s_acc32[tl], 1u);
               } else if (fixed) {
-                const int64_t qv = (int64_t)(int32_t)__builtin_rintf(__builtin_ldexpf(v[u][q], S));
-                atomicAdd((unsigned long long*)&s_acc[tl], (unsigned long long)qv);
+                const int32_t qv = (int32_t)__builtin_rintf(__builtin_ldexpf(v[u][q], S));
+                atomicAdd(&s_acc32[tl], (uint32_t)qv);
               } else {
                 atomicAdd((float*)&s_acc32[tl], v[u][q]);
               }
@@ -707,7 +699,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
     for (int j = threadIdx.x; j < pn; j += kSB) {
       float acc = accumulate ? o[j] : 0.0f;
       if (kHet && fixed) {
-        const float v = ldexpf(i64_to_f32((int64_t)s_acc[j]), -S);
+        const float v = ldexpf((float)(int32_t)s_acc32[j], -S);
         acc = accumulate ? acc + v : v;
       } else if (kHet) {
         acc += __uint_as_float(s_acc32[j]);
@@ -718,12 +710,8 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
       o[j] = acc;
     }
   } else {
-    uint64_t* dst = part + (int64_t)r * n_post + p0;
-    if (kHet && fixed) {
-      for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc[j];
-    } else {
-      for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
-    }
+    uint32_t* dst = part + (int64_t)r * n_post + p0;
+    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
   }
 }
 
@@ -739,9 +727,8 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
     const T* __restrict__ spk, int32_t n_pre, int32_t rows, int32_t R, int32_t Rmax, int32_t nb,
     int32_t P, const int32_t* __restrict__ seg, const uint16_t* __restrict__ lidx,
     const float* __restrict__ lw, const int32_t* __restrict__ qexp, int32_t n_post,
-    int32_t* __restrict__ hdr, int32_t* __restrict__ est_out, uint64_t* __restrict__ part) {
-  __shared__ uint64_t s_acc[kMaxP];        // fixed-point sums, fp32 sums or event counts
-  uint32_t* s_acc32 = (uint32_t*)s_acc;
+    int32_t* __restrict__ hdr, int32_t* __restrict__ est_out, uint32_t* __restrict__ part) {
+  __shared__ uint32_t s_acc32[kMaxP];      // fixed-point sums, fp32 sums or event counts
   constexpr int kU = kSpan / kSB;          // span rows per thread
   __shared__ int32_t s_beg[kSpan];
   __shared__ int32_t s_len[kSpan];
@@ -752,7 +739,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
   const int32_t r = blockIdx.x / nb;
   const int32_t p0 = b * P;
   const int32_t pn = n_post - p0 < P ? n_post - p0 : P;  // posts in this bucket
-  for (int j = threadIdx.x; j < pn; j += kSB) s_acc[j] = 0ull;
+  for (int j = threadIdx.x; j < pn; j += kSB) s_acc32[j] = 0u;
   // fixed point (S >= -999) unless a weight is not finite; scale = 2^S exactly
   const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
   const bool fixed = kHet && S > -1000;
@@ -841,8 +828,8 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
               if (!kHet) {
                 atomicAdd(&s_acc32[t[u][q]], 1u);
               } else if (fixed) {
-                const int64_t qv = (int64_t)(int32_t)__builtin_rintf(__builtin_ldexpf(v[u][q], S));
-                atomicAdd((unsigned long long*)&s_acc[t[u][q]], (unsigned long long)qv);
+                const int32_t qv = (int32_t)__builtin_rintf(__builtin_ldexpf(v[u][q], S));
+                atomicAdd(&s_acc32[t[u][q]], (uint32_t)qv);
               } else {
                 atomicAdd((float*)&s_acc32[t[u][q]], v[u][q]);
               }
@@ -860,70 +847,66 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
     *est_out = re < 1.0 ? 1 : (re > (double)Rmax ? Rmax : (int32_t)re);
   }
   __syncthreads();
-  uint64_t* dst = part + (int64_t)r * n_post + p0;
-  if (kHet && fixed) {
-    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc[j];
-  } else {
-    for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
-  }
+  uint32_t* dst = part + (int64_t)r * n_post + p0;
+  for (int j = threadIdx.x; j < pn; j += kSB) dst[j] = s_acc32[j];
 }
 
 // out[j] = (accumulate ? out[j] : 0) + the bucket sums of j, over the R = *hdr partials the
 // step kernel wrote (R = 1: it wrote out itself, nothing to do).  The first min(8, Rmax)
 // partials are loaded together with the header, not after it: one memory round trip, not two.
-//   fixed point: the R partials added exactly (64-bit), then fl32(sum) * 2^-S;
+//   fixed point: the R partials added exactly (32-bit two's complement: every partial and the
+//   total are below 2^31 in magnitude by the choice of S), then fl32(sum) * 2^-S;
 //   homogeneous: the total count c of events, then c additions of w (the sequential chain);
 //   fp32 fallback: the R partials added in row-group order.
 template <bool kHet>
 __global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t Rmax, int32_t Rfix,
                                                        const int32_t* __restrict__ hdr,
-                                                       const uint64_t* __restrict__ part,
+                                                       const uint32_t* __restrict__ part,
                                                        const int32_t* __restrict__ qexp,
                                                        float w_homo, int32_t accumulate,
                                                        float* __restrict__ out) {
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= n_post) return;
   constexpr int kFirst = 8;
-  uint64_t x0[kFirst];
+  uint32_t x0[kFirst];
 #pragma unroll
-  for (int u = 0; u < kFirst; ++u) x0[u] = u < Rmax ? part[(int64_t)u * n_post + j] : 0ull;
+  for (int u = 0; u < kFirst; ++u) x0[u] = u < Rmax ? part[(int64_t)u * n_post + j] : 0u;
   const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
   float acc = accumulate ? out[j] : 0.0f;
   // Rfix > 0: the host fixed the row groups, no header to wait for
   const int32_t R = Rfix > 0 ? Rfix : __builtin_amdgcn_readfirstlane(*hdr);
   // (the loads above are consumed on both paths, so they stay ahead of this test)
-  uint64_t any = __float_as_uint(acc) + (uint32_t)S;
+  uint32_t any = __float_as_uint(acc) + (uint32_t)S;
 #pragma unroll
   for (int u = 0; u < kFirst; ++u) any |= x0[u];
-  if (R <= 1 && any != 0x5A5A5A5A5A5A5A5Aull) return;
+  if (R <= 1 && any != 0x5A5A5A5Au) return;
   const int32_t r0 = R < kFirst ? R : kFirst;
   if (kHet && S > -1000) {
-    int64_t q = 0;
+    uint32_t q = 0;   // wrap-around adds: the true sum fits, so the result is exact
 #pragma unroll
-    for (int u = 0; u < kFirst; ++u) q += u < r0 ? (int64_t)x0[u] : 0;
+    for (int u = 0; u < kFirst; ++u) q += u < r0 ? x0[u] : 0u;
     int32_t r = r0;
     for (; r + 8 <= R; r += 8) {
-      int64_t x[8];
+      uint32_t x[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = (int64_t)part[(int64_t)(r + u) * n_post + j];
+      for (int u = 0; u < 8; ++u) x[u] = part[(int64_t)(r + u) * n_post + j];
 #pragma unroll
       for (int u = 0; u < 8; ++u) q += x[u];
     }
-    for (; r < R; ++r) q += (int64_t)part[(int64_t)r * n_post + j];
-    const float v = ldexpf(i64_to_f32(q), -S);
+    for (; r < R; ++r) q += part[(int64_t)r * n_post + j];
+    const float v = ldexpf((float)(int32_t)q, -S);
     acc = accumulate ? acc + v : v;
   } else if (kHet) {
     // fp32 fallback: the partials in row-group order
 #pragma unroll
     for (int u = 0; u < kFirst; ++u)
-      if (u < r0) acc += __uint_as_float((uint32_t)x0[u]);
-    for (int32_t r = r0; r < R; ++r)
-      acc += __uint_as_float((uint32_t)part[(int64_t)r * n_post + j]);
+      if (u < r0) acc += __uint_as_float(x0[u]);
+    for (int32_t r = r0; r < R; ++r) acc += __uint_as_float(part[(int64_t)r * n_post + j]);
   } else {
     uint32_t c = 0;
 #pragma unroll
-    for (int u = 0; u < kFirst; ++u) c += u < r0 ? (uint32_t)x0[u] : 0u;
-    for (int32_t r = r0; r < R; ++r) c += (uint32_t)part[(int64_t)r * n_post + j];
+    for (int u = 0; u < kFirst; ++u) c += u < r0 ? x0[u] : 0u;
+    for (int32_t r = r0; r < R; ++r) c += part[(int64_t)r * n_post + j];
     for (uint32_t u = 0; u < c; ++u) acc += w_homo;
   }
   out[j] = acc;
@@ -1020,7 +1003,7 @@ extern "C" int bs_bucket_build(int32_t n_pre, const int32_t* indptr, const int32
 extern "C" size_t bs_event_bucket_workspace_size(int32_t n_pre, int32_t n_post, int32_t nb) {
   bs_clear_error();
   if (n_pre <= 0 || n_post <= 0 || nb <= 0) return 0;
-  return (size_t)kHdr + (size_t)row_groups(n_pre, nb) * n_post * sizeof(uint64_t);
+  return (size_t)kHdr + (size_t)row_groups(n_pre, nb) * n_post * sizeof(uint32_t);
 }
 
 extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n_pre,
@@ -1059,14 +1042,14 @@ extern "C" int bs_event_bucket_f32(const void* spk, int32_t spk_dtype, int32_t n
     if (nsub > P) nsub = P;
     if (nsub < 1) nsub = 1;
   }
-  const size_t need = (size_t)kHdr + (single_launch ? 0 : (size_t)R * n_post * sizeof(uint64_t));
+  const size_t need = (size_t)kHdr + (single_launch ? 0 : (size_t)R * n_post * sizeof(uint32_t));
   BS_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                "bs_event_bucket_f32: workspace of %zu bytes needed (got %zu)", need,
                workspace ? workspace_bytes : (size_t)0);
   BS_CHECK_ARG((uintptr_t)workspace % 8 == 0,
                "bs_event_bucket_f32: workspace not 8-byte aligned");
   int32_t* hdr = (int32_t*)workspace;  // R_eff, written by the step kernel
-  uint64_t* part = (uint64_t*)((char*)workspace + kHdr);
+  uint32_t* part = (uint32_t*)((char*)workspace + kHdr);
   const int64_t g = (int64_t)nb * nsub * R;
   const bool vec = (uintptr_t)spk % 16 == 0;  // 16-byte spike loads
 #define BS_BK(T, H, V)                                                                      \

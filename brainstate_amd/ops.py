@@ -320,7 +320,7 @@ def _bucket_call_args(L):
     once per layout (the tensors they point into live in the layout dict)."""
     opt = lambda t: N.ptr(t) if t is not None else None
     nbytes = int(N.lib().bs_event_bucket_workspace_size(L['n_pre'], L['n_post'], L['nb']))
-    rmax = (nbytes - 256) // (8 * L['n_post']) if nbytes > 0 else 1   # row groups at most
+    rmax = (nbytes - 256) // (4 * L['n_post']) if nbytes > 0 else 1   # row groups at most
     return ((L['n_pre'], L['n_post'], L['nb'], L['P'], N.ptr(L['seg']), N.ptr(L['lidx']),
              opt(L['w']), opt(L['qexp']), L['w_homo']), nbytes,
             (L['seg'], L['lidx'], L['w'], L['qexp']), rmax)

@@ -157,7 +157,7 @@ BS_API int bs_event_matvec_vjp_batch_f32(const void* spk, int32_t spk_dtype, int
  *        below 2^30 in magnitude (-1000 if a weight is not finite or S < -100).
  * bs_event_bucket_f32: out[j] = (accumulate ? out[j] : 0) + v_j, where v_j is
  *   - per-synapse weights, finite: each weight of an event onto j rounded to a multiple of
- *     2^-S (round to nearest even), the rounded weights summed exactly (64-bit integers),
+ *     2^-S (round to nearest even), the rounded weights summed exactly (32-bit integers),
  *     the sum rounded once to fp32 and scaled by 2^-S: deterministic, whatever the order of
  *     the device's atomics;
  *   - homogeneous weight (lw == NULL): w_homo added once per event onto j, in one chain
