@@ -134,19 +134,19 @@ class _BatchedEINet:
     """Config [1]'s E/I net (examples/105_COBA_HH_2007_braincell.py:54-82) with states
     [B, n]: replica b starts from its own V0."""
 
-    def __init__(self, bs, V0s):
+    def __init__(self, bs, V0s, w_e=0.6, w_i=6.7):
         c = make_golden.CONFIG1
         self.bs = bs
         self.n_exc, self.num = c['n_exc'], c['n']
         self.N = bs.nn.LIFRef(self.num, V_rest=-60., V_th=-50., V_reset=-60., tau=20.,
                               tau_ref=5., V_initializer=V0s)
         self.E = bs.nn.AlignPostProj(
-            comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=0.02, conn_weight=0.6,
+            comm=bs.nn.EventFixedProb(self.n_exc, self.num, conn_num=0.02, conn_weight=w_e,
                                       seed=c['seed_e']),
             syn=bs.nn.Expon.desc(self.num, tau=5.), out=bs.nn.COBA.desc(E=0.), post=self.N)
         self.I = bs.nn.AlignPostProj(
             comm=bs.nn.EventFixedProb(self.num - self.n_exc, self.num, conn_num=0.02,
-                                      conn_weight=6.7, seed=c['seed_i']),
+                                      conn_weight=w_i, seed=c['seed_i']),
             syn=bs.nn.Expon.desc(self.num, tau=10.), out=bs.nn.COBA.desc(E=-80.), post=self.N)
         for m in (self.E.syn, self.I.syn, self.N):
             m.init_state(batch_size=V0s.shape[0])
@@ -248,3 +248,33 @@ def test_batched_net_per_replica_input(bs):
         r.write_back()
     for b in range(B):
         assert np.array_equal(net.N.V.value[b].cpu().numpy(), refs[b]['V']), b
+
+
+def test_batched_net_per_synapse_weights(bs):
+    """Replicas sharing per-synapse weights N(0.6, 0.06) / N(6.7, 0.67): the eager batched step
+    takes the bucketed operator row by row (the runner's fixed-point sums), so stepping eagerly,
+    for_loop through the union runner and each replica's oracle run agree bit for bit."""
+    import torch
+    B, T = 3, 200
+    say('batched net, per-synapse weights', B, T)
+    V0s = _replica_V0(B)
+    pe, pi, _, p = make_golden.config1_het_net()
+    p.deferred_reset = True
+    refs = [network.run_coba_lif(V0s[b], pe, pi, p, 3200, T) for b in range(B)]
+    assert all(int(r['counts'].sum()) > 300 for r in refs)
+    out = {}
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                net = _BatchedEINet(bs, V0s, w_e=pe.w, w_i=pi.w)
+                spikes = bs.transform.for_loop(net.update, torch.arange(T) * 0.1)
+        finally:
+            bs.transform.fuse_loops = True
+        assert bs.transform.last_loop == ('fused' if fused else 'eager')
+        out[fused] = spikes
+        for b in range(B):
+            assert np.array_equal(spikes[:, b].cpu().numpy() != 0, refs[b]['raster']), (fused, b)
+            assert np.array_equal(net.N.V.value[b].cpu().numpy(), refs[b]['V']), (fused, b)
+            assert np.array_equal(net.I.syn.g.value[b].cpu().numpy(), refs[b]['gi']), (fused, b)
+    assert torch.equal(out[False], out[True])
