@@ -70,6 +70,7 @@ constexpr int kSpan = 4096;       // active rows held in LDS before their synaps
 constexpr int kTargetWgs = 256;   // step grid the row groups aim for
 constexpr int kMinRows = 64;      // rows per row group, at least (and the group alignment)
 constexpr int kMinNb = 8;         // buckets, at least (the grid is nb x row groups)
+constexpr int kMaxR = kTargetWgs / kMinNb;  // row groups, at most (the reduce holds them all)
 constexpr int kSample = 16384;    // leading spike rows whose active count sets R_eff
 // active rows per row group the step aims for: measured at config [2] (mode 0, HIP graph)
 // p = 0.003 / 0.01 with 256: 16.5 / 19.05 us, 128: 15.4 / 19.07 us (one box); on another,
@@ -853,7 +854,10 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
 
 // out[j] = (accumulate ? out[j] : 0) + the bucket sums of j, over the R = *hdr partials the
 // step kernel wrote (R = 1: it wrote out itself, nothing to do).  The first min(8, Rmax)
-// partials are loaded together with the header, not after it: one memory round trip, not two.
+// partials are loaded together with the header, and the rest (R <= kMaxR) all together once R
+// is known: two memory round trips in all (issued 8 at a time, then one by one, they took up
+// to 7 at R = 28: 100k x 100k, K = 1000, p = 0.1 26.4 -> 25.4 us per call, p = 0.03 18.0 ->
+// 17.0 us).
 //   fixed point: the R partials added exactly (32-bit two's complement: every partial and the
 //   total are below 2^31 in magnitude by the choice of S), then fl32(sum) * 2^-S;
 //   homogeneous: the total count c of events, then c additions of w (the sequential chain);
@@ -868,9 +872,9 @@ __global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t R
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= n_post) return;
   constexpr int kFirst = 8;
-  uint32_t x0[kFirst];
+  uint32_t x[kMaxR];   // the partials of j in row-group order (0 past R)
 #pragma unroll
-  for (int u = 0; u < kFirst; ++u) x0[u] = u < Rmax ? part[(int64_t)u * n_post + j] : 0u;
+  for (int u = 0; u < kFirst; ++u) x[u] = u < Rmax ? part[(int64_t)u * n_post + j] : 0u;
   const int32_t S = kHet ? __builtin_amdgcn_readfirstlane(*qexp) : 0;
   float acc = accumulate ? out[j] : 0.0f;
   // Rfix > 0: the host fixed the row groups, no header to wait for
@@ -878,35 +882,29 @@ __global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t R
   // (the loads above are consumed on both paths, so they stay ahead of this test)
   uint32_t any = __float_as_uint(acc) + (uint32_t)S;
 #pragma unroll
-  for (int u = 0; u < kFirst; ++u) any |= x0[u];
+  for (int u = 0; u < kFirst; ++u) any |= x[u];
   if (R <= 1 && any != 0x5A5A5A5Au) return;
-  const int32_t r0 = R < kFirst ? R : kFirst;
+  // the rest in one round trip: all loads issued before any is added
+#pragma unroll
+  for (int u = 0; u < kFirst; ++u)
+    if (u >= R) x[u] = 0u;
+#pragma unroll
+  for (int u = kFirst; u < kMaxR; ++u) x[u] = u < R ? part[(int64_t)u * n_post + j] : 0u;
   if (kHet && S > -1000) {
     uint32_t q = 0;   // wrap-around adds: the true sum fits, so the result is exact
 #pragma unroll
-    for (int u = 0; u < kFirst; ++u) q += u < r0 ? x0[u] : 0u;
-    int32_t r = r0;
-    for (; r + 8 <= R; r += 8) {
-      uint32_t x[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) x[u] = part[(int64_t)(r + u) * n_post + j];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) q += x[u];
-    }
-    for (; r < R; ++r) q += part[(int64_t)r * n_post + j];
+    for (int u = 0; u < kMaxR; ++u) q += x[u];
     const float v = ldexpf((float)(int32_t)q, -S);
     acc = accumulate ? acc + v : v;
   } else if (kHet) {
     // fp32 fallback: the partials in row-group order
 #pragma unroll
-    for (int u = 0; u < kFirst; ++u)
-      if (u < r0) acc += __uint_as_float(x0[u]);
-    for (int32_t r = r0; r < R; ++r) acc += __uint_as_float(part[(int64_t)r * n_post + j]);
+    for (int u = 0; u < kMaxR; ++u)
+      if (u < R) acc += __uint_as_float(x[u]);
   } else {
     uint32_t c = 0;
 #pragma unroll
-    for (int u = 0; u < kFirst; ++u) c += u < r0 ? x0[u] : 0u;
-    for (int32_t r = r0; r < R; ++r) c += part[(int64_t)r * n_post + j];
+    for (int u = 0; u < kMaxR; ++u) c += x[u];
     for (uint32_t u = 0; u < c; ++u) acc += w_homo;
   }
   out[j] = acc;
@@ -914,6 +912,7 @@ __global__ __launch_bounds__(256) void k_bucket_reduce(int32_t n_post, int32_t R
 
 int32_t row_groups(int32_t n_pre, int32_t nb) {
   int64_t R = kTargetWgs / (nb > 0 ? nb : 1);
+  if (R > kMaxR) R = kMaxR;  // fewer than kMinNb buckets (a caller's own layout, tiny n_post)
   const int64_t rmax = ((int64_t)n_pre + kMinRows - 1) / kMinRows;
   if (R > rmax) R = rmax;
   if (R < 1) R = 1;
