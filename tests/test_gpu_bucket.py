@@ -248,12 +248,17 @@ def _bucket_ws_header(torch, dev_index=0):
 
 def _expected_row_groups(s, n_pre, nb):
     """The documented rule: R_eff = ceil(active rows of the leading min(n_pre, 16384) rows,
-    scaled to n_pre, / 128), within [1, R], R = min(256 // nb, ceil(n_pre / 64))."""
+    scaled to n_pre, / 128), within [1, R], R = min(256 // nb, 32, ceil(n_pre / 64))."""
     ns = min(n_pre, 16384)
     act = int(np.count_nonzero(np.asarray(s)[:ns]))
     re = -(-act * n_pre // (ns * 128))
-    R = max(1, min(256 // nb, -(-n_pre // 64)))
-    return max(1, min(R, re))
+    return max(1, min(_max_row_groups(n_pre, nb), re))
+
+
+def _max_row_groups(n_pre, nb):
+    """R = min(256 // nb, 32, ceil(n_pre / 64)): 32 row groups at most whatever nb (a layout
+    of fewer than 8 buckets would otherwise have up to 256 partial rows to add)."""
+    return max(1, min(256 // nb, 32, -(-n_pre // 64)))
 
 
 @pytest.mark.parametrize('n_pre,n_post,k,p,het,accumulate,sdt', [
@@ -265,7 +270,9 @@ def _expected_row_groups(s, n_pre, nb):
     (60_000, 30_000, 20, 0.002, False, True, 'f32'),     # R_eff = 1, f32 spikes
     (3_000, 500_000, 50, 0.01, True, False, 'u8'),       # 41 buckets: 6 sub-ranges each
     (50, 20_000, 30, 0.5, True, True, 'u8'),             # n_pre <= 64: one row group at most
-    (2_000, 1_600_000, 40, 0.3, True, True, 'u8')])      # 131 buckets: one row group at most
+    (2_000, 1_600_000, 40, 0.3, True, True, 'u8'),       # 131 buckets: one row group at most
+    (100_000, 6, 4, 0.3, True, False, 'u8'),             # 6 buckets: 32 row groups, not 42
+    (100_000, 6, 4, 0.3, False, True, 'u8')])
 def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, accumulate,
                                           sdt):
     """The step picks its number of row groups from the spikes on the device; whatever it
@@ -284,7 +291,7 @@ def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, 
     L = ops.build_buckets(dev(torch, idx), n_post, w=w, w_homo=0.6)
     base = rng.rand(n_post).astype(F)
     R_est = _expected_row_groups(s, n_pre, L['nb'])
-    R_max = max(1, min(256 // L['nb'], -(-n_pre // 64)))
+    R_max = _max_row_groups(n_pre, L['nb'])
     gots = {}
     want_hint = max(1, min(R_max, -(-int(np.count_nonzero(s)) // 128)))
     # 'single' last before 'auto': its estimate (from the exact count) steers 'auto': one
