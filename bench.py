@@ -429,6 +429,50 @@ def bench_conn(args):
              'speedup': (host + h2d) / min(dev), 'bit_equal_to_numpy': equal}]
 
 
+def bench_vjp(args):
+    """Reverse mode of the two event products (row f2): the event mat-vec at configs[1]'s shape
+    (100k x 100k, K = 1000, per-synapse w, spikes at p = 0.1, a dense upstream gradient):
+    grad_spk and grad_w by k_matvec_vjp, one wave per pre row gathering g[idx]; and EventLinear
+    at configs[3]'s shape (spikes [64, 4096] at 5 %, W [4096, 4096]): grad_spk = g W^T by
+    k_dense_gx and grad_W = spk^T g by k_dense_gw.  Byte models: mat-vec n_pre K (4 + 4 + 4)
+    (indices and weights read, grad_w written; g gathered from L2) + n_pre (1 + 4) + n_post 4;
+    EventLinear W read + grad_W written (n_in n_out 4 each) + spikes, g and grad_spk."""
+    import torch
+    from brainstate_amd import ops
+    lines = []
+    n, k = 100_000, 1000
+    rng = np.random.RandomState(7)
+    idx = torch.from_numpy(rng.randint(0, n, size=(n, k)).astype(np.int32)).cuda()
+    w = torch.from_numpy(rng.normal(0.5, 0.1, (n, k)).astype(np.float32)).cuda()
+    spk = torch.from_numpy((np.random.RandomState(1000).rand(n) < 0.1).astype(np.uint8)).cuda()
+    g = torch.from_numpy(rng.normal(0, 1, n).astype(np.float32)).cuda()
+
+    def mv():
+        ops.event_matvec_vjp(spk, idx, w, n, g)
+    t = _timed(mv, 10)
+    b = n * k * 12 + n * 5 + n * 4
+    lines.append({'workload': 'event_matvec_vjp_100k_K1000_p0.1 (grad_spk + grad_w)',
+                  'us': t * 1e6, 'alg_bytes': b, 'alg_GBs': b / t / 1e9,
+                  'frac': b / t / PEAK_HBM})
+    del idx, w
+    B, ni, no = 64, 4096, 4096
+    W = torch.from_numpy(rng.normal(0, 0.125, (ni, no)).astype(np.float32)).cuda()
+    s2 = torch.from_numpy((rng.rand(B, ni) < 0.05).astype(np.uint8)).cuda()
+    g2 = torch.from_numpy(rng.normal(0, 1, (B, no)).astype(np.float32)).cuda()
+    for name, need_spk, need_w in (('grad_spk', True, False), ('grad_W', False, True),
+                                   ('both', True, True)):
+        def dv():
+            ops.event_dense_vjp(s2, W, g2, need_spk=need_spk, need_w=need_w)
+        t = _timed(dv, 20)
+        b = (ni * no * 4 if need_spk else 0) + (ni * no * 4 if need_w else 0) + B * ni + \
+            B * no * 4 + (B * ni * 4 if need_spk else 0)
+        fl = (2 * B * ni * no if need_spk else 0) + (2 * B * ni * no if need_w else 0)
+        lines.append({'workload': f'event_dense_vjp_64x4096x4096_p0.05 ({name})',
+                      'us': t * 1e6, 'alg_bytes': b, 'alg_GBs': b / t / 1e9,
+                      'frac': b / t / PEAK_HBM, 'fp32_TFLOPs_if_dense': fl / t / 1e12})
+    return lines
+
+
 def bench_for_loop(args):
     """brainstate.transform.for_loop(net.update, times) of a module-built E/I net (LIFRef +
     two AlignPostProj on EventFixedProb, homogeneous 0.6 / 6.7, constant input 20) at
@@ -512,12 +556,13 @@ def main():
     ap.add_argument('--anchor', default=None, help='--summarize: kernel name substring')
     ap.add_argument('--workload', default='coba_lif_1m',
                     choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn', 'batch',
-                             'for_loop'],
+                             'for_loop', 'vjp'],
                     help='coba_lif_1m is the reported line; the others measure the other configs')
     args = ap.parse_args()
     if args.workload != 'coba_lif_1m':
         fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh,
-              'conn': bench_conn, 'batch': bench_batch, 'for_loop': bench_for_loop}
+              'conn': bench_conn, 'batch': bench_batch, 'for_loop': bench_for_loop,
+              'vjp': bench_vjp}
         for line in fn[args.workload](args):
             print(json.dumps(line), flush=True)
         return

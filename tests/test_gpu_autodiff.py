@@ -72,7 +72,8 @@ def test_value_matvec_matches_oracle(torch_cuda, homo):
     assert np.allclose(out.cpu().numpy(), event.value_matvec(x, idx, wv, 2000), rtol=RT, atol=AT)
 
 
-@pytest.mark.parametrize('shape', [(64, 512, 300), (5, 96, 64), (1, 33, 17)])
+@pytest.mark.parametrize('shape', [(64, 512, 300), (5, 96, 64), (1, 33, 17), (70, 100, 160),
+                                   (64, 1024, 4096)])
 @pytest.mark.parametrize('dtype', ['bool', 'f32'])
 def test_event_dense_vjp_matches_oracle(torch_cuda, shape, dtype):
     torch = torch_cuda
@@ -87,7 +88,14 @@ def test_event_dense_vjp_matches_oracle(torch_cuda, shape, dtype):
     gs, gW = ops.event_dense_vjp(torch.from_numpy(np.asarray(x)).cuda(), torch.from_numpy(W).cuda(),
                                  torch.from_numpy(g).cuda())
     rx, rW = event.dense_vjp(np.asarray(x, F), W, g)
-    assert np.allclose(gs.cpu().numpy(), rx, rtol=RT, atol=1e-4)
+    # grad_spk sums n_out fp32 products in an unspecified order (the matrix-core path adds
+    # 16-wide blocks per wave, then the waves' partials): its error is bounded by the fp32
+    # rounding of such a sum, 4 sqrt(n_out) 2^-24 sum_j |g W| (a dropped block or a
+    # transposed tile misses it by orders of magnitude), on top of rtol / 1e-4
+    err = np.abs(gs.cpu().numpy() - rx)
+    bound = 1e-4 + RT * np.abs(rx) + 4 * np.sqrt(n_out) * 2.0 ** -24 * (np.abs(g) @ np.abs(W).T)
+    say('  grad_spk max error / bound', float((err / bound).max()))
+    assert np.all(err <= bound)
     assert np.allclose(gW.cpu().numpy(), rW, rtol=RT, atol=AT)
 
 
