@@ -1,9 +1,9 @@
 // N1: spike compaction.  bool/float spike vector -> ascending active-index list + count.
 //
-// One pass.  Each workgroup takes a ticket (its tile number), ballots its tile one
-// 256-element sweep at a time (wave ballot + mbcnt rank, per-wave totals in LDS) into
-// an ordered LDS list, then finds its global offset by decoupled look-back over the
-// tiles with smaller tickets and writes the list out coalesced.
+// One pass.  Each workgroup takes a ticket (its tile number), loads its tile at once (64
+// consecutive spikes per thread), places each thread's active spikes by a wave prefix of the
+// per-thread counts and one round of per-wave totals in LDS, then finds its global offset by
+// decoupled look-back over the tiles with smaller tickets and writes its indices out.
 #include "common.h"
 
 #include <mutex>
@@ -11,8 +11,8 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kSweeps = 16;
-constexpr int kTile = kBlock * kSweeps;   // 4096 spikes per workgroup
+constexpr int kPerThread = 64;  // consecutive spikes per thread
+constexpr int kTile = kBlock * kPerThread;   // 16384 spikes per workgroup
 constexpr int kWaves = kBlock / BS_WAVE;
 
 __device__ __forceinline__ bool is_event(const uint8_t* p, int64_t i) { return p[i] != 0; }
@@ -22,13 +22,48 @@ __device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint32_t flag, u
   return ((uint64_t)(epoch + 1u) << 32) | ((uint64_t)flag << 30) | (uint64_t)(v & 0x3FFFFFFFu);
 }
 
-template <typename T>
+// 16 consecutive spikes of thread t as bit u = spike base + 16 t + u (kVec: one 16-byte load
+// of bytes, or four of floats, from a 16-byte aligned tile that lies wholly inside [0, n)).
+template <typename T, bool kVec>
+__device__ __forceinline__ uint32_t spike_bits16(const T* __restrict__ spk, int32_t n,
+                                                 int64_t e0) {
+  uint32_t m = 0;
+  if (kVec && e0 + 16 <= n) {
+    if constexpr (sizeof(T) == 1) {
+      const uint4 x = *(const uint4*)(spk + e0);
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // bit 7 of each nonzero byte, gathered into bits 21..24 by one multiply
+        const uint32_t hi = ((((w[q] & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w[q]) & 0x80808080u) >> 7;
+        m |= ((hi * 0x00204081u) >> 21 & 0xFu) << (4 * q);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 x = *(const float4*)(spk + e0 + 4 * q);
+        m |= (x.x != 0.0f ? 1u : 0u) << (4 * q) | (x.y != 0.0f ? 2u : 0u) << (4 * q) |
+             (x.z != 0.0f ? 4u : 0u) << (4 * q) | (x.w != 0.0f ? 8u : 0u) << (4 * q);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (e0 + u < n && is_event(spk, e0 + u)) m |= 1u << u;
+  }
+  return m;
+}
+
+// One tile of kTile spikes per workgroup: thread t loads spikes 16 t .. 16 t + 15 of the tile
+// together (one memory round trip for the whole tile), counts them, and a workgroup prefix of
+// the counts gives each thread its place in the tile's ascending list.
+template <typename T, bool kVec>
 __global__ __launch_bounds__(kBlock) void k_compact(const T* __restrict__ spk, int32_t n,
                                                     int32_t* __restrict__ idx_out,
                                                     int32_t* __restrict__ count_out,
                                                     bs_scan_ws* __restrict__ ws,
                                                     uint32_t nblocks) {
-  __shared__ int32_t s_list[kTile];
+  static_assert(kPerThread % 16 == 0 && kPerThread <= 64, "whole 16-spike loads, 64-bit mask");
   __shared__ int32_t s_wave[kWaves];
   __shared__ uint32_t s_ticket, s_epoch;
   __shared__ int32_t s_excl;
@@ -43,69 +78,106 @@ __global__ __launch_bounds__(kBlock) void k_compact(const T* __restrict__ spk, i
   const int lane = bs_lane();
   const int wid = threadIdx.x / BS_WAVE;
 
-  int32_t count = 0;  // uniform across the workgroup
   const int64_t base = (int64_t)tile * kTile;
-  for (int s = 0; s < kSweeps; ++s) {
-    const int64_t e = base + s * kBlock + threadIdx.x;
-    const bool p = e < n && is_event(spk, e);
-    const uint64_t m = bs_ballot(p);
-    if (lane == 0) s_wave[wid] = __popcll(m);
-    __syncthreads();
-    int32_t off = count, tot = 0;
+  const int64_t e0 = base + kPerThread * (int64_t)threadIdx.x;
+  uint64_t bits = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const int32_t c = s_wave[w];
-      off += (w < wid) ? c : 0;
-      tot += c;
-    }
-    if (p) s_list[off + bs_rank_below(m)] = (int32_t)e;
-    count += tot;
-    __syncthreads();
+  for (int q = 0; q < kPerThread / 16; ++q)
+    bits |= (uint64_t)spike_bits16<T, kVec>(spk, n, e0 + 16 * q) << (16 * q);
+  // inclusive prefix of the per-thread counts within the wave, then across the waves
+  const int32_t c = __popcll(bits);
+  int32_t inc = c;
+#pragma unroll
+  for (int o = 1; o < BS_WAVE; o <<= 1) {
+    const int32_t v = __shfl_up(inc, o);
+    if (lane >= o) inc += v;
+  }
+  if (lane == BS_WAVE - 1) s_wave[wid] = inc;
+  __syncthreads();
+  int32_t off = inc - c, count = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int32_t t = s_wave[w];
+    off += (w < wid) ? t : 0;
+    count += t;
   }
 
-  if (threadIdx.x == 0) {
+  // Status words carry their own value (epoch, flag and count in one 64-bit word), and no
+  // workgroup reads another's list, so relaxed device-scope atomics are all the look-back
+  // needs: no release / acquire, each of which costs an L2 write-back or invalidate here
+  // (with them every tile waited ~0.3 us on its predecessor: 61 us for 1M spikes).  The
+  // last tile's reset of the ticket and the epoch is read by the next launch only.
+  // The look-back is wave-wide: wave 0 reads the statuses of the 64 nearest tiles not yet
+  // added in one round trip (lane l: tile j - l), adds the published ones up to the nearest
+  // inclusive prefix, and goes on from the first unpublished one (at 4M spikes the one-status
+  // walk took 35 us, most of it round trips over tiles that had published only their count).
+  if (wid == 0) {
     uint64_t* st = bs_scan_status(ws);
     int32_t excl = 0;
     if (tile == 0) {
-      __hip_atomic_store(&st[0], pack_status(epoch, BS_ST_INC, count), __ATOMIC_RELEASE,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0)
+        __hip_atomic_store(&st[0], pack_status(epoch, BS_ST_INC, count), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     } else {
-      __hip_atomic_store(&st[tile], pack_status(epoch, BS_ST_AGG, count), __ATOMIC_RELEASE,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      int64_t j = (int64_t)tile - 1;
+      if (lane == 0)
+        __hip_atomic_store(&st[tile], pack_status(epoch, BS_ST_AGG, count), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      int64_t j = (int64_t)tile - 1;  // the newest tile not yet added (wave-uniform)
       while (true) {
-        const uint64_t v = __hip_atomic_load(&st[j], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-        if ((uint32_t)(v >> 32) != epoch + 1u) {  // tile j has not published yet
-          __builtin_amdgcn_s_sleep(1);
-          continue;
-        }
-        excl += (int32_t)(v & 0x3FFFFFFFu);
-        if (((v >> 30) & 3u) == BS_ST_INC) break;
-        --j;
+        const int64_t jj = j - lane;
+        const uint64_t v = jj >= 0 ? __hip_atomic_load(&st[jj], __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : pack_status(epoch, BS_ST_INC, 0);  // before tile 0
+        const bool pub = (uint32_t)(v >> 32) == epoch + 1u;
+        const uint64_t m_unpub = bs_ballot(!pub);
+        const uint64_t m_inc = bs_ballot(pub && ((v >> 30) & 3u) == BS_ST_INC);
+        const int f_unpub = m_unpub ? (int)__builtin_ctzll(m_unpub) : BS_WAVE;
+        const int f_inc = m_inc ? (int)__builtin_ctzll(m_inc) : BS_WAVE;
+        // lanes [0, take) are published: up to and including the nearest inclusive prefix
+        const int take = f_inc < f_unpub ? f_inc + 1 : f_unpub;
+        int32_t val = lane < take ? (int32_t)(v & 0x3FFFFFFFu) : 0;
+#pragma unroll
+        for (int o = BS_WAVE / 2; o > 0; o >>= 1) val += __shfl_xor(val, o);
+        excl += val;
+        if (f_inc < f_unpub) break;
+        j -= take;
+        if (take == 0) __builtin_amdgcn_s_sleep(1);  // the newest one has not published yet
       }
-      __hip_atomic_store(&st[tile], pack_status(epoch, BS_ST_INC, excl + count),
-                         __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0)
+        __hip_atomic_store(&st[tile], pack_status(epoch, BS_ST_INC, excl + count),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    s_excl = excl;
-    if (tile == nblocks - 1) *count_out = excl + count;
+    if (lane == 0) {
+      s_excl = excl;
+      if (tile == nblocks - 1) *count_out = excl + count;
+    }
   }
   __syncthreads();
-  const int32_t excl = s_excl;
-  for (int32_t i = threadIdx.x; i < count; i += kBlock) idx_out[excl + i] = s_list[i];
+  int32_t pos = s_excl + off;
+  for (uint64_t m = bits; m; m &= m - 1) idx_out[pos++] = (int32_t)(e0 + __builtin_ctzll(m));
 
-  if (threadIdx.x == 0) {
-    // The last workgroup to finish resets the tickets and opens a new epoch.
-    const uint32_t d = __hip_atomic_fetch_add(&ws->done, 1u, __ATOMIC_ACQ_REL,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-    if (d == nblocks - 1) {
-      __hip_atomic_store(&ws->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ws->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&ws->epoch, epoch + 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  if (threadIdx.x == 0 && tile == nblocks - 1) {
+    // The last tile resets the ticket and opens a new epoch: its look-back ended on an
+    // inclusive prefix, so every tile has taken its ticket and read the epoch (a counter of
+    // finished workgroups for this, like the ticket one atomic on one word per workgroup,
+    // serialised at ~7 ns each: 29.5 -> 22.7 us for 4M spikes without it).  Tickets (not the
+    // block index) order the tiles, so a tile waits only on tiles that have started.
+    __hip_atomic_store(&ws->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ws->epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 __global__ void k_set_i32(int32_t* p, int32_t v) { *p = v; }
+
+void launch_compact(const void* spk, int32_t spk_dtype, int32_t n, int32_t* idx_out,
+                    int32_t* count_out, bs_scan_ws* ws, uint32_t nb, hipStream_t s) {
+  const bool vec = ((uintptr_t)spk & 15) == 0;  // tiles start at multiples of 16 elements
+#define BS_CP(T, V) \
+  k_compact<T, V><<<nb, kBlock, 0, s>>>((const T*)spk, n, idx_out, count_out, ws, nb)
+  if (spk_dtype == BS_SPK_U8) { if (vec) BS_CP(uint8_t, true); else BS_CP(uint8_t, false); }
+  else { if (vec) BS_CP(float, true); else BS_CP(float, false); }
+#undef BS_CP
+}
 
 __global__ void k_zero_u64(uint64_t* p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -114,11 +186,11 @@ __global__ void k_zero_u64(uint64_t* p, int64_t n) {
 }
 
 // ---- bs_spike_compact_noalloc: the scan workspace in a file-scope device array ----
-// The scan header and one status word per 4096-spike tile, for up to kNoAllocTiles tiles.
+// The scan header and one status word per 16384-spike tile, for up to kNoAllocTiles tiles.
 // Each device holds its own copy; host code reaches it only through the address that
 // hipGetSymbolAddress returns for the current device (the array's name is a host-side
 // stand-in, not a device address).
-constexpr int64_t kNoAllocTiles = 16384;  // n <= 16384 * 4096 = 67,108,864 spikes
+constexpr int64_t kNoAllocTiles = 4096;  // n <= 4096 * 16384 = 67,108,864 spikes
 constexpr size_t kScratchBytes = BS_SCAN_WS_HEADER + (size_t)kNoAllocTiles * sizeof(uint64_t);
 constexpr int kMaxDevices = 64;
 
@@ -171,10 +243,7 @@ extern "C" int bs_spike_compact(const void* spk, int32_t spk_dtype, int32_t n, i
   BS_CHECK_ARG(spk && idx_out && workspace, "bs_spike_compact: NULL pointer");
   const uint32_t nb = (uint32_t)(((int64_t)n + kTile - 1) / kTile);
   bs_scan_ws* ws = (bs_scan_ws*)workspace;
-  if (spk_dtype == BS_SPK_U8)
-    k_compact<uint8_t><<<nb, kBlock, 0, s>>>((const uint8_t*)spk, n, idx_out, count_out, ws, nb);
-  else
-    k_compact<float><<<nb, kBlock, 0, s>>>((const float*)spk, n, idx_out, count_out, ws, nb);
+  launch_compact(spk, spk_dtype, n, idx_out, count_out, ws, nb, s);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }
@@ -201,12 +270,7 @@ extern "C" int bs_spike_compact_noalloc(const void* spk, int32_t spk_dtype, int3
   const int rc = scratch_for_current_device(s, &ws);
   if (rc) return rc;
   const uint32_t nb = (uint32_t)(((int64_t)n + kTile - 1) / kTile);
-  if (spk_dtype == BS_SPK_U8)
-    k_compact<uint8_t><<<nb, kBlock, 0, s>>>((const uint8_t*)spk, n, idx_out, count_out,
-                                             (bs_scan_ws*)ws, nb);
-  else
-    k_compact<float><<<nb, kBlock, 0, s>>>((const float*)spk, n, idx_out, count_out,
-                                           (bs_scan_ws*)ws, nb);
+  launch_compact(spk, spk_dtype, n, idx_out, count_out, (bs_scan_ws*)ws, nb, s);
   BS_CHECK_LAUNCH();
   return BS_OK;
 }

@@ -59,7 +59,7 @@ BS_API int bs_spike_compact(const void* spk, int32_t spk_dtype, int32_t n, int32
 /* bs_spike_compact without a workspace and without allocating: no counterpart in the
  * reference; for callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The scan state lives in a static
- * device array of 131,328 bytes that each device holds until the process ends, so
+ * device array of 33,024 bytes that each device holds until the process ends, so
  * n <= 67,108,864 (larger n: BS_ERR_INVALID; use bs_spike_compact).  The first call on a
  * device clears that array with a kernel on `stream`; every call leaves it ready for the
  * next.  All calls on one device share the array: calls that overlap in time on one device
