@@ -38,7 +38,9 @@ def dev(t, a):
 @pytest.mark.parametrize('n,p,dtype', [(0, 0.1, 'u8'), (1, 1.0, 'u8'), (100, 0.3, 'u8'),
                                        (4096, 0.05, 'u8'), (4097, 0.5, 'f32'),
                                        (100_000, 0.001, 'u8'), (1_000_000, 0.0015, 'u8'),
-                                       (1_000_003, 1.0, 'f32'), (300_000, 0.0, 'u8')])
+                                       (1_000_003, 1.0, 'f32'), (300_000, 0.0, 'u8'),
+                                       (16384, 1.0, 'u8'), (16385, 0.5, 'f32'),
+                                       (4_000_037, 0.3, 'u8')])   # 245 tiles: look-back rounds
 def test_compact(torch_cuda, n, p, dtype):
     torch = torch_cuda
     from brainstate_amd import ops
@@ -52,6 +54,23 @@ def test_compact(torch_cuda, n, p, dtype):
         torch.cuda.synchronize()
         assert int(cnt.item()) == c
         assert np.array_equal(idx[:c].cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize('dtype', ['u8', 'f32'])
+def test_compact_unaligned_view(torch_cuda, dtype):
+    """A spike view that starts one element into its buffer takes the element-wise loads
+    (tiles are no longer 16-byte aligned); the list is the same."""
+    torch = torch_cuda
+    from brainstate_amd import ops
+    n = 70_001
+    say('compact unaligned', n, dtype)
+    rng = np.random.RandomState(9)
+    spk = rng.rand(n + 1) < 0.2
+    arr = spk.astype(np.uint8) if dtype == 'u8' else np.where(spk, 1.0, 0.0).astype(F)
+    ref, c = event.compact(arr[1:])
+    idx, cnt = ops.spike_compact(dev(torch, arr)[1:])
+    assert int(cnt.item()) == c
+    assert np.array_equal(idx[:c].cpu().numpy(), ref)
 
 
 # ---------------------------------------------------------------- N2a scatter
