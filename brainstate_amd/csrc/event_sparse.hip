@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ 
                                                    const float* __restrict__ sell_w,
                                                    float w_homo, int32_t n_post,
                                                    float* __restrict__ out) {
-  constexpr int kU = 8;
+  constexpr int kGU = 8;  // 16-byte index groups per stage (16: slower, 2x the registers)
   extern __shared__ uint32_t s_bits[];
   const int32_t nwords = (n_pre + 31) / 32;
   if (kLds) {
@@ -118,25 +118,50 @@ __global__ __launch_bounds__(kBlock) void k_gather(const uint32_t* __restrict__ 
   };
   const float4* w4 = kHet ? (const float4*)(sell_w + beg) + lane : nullptr;
   int64_t g = 0;
-  for (; g + kU <= ngrp; g += kU) {  // kU 16-byte groups of indices in flight per lane
-    int4 q[kU];
+  // two stages of kGU 16-byte index groups: the next stage's indices are loaded before this
+  // stage's spike lookups, weight loads and adds, which stay in column order (100k x 100k,
+  // K = 1000: 121 / 146 / 165 -> 112 / 125 / 158 us at p = 0.001 / 0.01 / 0.1; a third stage
+  // for the weights, loaded one block ahead of their adds, measured slower)
+  auto ld = [&](int64_t g0, int4 (&q)[kGU]) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u) q[u] = pre4[(g + u) * BS_WAVE];
-    uint32_t act[kU];  // bit e: column 4(g+u)+e is an active synapse
-    float4 wq[kU];
+    for (int u = 0; u < kGU; ++u) q[u] = pre4[(g0 + u) * BS_WAVE];
+  };
+  auto use = [&](int64_t g0, const int4 (&q)[kGU]) {
+    uint32_t act[kGU];  // bit e: column 4(g0+u)+e is an active synapse
+    float4 wq[kGU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kGU; ++u) {
       act[u] = (uint32_t)on(q[u].x) | ((uint32_t)on(q[u].y) << 1) | ((uint32_t)on(q[u].z) << 2) |
                ((uint32_t)on(q[u].w) << 3);
       wq[u] = make_float4(w_homo, w_homo, w_homo, w_homo);
-      if (kHet && act[u]) wq[u] = w4[(g + u) * BS_WAVE];  // this lane's 4 weights, one load
+      if (kHet && act[u]) wq[u] = w4[(g0 + u) * BS_WAVE];  // this lane's 4 weights, one load
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < kGU; ++u) {
       if (act[u] & 1u) acc += wq[u].x;
       if (act[u] & 2u) acc += wq[u].y;
       if (act[u] & 4u) acc += wq[u].z;
       if (act[u] & 8u) acc += wq[u].w;
+    }
+  };
+  if (kGU <= ngrp) {
+    int4 qa[kGU], qb[kGU];
+    ld(0, qa);
+    for (; g + 2 * kGU <= ngrp; g += 2 * kGU) {
+      __builtin_amdgcn_sched_barrier(0);
+      ld(g + kGU, qb);
+      __builtin_amdgcn_sched_barrier(0);
+      use(g, qa);
+      if (g + 3 * kGU <= ngrp) {
+        __builtin_amdgcn_sched_barrier(0);
+        ld(g + 2 * kGU, qa);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      use(g + kGU, qb);
+    }
+    if (g + kGU <= ngrp) {  // qa holds stage g (loaded above, or before the loop)
+      use(g, qa);
+      g += kGU;
     }
   }
   for (; g < ngrp; ++g) {
