@@ -7,7 +7,8 @@
   compaction of the spike vector, then the pre-major scatter of the active rows) instead of
   brainevent's kernel.
   With ``event_kernel='bucket'`` (or ``'auto'`` with per-synapse weights, or with a
-  homogeneous weight onto more than 16,384 neurons), the event path of inference runs the
+  homogeneous weight onto more than 16,384 neurons whose rows average at least 4 synapses
+  per destination bucket), the event path of inference runs the
   destination-bucketed operator instead (``bs_event_bucket_f32``: no global or fp32 atomics,
   exact fixed-point sums with the persistent runner's exponent, deterministic) on a layout
   built on first use and rebuilt when the weight value changes.
@@ -47,7 +48,22 @@ def _to_dev(a, dtype):
 
 def _kw(w):
     """Weight argument for the kernels: a float for one (homogeneous) value, else the tensor."""
+    if not torch.is_tensor(w):
+        return float(w)
     return float(w.reshape(())) if w.numel() == 1 else w
+
+
+def _het(w):
+    """True for per-synapse weights (a tensor of more than one value)."""
+    return torch.is_tensor(w) and w.numel() > 1
+
+
+def _grad_weight(w, like):
+    """The weight as a tensor for the autograd Functions (a Python scalar becomes a 0-d
+    fp32 tensor on the device of ``like``)."""
+    if torch.is_tensor(w):
+        return w
+    return torch.tensor(float(w), dtype=torch.float32, device=like.device)
 
 
 class _EventMatvecFn(torch.autograd.Function):
@@ -118,13 +134,15 @@ def _no_autodiff(*ts):
 
 
 _BUCKET_AUTO_POSTS = 16384   # 'auto', homogeneous weight: bucketed above this many outputs
+_BUCKET_AUTO_SEG = 4         # ... and with at least this many synapses per row and bucket
 
 
 def _wants_grad(*ts):
-    """Route through the autograd Functions whenever autodiff may be recording: grad mode on
-    and a tensor operand (forward-mode dual tensors do not set requires_grad).  Under
-    torch.no_grad the kernels are called directly."""
-    return torch.is_grad_enabled() and any(torch.is_tensor(t) for t in ts)
+    """Route through the autograd Functions only when autodiff may record this call: grad
+    mode on and an operand that requires grad, carries a forward-mode tangent or is wrapped
+    by a torch.func transform.  Otherwise the kernels are called directly (no Function
+    dispatch: its argument binding cost ~40 us of host time per call)."""
+    return torch.is_grad_enabled() and not _no_autodiff(*ts)
 
 
 class FixedPostNumConn:
@@ -147,7 +165,8 @@ class FixedPostNumConn:
         if torch.is_tensor(w) and w.numel() > 1:
             w = w.expand(self.indices.shape) if w.shape != self.indices.shape else w
         if _wants_grad(spk, w):
-            return _EventMatvecFn.apply(spk, w, self.indices, None, n_post, value)
+            return _EventMatvecFn.apply(spk, _grad_weight(w, spk), self.indices, None, n_post,
+                                        value)
         wk = _kw(w) if torch.is_tensor(w) else w
         if value:
             return ops.value_matvec(spk, self.indices, wk, n_post)
@@ -171,7 +190,8 @@ class CSR:
         if torch.is_tensor(w) and w.numel() > 1 and w.shape != self.indices.shape:
             w = w.expand(self.indices.shape)
         if _wants_grad(spk, w):
-            return _EventMatvecFn.apply(spk, w, self.indices, self.indptr, n_post, value)
+            return _EventMatvecFn.apply(spk, _grad_weight(w, spk), self.indices, self.indptr,
+                                        n_post, value)
         wk = _kw(w) if torch.is_tensor(w) else w
         if value:
             return ops.value_matvec(spk, self.indices, wk, n_post, indptr=self.indptr)
@@ -179,13 +199,29 @@ class CSR:
 
 
 def _weight_for_kernel(w):
-    """fp32 device tensor of the weight (0-d for one homogeneous value); a tensor that
-    requires grad keeps its autograd graph."""
+    """fp32 device tensor of the weight, or a Python float for a scalar weight that is not a
+    tensor (no host-to-device copy and no read-back per call); a tensor that requires grad
+    keeps its autograd graph."""
     if torch.is_tensor(w):
         return _to_dev(w, torch.float32)
     if init._is_scalar(w):
-        return torch.tensor(float(w), dtype=torch.float32, device=_device())
+        return float(w)   # one homogeneous value: passed to the kernels as a float
     return _to_dev(w, torch.float32)
+
+
+def _module_weight(mod, v):
+    """``_weight_for_kernel(v)`` for the weight State value ``v`` of module ``mod``; the device
+    copy of a numpy weight is kept on the module while the State holds the same array object
+    (an eager step would otherwise copy every synapse's weight to the device: 400 MB per step
+    for 1M neurons x 100 synapses).  A numpy array changed in place is not seen (it carries
+    no version): assign a new array, or a tensor."""
+    if isinstance(v, np.ndarray) and not init._is_scalar(v):
+        c = getattr(mod, '_wdev', None)
+        if c is None or c[0] is not v:
+            c = (v, _to_dev(v, torch.float32))
+            mod._wdev = c
+        return c[1]
+    return _weight_for_kernel(v)
 
 
 class FixedNumConn(Module):
@@ -286,7 +322,7 @@ class FixedNumConn(Module):
             lead = tuple(x.shape[:-1]) if torch.is_tensor(x) else ()
             return torch.zeros(lead + (self.out_size[-1],), dtype=torch.float32,
                                device=_device())
-        w = _weight_for_kernel(self.weight.value)
+        w = _module_weight(self, self.weight.value)
         x = x if torch.is_tensor(x) else _to_dev(x, torch.float32)
         if x.device.type != 'cuda':
             x = x.to(_device())
@@ -309,13 +345,23 @@ class FixedNumConn(Module):
         """'auto': per-synapse weights always take the bucketed operator -- its exact
         fixed-point sums are those the persistent runner adds (same exponent rule), so an
         eager step equals the fused one bit for bit and does not depend on the order of the
-        device's atomics -- and a homogeneous weight above 16,384 outputs (below, the atomic
-        kernel adds equal addends, whose sums do not depend on their order)."""
+        device's atomics -- and a homogeneous weight above 16,384 outputs when a row's
+        synapses average at least 4 per bucket (elsewhere the atomic kernel, which adds equal
+        addends, whose sums do not depend on their order: both give the same bits).  Measured
+        (us per call at p = 0.0005 / 0.01 / 0.1): 800k x 1M, K = 100 (82 buckets, 1.2 synapses
+        per bucket) bucketed 31 / 64 / 425, atomic 14 / 46 / 393; 100k x 100k, K = 100 (9
+        buckets, 11 per bucket) bucketed 11 / 15 / 21, atomic 13 / 14 / 57; 400k x 400k, K =
+        300 (33 buckets, 9 per bucket) 21 / 26 / 108 against 13 / 65 / 581."""
         if self.event_kernel == 'bucket':
             return True
         if self.event_kernel != 'auto':
             return False
-        return w.numel() > 1 or self.out_size[-1] > _BUCKET_AUTO_POSTS
+        if _het(w):
+            return True
+        n_post = self.out_size[-1]
+        if n_post <= _BUCKET_AUTO_POSTS:
+            return False
+        return self.conn_num >= _BUCKET_AUTO_SEG * ops.bucket_plan(n_post)[0]
 
     def _bucket_layout(self, w):
         """Destination-bucketed layout of the current connectivity and weight; rebuilt when the
@@ -327,7 +373,7 @@ class FixedNumConn(Module):
         key = (v._version if torch.is_tensor(v) else None,
                float(v) if init._is_scalar(v) else None)
         if self._bucket is None or self._bucket[0] is not v or self._bucket[1] != key:
-            homo = w.numel() == 1
+            homo = not _het(w)
             conn = self.conn
             indptr = getattr(conn, 'indptr', None)
             wt = None
@@ -336,7 +382,7 @@ class FixedNumConn(Module):
                 if indptr is None and wt.shape != conn.indices.shape:
                     wt = wt.expand(conn.indices.shape)
             layout = ops.build_buckets(conn.indices, self.out_size[-1], w=wt,
-                                       w_homo=float(w.reshape(())) if homo else 0.0,
+                                       w_homo=_kw(w) if homo else 0.0,
                                        indptr=indptr)
             self._bucket = (v, key, layout)
         return self._bucket[2]
@@ -497,9 +543,9 @@ class EventLinear(Module):
         n_w = 1 if init._is_scalar(w) else int(np.prod(w.shape))
         if n_w == 1:
             # homogeneous shortcut, :77-97 (reference-owned arithmetic on the reduction)
-            wt = _weight_for_kernel(w).reshape(())
+            wt = _grad_weight(_weight_for_kernel(w), x).reshape(())
             return _HomoLinearFn.apply(x, wt, self.out_size[-1], self.float_as_event)
-        W = _to_dev(w, torch.float32)
+        W = _module_weight(self, w)
         W = W.expand(self.in_size[-1], self.out_size[-1]).contiguous()
         if x.dtype not in (torch.bool, torch.uint8, torch.float32):
             x = x.to(torch.float32)

@@ -276,6 +276,16 @@ def build_sell(indptr, indices, n_pre, n_post, w=None, w_homo=0.0, device='cuda'
                 padded=total, nnz=nnz)
 
 
+def bucket_plan(n_post):
+    """(nb, P): the destination buckets and the posts per bucket that ``build_buckets`` lays
+    ``n_post`` outputs out in (``bs_bucket_plan``)."""
+    P = ctypes.c_int32(0)
+    nb = int(N.lib().bs_bucket_plan(int(n_post), ctypes.byref(P)))
+    if nb < 0:
+        N.check(N.BS_ERR_INVALID, 'bs_bucket_plan')
+    return nb, P.value
+
+
 def build_buckets(indices, n_post, w=None, w_homo=0.0, indptr=None, k=None):
     """Destination-bucketed layout of a fixed-num ([n_pre, k] indices) or CSR connectivity, built
     on the device (layout contract of ``bs_bucket_build``); ``w`` per synapse or None."""
@@ -294,10 +304,7 @@ def build_buckets(indices, n_post, w=None, w_homo=0.0, indptr=None, k=None):
         n_pre = ip.numel() - 1
         k = 0
     nnz = idx.numel()
-    P = ctypes.c_int32(0)
-    nb = int(N.lib().bs_bucket_plan(int(n_post), ctypes.byref(P)))
-    if nb < 0:
-        N.check(N.BS_ERR_INVALID, 'bs_bucket_plan')
+    nb, P = bucket_plan(n_post)
     seg = torch.empty(max(n_pre * (nb + 1), 1), dtype=torch.int32, device=dev)
     lidx = torch.empty(max(nnz, 1), dtype=torch.int16, device=dev)
     lw = qexp = scratch = None
@@ -309,9 +316,9 @@ def build_buckets(indices, n_post, w=None, w_homo=0.0, indptr=None, k=None):
     opt = lambda t: N.ptr(t) if t is not None else None
     N.check(N.lib().bs_bucket_build(int(n_pre), opt(ip), N.ptr(idx), int(k),
                                     N.ptr(wt) if w is not None else None, int(n_post), nb,
-                                    P.value, N.ptr(seg), N.ptr(lidx), opt(lw), opt(qexp),
+                                    P, N.ptr(seg), N.ptr(lidx), opt(lw), opt(qexp),
                                     opt(scratch), N.stream_handle(dev)), 'bs_bucket_build')
-    return dict(n_pre=int(n_pre), n_post=int(n_post), nb=nb, P=P.value, seg=seg, lidx=lidx,
+    return dict(n_pre=int(n_pre), n_post=int(n_post), nb=nb, P=P, seg=seg, lidx=lidx,
                 w=lw, qexp=qexp, w_homo=float(w_homo))
 
 
@@ -337,6 +344,7 @@ def _bucket_hint(L):
 
 
 _BUCKET_MODES = {'split': 0, 'single': 1, 'dense': 2}
+_DENSE_MAX_ROWS = 8192   # spike rows per row group, at most, for the fixed-grid mode
 
 
 def bucket_auto_mode(layout):
@@ -346,11 +354,19 @@ def bucket_auto_mode(layout):
     One launch when the estimate is one row group; the row groups fixed at their maximum
     when it is more than half of that (at config [2] the fixed grid took 19.9 us at p = 0.03,
     estimate 23 of 28, where row groups chosen on the device took 23.2 us, and 21.1 against
-    17.7 us at p = 0.01, estimate 9); else row groups chosen on the device."""
+    17.7 us at p = 0.01, estimate 9); else row groups chosen on the device.  The fixed grid
+    also needs short row groups: each of its workgroups sweeps its rows 4,096 at a time, one
+    memory round trip and two barriers per sweep, so with few row groups of many rows (a wide
+    output: 82 buckets of 1M posts leave 3 row groups of 266,667 rows for 800k spike rows)
+    it took 129 - 595 us where row groups chosen on the device took 31 - 425 us (p = 0.0005 -
+    0.1); at most 8,192 rows per group."""
     h = int(_bucket_hint(layout)[1][0])
     cached = layout.get('_call')
     rmax = cached[3] if cached is not None else _bucket_call_args(layout)[3]
-    return 'single' if h == 1 else ('dense' if 2 * h > rmax > 1 else 'split')
+    if h == 1:
+        return 'single'
+    short = -(-layout['n_pre'] // max(rmax, 1)) <= _DENSE_MAX_ROWS
+    return 'dense' if 2 * h > rmax > 1 and short else 'split'
 
 
 def event_bucket(spk, layout, out=None, accumulate=False, mode='auto'):
@@ -645,7 +661,7 @@ def coba_lif_step(V, ge, gi, ref, in_e, in_i, params, spk_out=None, I_ext=None, 
     if params.deferred_reset:
         if spk_out is None:
             spk_out = (torch.zeros(n, dtype=torch.uint8, device=V.device) if spk_prev is None
-                       else spk_prev.reshape(-1).to(torch.uint8).clone())
+                       else spk_prev.reshape(-1).to(torch.uint8, copy=True))
         elif spk_prev is not None:
             spk_out.copy_(spk_prev.reshape(-1))
     elif spk_out is None:

@@ -40,8 +40,9 @@ def test_host_only_calls_without_gpu():
     lib = N.load_library()
     assert lib.bs_version() >= 1
     assert lib.bs_spike_compact_workspace_size(0) == 256
-    assert lib.bs_spike_compact_workspace_size(4096) == 256 + 8
-    assert lib.bs_spike_compact_workspace_size(4097) == 256 + 16
+    # one 8-byte status word per tile of 16,384 spikes after a 256-byte header
+    assert lib.bs_spike_compact_workspace_size(16384) == 256 + 8
+    assert lib.bs_spike_compact_workspace_size(16385) == 256 + 16
     assert lib.bs_net_workspace_size(None) == 0 and b'net is NULL' in lib.bs_last_error()
     # argument validation happens before any device work
     rc = lib.bs_spike_compact(None, 7, 10, None, None, None, None)

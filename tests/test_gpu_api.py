@@ -222,12 +222,15 @@ def test_module_ei_network_per_neuron_input(bs):
         assert np.array_equal(net.N.ref.value.cpu().numpy(), ref['ref'])
 
 
-def test_for_loop_1m_fused_equals_eager(bs):
+@pytest.mark.parametrize('kernel', ['auto', 'bucket'])
+def test_for_loop_1m_fused_equals_eager(bs, kernel):
     """A 1M-neuron module net (K = 100, homogeneous weights): for_loop handed to the runner
-    equals the loop stepped eagerly, whose mat-vecs take the bucketed layout while the fused
-    loop's two recorded steps take the one-launch kernel (no layout built)."""
+    equals the loop stepped eagerly.  The eager mat-vecs take the atomic kernel under 'auto'
+    (82 buckets of 1M posts hold ~1.2 of a row's 100 synapses each: too few for the bucketed
+    layout) and the bucketed layout under 'bucket'; the fused loop's recorded steps take the
+    one-launch kernel (no layout built)."""
     import torch
-    print('[case] 1M module net, for_loop fused = eager', flush=True)
+    print('[case] 1M module net, for_loop fused = eager', kernel, flush=True)
     n, k, T = 1_000_000, 100, 40
     n_exc = n * 4 // 5
     V0 = np.random.RandomState(3).uniform(-60., -50., n).astype(F)
@@ -235,10 +238,12 @@ def test_for_loop_1m_fused_equals_eager(bs):
     def make():
         N = bs.nn.LIFRef(n, V_rest=-60., V_th=-50., V_reset=-60., tau=20., tau_ref=5.,
                          V_initializer=lambda s: V0)
-        E = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n_exc, n, k, 0.6, seed=1),
+        E = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n_exc, n, k, 0.6, seed=1,
+                                                           event_kernel=kernel),
                                 syn=bs.nn.Expon.desc(n, tau=5.), out=bs.nn.COBA.desc(E=0.),
                                 post=N)
-        I = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n - n_exc, n, k, 6.7, seed=2),
+        I = bs.nn.AlignPostProj(comm=bs.nn.EventFixedProb(n - n_exc, n, k, 6.7, seed=2,
+                                                           event_kernel=kernel),
                                 syn=bs.nn.Expon.desc(n, tau=10.), out=bs.nn.COBA.desc(E=-80.),
                                 post=N)
         for m in (E.syn, I.syn, N):
@@ -251,7 +256,7 @@ def test_for_loop_1m_fused_equals_eager(bs):
             return N(20.)
         return step, (N, E)
     (eager, (Ne, Ee)), (fused, (Nf, Ef)) = _for_loop_paths(bs, make, T)
-    assert Ee.comm._bucket is not None and Ef.comm._bucket is None
+    assert (Ee.comm._bucket is not None) == (kernel == 'bucket') and Ef.comm._bucket is None
     assert int(eager.sum()) > T * 500
     assert torch.equal(eager, fused)
     assert torch.equal(Ne.V.value, Nf.V.value)
