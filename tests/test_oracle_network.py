@@ -431,20 +431,28 @@ def test_c_restatement_cuba_soft_reset_equals_golden():
 
 def test_tutorial_spike_total_within_seed_spread():
     """docs/tutorials/brain_dynamics/04_building_an_snn.ipynb cell 14 prints 'total spikes:
-    4356' for its 400 E / 100 I soft-reset CUBA net over 200 ms.  Its connectivity (global
-    numpy stream, unseeded) and V0 (braintools / JAX stream) cannot be reproduced, so the
-    same net is run for 20 seeds: the printed total must lie within 3 standard deviations of
-    their mean (observed here: mean 4451.75, sd 46.3, range 4336-4531)."""
-    from oracle import network as onet
+    4356' for its 400 E / 100 I soft-reset CUBA net over 200 ms.  Its connectivity is
+    reproducible: cell 2's brainstate.random.seed(0) also seeds numpy's global stream with 0
+    (brainstate/random/_seed.py:694-698), EventFixedProb without a seed draws its indices
+    from that stream (brainstate/nn/_event_fixedprob.py:165-168), and the only draw before
+    the net's is cell 8's 4 x 2 one.  V0 (braintools' Normal(-60, 10) on the JAX stream) is
+    not, so the net runs with 20 numpy V0 draws: the printed total must lie within 3
+    standard deviations of their mean (mean 4468.4, sd 46.3, range 4402-4540: the printed
+    total sits 2.43 sd low).  Alternatives examined on 30 draws (mean 4470.0): spikes read
+    from V0 at step 0 (brainpy.state's get_spike is a function of V) 4475.3; delta inputs
+    added before the synaptic decay 4436.7; conductance read one step later 4466.3 -- none
+    moves the mean to the printed total, so no step semantics is changed on this evidence."""
     c = make_golden.TUT_NET
+    rs = np.random.RandomState(0)
+    rs.randint(0, 4, size=(4, 2))                                   # cell 8
+    idx_e = rs.randint(0, c['n'], size=(c['n_exc'], 50)).astype(np.int32)
+    idx_i = rs.randint(0, c['n'], size=(c['n'] - c['n_exc'], 50)).astype(np.int32)
     totals = []
     for seed in range(20):
-        pe = onet.Projection(0, c['n_exc'], c['n'], c['p'], c['w_e'], seed=1000 + seed)
-        pi = onet.Projection(c['n_exc'], c['n'], c['n'], c['p'], c['w_i'], seed=2000 + seed)
         V0 = np.random.RandomState(3000 + seed).normal(-60., 10., c['n']).astype(F)
         st = cbuild.lif_state(V0)
-        totals.append(cbuild.coba_lif_run(st, pe.idx, pi.idx, pe.w_scalar, pi.w_scalar,
+        totals.append(cbuild.coba_lif_run(st, idx_e, idx_i, F(c['w_e']), F(c['w_i']),
                                           _tut_params(), c['n_exc'], c['steps'], nthreads=1))
     mean, sd = float(np.mean(totals)), float(np.std(totals, ddof=1))
-    assert abs(mean - 4451.75) < 1e-9 and abs(sd - 46.263) < 1e-3
+    assert abs(mean - 4468.4) < 1e-9 and abs(sd - 46.274) < 1e-3
     assert abs(4356 - mean) < 3 * sd
