@@ -83,12 +83,12 @@ __host__ __device__ __forceinline__ uint32_t bs_mix32(uint32_t x) {
 // (Merrill & Garland, "Single-pass Parallel Prefix Scan with Decoupled Look-back", 2016).
 // Blocks take tickets in launch order, so a block only ever waits for blocks that
 // already hold a ticket, i.e. that are resident and running: every wait ends.
-// The last block to finish advances the epoch and clears the counters, so the
-// workspace needs one zero-fill when allocated and never again.
+// The block with the last ticket resets the ticket and advances the epoch once its
+// look-back is done, so the workspace needs one zero-fill when allocated and never again.
 struct bs_scan_ws {
   uint32_t ticket;
-  uint32_t done;
-  uint32_t epoch;     // starts at 0; status words carry (epoch+1)
+  uint32_t done;      // unused (kept for the layout)
+  uint32_t epoch;     // starts at 0, stays below 2^32 - 1; status words carry (epoch+1)
   uint32_t pad[61];   // status words start at 256 B
   // uint64_t status[nblocks] follows
 };

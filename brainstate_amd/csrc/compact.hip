@@ -18,8 +18,17 @@ constexpr int kWaves = kBlock / BS_WAVE;
 __device__ __forceinline__ bool is_event(const uint8_t* p, int64_t i) { return p[i] != 0; }
 __device__ __forceinline__ bool is_event(const float* p, int64_t i) { return p[i] != 0.0f; }
 
+// Status word: tag epoch + 1 (never 0, the value of a cleared word: the epoch stays in
+// [0, 2^32 - 2]), 2 flag bits, a 30-bit count.
 __device__ __forceinline__ uint64_t pack_status(uint32_t epoch, uint32_t flag, uint32_t v) {
   return ((uint64_t)(epoch + 1u) << 32) | ((uint64_t)flag << 30) | (uint64_t)(v & 0x3FFFFFFFu);
+}
+
+// The epoch after `e`, skipping 2^32 - 1 so that no tag is 0.  A tag comes back after
+// 2^32 - 1 calls on one workspace; a status word left from that long ago (a tile no call in
+// between reached) would read as published, which needs 2^32 - 1 calls of fewer tiles first.
+__device__ __forceinline__ uint32_t next_epoch(uint32_t e) {
+  return e >= 0xFFFFFFFEu ? 0u : e + 1u;
 }
 
 // 16 consecutive spikes of thread t as bit u = spike base + 16 t + u (kVec: one 16-byte load
@@ -163,7 +172,8 @@ __global__ __launch_bounds__(kBlock) void k_compact(const T* __restrict__ spk, i
     // serialised at ~7 ns each: 29.5 -> 22.7 us for 4M spikes without it).  Tickets (not the
     // block index) order the tiles, so a tile waits only on tiles that have started.
     __hip_atomic_store(&ws->ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&ws->epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ws->epoch, next_epoch(epoch), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

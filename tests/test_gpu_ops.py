@@ -56,6 +56,32 @@ def test_compact(torch_cuda, n, p, dtype):
         assert np.array_equal(idx[:c].cpu().numpy(), ref)
 
 
+def test_compact_epoch_wraps_without_a_zero_tag(torch_cuda):
+    """Status words are tagged epoch + 1, and a cleared word is 0: across the epoch's wrap
+    (2^32 - 2 -> 0) no call may use tag 0, or the tiles a larger call reaches for the first
+    time would read as published with count 0.  A workspace at epoch 2^32 - 2 compacts 2 tiles,
+    then 40 (38 never written), then 40 again."""
+    torch = torch_cuda
+    from brainstate_amd import _native as N
+    say('compact epoch wrap')
+    dev_ = torch.device('cuda')
+    ws = torch.zeros(int(N.lib().bs_spike_compact_workspace_size(40 * 16384)),
+                     dtype=torch.uint8, device=dev_)
+    ws.view(torch.int32)[2] = -2                  # epoch 0xFFFFFFFE
+    rng = np.random.RandomState(17)
+    for n in (2 * 16384, 40 * 16384, 40 * 16384):
+        arr = (rng.rand(n) < 0.1).astype(np.uint8)
+        ref, c = event.compact(arr)
+        spk = dev(torch, arr)
+        idx = torch.empty(n, dtype=torch.int32, device=dev_)
+        cnt = torch.empty(1, dtype=torch.int32, device=dev_)
+        N.check(N.lib().bs_spike_compact(N.ptr(spk), N.BS_SPK_U8, n, N.ptr(idx), N.ptr(cnt),
+                                         N.ptr(ws), N.stream_handle(dev_)), 'bs_spike_compact')
+        assert int(cnt.item()) == c
+        assert np.array_equal(idx[:c].cpu().numpy(), ref)
+    assert int(ws.view(torch.int32)[2]) == 2     # 0xFFFFFFFE -> 0 -> 1 -> 2
+
+
 @pytest.mark.parametrize('dtype', ['u8', 'f32'])
 def test_compact_unaligned_view(torch_cuda, dtype):
     """A spike view that starts one element into its buffer takes the element-wise loads
