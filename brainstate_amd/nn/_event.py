@@ -361,7 +361,9 @@ class FixedNumConn(Module):
         n_post = self.out_size[-1]
         if n_post <= _BUCKET_AUTO_POSTS:
             return False
-        return self.conn_num >= _BUCKET_AUTO_SEG * ops.bucket_plan(n_post)[0]
+        if getattr(self, '_plan', None) is None or self._plan[0] != n_post:
+            self._plan = (n_post, ops.bucket_plan(n_post)[0])
+        return self.conn_num >= _BUCKET_AUTO_SEG * self._plan[1]
 
     def _bucket_layout(self, w):
         """Destination-bucketed layout of the current connectivity and weight; rebuilt when the

@@ -133,16 +133,17 @@ class _COBANeuron(Dynamics):
     def _cuba(self):
         return bool(self._channels) and isinstance(self._channels[0].out, CUBA)
 
-    def _channel_args(self):
-        zeros = torch.zeros_like(self.V.value)
+    def _channel_args(self, need_g=True):
+        """(g, inputs, E, tau) of the two channels; a missing channel has a zero conductance
+        (allocated only when ``need_g``), no input, E = 0 and tau = 1."""
         g, ins, E, tau = [], [], [], []
         for ch in self._channels:
             g.append(ch.syn.g.value)
             ins.append(ch.syn.delta)
             E.append(ch.out.scale if isinstance(ch.out, CUBA) else ch.out.E)
             tau.append(ch.syn.tau)
-        while len(g) < 2:
-            g.append(zeros.clone())
+        while len(E) < 2:
+            g.append(torch.zeros_like(self.V.value) if need_g else None)
             ins.append(None)
             E.append(0.0)
             tau.append(1.0)
@@ -294,7 +295,7 @@ class LIFRef(_COBANeuron, _Describable):
     def params(self, I_ext=0.0):
         """The scalar parameters (an array-valued one takes a placeholder here; the step
         reads it per neuron)."""
-        _, _, E, tau = self._channel_args()   # E holds the CUBA scales for CUBA channels
+        _, _, E, tau = self._channel_args(need_g=False)   # E holds the CUBA scales for CUBA channels
         sc = lambda v, d: d if isinstance(v, np.ndarray) else v   # noqa: E731
         V_rest, V_th, V_reset = sc(self.V_rest, 0.0), sc(self.V_th, 0.0), sc(self.V_reset, 0.0)
         tau_m, R, tau_ref = sc(self.tau, 1.0), sc(self.R, 1.0), sc(self.tau_ref, 0.0)
@@ -382,7 +383,7 @@ class HH(_COBANeuron, _Describable):
         """The scalar parameters (an array-valued one takes a placeholder here)."""
         if self._cuba():
             raise NotImplementedError('the HH kernels implement COBA channels only')
-        _, _, E, tau = self._channel_args()
+        _, _, E, tau = self._channel_args(need_g=False)
         sc = lambda v, d: d if isinstance(v, np.ndarray) else v   # noqa: E731
         return ops.hh_params(ENa=sc(self.ENa, 0.), gNa=sc(self.gNa, 0.), EK=sc(self.EK, 0.),
                              gK=sc(self.gK, 0.), EL=sc(self.EL, 0.), gL=sc(self.gL, 0.),

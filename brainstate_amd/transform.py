@@ -27,6 +27,67 @@ def _stack(outs):
     return outs
 
 
+def _prealloc(o, length):
+    """Stacked buffers [length, ...] for step outputs shaped like ``o`` (tensors that take no
+    part in autodiff, in tuples, lists and dicts, None allowed), or None for anything else."""
+    if torch.is_tensor(o):
+        if o.requires_grad:
+            return None
+        return torch.empty((length,) + tuple(o.shape), dtype=o.dtype, device=o.device)
+    if o is None:
+        return _NONE
+    if isinstance(o, (tuple, list)):
+        parts = [_prealloc(x, length) for x in o]
+        return None if any(b is None for b in parts) else type(o)(parts)
+    if isinstance(o, dict):
+        parts = {k: _prealloc(v, length) for k, v in o.items()}
+        return None if any(b is None for b in parts.values()) else parts
+    return None
+
+
+_NONE = object()   # a None output leaf inside the preallocated structure
+
+
+def _put(buf, i, o):
+    """Copy step i's outputs into row i of the buffers; False (nothing guaranteed written)
+    when ``o`` differs from the first step's outputs in structure, shape, dtype or device."""
+    if buf is _NONE:
+        return o is None
+    if torch.is_tensor(buf):
+        if not (torch.is_tensor(o) and o.shape == buf.shape[1:] and o.dtype == buf.dtype
+                and o.device == buf.device and not o.requires_grad):
+            return False
+        buf[i].copy_(o)
+        return True
+    if isinstance(buf, (tuple, list)):
+        return (isinstance(o, (tuple, list)) and len(o) == len(buf)
+                and all(_put(b, i, x) for b, x in zip(buf, o)))
+    return (isinstance(o, dict) and o.keys() == buf.keys()
+            and all(_put(buf[k], i, o[k]) for k in buf))
+
+
+def _take(buf, i):
+    """Step i's outputs as views into the buffers."""
+    if buf is _NONE:
+        return None
+    if torch.is_tensor(buf):
+        return buf[i]
+    if isinstance(buf, (tuple, list)):
+        return type(buf)(_take(b, i) for b in buf)
+    return {k: _take(b, i) for k, b in buf.items()}
+
+
+def _finish(buf):
+    """The preallocated buffers as for_loop's result (None leaves back to None)."""
+    if buf is _NONE:
+        return None
+    if torch.is_tensor(buf):
+        return buf
+    if isinstance(buf, (tuple, list)):
+        return type(buf)(_finish(b) for b in buf)
+    return {k: _finish(b) for k, b in buf.items()}
+
+
 fuse_loops = True   # False: for_loop always steps eagerly
 last_loop = None    # how the last for_loop ran: 'fused' (persistent runner) or 'eager'
 
@@ -410,15 +471,27 @@ def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
                     bar.advance(length, length - 1)
                 last_loop = 'fused'
                 return stacked if torch.is_tensor(stacked) else _stack(stacked)
+        # Each step's outputs are copied into buffers allocated for all steps after the first
+        # (a snapshot, so an output that is a state tensor the next step updates in place
+        # keeps this step's value; no list of per-step tensors for the allocator to grow
+        # under, and no second copy to stack them); outputs of other kinds are kept as they
+        # come and stacked at the end.
         order = range(length - 1, -1, -1) if reverse else range(length)
-        outs = []
-        for i in order:
-            outs.append(f(*[x[i] for x in xs]))
+        buf, outs = None, [None] * length
+        for n_done, i in enumerate(order):
+            o = f(*[x[i] for x in xs])
+            if n_done == 0:
+                buf = _prealloc(o, length)
+            if buf is not None and not _put(buf, i, o):
+                # outputs unlike the first step's: the steps so far as views, then a list
+                for j in order[:n_done]:
+                    outs[j] = _take(buf, j)
+                buf = None
+            if buf is None:
+                outs[i] = o
             if bar is not None:
                 bar.step(i)
-        if reverse:
-            outs = outs[::-1]
-        return _stack(outs)
+        return _finish(buf) if buf is not None else _stack(outs)
     finally:
         if bar is not None:
             bar.close()

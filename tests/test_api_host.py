@@ -191,3 +191,36 @@ def test_external_input_forms():                 # N(x): scalar, one element, or
     assert arr[:, 3].tolist() == [1., 2.]
     with pytest.raises(ValueError, match='does not broadcast'):
         _ext_input(torch.ones(3), V)
+
+
+def test_for_loop_eager_outputs_are_snapshots():
+    """Each step's outputs are copied when the step returns them: a tensor the next step
+    updates in place keeps each step's value, as scan's stacked ys do; outputs whose shape
+    changes fall back to stacking what came, None leaves stay None, reverse order and empty
+    loops stack as before."""
+    import brainstate_amd as bs
+    import torch
+    old = bs.transform.fuse_loops
+    bs.transform.fuse_loops = False
+    try:
+        v = torch.zeros(3)
+
+        def f(x):
+            v.add_(x)            # in place: every step returns the same tensor object
+            return v, None, {'twice': 2 * v}
+
+        ys, none, d = bs.transform.for_loop(f, torch.arange(1.0, 5.0))
+        assert none is None
+        assert ys[:, 0].tolist() == [1, 3, 6, 10] and d['twice'][:, 0].tolist() == [2, 6, 12, 20]
+        ys = bs.transform.for_loop(lambda x: x * torch.ones(2), torch.arange(3.0), reverse=True)
+        assert ys.tolist() == [[0, 0], [1, 1], [2, 2]]
+        with pytest.raises(RuntimeError):   # shapes that differ cannot be stacked
+            bs.transform.for_loop(lambda x: torch.ones(int(x) + 1), torch.arange(3.0))
+        ys = bs.transform.for_loop(lambda x: torch.ones(2, dtype=torch.int64) * int(x)
+                                   if x < 1 else torch.ones(2) * x, torch.arange(3.0))
+        assert ys.dtype == torch.float32 and ys.tolist() == [[0, 0], [1, 1], [2, 2]]
+        assert bs.transform.for_loop(lambda x: x, torch.zeros(0)) == []
+        ys = bs.transform.for_loop(lambda x: float(x), torch.arange(3.0))
+        assert ys == [0.0, 1.0, 2.0]
+    finally:
+        bs.transform.fuse_loops = old
