@@ -846,6 +846,26 @@ def test_hh_single_neuron_trace_matches_fixture(bs):
     assert [float(v) for v in trace[999::1000]] == gold['V_every_1000']
 
 
+@pytest.mark.parametrize('k,bucketed', [(50, False), (100, True)])
+def test_event_fixed_prob_auto_homogeneous_choice(bs, k, bucketed):
+    """'auto' with a homogeneous weight onto 200,000 neurons (17 buckets): the bucketed
+    layout when a row averages at least 4 synapses per bucket (K >= 68), else the atomic
+    kernel; both give the sequential scatter's sums of one repeated value."""
+    import torch
+    print('[case] auto homogeneous choice', k, flush=True)
+    n_pre, n_post = 1000, 200_000
+    auto = bs.nn.EventFixedProb(n_pre, n_post, conn_num=k, conn_weight=0.6, seed=7)
+    spk = torch.from_numpy(np.random.RandomState(4).rand(n_pre) < 0.3).cuda()
+    got = auto(spk).cpu().numpy()
+    assert (auto._bucket is not None) == bucketed
+    idx = auto.conn.indices.cpu().numpy()
+    cnt = np.bincount(idx[spk.cpu().numpy()].reshape(-1), minlength=n_post)
+    want = np.zeros(n_post, F)
+    for c in range(1, int(cnt.max()) + 1):
+        want = np.where(cnt >= c, (want + F(0.6)).astype(F), want).astype(F)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize('het,ratio', [(True, 1.0), (False, 1.0), (True, 0.6)])
 def test_event_fixed_prob_bucketed_path(bs, het, ratio):
     """event_kernel='auto' on a wide output (> 16,384 posts) runs the bucketed operator; it

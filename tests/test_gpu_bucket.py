@@ -272,7 +272,9 @@ def _max_row_groups(n_pre, nb):
     (50, 20_000, 30, 0.5, True, True, 'u8'),             # n_pre <= 64: one row group at most
     (2_000, 1_600_000, 40, 0.3, True, True, 'u8'),       # 131 buckets: one row group at most
     (100_000, 6, 4, 0.3, True, False, 'u8'),             # 6 buckets: 32 row groups, not 42
-    (100_000, 6, 4, 0.3, False, True, 'u8')])
+    (100_000, 6, 4, 0.3, False, True, 'u8'),
+    (800_000, 1_000_000, 4, 0.05, True, False, 'u8'),   # 82 buckets: 3 groups of 266,667 rows
+    (800_000, 1_000_000, 4, 0.05, False, True, 'u8')])
 def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, accumulate,
                                           sdt):
     """The step picks its number of row groups from the spikes on the device; whatever it
@@ -295,8 +297,11 @@ def test_bucket_row_groups_follow_density(torch_cuda, n_pre, n_post, k, p, het, 
     gots = {}
     want_hint = max(1, min(R_max, -(-int(np.count_nonzero(s)) // 128)))
     # 'single' last before 'auto': its estimate (from the exact count) steers 'auto': one
-    # launch at 1, the fixed grid above half the maximum, else groups chosen on the device
-    auto = 'single' if want_hint == 1 else ('dense' if 2 * want_hint > R_max > 1 else 'split')
+    # launch at 1, the fixed grid above half the maximum when its row groups hold at most
+    # 8,192 rows, else groups chosen on the device
+    short = -(-n_pre // R_max) <= 8192
+    auto = 'single' if want_hint == 1 else (
+        'dense' if 2 * want_hint > R_max > 1 and short else 'split')
     for mode in ('split', 'dense', 'single', 'auto'):
         out = dev(torch, base.copy())
         gots[mode] = ops.event_bucket(dev(torch, s), L, out=out, accumulate=accumulate,
