@@ -2,7 +2,7 @@
 // atomics and without fp32 atomics.
 //
 // Why: scattered global fp32 atomics on MI355X sustain ~20 G/s chip-wide, so the pre-major
-// scatter of config [2] at p = 0.1 (1e7 events) costs > 500 us, while its compulsory bytes
+// scatter of a 100k x 100k, K = 1000 mat-vec at p = 0.1 (1e7 events) costs > 500 us, while its compulsory bytes
 // (indices + weights of the active rows) take ~10 us at HBM speed.  LDS atomics are cheaper,
 // but measured on gfx950 ds_add_f32 sustains only ~0.3 lanes per clock per CU (76 us for the
 // p = 0.1 case), while integer LDS atomics run at the speed of plain LDS stores (~30 us).
@@ -24,7 +24,7 @@
 // atomics: each weight rounded to a multiple of 2^-S and added as a 32-bit integer (event
 // counts for a homogeneous weight); every sum of rounded weights stays below 2^31 in
 // magnitude, so 32-bit two's complement adds are exact (64-bit accumulators and partials
-// before the runner's exponent rule made that bound hold: config [2] p = 0.1 ... us).  It writes the bucket as partial r; a second kernel adds
+// before the runner's exponent rule made that bound hold: 100k x 100k, K = 1000, p = 0.1 ... us).  It writes the bucket as partial r; a second kernel adds
 // the partials exactly and rounds once: out = fl32(sum) * 2^-S, whatever the order of the
 // atomics (deterministic), within half an fp32 ulp of the exact sum of the rounded weights.
 // Homogeneous weights: the exact event count c, then w added c times in one chain, which is
@@ -53,16 +53,16 @@ constexpr int kBB = 256;          // build: threads per workgroup (one wave per 
 constexpr int kSB = 1024;         // step: threads per workgroup
 constexpr int kMaxP = 12288;      // posts per bucket (48 KiB of 32-bit LDS accumulators)
 constexpr int kMaxNb = 1024;      // buckets
-// Measured on MI355X at config [2] (100k x 100k, K = 1000, p = 0.1): 9 buckets of 11,112
+// Measured on MI355X for 100k x 100k, K = 1000, p = 0.1: 9 buckets of 11,112
 // posts with 28 row groups 30 us; 16 buckets 34 us; 32 buckets 48 us; 8 rows per wave with one
 // pass 53 us; a 512-workgroup target 40 us.  fp32 LDS atomics instead of 64-bit integers:
 // 76 us.
 constexpr int kRowsPer = 4;       // active rows a wave works on at once
-// the same in the fixed-grid dense kernel: measured at config [2] p = 0.1 / 0.3 with 2, 4, 6, 8
+// the same in the fixed-grid dense kernel: measured for 100k x 100k, K = 1000 at p = 0.1 / 0.3 with 2, 4, 6, 8
 // rows per wave: 28.4-28.6 / 55.5-56.2, 28.6-28.8 / 53.2-53.5, 29.2-29.4 / 54.3-54.5,
 // 29.6-29.8 / 54.9-55.1 us per step
 constexpr int kRowsDense = 4;
-// the same in the single launch: measured at config [2] p = 0.001 (~100 active rows) with
+// the same in the single launch: measured for 100k x 100k, K = 1000 at p = 0.001 (~100 active rows) with
 // 1 .. 8 rows per wave: 10.9, 10.2, 9.96, 10.9, 10.4, 10.6, 10.8, 11.0 us per step
 constexpr int kRowsSingle = 3;
 constexpr int kPasses = 2;        // 64-synapse passes per row issued together
@@ -72,13 +72,13 @@ constexpr int kMinRows = 64;      // rows per row group, at least (and the group
 constexpr int kMinNb = 8;         // buckets, at least (the grid is nb x row groups)
 constexpr int kMaxR = kTargetWgs / kMinNb;  // row groups, at most (the reduce holds them all)
 constexpr int kSample = 16384;    // leading spike rows whose active count sets R_eff
-// active rows per row group the step aims for: measured at config [2] (mode 0, HIP graph)
+// active rows per row group the step aims for: measured for 100k x 100k, K = 1000 (mode 0, HIP graph)
 // p = 0.003 / 0.01 with 256: 16.5 / 19.05 us, 128: 15.4 / 19.07 us (one box); on another,
 // 256: 16.7 / 18.8 us, 64: 14.9 / 20.5 us
 constexpr int kActivePer = 128;
 constexpr int kDepth = 8;         // 16-byte spike loads per thread in flight together
 constexpr int kHdr = 256;         // workspace bytes ahead of the partials (word 0: R_eff)
-// single launch: workgroups per bucket.  Measured at config [2] p = 0.001 (one launch of
+// single launch: workgroups per bucket.  Measured for 100k x 100k, K = 1000 at p = 0.001 (one launch of
 // 9 x n workgroups): n = 2 13.0 us, 4 12.7 us, 8 12.55 us per step (HIP graph replay).
 constexpr int kSubSingle = 8;
 
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
   // single launch, all rows in the first round: each thread loads the bucket bounds of up to
   // two of its active rows before the prefix that places them, so that round trip overlaps
   // the prefix's barrier and the list is complete after it (more rows in any thread, or more
-  // than kSpan in all: the general path below).  At config [2] p = 0.001 (a thread holds ~0.1
+  // than kSpan in all: the general path below).  For 100k x 100k, K = 1000 at p = 0.001 (a thread holds ~0.1
   // active rows; one with three or more turns up in ~14 % of spike vectors, which then take
   // ~12 us) 11.6 -> 11.0 us; up to three or four rows per thread (fallback in 0.4 % / 0.01 %)
   // measured 11.2 us.
@@ -720,9 +720,10 @@ __global__ __launch_bounds__(kSB) void k_bucket_scatter(
 // fixed row group of `rows` rows, known on the host, so nothing waits for an estimate.  Per
 // span of kSpan rows: kU spike bytes per thread and the bucket bounds of the active ones,
 // loaded together, then ballots and one workgroup prefix that lists the active rows' bounds
-// in ascending row order; then phase 3 as in the adaptive kernel.  This compact form is what dense steps are fastest with (config [2] at
-// p = 0.1: 31.6 us against 33.6 us for the adaptive kernel run at R = max).  Workgroup 0
-// writes R to the header and the next call's estimate from its own group's active rows.
+// in ascending row order; then phase 3 as in the adaptive kernel.  This compact form is what
+// dense steps are fastest with (100k x 100k, K = 1000 at p = 0.1: 31.6 us against 33.6 us for
+// the adaptive kernel run at R = max).  Workgroup 0 writes R to the header and the next
+// call's estimate from its own group's active rows.
 template <typename T, bool kHet>
 __global__ __launch_bounds__(kSB) void k_bucket_scatter_dense(
     const T* __restrict__ spk, int32_t n_pre, int32_t rows, int32_t R, int32_t Rmax, int32_t nb,

@@ -1,7 +1,7 @@
 // N2c: batched event x dense weight (EventLinear).
 //
 // out[b, j] = sum of W[i, j] over the inputs i with spk[b, i] != 0 (or spk[b, i] * W[i, j]).
-// At config [4] (64 x 4096 spikes at 5 %, W 4096 x 4096 fp32) about 3,940 of the 4,096 rows
+// For 64 x 4096 spikes at 5 % and a 4096 x 4096 fp32 W about 3,940 of the 4,096 rows
 // of W are selected by at least one batch row, so every step reads almost all of W (64 MiB),
 // while the (batch row, active input) pairs number ~13,100: a kernel that fetches a W row
 // segment once per pair moves ~210 MB from L2, one that fetches it once per step 64 MiB.
@@ -46,7 +46,7 @@ constexpr int kRowsPerWave = kGroupRows / kDWaves;  // 4
 constexpr int kBlk = 64;                  // input rows per LDS block (one ballot)
 constexpr int kList = kBlk + 12;          // list entries per (wave, batch row): 64 + padding
 constexpr int kDump = kList - 1;          // slot written by lanes with nothing to record
-// Measured on MI355X at config [4] (64 x 4096 @ 5 %, W 4096^2): V = 2 with 8 chunks 28 us,
+// Measured on MI355X for 64 x 4096 spikes at 5 % and W 4096^2: V = 2 with 8 chunks 28 us,
 // V = 1 with 4 chunks 30 us, V = 4 120 us (LDS of 152 KiB per workgroup and 64 KiB partials);
 // a 256-workgroup launch alone costs ~4.3 us.
 constexpr int kV = 2;                     // output columns per lane (workgroup: 64 * V)

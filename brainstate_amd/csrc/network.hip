@@ -161,7 +161,7 @@ struct LifModel {
   }
   // Whether the neuron may spike this step: a zero-input forward-Euler estimate of the next
   // V within 7 % of (V_th - V_reset) of threshold.  Only steers the row prefetch; the
-  // estimate never decides a spike.  Measured at config [3] (us per step): margin 0.02 7.45,
+  // estimate never decides a spike.  Measured on the 1M-neuron COBA-LIF net (us per step): margin 0.02 7.45,
   // 0.05 7.24, 0.07 7.235, 0.10 7.25, 0.15 7.33, 0.20 7.51; V alone against a 0.15 / 0.25
   // margin 7.96 / 8.13 (too many rows); extrapolating V by the step's own change 7.76-8.03
   // (misses the neurons the next input pushes over).
@@ -204,9 +204,9 @@ struct HhModel {
   static constexpr bool kPrepare = true;
   // HH keeps 11 values per neuron in registers: its 14 parameters and the row pointers stay
   // scalar (in VGPRs they pushed the 4-neuron kernel to 128 VGPRs and 76 bytes of spills;
-  // config [5] 9.86 -> 9.49 us per step without them)
+  // 1M-neuron COBA-HH net 9.86 -> 9.49 us per step without them)
   static constexpr bool kParamVgprs = false;
-  // count words published one destination per lane (config [5] 9.48 -> 9.17 us per step;
+  // count words published one destination per lane (1M-neuron COBA-HH net 9.48 -> 9.17 us per step;
   // the LIF runner measured 7.21 -> 7.25 with it)
   static constexpr bool kPubByLane = true;
   __device__ static void prepare(const Params& p, Regs& r) {
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // E spikes fill s_list from the front and I spikes from the back; each wave reserves its
     // two ranges with one LDS atomic on a word holding both counts (at most 8192 each: no
     // carry between the halves), no scan, one barrier.  One atomic per wave instead of one
-    // per kind: config [3] 7.20 -> 7.16 us per step.
+    // per kind: 7.20 -> 7.16 us per step for the 1M-neuron COBA-LIF net.
     uint32_t* nsp2 = &s_nsp[ta & 1];  // this step's E spikes (bits 0-15), I spikes (16-31)
     {
       uint64_t mE[NPT], mI[NPT];
@@ -604,7 +604,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
         const int d = x / kSlots;
         const uint32_t slot = (uint32_t)(x - d * kSlots);
         // one LDS round trip: the round count, the cursor and the slot (read even when
-        // empty), the cursor reused for its advance (7.24 -> 7.19 us per step at config [3])
+        // empty), the cursor reused for its advance (7.24 -> 7.19 us per step for the 1M-neuron COBA-LIF net)
         const uint32_t rc = s_rcnt[d];
         const uint32_t p0 = s_pos[d];
         uint64_t ent = s_stage[x];

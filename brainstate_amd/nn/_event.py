@@ -498,7 +498,7 @@ class EventLinear(Module):
     writes ~1.25x its size, so the packed form pays from the second call with one weight.
     Accuracy of the packed form: |out - exact| <= 2^-24 * max|W[:, j]| + half an ulp of the
     output, in column j -- within abs 1e-6 + rel 1e-5 of the exact sum whenever the columns'
-    largest |w| is at most 16 (config [4]'s W ~ N(0, 1/64) has max |w| ~ 0.6); an fp32 sum in
+    largest |w| is at most 16 (a 4096 x 4096 W ~ N(0, 1/64) has max |w| ~ 0.6); an fp32 sum in
     any order has errors of the same size, ulps of its partial sums, on larger weights."""
     __module__ = 'brainstate_amd.nn'
 

@@ -352,7 +352,7 @@ def bucket_auto_mode(layout):
     on this layout, from the estimate the previous step left (none yet: 'split').
 
     One launch when the estimate is one row group; the row groups fixed at their maximum
-    when it is more than half of that (at config [2] the fixed grid took 19.9 us at p = 0.03,
+    when it is more than half of that (on the 100k x 100k, K = 1000 mat-vec the fixed grid took 19.9 us at p = 0.03,
     estimate 23 of 28, where row groups chosen on the device took 23.2 us, and 21.1 against
     17.7 us at p = 0.01, estimate 9); else row groups chosen on the device.  The fixed grid
     also needs short row groups: each of its workgroups sweeps its rows 4,096 at a time, one
