@@ -51,7 +51,9 @@ def _union_perm(B, n, n_exc):
     return np.where(j < n_exc, b * n_exc + j, B * n_exc + b * (n - n_exc) + (j - n_exc))
 
 
-def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
+def _check_start(neuron, proj_e, proj_i, delay):
+    """Raise unless the runner can start from the modules' current state; returns whether
+    the neurons hold spikes of their last step (pending inputs of the first step)."""
     if len(neuron._channels) != 2 or neuron._channels[0] is not proj_e or \
             neuron._channels[1] is not proj_i:
         raise ValueError('proj_e and proj_i must be the two projections onto neuron, in order')
@@ -70,6 +72,18 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     if getattr(neuron, 'has_param_arrays', lambda: False)():
         raise NotImplementedError('fuse(): the runner takes scalar neuron parameters; a '
                                   'population with per-neuron parameters steps eagerly')
+    return pending
+
+
+def _scalar_input(inp):
+    """The input as one number, or None when it is an array of more than one value."""
+    if (torch.is_tensor(inp) or isinstance(inp, np.ndarray)) and np.prod(tuple(inp.shape)) != 1:
+        return None
+    return float(inp.reshape(()).item() if torch.is_tensor(inp) else np.reshape(inp, ()))
+
+
+def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
+    pending = _check_start(neuron, proj_e, proj_i, delay)
     n = neuron.num
     Vs = neuron.V.value
     B = int(Vs.shape[0]) if Vs.dim() == 2 else 1   # init_all_states(batch_size=B)
@@ -107,23 +121,26 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     else:
         raise NotImplementedError(type(neuron).__name__)
     delay_steps = _get_delay(delay, environ.get_dt())[1]
-    if (torch.is_tensor(inp) or isinstance(inp, np.ndarray)) and np.prod(tuple(inp.shape)) != 1:
+    I0 = _scalar_input(inp)
+    if I0 is None:
         I0, I_arr = 0.0, to_runner(torch.broadcast_to(
             torch.as_tensor(inp, dtype=torch.float32, device=Vs.device), Vs.shape))
     else:
-        I0 = float(inp.reshape(()).item() if torch.is_tensor(inp) else np.reshape(inp, ()))
         I_arr = None
     r = EINetRunner(model, B * n, B * n_exc, idx_e, idx_i, w_e, w_i, neuron.params(I0),
                     V0, delay_steps=delay_steps, I_ext=I_arr)
-    # carry the current state over (the runner initialised HH gates at steady state)
-    r.state['ge'].copy_(to_runner(proj_e.syn.g.value))
-    r.state['gi'].copy_(to_runner(proj_i.syn.g.value))
-    if model == 'lif':
-        r.state['ref'].copy_(to_runner(neuron.ref.value))
-    else:
-        r.state['m'].copy_(to_runner(neuron.m.value))
-        r.state['h'].copy_(to_runner(neuron.h.value))
-        r.state['n'].copy_(to_runner(neuron.n.value))
+    def load_state():
+        # carry the current state over (the runner initialised HH gates at steady state)
+        r.state['ge'].copy_(to_runner(proj_e.syn.g.value))
+        r.state['gi'].copy_(to_runner(proj_i.syn.g.value))
+        if model == 'lif':
+            r.state['ref'].copy_(to_runner(neuron.ref.value))
+        else:
+            r.state['m'].copy_(to_runner(neuron.m.value))
+            r.state['h'].copy_(to_runner(neuron.h.value))
+            r.state['n'].copy_(to_runner(neuron.n.value))
+
+    load_state()
 
     def write_back():
         neuron.V.value = from_runner(r.state['V'])
@@ -153,8 +170,27 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
     if pending:   # the spikes of the last step drive the runner's first step
         r.seed(to_runner(neuron.spike.value.to(torch.uint8)), 1)
 
+    def reload(v):
+        """Start the next run from the modules' current state (a runner kept across
+        loops on the same connectivity and weights): neuron parameters, input, state, and
+        the current spikes as the inputs of the first step -- published as the events of
+        the step after the last one this runner ran, so no count word of an earlier run can
+        be taken for one of this run.  Synaptic delay 0 only."""
+        if delay_steps:
+            raise NotImplementedError('reload(): a runner with a synaptic delay is rebuilt')
+        _check_start(neuron, proj_e, proj_i, None)
+        if (_scalar_input(v) is None) != (I_arr is not None):
+            raise ValueError('reload(): the input kind (one number or one per neuron) changed')
+        r.params = neuron.params(0.0 if I_arr is not None else _scalar_input(v))
+        if I_arr is not None:
+            set_input(v)
+        r.state['V'].copy_(to_runner(neuron.V.value))
+        load_state()
+        r.seed(to_runner(neuron.spike.value.to(torch.uint8)), r.t + 1)
+
     r.write_back = write_back
     r.set_input = set_input
+    r.reload = reload
     r.replica_index = perm   # runner neuron of (replica b, neuron j), for rasters
     r.replica_identity = B == 1   # replica_index is the identity
     r.dt = environ.get_dt()

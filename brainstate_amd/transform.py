@@ -395,20 +395,68 @@ def _record(f, xs, length):
         return neuron, pe, pi, n_exc, segs, rd
 
 
+def _fuse_key(neuron, pe, pi, n_exc, inp):
+    """What a runner built by ``fuse`` depends on besides the state it reloads: the modules,
+    the connectivity and weight objects (tensors with their version counters; a numpy array
+    changed in place is not seen), the population's shape and model, and the input kind."""
+    from .nn._fuse import _scalar_input
+    parts = [neuron, pe, pi, int(n_exc), type(neuron), tuple(neuron.V.value.shape),
+             _scalar_input(inp) is None]
+    for proj in (pe, pi):
+        conn = getattr(proj.comm, 'conn', None)
+        idx = getattr(conn, 'indices', None)
+        w = proj.comm.weight.value
+        parts += [idx, getattr(idx, '_version', None), w,
+                  w._version if torch.is_tensor(w) else None,
+                  None if torch.is_tensor(w) or np.ndim(w) else float(w)]
+    return parts
+
+
+def _same_key(a, b):
+    if a is None or b is None or len(a) != len(b):
+        return False
+    for x, y in zip(a, b):
+        if isinstance(x, (int, float, bool, tuple, type(None))) and not torch.is_tensor(x):
+            if x != y:
+                return False
+        elif x is not y:
+            return False
+    return True
+
+
+def _runner_for(neuron, pe, pi, n_exc, inp):
+    """The persistent runner of this net: the one the last loop on it built, reloaded with
+    the modules' current state, while connectivity, weights and input kind are unchanged
+    (its set-up -- layout, in-degrees, inbox capacities, workspace -- takes ~15-30 ms at 1M
+    neurons, more than 2,000 of its steps), else a new one (kept for the next loop)."""
+    from .nn._fuse import fuse
+    key = _fuse_key(neuron, pe, pi, n_exc, inp)
+    cached = getattr(neuron, '_fused_runner', None)
+    if cached is not None and _same_key(cached[0], key):
+        try:
+            cached[1].reload(inp)
+            return cached[1]
+        except (NotImplementedError, ValueError):
+            pass
+    neuron._fused_runner = None   # the old runner's memory goes before the new one is built
+    r = fuse(neuron, pe, pi, n_exc, inp)
+    neuron._fused_runner = (key, r)
+    return r
+
+
 def _fused_loop(f, xs, length):
     """for_loop through the persistent runner: the steps are recorded first (``_record``);
     when every one is the E/I step the runner implements, the runner advances all of them
     from the modules' state -- one launch per run of equal inputs -- and writes the final
     state back.  Returns the stacked output (a tensor, or a list of None), or None when the
     loop must run eagerly."""
-    from .nn._fuse import fuse
     plan = _record(f, xs, length)
     if plan is None:
         return None
     neuron, proj_e, proj_i, n_exc, segs, rdtype = plan
     first = next((v for _, _, v in segs if torch.is_tensor(v)), segs[0][2])
     try:
-        r = fuse(neuron, proj_e, proj_i, n_exc, first)
+        r = _runner_for(neuron, proj_e, proj_i, n_exc, first)
     except NotImplementedError:   # a state the runner cannot start from
         return None
     T = length
@@ -453,7 +501,10 @@ def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
     the end.  Anything else -- other modules, State assignments outside modules, state used
     for anything but the projections' spike vectors, inputs the runner does not take --
     runs eagerly step by step.  Python side effects of ``f`` happen in the recording pass
-    (once, or once per step) and again per step when the loop then runs eagerly."""
+    (once, or once per step) and again per step when the loop then runs eagerly.  The runner
+    stays on the population for the next loop on the same connectivity, weights and input
+    kind, which reloads it from the modules' state instead of building a new one (its
+    workspace, ~1.6 GB at 1e8 synapses, stays allocated until then)."""
     global last_loop
     if length is None:
         if not xs:

@@ -172,6 +172,43 @@ def _for_loop_paths(bs, make_step, T, dt=0.1):
     return res
 
 
+def test_for_loop_chunks_reuse_the_runner(bs):
+    """Loops run in chunks on one net keep its persistent runner (no new set-up) and reload
+    the modules' state each time: chunks of 60, 40 and 50 steps with the state changed
+    between chunks (V shifted, the E conductances scaled) equal the same chunks stepped
+    eagerly with the same changes; a new weight value builds a new runner."""
+    import torch
+    print('[case] for_loop chunks reuse the runner', flush=True)
+    res = []
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                net = _EINet(bs)
+                outs, runners = [], []
+                for i, T in enumerate((60, 40, 50)):
+                    if i == 1:
+                        net.N.V.value = net.N.V.value + 0.25
+                        net.E.syn.g.value = net.E.syn.g.value * 1.5
+                    if i == 2:
+                        net.E.comm.weight.value = 0.7
+                    outs.append(bs.transform.for_loop(net.update, torch.arange(T) * 0.1))
+                    assert bs.transform.last_loop == ('fused' if fused else 'eager')
+                    r = getattr(net.N, '_fused_runner', None)
+                    runners.append(None if r is None else r[1])
+                if fused:
+                    assert runners[1] is runners[0] and runners[2] is not runners[1]
+                res.append((torch.cat(outs), net))
+        finally:
+            bs.transform.fuse_loops = True
+    (a, na), (b, nb) = res
+    assert int(a.sum()) > 0
+    assert torch.equal(a, b)
+    assert torch.equal(na.N.V.value, nb.N.V.value)
+    assert torch.equal(na.E.syn.g.value, nb.E.syn.g.value)
+    assert torch.equal(na.N.ref.value, nb.N.ref.value)
+
+
 def test_module_ei_network_matches_oracle(bs):
     """The reference's E/I script shape (examples/105_COBA_HH_2007_braincell.py:76-91):
     for_loop(net.update, times) stepped eagerly and through the persistent runner; both
