@@ -438,7 +438,9 @@ def _runner_for(neuron, pe, pi, n_exc, inp):
             return cached[1]
         except (NotImplementedError, ValueError):
             pass
-    neuron._fused_runner = None   # the old runner's memory goes before the new one is built
+    if cached is not None:   # its workspace goes before the new one is allocated (the
+        cached[1].ws = None  # runner and its closures form a cycle that waits for the gc)
+    neuron._fused_runner = None
     r = fuse(neuron, pe, pi, n_exc, inp)
     neuron._fused_runner = (key, r)
     return r
