@@ -372,6 +372,48 @@ def test_hh_module_network_for_loop(bs):
         assert make_golden.sha(N.V.value.cpu().numpy()) == gold['final_V_sha256']
 
 
+def test_hh_module_network_for_loop_in_chunks(bs):
+    """The HH net of the previous test run through the runner in three for_loop chunks: one
+    runner kept and reloaded between them, and the concatenated raster and the final V equal
+    the oracle's single golden run."""
+    import torch
+    print('[case] HH module net for_loop in chunks', flush=True)
+    c = make_golden.HH_NET
+    with open(os.path.join(GOLD, 'coba_hh_2000.json')) as f:
+        gold = json.load(f)
+    V0 = np.random.RandomState(c['seed_v']).uniform(-70., -50., c['n']).astype(F)
+    with bs.environ.context(dt=0.05):
+        N = bs.nn.HH(c['n'], V_initializer=lambda s: V0)
+        E = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n_exc'], c['n'], c['k'], c['w_e'], seed=c['seed_e']),
+            syn=bs.nn.Expon.desc(c['n'], tau=5.), out=bs.nn.COBA.desc(E=0.), post=N)
+        I = bs.nn.AlignPostProj(
+            comm=bs.nn.EventFixedProb(c['n'] - c['n_exc'], c['n'], c['k'], c['w_i'],
+                                      seed=c['seed_i']),
+            syn=bs.nn.Expon.desc(c['n'], tau=10.), out=bs.nn.COBA.desc(E=-80.), post=N)
+        bs.nn.init_all_states(N)
+        for m in (E.syn, I.syn):
+            m.init_state()
+
+        def step(t):
+            spk = N.get_spike() != 0.
+            E(spk[:c['n_exc']])
+            I(spk[c['n_exc']:])
+            return N(c['I_ext'])
+        T = c['steps']
+        cuts = [0, T * 2 // 5, T * 3 // 4, T]
+        outs, runners = [], []
+        for a, b in zip(cuts[:-1], cuts[1:]):
+            outs.append(bs.transform.for_loop(step, torch.arange(a, b) * 0.05))
+            assert bs.transform.last_loop == 'fused'
+            runners.append(N._fused_runner[1])
+        assert runners[0] is runners[1] is runners[2]
+    ras = torch.cat(outs).cpu().numpy() != 0
+    assert ras.sum(1).tolist() == gold['counts']
+    assert make_golden.sha(np.packbits(ras)) == gold['raster_sha256']
+    assert make_golden.sha(N.V.value.cpu().numpy()) == gold['final_V_sha256']
+
+
 def test_hh_module_network_per_neuron_parameters(bs):
     """HH with array-valued gL, gK and V_th (one value per neuron): the eager steps
     (bs_coba_hh_step_arr) equal the oracle given the same arrays; for_loop stays eager."""

@@ -278,3 +278,33 @@ def test_batched_net_per_synapse_weights(bs):
             assert np.array_equal(net.N.V.value[b].cpu().numpy(), refs[b]['V']), (fused, b)
             assert np.array_equal(net.I.syn.g.value[b].cpu().numpy(), refs[b]['gi']), (fused, b)
     assert torch.equal(out[False], out[True])
+
+
+def test_batched_for_loop_chunks_reuse_the_runner(bs):
+    """A batched net (B = 3 replicas, one union runner) run in three for_loop chunks keeps
+    its runner between them and equals the same chunks stepped eagerly."""
+    import torch
+    B = 3
+    say('batched for_loop chunks', B)
+    res = []
+    for fused in (False, True):
+        bs.transform.fuse_loops = fused
+        try:
+            with bs.environ.context(dt=0.1):
+                net = _BatchedEINet(bs, _replica_V0(B))
+                outs, runners = [], []
+                for T in (50, 30, 40):
+                    outs.append(bs.transform.for_loop(net.update, torch.arange(T) * 0.1))
+                    assert bs.transform.last_loop == ('fused' if fused else 'eager')
+                    r = getattr(net.N, '_fused_runner', None)
+                    runners.append(None if r is None else r[1])
+                if fused:
+                    assert runners[0] is runners[1] is runners[2]
+                res.append((torch.cat(outs), net))
+        finally:
+            bs.transform.fuse_loops = True
+    (a, na), (b, nb) = res
+    assert int(a.sum()) > 0
+    assert torch.equal(a, b)
+    assert torch.equal(na.N.V.value, nb.N.V.value)
+    assert torch.equal(na.I.syn.g.value, nb.I.syn.g.value)
