@@ -140,6 +140,12 @@ SIGNATURES = {
     'bs_coba_hh_run': (ctypes.c_int, [ctypes.POINTER(Net), ctypes.POINTER(HhState),
                                       ctypes.POINTER(HhParams), ctypes.c_int64, c_i32, c_vp,
                                       c_vp, c_vp, c_vp, c_vp]),
+    'bs_coba_lif_run_inputs': (ctypes.c_int, [ctypes.POINTER(Net), ctypes.POINTER(LifState),
+                                              ctypes.POINTER(LifParams), c_vp, ctypes.c_int64,
+                                              c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    'bs_coba_hh_run_inputs': (ctypes.c_int, [ctypes.POINTER(Net), ctypes.POINTER(HhState),
+                                             ctypes.POINTER(HhParams), c_vp, ctypes.c_int64,
+                                             c_i32, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'bs_net_grid_blocks': (ctypes.c_int, [ctypes.POINTER(Net)]),
     'bs_net_error': (ctypes.c_int, [c_vp, c_vp]),
     'bs_net_seed_spikes': (ctypes.c_int, [c_vp, c_vp, ctypes.c_int64, c_vp, c_vp]),

@@ -120,9 +120,17 @@ struct NetArgs {
   uint32_t* hash;    // per-workgroup spike hashes [steps][nb] (workspace), or NULL
   uint8_t* raster;
   const float* iext;  // per-neuron external input [n], or NULL (the parameters' I_ext)
+  const float* isched;  // external input of each step of the launch [steps], or NULL
   char* ws;
   NetLayout L;
 };
+
+// One float of a read-only input array, loaded into a VGPR (a vector load: a scalar load
+// would share the LDS accesses' wait counter, and the next LDS wait would wait for it too).
+__device__ __forceinline__ float ld_input(const float* p) {
+  return __uint_as_float(
+      __hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+}
 
 // The parameters with a neuron's own external input.
 template <class P>
@@ -261,7 +269,7 @@ __device__ __forceinline__ int32_t quantize(float w, float scale) {
   return (int32_t)bs_rint(w * scale);
 }
 
-template <class Model, int NPT, bool kHet, bool kIn>
+template <class Model, int NPT, bool kHet, int kIn>
 __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State st,
                                                 typename Model::Params p_arg) {
   // The parameters live in VGPRs (uniform values, one register each) where the model allows:
@@ -344,14 +352,15 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   }
 
   typename Model::Regs r[NPT];
-  float iext[NPT];  // kIn: each neuron's external input, read once per launch
+  // kIn: 0 the parameters' I_ext, 1 each neuron's own (read once per launch), 2 each step's
+  float iext[NPT];  // kIn == 1: each neuron's external input
 #pragma unroll
   for (int q = 0; q < NPT; ++q) {
     const int64_t j = base + q * kBlock + threadIdx.x;
     iext[q] = 0.0f;
     if (j < n) {
       r[q] = Model::load(st, j);
-      if constexpr (kIn) iext[q] = a.iext[j];
+      if constexpr (kIn == 1) iext[q] = a.iext[j];
     }
   }
   bool last[NPT];
@@ -376,10 +385,15 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
   const int ring = L.ring;
   const int64_t dly = L.delay;
   int slot_rd = a.slot_rd, slot_wr = a.slot_wr;  // advance by one slot per step
+  // a per-step input: step t's value, loaded during step t - 1 (at the start of its phase A,
+  // beside the count-word polls, so no wait is added for it)
+  float I_cur = 0.0f, I_next = 0.0f;
+  if constexpr (kIn == 2) I_cur = ld_input(a.isched);
   __syncthreads();
 
   for (int32_t t = 0; t < a.steps; ++t) {
     const int64_t ta = a.t0 + t;  // absolute step index
+    if constexpr (kIn == 2) p.I_ext = I_cur;
 
     // ---- prefetch: synapse rows of neurons that may spike this step, into L2 ----
     // Issued before the waits of phase A, whose loads wait for them anyway, so they cost no
@@ -387,7 +401,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // loads write to LDS (s_junk) rather than registers, so no register is held for them.
 #pragma unroll
     for (int q = 0; q < NPT; ++q) {
-      if (((valid >> q) & 1u) && Model::near(kIn ? with_input(p, iext[q]) : p, r[q])) {
+      if (((valid >> q) & 1u) && Model::near(kIn == 1 ? with_input(p, iext[q]) : p, r[q])) {
         int32_t jv = (int32_t)(jv0 + q * kBlock);
         asm volatile("" : "+v"(jv));  // keeps the row addresses from being hoisted out of the loop
         const Row rw = row_of(a, jv);
@@ -410,6 +424,9 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     // The first look at each count word is issued before the input-independent part of the
     // update (Model::prepare), which runs while those loads are in flight.
     const uint64_t* cin = cnt + ((int64_t)slot_rd * nb + me) * nb;
+    if constexpr (kIn == 2) {
+      if (t + 1 < a.steps) I_next = ld_input(a.isched + t + 1);
+    }
     uint64_t v_first = 0;
     if (Model::kPrepare) {
       if (ta > dly && (int)threadIdx.x < nb * tps) v_first = ld_dev64(cin + threadIdx.x / tps);
@@ -481,7 +498,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
           in_e = repeated_sum(s_tab[0], a.w_e_homo, acc.x);
           in_i = repeated_sum(s_tab[1], a.w_i_homo, acc.y);
         }
-        last[q] = Model::update(kIn ? with_input(p, iext[q]) : p, r[q], in_e, in_i);
+        last[q] = Model::update(kIn == 1 ? with_input(p, iext[q]) : p, r[q], in_e, in_i);
         if (last[q]) h += bs_mix32(jv0 + q * kBlock);
         if (a.raster) a.raster[(int64_t)t * n + (jv0 + q * kBlock)] = last[q] ? 1 : 0;
       }
@@ -664,6 +681,7 @@ __global__ __launch_bounds__(kBlock) void k_run(NetArgs a, typename Model::State
     }
     slot_rd = slot_rd + 1 == ring ? 0 : slot_rd + 1;
     slot_wr = slot_wr + 1 == ring ? 0 : slot_wr + 1;
+    if constexpr (kIn == 2) I_cur = I_next;
   }
 
 #pragma unroll
@@ -984,12 +1002,13 @@ NetArgs make_args(const bs_net* net, const NetLayout& L, void* ws) {
   a.hash = nullptr;
   a.raster = nullptr;
   a.iext = net->I_ext;
+  a.isched = nullptr;
   a.ws = (char*)ws;
   a.L = L;
   return a;
 }
 
-template <class Model, int NPT, bool kHet, bool kIn>
+template <class Model, int NPT, bool kHet, int kIn>
 int launch_one(const NetArgs& a, const typename Model::State& st, const typename Model::Params& p,
                hipStream_t s) {
   int occ = 0;
@@ -1009,7 +1028,7 @@ int launch_one(const NetArgs& a, const typename Model::State& st, const typename
   return BS_OK;
 }
 
-template <class Model, bool kHet, bool kIn>
+template <class Model, bool kHet, int kIn>
 int dispatch_npt(const NetArgs& a, const typename Model::State& st,
                  const typename Model::Params& p, hipStream_t s) {
   switch (a.L.npt) {
@@ -1025,7 +1044,7 @@ int dispatch_npt(const NetArgs& a, const typename Model::State& st,
 template <class Model>
 int run(const bs_net* net, const typename Model::State* st, const typename Model::Params* p,
         int64_t t0, int32_t steps, int32_t* counts_out, uint32_t* hash_out, uint8_t* raster_out,
-        void* workspace, bs_stream_t stream, const char* who) {
+        void* workspace, bs_stream_t stream, const char* who, const float* isched = nullptr) {
   int rc = check_net(net, who);
   if (rc) return rc;
   BS_CHECK_ARG(st && p && workspace, "%s: NULL state/params/workspace", who);
@@ -1054,12 +1073,16 @@ int run(const bs_net* net, const typename Model::State* st, const typename Model
     a.counts = counts_out ? part : nullptr;
     a.hash = hash_out ? part + (size_t)kRunSteps * L.nb : nullptr;
     a.raster = raster_out ? raster_out + (int64_t)done * net->n : nullptr;
-    if (net->I_ext)
-      rc = net->w_e != nullptr ? dispatch_npt<Model, true, true>(a, *st, *p, s)
-                               : dispatch_npt<Model, false, true>(a, *st, *p, s);
+    a.isched = isched ? isched + done : nullptr;
+    if (isched)
+      rc = net->w_e != nullptr ? dispatch_npt<Model, true, 2>(a, *st, *p, s)
+                               : dispatch_npt<Model, false, 2>(a, *st, *p, s);
+    else if (net->I_ext)
+      rc = net->w_e != nullptr ? dispatch_npt<Model, true, 1>(a, *st, *p, s)
+                               : dispatch_npt<Model, false, 1>(a, *st, *p, s);
     else
-      rc = net->w_e != nullptr ? dispatch_npt<Model, true, false>(a, *st, *p, s)
-                               : dispatch_npt<Model, false, false>(a, *st, *p, s);
+      rc = net->w_e != nullptr ? dispatch_npt<Model, true, 0>(a, *st, *p, s)
+                               : dispatch_npt<Model, false, 0>(a, *st, *p, s);
     if (rc) return rc;
     if (counts_out || hash_out) {
       k_sum_parts<<<(len + 3) / 4, 256, 0, s>>>(L.nb, len, a.counts, a.hash,
@@ -1176,7 +1199,8 @@ template <bool kCuba>
 __global__ __launch_bounds__(256) void k_lif_defer_out(int32_t n, float* V, const float* vprev,
                                                        const float* ge, const float* gi,
                                                        const uint8_t* spk, const float* iext,
-                                                       bs_lif_params p) {
+                                                       const float* istep, bs_lif_params p) {
+  if (istep) p.I_ext = *istep;   // the last step's input of a run with per-step inputs
   for (int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x; j < n;
        j += (int64_t)gridDim.x * 256) {
     if (!spk[j]) continue;
@@ -1189,11 +1213,10 @@ __global__ __launch_bounds__(256) void k_lif_defer_out(int32_t n, float* V, cons
 template <bool kCuba, bool kSoft>
 int lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p, int64_t t0,
             int32_t steps, int32_t* counts_out, uint32_t* hash_out, uint8_t* raster_out,
-            void* workspace, bs_stream_t stream) {
-  const char* who = "bs_coba_lif_run";
+            void* workspace, bs_stream_t stream, const char* who, const float* isched) {
   if (!p || !p->deferred_reset || steps <= 0)
     return run<LifModel<kCuba, kSoft>>(net, st, p, t0, steps, counts_out, hash_out, raster_out,
-                                       workspace, stream, who);
+                                       workspace, stream, who, isched);
   int rc = check_net(net, who);
   if (rc) return rc;
   BS_CHECK_ARG(st && workspace, "%s: NULL state/workspace", who);
@@ -1209,7 +1232,7 @@ int lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p, i
   // all but the last step, then V before it, then the last step
   if (steps > 1) {
     rc = run<LifModel<kCuba, kSoft>>(net, st, p, t0, steps - 1, counts_out, hash_out,
-                                     raster_out, workspace, stream, who);
+                                     raster_out, workspace, stream, who, isched);
     if (rc) return rc;
   }
   float* vprev = (float*)((char*)workspace + L.off_vprev);
@@ -1219,11 +1242,52 @@ int lif_run(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p, i
   rc = run<LifModel<kCuba, kSoft>>(net, st, p, t0 + k, 1, counts_out ? counts_out + k : nullptr,
                                    hash_out ? hash_out + k : nullptr,
                                    raster_out ? raster_out + k * net->n : nullptr, workspace,
-                                   stream, who);
+                                   stream, who, isched ? isched + k : nullptr);
   if (rc) return rc;
   k_lif_defer_out<kCuba><<<g, 256, 0, s>>>(net->n, st->V, vprev, st->ge, st->gi, net->spk,
-                                           net->I_ext, *p);
+                                           net->I_ext, isched ? isched + k : nullptr, *p);
   BS_CHECK_LAUNCH();
+  return BS_OK;
+}
+
+}  // namespace
+
+namespace {
+
+int lif_run_any(const bs_net* net, const bs_lif_state* st, const bs_lif_params* p, int64_t t0,
+                int32_t steps, const float* isched, int32_t* counts_out, uint32_t* hash_out,
+                uint8_t* raster_out, void* workspace, bs_stream_t stream, const char* who) {
+  if (st) BS_CHECK_ARG(st->V && st->ge && st->gi && st->ref, "%s: NULL state pointer", who);
+  if (p) BS_CHECK_ARG(p->inv_tau == p->inv_tau, "%s: inv_tau is NaN", who);
+#define BS_RUN(C, S)                                                                    \
+  return lif_run<C, S>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,  \
+                       stream, who, isched)
+  const bool cuba = p && p->cuba, soft = p && p->soft_reset;
+  if (cuba) { if (soft) BS_RUN(true, true); else BS_RUN(true, false); }
+  if (soft) BS_RUN(false, true);
+  BS_RUN(false, false);
+#undef BS_RUN
+}
+
+int hh_run_any(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p, int64_t t0,
+               int32_t steps, const float* isched, int32_t* counts_out, uint32_t* hash_out,
+               uint8_t* raster_out, void* workspace, bs_stream_t stream, const char* who) {
+  if (st) {
+    BS_CHECK_ARG(st->V && st->m && st->h && st->n && st->ge && st->gi,
+                 "%s: NULL state pointer", who);
+  }
+  if (p) BS_CHECK_ARG(p->inv_C == p->inv_C, "%s: inv_C is NaN", who);
+  return run<HhModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
+                      stream, who, isched);
+}
+
+// Checks of the per-step input array of the *_run_inputs entry points.
+int check_inputs(const bs_net* net, const float* I_steps, int32_t steps, const char* who) {
+  BS_CHECK_ARG(net != nullptr, "%s: net is NULL", who);
+  BS_CHECK_ARG(I_steps != nullptr || steps <= 0, "%s: I_steps is NULL", who);
+  BS_CHECK_ARG(net->I_ext == nullptr,
+               "%s: per-step inputs and per-neuron inputs (net->I_ext) do not combine", who);
+  BS_CHECK_ARG(((uintptr_t)I_steps & 3) == 0, "%s: I_steps not 4-byte aligned", who);
   return BS_OK;
 }
 
@@ -1234,18 +1298,21 @@ extern "C" int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const 
                                uint32_t* hash_out, uint8_t* raster_out, void* workspace,
                                bs_stream_t stream) {
   bs_clear_error();
-  if (st) {
-    BS_CHECK_ARG(st->V && st->ge && st->gi && st->ref, "bs_coba_lif_run: NULL state pointer");
-  }
-  if (p) BS_CHECK_ARG(p->inv_tau == p->inv_tau, "bs_coba_lif_run: inv_tau is NaN");
-#define BS_RUN(C, S)                                                                    \
-  return lif_run<C, S>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,  \
-                       stream)
-  const bool cuba = p && p->cuba, soft = p && p->soft_reset;
-  if (cuba) { if (soft) BS_RUN(true, true); else BS_RUN(true, false); }
-  if (soft) BS_RUN(false, true);
-  BS_RUN(false, false);
-#undef BS_RUN
+  return lif_run_any(net, st, p, t0, steps, nullptr, counts_out, hash_out, raster_out,
+                     workspace, stream, "bs_coba_lif_run");
+}
+
+extern "C" int bs_coba_lif_run_inputs(const bs_net* net, const bs_lif_state* st,
+                                      const bs_lif_params* p, const float* I_steps, int64_t t0,
+                                      int32_t steps, int32_t* counts_out, uint32_t* hash_out,
+                                      uint8_t* raster_out, void* workspace,
+                                      bs_stream_t stream) {
+  bs_clear_error();
+  const char* who = "bs_coba_lif_run_inputs";
+  int rc = check_inputs(net, I_steps, steps, who);
+  if (rc) return rc;
+  return lif_run_any(net, st, p, t0, steps, I_steps, counts_out, hash_out, raster_out,
+                     workspace, stream, who);
 }
 
 extern "C" int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,
@@ -1253,13 +1320,20 @@ extern "C" int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs
                               uint32_t* hash_out, uint8_t* raster_out, void* workspace,
                               bs_stream_t stream) {
   bs_clear_error();
-  if (st) {
-    BS_CHECK_ARG(st->V && st->m && st->h && st->n && st->ge && st->gi,
-                 "bs_coba_hh_run: NULL state pointer");
-  }
-  if (p) BS_CHECK_ARG(p->inv_C == p->inv_C, "bs_coba_hh_run: inv_C is NaN");
-  return run<HhModel>(net, st, p, t0, steps, counts_out, hash_out, raster_out, workspace,
-                      stream, "bs_coba_hh_run");
+  return hh_run_any(net, st, p, t0, steps, nullptr, counts_out, hash_out, raster_out,
+                    workspace, stream, "bs_coba_hh_run");
+}
+
+extern "C" int bs_coba_hh_run_inputs(const bs_net* net, const bs_hh_state* st,
+                                     const bs_hh_params* p, const float* I_steps, int64_t t0,
+                                     int32_t steps, int32_t* counts_out, uint32_t* hash_out,
+                                     uint8_t* raster_out, void* workspace, bs_stream_t stream) {
+  bs_clear_error();
+  const char* who = "bs_coba_hh_run_inputs";
+  int rc = check_inputs(net, I_steps, steps, who);
+  if (rc) return rc;
+  return hh_run_any(net, st, p, t0, steps, I_steps, counts_out, hash_out, raster_out,
+                    workspace, stream, who);
 }
 
 extern "C" int bs_net_error(const void* workspace, bs_stream_t stream) {

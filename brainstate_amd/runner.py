@@ -120,28 +120,42 @@ class EINetRunner:
     def grid_blocks(self):
         return int(N.lib().bs_net_grid_blocks(ctypes.byref(self._net)))
 
-    def run(self, steps, counts=None, hashes=None, raster=None):
+    def run(self, steps, counts=None, hashes=None, raster=None, inputs=None):
         """Advance ``steps`` steps in one launch.  Optional int32/uint32 [steps] outputs and a
-        uint8 [steps, n] raster are filled on the device."""
+        uint8 [steps, n] raster are filled on the device.  ``inputs`` (optional, [steps]):
+        each step's external input in place of ``params.I_ext`` (bs_coba_*_run_inputs)."""
         s = self.state
         stream = N.stream_handle(self.device)
+        steps = int(steps)
+        tail = (N.ptr(counts), N.ptr(hashes), N.ptr(raster), N.ptr(self.ws), stream)
+        if inputs is not None:
+            inputs = torch.as_tensor(inputs, dtype=torch.float32,
+                                     device=self.device).reshape(-1).contiguous()
+            if inputs.numel() != steps:
+                raise ValueError(f'run: {inputs.numel()} inputs for {steps} steps')
         if self.model == 'lif':
             st = N.LifState(s['V'].data_ptr(), s['ge'].data_ptr(), s['gi'].data_ptr(),
                             s['ref'].data_ptr())
-            rc = N.lib().bs_coba_lif_run(ctypes.byref(self._net), ctypes.byref(st),
-                                         ctypes.byref(self.params), self.t, int(steps),
-                                         N.ptr(counts), N.ptr(hashes), N.ptr(raster),
-                                         N.ptr(self.ws), stream)
+            if inputs is None:
+                rc = N.lib().bs_coba_lif_run(ctypes.byref(self._net), ctypes.byref(st),
+                                             ctypes.byref(self.params), self.t, steps, *tail)
+            else:
+                rc = N.lib().bs_coba_lif_run_inputs(ctypes.byref(self._net), ctypes.byref(st),
+                                                    ctypes.byref(self.params), N.ptr(inputs),
+                                                    self.t, steps, *tail)
             N.check(rc, 'bs_coba_lif_run')
         else:
             st = N.HhState(s['V'].data_ptr(), s['m'].data_ptr(), s['h'].data_ptr(),
                            s['n'].data_ptr(), s['ge'].data_ptr(), s['gi'].data_ptr())
-            rc = N.lib().bs_coba_hh_run(ctypes.byref(self._net), ctypes.byref(st),
-                                        ctypes.byref(self.params), self.t, int(steps),
-                                        N.ptr(counts), N.ptr(hashes), N.ptr(raster),
-                                        N.ptr(self.ws), stream)
+            if inputs is None:
+                rc = N.lib().bs_coba_hh_run(ctypes.byref(self._net), ctypes.byref(st),
+                                            ctypes.byref(self.params), self.t, steps, *tail)
+            else:
+                rc = N.lib().bs_coba_hh_run_inputs(ctypes.byref(self._net), ctypes.byref(st),
+                                                   ctypes.byref(self.params), N.ptr(inputs),
+                                                   self.t, steps, *tail)
             N.check(rc, 'bs_coba_hh_run')
-        self.t += int(steps)
+        self.t += steps
 
     def check(self):
         """Synchronise and raise if a run's wait hit its spin limit or the per-synapse weights

@@ -424,6 +424,16 @@ def _same_key(a, b):
     return True
 
 
+def _scalar_of(v):
+    """A recorded input as one float (a number, or a one-element array or tensor), or None."""
+    if torch.is_tensor(v) or isinstance(v, np.ndarray):
+        return float(v.reshape(-1)[0]) if int(np.prod(tuple(v.shape))) == 1 else None
+    try:
+        return float(v)
+    except (TypeError, ValueError):
+        return None
+
+
 def _runner_for(neuron, pe, pi, n_exc, inp):
     """The persistent runner of this net: the one the last loop on it built, reloaded with
     the modules' current state, while connectivity, weights and input kind are unchanged
@@ -449,7 +459,8 @@ def _runner_for(neuron, pe, pi, n_exc, inp):
 def _fused_loop(f, xs, length):
     """for_loop through the persistent runner: the steps are recorded first (``_record``);
     when every one is the E/I step the runner implements, the runner advances all of them
-    from the modules' state -- one launch per run of equal inputs -- and writes the final
+    from the modules' state -- one launch with the per-step inputs when they are numbers,
+    else one per run of equal inputs -- and writes the final
     state back.  Returns the stacked output (a tensor, or a list of None), or None when the
     loop must run eagerly."""
     plan = _record(f, xs, length)
@@ -475,9 +486,17 @@ def _fused_loop(f, xs, length):
         direct = ident and rdtype in (torch.bool, torch.uint8)
         raster = (res.view(torch.uint8).view(T, -1) if direct else
                   torch.empty(T, r.n, dtype=torch.uint8, device=r.device))
-    for t0, steps, v in segs:
-        r.set_input(v)
-        r.run(steps, raster=None if raster is None else raster[t0:t0 + steps])
+    scalars = [_scalar_of(v) for _, _, v in segs]
+    if len(segs) > 1 and r.I_ext is None and all(x is not None for x in scalars):
+        # inputs that change between steps: every step's value in one array, one launch
+        per_step = np.empty(T, np.float32)
+        for (t0, steps, _), x in zip(segs, scalars):
+            per_step[t0:t0 + steps] = x
+        r.run(T, raster=raster, inputs=torch.from_numpy(per_step).to(r.device))
+    else:
+        for t0, steps, v in segs:
+            r.set_input(v)
+            r.run(steps, raster=None if raster is None else raster[t0:t0 + steps])
     r.check()
     r.write_back()
     if rdtype is None:
@@ -499,7 +518,8 @@ def for_loop(f, *xs, length=None, reverse=False, unroll=1, pbar=None):
     network step the persistent runner implements (the two event projections of one LIFRef
     or HH population fed its spikes, then the population called with one input -- the
     update of examples/105_COBA_HH_2007_braincell.py and of the SNN tutorial), the runner
-    advances all steps, one launch per run of equal inputs, and the state is written back at
+    advances all steps (one launch, with the per-step inputs when they are numbers; one per
+    run of equal per-neuron input arrays), and the state is written back at
     the end.  Anything else -- other modules, State assignments outside modules, state used
     for anything but the projections' spike vectors, inputs the runner does not take --
     runs eagerly step by step.  Python side effects of ``f`` happen in the recording pass

@@ -420,6 +420,18 @@ BS_API int bs_coba_lif_run(const bs_net* net, const bs_lif_state* st, const bs_l
 BS_API int bs_coba_hh_run(const bs_net* net, const bs_hh_state* st, const bs_hh_params* p,
                           int64_t t0, int32_t steps, int32_t* counts_out, uint32_t* hash_out,
                           uint8_t* raster_out, void* workspace, bs_stream_t stream);
+/* The same runs with an external input per step: I_steps [steps] (device, fp32) is step
+ * t0 + k's input in place of p->I_ext, as a loop over xs passes each step its own x
+ * (`for_loop(f, xs)`, brainstate/transform/_loop_collect_return.py:487-572, whose scan body
+ * calls N(x_t)); one launch however the input changes.  Not combined with net->I_ext. */
+BS_API int bs_coba_lif_run_inputs(const bs_net* net, const bs_lif_state* st,
+                                  const bs_lif_params* p, const float* I_steps, int64_t t0,
+                                  int32_t steps, int32_t* counts_out, uint32_t* hash_out,
+                                  uint8_t* raster_out, void* workspace, bs_stream_t stream);
+BS_API int bs_coba_hh_run_inputs(const bs_net* net, const bs_hh_state* st,
+                                 const bs_hh_params* p, const float* I_steps, int64_t t0,
+                                 int32_t steps, int32_t* counts_out, uint32_t* hash_out,
+                                 uint8_t* raster_out, void* workspace, bs_stream_t stream);
 
 /* Pending spikes for a run that starts at step t0 >= 1 (synaptic delay 0): spk [n] (nonzero
  * = spike) are taken as the spikes of step t0 - 1, so step t0's inputs come from them, as

@@ -6,7 +6,7 @@ import sys
 import numpy as np
 import pytest
 
-from oracle import network
+from oracle import network, neuron
 
 pytestmark = pytest.mark.gpu
 
@@ -640,3 +640,64 @@ def test_config5_full_length_matches_c(torch_cuda):
     assert hashes.tolist() == h_ref.tolist()
     for key in ('V', 'm', 'h', 'n', 'ge', 'gi'):
         assert np.array_equal(r.state[key].cpu().numpy(), st[key]), key
+
+
+@pytest.mark.parametrize('model,deferred', [('lif', False), ('lif', True), ('hh', False)])
+def test_runner_per_step_inputs(torch_cuda, model, deferred):
+    """bs_coba_*_run_inputs: one launch whose steps each take their own external input equals
+    the same steps run one launch each with that input in the parameters, bit for bit
+    (raster, final state); the LIF runs also equal the oracle stepped with the same inputs."""
+    from brainstate_amd import ops
+    from brainstate_amd.runner import EINetRunner
+    torch = torch_cuda
+    T = 60
+    say('runner per-step inputs', model, deferred, T)
+    rng = np.random.RandomState(11)
+    if model == 'lif':
+        pe, pi, V0, _ = make_golden.config1_net()
+        c = make_golden.CONFIG1
+        I = (20.0 + rng.uniform(-4.0, 4.0, T)).astype(F)
+        mk = lambda: EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx, c['w_e'], c['w_i'],  # noqa: E731
+                                 ops.lif_params(deferred_reset=deferred), V0)
+    else:
+        pe, pi, V0, _ = make_golden.hh_net()
+        c = make_golden.HH_NET
+        I = (c['I_ext'] + rng.uniform(-1.0, 1.0, T)).astype(F)
+        mk = lambda: EINetRunner('hh', c['n'], c['n_exc'], pe.idx, pi.idx, c['w_e'], c['w_i'],  # noqa: E731
+                                 ops.hh_params(I_ext=c['I_ext']), V0)
+    ra, rb = mk(), mk()
+    ras_a = torch.zeros(T, c['n'], dtype=torch.uint8, device='cuda')
+    ras_b = torch.zeros_like(ras_a)
+    ra.run(T, raster=ras_a, inputs=torch.from_numpy(I))
+    for t in range(T):
+        rb.params.I_ext = float(I[t])
+        rb.run(1, raster=ras_b[t:t + 1])
+    ra.check()
+    rb.check()
+    assert int(ras_a.sum()) > 0
+    assert torch.equal(ras_a, ras_b)
+    for k in ra.state:
+        assert torch.equal(ra.state[k], rb.state[k]), k
+    if model == 'lif':
+        init = None
+        rows = []
+        for t in range(T):
+            p = neuron.LIFParams(I_ext=float(I[t]), deferred_reset=deferred)
+            res = network.run_coba_lif(V0, pe, pi, p, c['n_exc'], 1, init=init)
+            init = (res['V'], res['ge'], res['gi'], res['ref'], res['spk'])
+            rows.append(res['raster'][0])
+        assert np.array_equal(ras_a.cpu().numpy() != 0, np.stack(rows))
+        assert np.array_equal(ra.state['V'].cpu().numpy(), init[0])
+
+
+def test_runner_per_step_inputs_rejects_per_neuron_inputs(torch_cuda):
+    """Per-step inputs do not combine with a runner built with one input per neuron."""
+    from brainstate_amd import _native as N, ops
+    from brainstate_amd.runner import EINetRunner
+    torch = torch_cuda
+    pe, pi, V0, _ = make_golden.config1_net()
+    c = make_golden.CONFIG1
+    r = EINetRunner('lif', c['n'], c['n_exc'], pe.idx, pi.idx, c['w_e'], c['w_i'],
+                    ops.lif_params(), V0, I_ext=np.full(c['n'], 20.0, F))
+    with pytest.raises(N.NativeError, match='do not combine'):
+        r.run(3, inputs=torch.full((3,), 20.0))
