@@ -187,6 +187,7 @@ def fuse(neuron, proj_e, proj_i, n_exc, inp=0.0, delay=None):
         r.state['V'].copy_(to_runner(neuron.V.value))
         load_state()
         r.seed(to_runner(neuron.spike.value.to(torch.uint8)), r.t + 1)
+        r.dt = environ.get_dt()
 
     r.write_back = write_back
     r.set_input = set_input
