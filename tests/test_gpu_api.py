@@ -172,26 +172,35 @@ def _for_loop_paths(bs, make_step, T, dt=0.1):
     return res
 
 
-def test_for_loop_chunks_reuse_the_runner(bs):
+@pytest.mark.parametrize('het', [False, True])
+def test_for_loop_chunks_reuse_the_runner(bs, het):
     """Loops run in chunks on one net keep its persistent runner (no new set-up) and reload
     the modules' state each time: chunks of 60, 40 and 50 steps with the state changed
     between chunks (V shifted, the E conductances scaled) equal the same chunks stepped
-    eagerly with the same changes; a new weight value builds a new runner."""
+    eagerly with the same changes; a new weight value builds a new runner.  With per-synapse
+    weights (N(0.6, 0.06) / N(6.7, 0.67)) the eager steps use the runner's fixed-point sums,
+    so both paths stay bit-equal."""
     import torch
-    print('[case] for_loop chunks reuse the runner', flush=True)
+    print('[case] for_loop chunks reuse the runner', het, flush=True)
     res = []
     for fused in (False, True):
         bs.transform.fuse_loops = fused
         try:
             with bs.environ.context(dt=0.1):
-                net = _EINet(bs)
+                if het:
+                    net = _EINet(bs, w_e=bs.nn.init.Normal(0.6, 0.06, seed=5),
+                                 w_i=bs.nn.init.Normal(6.7, 0.67, seed=6))
+                else:
+                    net = _EINet(bs)
                 outs, runners = [], []
                 for i, T in enumerate((60, 40, 50)):
                     if i == 1:
                         net.N.V.value = net.N.V.value + 0.25
                         net.E.syn.g.value = net.E.syn.g.value * 1.5
                     if i == 2:
-                        net.E.comm.weight.value = 0.7
+                        w = net.E.comm.weight.value
+                        net.E.comm.weight.value = (np.asarray(w) * F(1.1)).astype(F) if het \
+                            else 0.7
                     outs.append(bs.transform.for_loop(net.update, torch.arange(T) * 0.1))
                     assert bs.transform.last_loop == ('fused' if fused else 'eager')
                     r = getattr(net.N, '_fused_runner', None)
