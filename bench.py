@@ -429,6 +429,30 @@ def bench_conn(args):
              'speedup': (host + h2d) / min(dev), 'bit_equal_to_numpy': equal}]
 
 
+def bench_compact(args):
+    """Spike compaction (row a8: bool -> ascending int32 index list + count) at 100k, 1M and
+    4M spikes, p = 0.002 and 0.1, u8 spikes: per call through ops.spike_compact (the Python
+    wrapper included) and per launch captured in a HIP graph.  Byte model: n bytes of spikes
+    read + 4 bytes per active index written."""
+    import torch
+    from brainstate_amd import ops
+    lines = []
+    for n in (100_000, 1_000_000, 4_000_000):
+        for p in (0.002, 0.1):
+            spk = torch.from_numpy((np.random.RandomState(n % 997).rand(n) < p)
+                                   .astype(np.uint8)).cuda()
+            idx, cnt = ops.spike_compact(spk)
+            act = int(cnt.item())
+            assert act == int(spk.sum())
+            t = _timed(lambda: ops.spike_compact(spk), 50)
+            tg = _graph_timed(lambda: ops.spike_compact(spk), 20)
+            b = n + 4 * act
+            lines.append({'workload': f'spike_compact_{n}_p{p}', 'n': n, 'active': act,
+                          'us_per_call': t * 1e6, 'graph_us_per_call': tg * 1e6,
+                          'alg_bytes': b, 'frac': b / tg / PEAK_HBM})
+    return lines
+
+
 def bench_vjp(args):
     """Reverse mode of the two event products (row f2): the event mat-vec at configs[1]'s shape
     (100k x 100k, K = 1000, per-synapse w, spikes at p = 0.1, a dense upstream gradient):
@@ -556,13 +580,13 @@ def main():
     ap.add_argument('--anchor', default=None, help='--summarize: kernel name substring')
     ap.add_argument('--workload', default='coba_lif_1m',
                     choices=['coba_lif_1m', 'sparse', 'event_linear', 'hh', 'conn', 'batch',
-                             'for_loop', 'vjp'],
+                             'for_loop', 'vjp', 'compact'],
                     help='coba_lif_1m is the reported line; the others measure the other configs')
     args = ap.parse_args()
     if args.workload != 'coba_lif_1m':
         fn = {'sparse': bench_sparse, 'event_linear': bench_event_linear, 'hh': bench_hh,
               'conn': bench_conn, 'batch': bench_batch, 'for_loop': bench_for_loop,
-              'vjp': bench_vjp}
+              'vjp': bench_vjp, 'compact': bench_compact}
         for line in fn[args.workload](args):
             print(json.dumps(line), flush=True)
         return
