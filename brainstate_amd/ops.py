@@ -445,11 +445,23 @@ def dense_digits(n_in):
     return int(N.lib().bs_event_dense_digits(int(n_in)))
 
 
+class _PackedW(dict):
+    """``pack_dense``'s result.  ``P['finite']`` is read from the packed buffer's status word
+    on first use (one synchronisation), so packing alone does not stop the host."""
+
+    def __missing__(self, key):
+        if key != 'finite':
+            raise KeyError(key)
+        v = int(self['packed'][:4].view(torch.int32).item()) == 0
+        self['finite'] = v
+        return v
+
+
 def pack_dense(W):
     """Pack W [n_in, n_out] fp32 for ``event_dense_packed`` (bs_event_dense_pack): per-column
     fixed-point digits in the matrix-core operand order.  Returns a dict with the packed
     buffer and ``finite`` (False when a weight is inf or NaN: the packed product then returns
-    NaN everywhere).  Reading the status synchronises the stream once per packing."""
+    NaN everywhere), read from the device on first access (one synchronisation)."""
     W = W.contiguous()
     n_in, n_out = int(W.shape[0]), int(W.shape[1])
     nbytes = int(N.lib().bs_event_dense_packed_bytes(n_in, n_out))
@@ -458,9 +470,7 @@ def pack_dense(W):
     buf = torch.empty(nbytes, dtype=torch.uint8, device=W.device)   # 256-byte aligned
     N.check(N.lib().bs_event_dense_pack(N.ptr(W), n_in, n_out, N.ptr(buf), nbytes,
                                         N.stream_handle(W.device)), 'bs_event_dense_pack')
-    finite = int(buf[:4].view(torch.int32).item()) == 0
-    return {'packed': buf, 'n_in': n_in, 'n_out': n_out, 'L': dense_digits(n_in),
-            'finite': finite}
+    return _PackedW(packed=buf, n_in=n_in, n_out=n_out, L=dense_digits(n_in))
 
 
 def event_dense_packed(spk, P, out=None):
